@@ -1,0 +1,198 @@
+/* SPDX-License-Identifier: MIT
+ *
+ * libornith_hip — HIP/gfx950 backend extensions for the routed-MoE hot path.
+ *
+ * Plain C ABI: opaque handles, plain pointers and sizes, int status codes
+ * (ORN_OK = 0, negative on error) with a per-context message from
+ * gpu_last_error().  One HIP stream per context; single host thread per
+ * context.  Unless ORN_MOE_ASYNC is given, calls are synchronous at return
+ * like every gpu.h call.
+ */
+#ifndef ORNITH_HIP_H
+#define ORNITH_HIP_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "gpu.h"
+#include "kquant.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ORN_OK 0
+#define ORN_EINVAL (-1)
+#define ORN_ENOMEM (-2)
+#define ORN_EHIP (-3)
+#define ORN_EUNSUPPORTED (-4)
+
+/* Last error message of a context ("" if none).  No reference counterpart:
+ * the reference reports errors through err_buf strings (gguf.c:408-429). */
+const char *gpu_last_error(gpu_context *ctx);
+
+/* Device address of a buffer (for interop and tests). */
+void *gpu_device_ptr(gpu_context *ctx, gpu_buffer *buf);
+
+/* Name, compute-unit count and HBM size of the context's device. */
+int gpu_device_info(gpu_context *ctx, char *name, size_t name_len, int *n_cus, size_t *hbm_bytes);
+
+/* ---------------------------------------------------------------------------
+ * Dequantization on the device — the expert-slice / dequant API of
+ * engine/src/gguf.h:111-137 with the same validation and bool results.
+ *
+ * orn_tensor_info is layout-compatible with gguf_tensor_info (gguf.h:15-23),
+ * so the engine can pass its descriptors directly.
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    const char *name;
+    int type; /* orn_type / ggml_type */
+    uint32_t n_dims;
+    uint64_t dims[4];
+    size_t offset;
+    size_t size_bytes;
+    size_t n_elems;
+} orn_tensor_info;
+
+/* gguf_dequantize_tensor_from_buf (gguf.h:115-117, gguf.c:605-638):
+ * host bytes in, host floats out; the work runs on the GPU. */
+bool gpu_dequantize_tensor_from_buf(gpu_context *ctx, const void *data,
+                                    const orn_tensor_info *tensor, float *output);
+
+/* gguf_dequantize_expert_slice_from_buf (gguf.h:119-127, gguf.c:652-711):
+ * interleaved fused tensor, slice[i] = full[i*E + expert], E = last dim. */
+bool gpu_dequantize_expert_slice_from_buf(gpu_context *ctx, const void *data,
+                                          const orn_tensor_info *tensor, int expert_idx,
+                                          float *output);
+
+/* Device-resident variants of the two calls above (data and output are
+ * buffers of this context; output must hold n_elems (or n_elems/E) floats). */
+bool gpu_dequantize_tensor_buf(gpu_context *ctx, const gpu_buffer *data,
+                               const orn_tensor_info *tensor, gpu_buffer *output);
+bool gpu_dequantize_expert_slice_buf(gpu_context *ctx, const gpu_buffer *data,
+                                     const orn_tensor_info *tensor, int expert_idx,
+                                     gpu_buffer *output);
+
+/* ---------------------------------------------------------------------------
+ * Resident routed-MoE layers.  Replaces the per-token expert loop of
+ * model.c:1009-1143 (router model.c:1017-1025, selection model.c:1027-1049 /
+ * model_get_routing model.c:264-321, slice cache model.c:692-753, expert FFN
+ * model.c:1080-1090, combine model.c:1056-1090) and the shared expert of
+ * model.c:1003-1007 with one call per layer.
+ * ------------------------------------------------------------------------- */
+typedef struct ornith_moe_store ornith_moe_store;
+
+typedef struct {
+    int n_layers;   /* 40 for Ornith */
+    int d_model;    /* D = 2048; multiple of 256 */
+    int hidden;     /* H = 512 (expert_feed_forward_length); multiple of 256, <= 1024 */
+    int n_experts;  /* E = 256 (<= 256) */
+    int top_k;      /* k = 8 (<= 16) */
+    int has_shared; /* 1: one always-on shared expert (model.c:1001-1007) */
+} ornith_moe_shape;
+
+enum { ORN_MAT_GATE = 0, ORN_MAT_UP = 1, ORN_MAT_DOWN = 2 };
+
+ornith_moe_store *gpu_moe_store_create(gpu_context *ctx, const ornith_moe_shape *shape);
+void gpu_moe_store_destroy(gpu_context *ctx, ornith_moe_store *store);
+size_t gpu_moe_store_bytes(const ornith_moe_store *store);
+
+/* Upload n consecutive experts of one matrix of one layer.  `blocks` holds,
+ * for each expert, the GGUF block stream of its matrix in the reference's
+ * vec@mat orientation (gate/up: K=D rows x M=H cols, Q4_K; down: K=H rows x
+ * M=D cols, Q6_K), i.e. what gguf_dequantize_tensor_from_buf would read for
+ * that expert.  expert_first == n_experts selects the shared expert.  The
+ * store permutes whole blocks (never re-quantizes). */
+int gpu_moe_store_set_experts(gpu_context *ctx, ornith_moe_store *store, int layer, int matrix,
+                              int expert_first, int n, const void *blocks);
+
+/* Router weights W[d*E + e] (model.c:1022 layout) and an optional additive
+ * per-expert logit bias (NULL = none).  */
+int gpu_moe_store_set_router(gpu_context *ctx, ornith_moe_store *store, int layer,
+                             const float *W, const float *bias);
+
+/* RMSNorm weights applied when ORN_MOE_NORM is set (post_attention_norm,
+ * model.c:996).  Default: all ones. */
+int gpu_moe_store_set_norm(gpu_context *ctx, ornith_moe_store *store, int layer,
+                           const float *w);
+
+/* Fill one layer from the deterministic synthetic generator (orn_synth_*),
+ * with an optional Zipf(s) router bias when zipf_s > 0. */
+int gpu_moe_store_fill_synthetic(gpu_context *ctx, ornith_moe_store *store, int layer,
+                                 uint64_t seed, float zipf_s);
+
+enum { ORN_ROUTE_RENORM = 0, ORN_ROUTE_LITERAL = 1 };
+#define ORN_MOE_ASYNC 1u /* return without synchronising the stream */
+#define ORN_MOE_NORM 2u  /* expert input = rmsnorm(x, layer norm weights) */
+
+typedef struct {
+    int route_mode; /* ORN_ROUTE_RENORM (default, model_get_routing) or ORN_ROUTE_LITERAL */
+    unsigned flags; /* ORN_MOE_* */
+} ornith_moe_opts;
+
+/* One MoE block for n_tokens rows of x ([T][D] fp32):
+ *   out = (resid + shared(xin)) + sum_a w_a * expert_a(xin),
+ *   xin = (flags & ORN_MOE_NORM) ? rmsnorm(x) : x;  resid may be NULL (zeros).
+ * idx_out ([T][k] uint32) and w_out ([T][k] fp32) may be NULL.  out may not
+ * alias x or resid. */
+int gpu_moe_forward(gpu_context *ctx, ornith_moe_store *store, int layer, const gpu_buffer *x,
+                    int n_tokens, const gpu_buffer *resid, gpu_buffer *out, gpu_buffer *idx_out,
+                    gpu_buffer *w_out, const ornith_moe_opts *opts);
+
+/* Layer stack: for l in [first, first+n): x <- x + MoE_l(rmsnorm(x)) (the
+ * per-layer MoE residual structure of model.c:992-1144).  tmp must hold
+ * n_tokens*D floats. */
+int gpu_moe_forward_stack(gpu_context *ctx, ornith_moe_store *store, int first_layer,
+                          int n_layers, gpu_buffer *x, gpu_buffer *tmp, int n_tokens,
+                          const ornith_moe_opts *opts);
+
+/* Counters of the last forward: number of active expert slots (incl. the
+ * shared expert), token rows, and tokens whose top-k needed the exact
+ * sequential fallback. */
+int gpu_moe_last_stats(gpu_context *ctx, int *n_slots, int *n_rows, int *n_exact);
+
+/* ---------------------------------------------------------------------------
+ * Kernel timing with HIP events recorded on the context's stream around every
+ * launch of the MoE path (no reference counterpart; the reference times the
+ * MoE block with clock_gettime, model.c:940-1148).
+ * ------------------------------------------------------------------------- */
+int gpu_profile_enable(gpu_context *ctx, int on);
+void gpu_profile_reset(gpu_context *ctx);
+int gpu_profile_count(gpu_context *ctx);
+const char *gpu_profile_name(gpu_context *ctx, int i);
+double gpu_profile_total_ms(gpu_context *ctx, int i);
+long gpu_profile_calls(gpu_context *ctx, int i);
+
+/* ---------------------------------------------------------------------------
+ * Deterministic synthetic workload generator (host).  Counter-based
+ * (SplitMix64 finaliser), so any block of any tensor can be produced
+ * independently; quantized blocks use integer arithmetic only and halves are
+ * rounded to nearest-even, so the bytes are identical on every host.
+ * ------------------------------------------------------------------------- */
+enum {
+    ORN_SYN_GATE = 1,
+    ORN_SYN_UP = 2,
+    ORN_SYN_DOWN = 3,
+    ORN_SYN_ROUTER = 4,
+    ORN_SYN_ACT = 5,
+    ORN_SYN_ZIPF = 6
+};
+uint64_t orn_synth_stream(int layer, int kind, int expert);
+/* Q4_K: d, dmin ~ fp16(U(0.001, 0.01)); 12 random scale bytes; random qs. */
+void orn_synth_q4k(uint64_t seed, uint64_t stream, uint64_t first_block, uint64_t n_blocks,
+                   void *out);
+/* Q6_K: random ql/qh; int8 scales uniform in [-32, 31]; d ~ fp16(U(0.001, 0.01)). */
+void orn_synth_q6k(uint64_t seed, uint64_t stream, uint64_t first_block, uint64_t n_blocks,
+                   void *out);
+/* Approximately normal (Irwin-Hall sum of 12 16-bit uniforms, exact in
+ * binary) scaled by sigma and rounded once to fp32. */
+void orn_synth_normal(uint64_t seed, uint64_t stream, uint64_t n, float sigma, float *out);
+/* Zipf(s) logit bias: b_e = -s * ln(rank_e), rank a seeded permutation of 1..E. */
+void orn_synth_zipf_bias(uint64_t seed, uint64_t stream, int n_experts, float s, float *out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ORNITH_HIP_H */

@@ -1,0 +1,118 @@
+/* SPDX-License-Identifier: MIT
+ *
+ * ORACLE — test infrastructure only.
+ *
+ * A C99 restatement of instax-dutta/ornith-flight's CPU arithmetic for the
+ * routed-MoE hot path.  It is the checker for the HIP implementation: only
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it,
+ * and never as the thing that is measured or shipped.
+ *
+ * Every function states the reference file:line it follows.  Arithmetic is
+ * plain fp32 in the reference's operation order; build with
+ * -O2 -ffp-contract=off (no FMA contraction, no reassociation).
+ *
+ * Pinning (what checks each function against something independent):
+ *   orc_fp16_to_fp32        golden vectors from the compiled reference dequant
+ *                           (special patterns 0x0000/0x8000/subnormal/inf/nan)
+ *                           + closed form over all 65536 inputs in tests
+ *   orc_dequant_block_*     reference known-answer tests (1.0 / -31.0), golden
+ *                           vectors from the compiled reference, closed form
+ *   orc_q4k_one/q6k_one     equality with the block dequant at all 256 positions
+ *   orc_dequant_tensor      golden vectors from the compiled reference
+ *   orc_dequant_expert_slice golden vectors + the reference's slice identity
+ *   orc_router_logits       golden routing from the compiled reference
+ *                           (model_get_routing) + fp64 bound
+ *   orc_topk_renorm         golden routing from the compiled reference incl.
+ *                           constructed exact ties
+ *   orc_topk_literal        golden layer outputs from the compiled reference
+ *                           model_forward (selection changes the output)
+ *   orc_moe_layer (both layouts, both modes) golden layer outputs from the
+ *                           compiled reference model_forward (interleaved
+ *                           layout) + fp64 brute force (contiguous layout)
+ */
+#ifndef ORNITH_ORACLE_H
+#define ORNITH_ORACLE_H
+
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+float orc_fp16_to_fp32(uint16_t h);
+void orc_scale_min_k4(int j, const uint8_t *scales, uint8_t *sc, uint8_t *m);
+void orc_dequant_block_q4k(const uint8_t *blk, float *y);
+void orc_dequant_block_q6k(const uint8_t *blk, float *y);
+float orc_q4k_one(const uint8_t *blk, int pos);
+float orc_q6k_one(const uint8_t *blk, int pos);
+
+/* Whole-tensor dequant. Returns 1 on success, 0 on NULL args / unsupported type. */
+int orc_dequant_tensor(const void *data, int type, uint64_t n_elems, float *out);
+
+/* Interleaved expert slice: slice[i] = full[i * n_experts + expert].
+ * Returns 1 on success, 0 on NULL args, expert < 0, expert >= n_experts,
+ * n_experts == 0 or unsupported type. */
+int orc_dequant_expert_slice(const void *data, int type, uint64_t n_elems,
+                             uint64_t n_experts, int expert, float *out);
+
+/* Sequential fp32 router logits, logits[e] = sum_d x[d] * W[d*E + e]; an
+ * optional bias is added after the sum (bias may be NULL). */
+void orc_router_logits(const float *x, const float *W, int D, int E,
+                       const float *bias, float *logits);
+
+/* Exchange sort on logits + softmax over the top-k (model_get_routing). */
+int orc_topk_renorm(const float *logits, int E, int k, uint32_t *idx, float *w);
+
+/* Full softmax, then k passes of exchange selection on the probabilities
+ * (model_forward inline routing). Weights are not renormalised. */
+int orc_topk_literal(const float *logits, int E, int k, uint32_t *idx, float *w);
+
+float orc_silu_clamped(float x);
+float orc_silu_plain(float x);
+void orc_matvec(float *out, const float *vec, const float *mat, int K, int M);
+void orc_rmsnorm(float *out, const float *x, const float *w, int dim);
+
+/* Routing modes. */
+#define ORC_MODE_RENORM 0  /* exchange on logits, softmax over top-k */
+#define ORC_MODE_LITERAL 1 /* full softmax, exchange on probabilities */
+
+/* Weight layouts for the routed experts. */
+#define ORC_LAYOUT_CONTIGUOUS 0  /* expert e's blocks at e * blocks_per_matrix */
+#define ORC_LAYOUT_INTERLEAVED 1 /* fused tensor, element i of e at i*E + e */
+
+typedef struct {
+    int D;       /* model dim (2048) */
+    int H;       /* expert hidden dim (512) */
+    int E;       /* routed experts (256) */
+    int k;       /* experts per token (8) */
+    int mode;    /* ORC_MODE_* */
+    int layout;  /* ORC_LAYOUT_* */
+    int gate_type, up_type, down_type;          /* routed tensors (Q4_K/Q4_K/Q6_K/F32/F16) */
+    int sh_gate_type, sh_up_type, sh_down_type; /* shared expert tensors */
+} orc_moe_cfg;
+
+/* One MoE block for T tokens, following model.c:992-1144 per token:
+ *   ffn_x = norm_w ? rmsnorm(x, norm_w) : x
+ *   y     = (resid + shared(ffn_x)) + sum_a w_a * expert_a(ffn_x)
+ * resid may be NULL (treated as all zeros, i.e. y = (0 + shared) + routed);
+ * norm_w may be NULL (no normalisation); bias may be NULL.
+ * Shared expert tensors may be NULL (no shared expert, as model.c:993).
+ * idx_out / w_out (T*k each) may be NULL.
+ * Returns 0 on success, negative on bad arguments / allocation failure. */
+int orc_moe_layer(const orc_moe_cfg *cfg, int T, const float *x, const float *resid,
+                  const float *norm_w, const float *router_W, const float *bias,
+                  const void *gate, const void *up, const void *down,
+                  const void *sh_gate, const void *sh_up, const void *sh_down,
+                  float *out, uint32_t *idx_out, float *w_out);
+
+/* Single (token, expert) FFN with the routed-expert SiLU clamp
+ * (model.c:1085-1088) on already dequantized fp32 weights. */
+void orc_expert_ffn(const float *x, const float *Wg, const float *Wu, const float *Wd,
+                    int D, int H, int clamp, float *out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ORNITH_ORACLE_H */

@@ -1,0 +1,355 @@
+/* SPDX-License-Identifier: MIT
+ *
+ * gpu.h implemented on HIP for MI355X (gfx950).  C99.
+ *
+ * Contract followed (reference engine/src/gpu.c, the CPU backend):
+ *   - gpu_init/gpu_destroy create/free a context (gpu.c:24-37);
+ *   - gpu_alloc returns zero-filled buffers, NULL for size 0 or failure, and
+ *     gpu_memory_used counts exactly the requested bytes (gpu.c:41-64);
+ *   - copies clamp to the buffer sizes (gpu.c:76-100);
+ *   - every call is synchronous at return and a silent no-op on NULL or
+ *     out-of-range arguments (here: also when sizes exceed the buffers,
+ *     because a device kernel must never read past an allocation).
+ * GPU_BUF_SHARED buffers are pinned host allocations mapped into the device
+ * address space, so host writes through gpu_get_cpu_ptr are visible to later
+ * calls (t_gpu.c:46-66, inference.c:169-172).
+ */
+#include "internal.h"
+
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+int orn_set_err(gpu_context *ctx, int code, const char *fmt, ...)
+{
+    if (ctx) {
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(ctx->err, sizeof ctx->err, fmt, ap);
+        va_end(ap);
+    }
+    return code;
+}
+
+int orn_hip_check(gpu_context *ctx, hipError_t e, const char *what)
+{
+    if (e == hipSuccess) return ORN_OK;
+    return orn_set_err(ctx, ORN_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+const char *gpu_last_error(gpu_context *ctx) { return ctx ? ctx->err : "no context"; }
+
+gpu_context *gpu_init(void)
+{
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return NULL;
+    gpu_context *ctx = (gpu_context *)calloc(1, sizeof(gpu_context));
+    if (!ctx) return NULL;
+    if (hipGetDevice(&ctx->device) != hipSuccess) ctx->device = 0;
+    if (hipSetDevice(ctx->device) != hipSuccess ||
+        hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
+        free(ctx);
+        return NULL;
+    }
+    if (hipHostMalloc((void **)&ctx->ctl_host, 64 * sizeof(int), hipHostMallocDefault) !=
+        hipSuccess) {
+        hipStreamDestroy(ctx->stream);
+        free(ctx);
+        return NULL;
+    }
+    memset(ctx->ctl_host, 0, 64 * sizeof(int));
+    return ctx;
+}
+
+void gpu_destroy(gpu_context *ctx)
+{
+    if (!ctx) return;
+    hipStreamSynchronize(ctx->stream);
+    gpu_profile_enable(ctx, 0);
+    orn_ws_release(ctx);
+    if (ctx->ctl_host) hipHostFree(ctx->ctl_host);
+    hipStreamDestroy(ctx->stream);
+    memset(ctx, 0, sizeof *ctx);
+    free(ctx);
+}
+
+gpu_buffer *gpu_alloc(gpu_context *ctx, size_t size, gpu_buffer_flags flags)
+{
+    if (!ctx || size == 0) return NULL;
+    gpu_buffer *b = (gpu_buffer *)calloc(1, sizeof(gpu_buffer));
+    if (!b) return NULL;
+    b->size = size;
+    b->flags = flags;
+    if (flags & GPU_BUF_SHARED) {
+        if (hipHostMalloc(&b->host, size, hipHostMallocMapped) != hipSuccess) {
+            free(b);
+            return NULL;
+        }
+        memset(b->host, 0, size);
+        if (hipHostGetDevicePointer(&b->dev, b->host, 0) != hipSuccess) {
+            hipHostFree(b->host);
+            free(b);
+            return NULL;
+        }
+    } else {
+        if (hipMalloc(&b->dev, size) != hipSuccess) {
+            free(b);
+            return NULL;
+        }
+        if (hipMemsetAsync(b->dev, 0, size, ctx->stream) != hipSuccess ||
+            hipStreamSynchronize(ctx->stream) != hipSuccess) {
+            hipFree(b->dev);
+            free(b);
+            return NULL;
+        }
+    }
+    ctx->used_memory += size;
+    return b;
+}
+
+void gpu_free(gpu_context *ctx, gpu_buffer *buf)
+{
+    if (!ctx || !buf) return;
+    hipStreamSynchronize(ctx->stream);
+    ctx->used_memory -= buf->size;
+    if (buf->flags & GPU_BUF_SHARED) hipHostFree(buf->host);
+    else hipFree(buf->dev);
+    memset(buf, 0, sizeof *buf);
+    free(buf);
+}
+
+void *gpu_get_cpu_ptr(gpu_context *ctx, gpu_buffer *buf)
+{
+    if (!buf) return NULL;
+    if (ctx) hipStreamSynchronize(ctx->stream);
+    return (buf->flags & GPU_BUF_SHARED) ? buf->host : NULL;
+}
+
+size_t gpu_buffer_size(gpu_context *ctx, const gpu_buffer *buf)
+{
+    (void)ctx;
+    return buf ? buf->size : 0;
+}
+
+void *gpu_device_ptr(gpu_context *ctx, gpu_buffer *buf)
+{
+    (void)ctx;
+    return buf ? buf->dev : NULL;
+}
+
+int gpu_device_info(gpu_context *ctx, char *name, size_t name_len, int *n_cus, size_t *hbm_bytes)
+{
+    if (!ctx) return ORN_EINVAL;
+    hipDeviceProp_t p;
+    int rc = orn_hip_check(ctx, hipGetDeviceProperties(&p, ctx->device), "hipGetDeviceProperties");
+    if (rc) return rc;
+    if (name && name_len) snprintf(name, name_len, "%s (%s)", p.name, p.gcnArchName);
+    if (n_cus) *n_cus = p.multiProcessorCount;
+    if (hbm_bytes) *hbm_bytes = p.totalGlobalMem;
+    return ORN_OK;
+}
+
+static void sync_ctx(gpu_context *ctx) { hipStreamSynchronize(ctx->stream); }
+
+void gpu_copy_to_device(gpu_context *ctx, gpu_buffer *dst, const void *src, size_t size)
+{
+    if (!ctx || !dst || !src) return;
+    size_t n = size < dst->size ? size : dst->size;
+    if (n == 0) return;
+    if (dst->flags & GPU_BUF_SHARED) {
+        sync_ctx(ctx);
+        memcpy(dst->host, src, n);
+        return;
+    }
+    hipMemcpyAsync(dst->dev, src, n, hipMemcpyHostToDevice, ctx->stream);
+    sync_ctx(ctx);
+}
+
+void gpu_copy_to_host(gpu_context *ctx, void *dst, const gpu_buffer *src, size_t size)
+{
+    if (!ctx || !dst || !src) return;
+    size_t n = size < src->size ? size : src->size;
+    if (n == 0) return;
+    sync_ctx(ctx);
+    if (src->flags & GPU_BUF_SHARED) {
+        memcpy(dst, src->host, n);
+        return;
+    }
+    hipMemcpyAsync(dst, src->dev, n, hipMemcpyDeviceToHost, ctx->stream);
+    sync_ctx(ctx);
+}
+
+void gpu_copy_buffer(gpu_context *ctx, gpu_buffer *dst, const gpu_buffer *src, size_t size)
+{
+    if (!ctx || !dst || !src) return;
+    size_t n = size;
+    if (n > dst->size) n = dst->size;
+    if (n > src->size) n = src->size;
+    if (n == 0) return;
+    hipMemcpyAsync(dst->dev, src->dev, n, hipMemcpyDefault, ctx->stream);
+    sync_ctx(ctx);
+}
+
+static int fits(const gpu_buffer *b, size_t n_floats) { return b && n_floats <= b->size / 4; }
+
+void gpu_matmul(gpu_context *ctx, gpu_buffer *C, const gpu_buffer *A, const gpu_buffer *B, int M,
+                int N, int K, quant_mode a_quant, quant_mode b_quant)
+{
+    (void)a_quant;
+    (void)b_quant;
+    if (!ctx || !C || !A || !B || M <= 0 || N <= 0 || K < 0) return;
+    if (!fits(A, (size_t)M * K) || !fits(B, (size_t)K * N) || !fits(C, (size_t)M * N)) return;
+    orn_hip_check(ctx, (hipError_t)ornk_matmul_f32((float *)C->dev, (const float *)A->dev,
+                                                   (const float *)B->dev, M, N, K, ctx->stream),
+                  "gpu_matmul");
+    sync_ctx(ctx);
+}
+
+void gpu_matmul_int4(gpu_context *ctx, gpu_buffer *C, const gpu_buffer *A_quant,
+                     const gpu_buffer *A_scale, int M, int N, int K)
+{
+    /* The CPU backend zero-fills C (gpu.c:131-140); no int4 format is defined. */
+    (void)A_quant;
+    (void)A_scale;
+    (void)K;
+    if (!ctx || !C || M <= 0 || N <= 0) return;
+    size_t n = (size_t)M * N;
+    if (n > C->size / 4) n = C->size / 4;
+    ornk_fill_f32((float *)C->dev, 0.0f, n, ctx->stream);
+    sync_ctx(ctx);
+}
+
+void gpu_rmsnorm(gpu_context *ctx, gpu_buffer *out, const gpu_buffer *x, const gpu_buffer *weight,
+                 int rows, int dim)
+{
+    (void)rows; /* one row, as gpu.c:144-156 */
+    if (!ctx || !out || !x || !weight || dim <= 0) return;
+    if (!fits(out, (size_t)dim) || !fits(x, (size_t)dim) || !fits(weight, (size_t)dim)) return;
+    ornk_rmsnorm((float *)out->dev, (const float *)x->dev, (const float *)weight->dev, 1, dim,
+                 ctx->stream);
+    sync_ctx(ctx);
+}
+
+void gpu_silu(gpu_context *ctx, gpu_buffer *out, const gpu_buffer *x, int n)
+{
+    if (!ctx || !out || !x || n <= 0) return;
+    if (!fits(out, (size_t)n) || !fits(x, (size_t)n)) return;
+    ornk_silu((float *)out->dev, (const float *)x->dev, n, ctx->stream);
+    sync_ctx(ctx);
+}
+
+void gpu_silu_mul(gpu_context *ctx, gpu_buffer *out, const gpu_buffer *gate, const gpu_buffer *up,
+                  int n)
+{
+    if (!ctx || !out || !gate || !up || n <= 0) return;
+    if (!fits(out, (size_t)n) || !fits(gate, (size_t)n) || !fits(up, (size_t)n)) return;
+    ornk_silu_mul((float *)out->dev, (const float *)gate->dev, (const float *)up->dev, n,
+                  ctx->stream);
+    sync_ctx(ctx);
+}
+
+/* RoPE, attention and the DeltaNet step are no-ops in the CPU backend
+ * (gpu.c:188-206); the MoE hot path does not use them. */
+void gpu_rope(gpu_context *ctx, gpu_buffer *Q, gpu_buffer *K, int seq_len, int head_dim,
+              int n_heads, int n_kv_heads, float base, int pos_start)
+{
+    (void)ctx; (void)Q; (void)K; (void)seq_len; (void)head_dim;
+    (void)n_heads; (void)n_kv_heads; (void)base; (void)pos_start;
+}
+
+void gpu_attention(gpu_context *ctx, gpu_buffer *out, const gpu_buffer *Q,
+                   const gpu_buffer *K_cache, const gpu_buffer *V_cache, int seq_len, int head_dim)
+{
+    (void)ctx; (void)out; (void)Q; (void)K_cache; (void)V_cache; (void)seq_len; (void)head_dim;
+}
+
+void gpu_deltanet_step(gpu_context *ctx, gpu_buffer *state, const gpu_buffer *Q,
+                       const gpu_buffer *K, const gpu_buffer *V, int dim)
+{
+    (void)ctx; (void)state; (void)Q; (void)K; (void)V; (void)dim;
+}
+
+/* mlp.metal:49-87: out = (silu(x@gate) * (x@up)) @ down in fp32, no clamp. */
+void gpu_expert_mlp(gpu_context *ctx, gpu_buffer *out, const gpu_buffer *x,
+                    const gpu_buffer *gate_w, const gpu_buffer *up_w, const gpu_buffer *down_w,
+                    int d_model, int hidden_dim, quant_mode quant)
+{
+    (void)quant;
+    if (!ctx || !out || !x || !gate_w || !up_w || !down_w || d_model <= 0 || hidden_dim <= 0)
+        return;
+    const size_t D = (size_t)d_model, H = (size_t)hidden_dim;
+    if (!fits(out, D) || !fits(x, D) || !fits(gate_w, D * H) || !fits(up_w, D * H) ||
+        !fits(down_w, H * D))
+        return;
+    float *tmp = (float *)orn_ws_get(ctx, 3 * H * sizeof(float));
+    if (!tmp) return;
+    float *g = tmp, *u = tmp + H, *mid = tmp + 2 * H;
+    hipStream_t s = ctx->stream;
+    ornk_matmul_f32(g, (const float *)x->dev, (const float *)gate_w->dev, 1, hidden_dim, d_model, s);
+    ornk_matmul_f32(u, (const float *)x->dev, (const float *)up_w->dev, 1, hidden_dim, d_model, s);
+    ornk_silu_mul(mid, g, u, hidden_dim, s);
+    ornk_matmul_f32((float *)out->dev, mid, (const float *)down_w->dev, 1, d_model, hidden_dim, s);
+    sync_ctx(ctx);
+}
+
+/* mlp.metal:94-109 / model.c:1017-1025: sequential fp32 logits. */
+void gpu_router(gpu_context *ctx, gpu_buffer *out, const gpu_buffer *x,
+                const gpu_buffer *router_weight, int d_model, int n_experts)
+{
+    if (!ctx || !out || !x || !router_weight || d_model <= 0 || n_experts <= 0) return;
+    if (!fits(out, (size_t)n_experts) || !fits(x, (size_t)d_model) ||
+        !fits(router_weight, (size_t)d_model * n_experts))
+        return;
+    ornk_router_exact((const float *)x->dev, (const float *)router_weight->dev, NULL, 1, d_model,
+                      n_experts, (float *)out->dev, ctx->stream);
+    sync_ctx(ctx);
+}
+
+/* gpu_metal.m:663-685: exchange sort on the logits (n capped at 1024), softmax
+ * over the first k; indices/weights are host arrays. */
+void gpu_topk_softmax(gpu_context *ctx, uint32_t *indices, float *weights,
+                      const gpu_buffer *logits, int n_experts, int top_k)
+{
+    if (!ctx || !indices || !weights || !logits) return;
+    int n = n_experts < 1024 ? n_experts : 1024;
+    int k = top_k < n ? top_k : n;
+    if (n <= 0 || k <= 0 || !fits(logits, (size_t)n)) return;
+    uint8_t *ws = (uint8_t *)orn_ws_get(ctx, 2 * 1024 * sizeof(float) + 256);
+    if (!ws) return;
+    uint32_t *d_idx = (uint32_t *)ws;
+    float *d_w = (float *)(ws + 1024 * sizeof(float));
+    if (ornk_topk((const float *)logits->dev, 1, n, k, 0, d_idx, d_w, NULL, ctx->stream) !=
+        hipSuccess)
+        return;
+    hipMemcpyAsync(indices, d_idx, (size_t)k * sizeof(uint32_t), hipMemcpyDeviceToHost,
+                   ctx->stream);
+    hipMemcpyAsync(weights, d_w, (size_t)k * sizeof(float), hipMemcpyDeviceToHost, ctx->stream);
+    sync_ctx(ctx);
+}
+
+void gpu_add(gpu_context *ctx, gpu_buffer *out, const gpu_buffer *a, const gpu_buffer *b, int n)
+{
+    if (!ctx || !out || !a || !b || n <= 0) return;
+    if (!fits(out, (size_t)n) || !fits(a, (size_t)n) || !fits(b, (size_t)n)) return;
+    ornk_add((float *)out->dev, (const float *)a->dev, (const float *)b->dev, n, ctx->stream);
+    sync_ctx(ctx);
+}
+
+void gpu_sync(gpu_context *ctx)
+{
+    if (ctx) sync_ctx(ctx);
+}
+
+size_t gpu_memory_used(gpu_context *ctx) { return ctx ? ctx->used_memory : 0; }
+
+void gpu_print_info(gpu_context *ctx)
+{
+    if (!ctx) return;
+    char name[128] = "";
+    int cus = 0;
+    size_t hbm = 0;
+    gpu_device_info(ctx, name, sizeof name, &cus, &hbm);
+    printf("=== GPU Info (HIP backend) ===\n");
+    printf("Device:   %s, %d CUs, %.1f GiB HBM\n", name, cus, (double)hbm / (1024.0 * 1024 * 1024));
+    printf("Memory:   %zu bytes\n", ctx->used_memory);
+}

@@ -1,0 +1,69 @@
+/* SPDX-License-Identifier: MIT
+ *
+ * Internal definitions shared by the C99 host files of libornith_hip.
+ */
+#ifndef ORNITH_HOST_INTERNAL_H
+#define ORNITH_HOST_INTERNAL_H
+
+#include <stdarg.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../../include/ornith/gpu.h"
+#include "../../../include/ornith/ornith_hip.h"
+#include "../kernels/launch.h"
+
+#define ORN_PROF_MAX_NAMES 32
+#define ORN_PROF_MAX_PENDING 8192
+
+typedef struct {
+    int name_id;
+    hipEvent_t start, stop;
+} orn_prof_rec;
+
+struct gpu_buffer {
+    void *dev;   /* device address used by kernels */
+    void *host;  /* host address for GPU_BUF_SHARED (pinned, device-mapped) */
+    size_t size;
+    gpu_buffer_flags flags;
+};
+
+typedef struct {
+    /* grow-only device workspace for the MoE forward */
+    void *base;
+    size_t bytes;
+} orn_workspace;
+
+struct gpu_context {
+    int device;
+    hipStream_t stream;
+    size_t used_memory;
+    char err[256];
+    orn_workspace ws;
+    /* device counters read back after a forward */
+    int *ctl_host; /* pinned mirror of the last forward's counters */
+    /* profiling */
+    int prof_on;
+    int prof_n_names;
+    char prof_names[ORN_PROF_MAX_NAMES][32];
+    double prof_total_ms[ORN_PROF_MAX_NAMES];
+    long prof_calls[ORN_PROF_MAX_NAMES];
+    orn_prof_rec *prof_pending;
+    int prof_n_pending;
+    hipEvent_t *prof_pool;
+    int prof_pool_n, prof_pool_used;
+};
+
+/* error helpers (gpu_hip.c) */
+int orn_set_err(gpu_context *ctx, int code, const char *fmt, ...);
+int orn_hip_check(gpu_context *ctx, hipError_t e, const char *what);
+
+/* profiling hooks (moe.c) */
+int orn_prof_begin(gpu_context *ctx, const char *name);
+void orn_prof_end(gpu_context *ctx, int slot);
+
+/* workspace (moe.c) */
+void *orn_ws_get(gpu_context *ctx, size_t bytes);
+void orn_ws_release(gpu_context *ctx);
+
+#endif /* ORNITH_HOST_INTERNAL_H */

@@ -1,0 +1,597 @@
+/* SPDX-License-Identifier: MIT
+ *
+ * Resident routed-MoE layers and the per-layer forward (C99 host side).
+ *
+ * The forward replaces model.c:992-1144 for a batch of tokens:
+ *   norm/reset -> certified router + top-k -> dispatch -> gate/up -> mid ->
+ *   down -> combine,
+ * all enqueued on the context's stream; no host round trip between steps.
+ */
+#include "internal.h"
+
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+struct ornith_moe_store {
+    ornith_moe_shape sh;
+    size_t blocks_per_matrix; /* D*H/256 */
+    uint8_t *gate, *up;       /* [L][E+1][H/256][D] * 144 B */
+    uint8_t *down_body;       /* [L][E+1][D/256][H] * 208 B */
+    uint16_t *down_d;         /* [L][E+1][D/256][H] */
+    float *router_t;          /* [L][E][D] */
+    float *bias;              /* [L][E] */
+    int *has_bias;            /* host [L] */
+    float *norm;              /* [L][D] */
+    size_t bytes;
+};
+
+/* ---------------------------------------------------------------------------
+ * Workspace (grow-only device scratch owned by the context)
+ * ------------------------------------------------------------------------- */
+void *orn_ws_get(gpu_context *ctx, size_t bytes)
+{
+    if (bytes <= ctx->ws.bytes) return ctx->ws.base;
+    hipStreamSynchronize(ctx->stream);
+    if (ctx->ws.base) hipFree(ctx->ws.base);
+    ctx->ws.base = NULL;
+    ctx->ws.bytes = 0;
+    size_t want = bytes + (bytes >> 3);
+    if (hipMalloc(&ctx->ws.base, want) != hipSuccess) {
+        orn_set_err(ctx, ORN_ENOMEM, "workspace allocation of %zu bytes failed", want);
+        ctx->ws.base = NULL;
+        return NULL;
+    }
+    ctx->ws.bytes = want;
+    return ctx->ws.base;
+}
+
+void orn_ws_release(gpu_context *ctx)
+{
+    if (ctx->ws.base) hipFree(ctx->ws.base);
+    ctx->ws.base = NULL;
+    ctx->ws.bytes = 0;
+}
+
+/* ---------------------------------------------------------------------------
+ * Profiling: HIP events around each launch on the context's stream
+ * ------------------------------------------------------------------------- */
+static void prof_collect(gpu_context *ctx)
+{
+    if (!ctx->prof_n_pending) return;
+    hipStreamSynchronize(ctx->stream);
+    for (int i = 0; i < ctx->prof_n_pending; ++i) {
+        orn_prof_rec *r = &ctx->prof_pending[i];
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, r->start, r->stop) == hipSuccess) {
+            ctx->prof_total_ms[r->name_id] += ms;
+            ctx->prof_calls[r->name_id] += 1;
+        }
+    }
+    ctx->prof_n_pending = 0;
+    ctx->prof_pool_used = 0;
+}
+
+int gpu_profile_enable(gpu_context *ctx, int on)
+{
+    if (!ctx) return ORN_EINVAL;
+    if (on && !ctx->prof_pool) {
+        ctx->prof_pool_n = 2 * ORN_PROF_MAX_PENDING;
+        ctx->prof_pool = (hipEvent_t *)calloc((size_t)ctx->prof_pool_n, sizeof(hipEvent_t));
+        ctx->prof_pending = (orn_prof_rec *)calloc(ORN_PROF_MAX_PENDING, sizeof(orn_prof_rec));
+        if (!ctx->prof_pool || !ctx->prof_pending) return ORN_ENOMEM;
+        for (int i = 0; i < ctx->prof_pool_n; ++i)
+            if (hipEventCreate(&ctx->prof_pool[i]) != hipSuccess) return ORN_EHIP;
+    }
+    if (!on && ctx->prof_pool) {
+        prof_collect(ctx);
+        for (int i = 0; i < ctx->prof_pool_n; ++i) hipEventDestroy(ctx->prof_pool[i]);
+        free(ctx->prof_pool);
+        free(ctx->prof_pending);
+        ctx->prof_pool = NULL;
+        ctx->prof_pending = NULL;
+        ctx->prof_pool_n = 0;
+    }
+    ctx->prof_on = on ? 1 : 0;
+    return ORN_OK;
+}
+
+void gpu_profile_reset(gpu_context *ctx)
+{
+    if (!ctx) return;
+    prof_collect(ctx);
+    for (int i = 0; i < ORN_PROF_MAX_NAMES; ++i) {
+        ctx->prof_total_ms[i] = 0.0;
+        ctx->prof_calls[i] = 0;
+    }
+}
+
+int gpu_profile_count(gpu_context *ctx)
+{
+    if (!ctx) return 0;
+    prof_collect(ctx);
+    return ctx->prof_n_names;
+}
+
+const char *gpu_profile_name(gpu_context *ctx, int i)
+{
+    return (ctx && i >= 0 && i < ctx->prof_n_names) ? ctx->prof_names[i] : "";
+}
+
+double gpu_profile_total_ms(gpu_context *ctx, int i)
+{
+    if (!ctx || i < 0 || i >= ctx->prof_n_names) return 0.0;
+    prof_collect(ctx);
+    return ctx->prof_total_ms[i];
+}
+
+long gpu_profile_calls(gpu_context *ctx, int i)
+{
+    if (!ctx || i < 0 || i >= ctx->prof_n_names) return 0;
+    prof_collect(ctx);
+    return ctx->prof_calls[i];
+}
+
+int orn_prof_begin(gpu_context *ctx, const char *name)
+{
+    if (!ctx->prof_on) return -1;
+    if (ctx->prof_n_pending >= ORN_PROF_MAX_PENDING || ctx->prof_pool_used + 2 > ctx->prof_pool_n)
+        prof_collect(ctx);
+    int id = -1;
+    for (int i = 0; i < ctx->prof_n_names; ++i)
+        if (strcmp(ctx->prof_names[i], name) == 0) { id = i; break; }
+    if (id < 0) {
+        if (ctx->prof_n_names >= ORN_PROF_MAX_NAMES) return -1;
+        id = ctx->prof_n_names++;
+        snprintf(ctx->prof_names[id], sizeof ctx->prof_names[id], "%s", name);
+    }
+    orn_prof_rec *r = &ctx->prof_pending[ctx->prof_n_pending];
+    r->name_id = id;
+    r->start = ctx->prof_pool[ctx->prof_pool_used++];
+    r->stop = ctx->prof_pool[ctx->prof_pool_used++];
+    hipEventRecord(r->start, ctx->stream);
+    return ctx->prof_n_pending++;
+}
+
+void orn_prof_end(gpu_context *ctx, int slot)
+{
+    if (slot < 0) return;
+    hipEventRecord(ctx->prof_pending[slot].stop, ctx->stream);
+}
+
+/* ---------------------------------------------------------------------------
+ * Store
+ * ------------------------------------------------------------------------- */
+static int shape_ok(const ornith_moe_shape *s)
+{
+    return s && s->n_layers > 0 && s->d_model > 0 && s->d_model % 256 == 0 && s->hidden > 0 &&
+           s->hidden % 256 == 0 && s->hidden <= 1024 && s->n_experts > 0 &&
+           s->n_experts <= 256 && s->top_k > 0 && s->top_k <= 16 && s->top_k <= s->n_experts &&
+           (s->has_shared == 0 || s->has_shared == 1) && s->d_model % 128 == 0;
+}
+
+static void store_free(ornith_moe_store *st)
+{
+    if (!st) return;
+    hipFree(st->gate);
+    hipFree(st->up);
+    hipFree(st->down_body);
+    hipFree(st->down_d);
+    hipFree(st->router_t);
+    hipFree(st->bias);
+    hipFree(st->norm);
+    free(st->has_bias);
+    free(st);
+}
+
+ornith_moe_store *gpu_moe_store_create(gpu_context *ctx, const ornith_moe_shape *shape)
+{
+    if (!ctx) return NULL;
+    if (!shape_ok(shape)) {
+        orn_set_err(ctx, ORN_EINVAL, "unsupported MoE shape");
+        return NULL;
+    }
+    ornith_moe_store *st = (ornith_moe_store *)calloc(1, sizeof *st);
+    if (!st) return NULL;
+    st->sh = *shape;
+    const size_t L = (size_t)shape->n_layers, E1 = (size_t)shape->n_experts + 1;
+    const size_t D = (size_t)shape->d_model, H = (size_t)shape->hidden,
+                 E = (size_t)shape->n_experts;
+    st->blocks_per_matrix = D * H / 256;
+    const size_t nb = L * E1 * st->blocks_per_matrix;
+    size_t sizes[7] = {nb * 144, nb * 144, nb * 208, nb * 2, L * E * D * 4, L * E * 4, L * D * 4};
+    void **ptrs[7] = {(void **)&st->gate, (void **)&st->up, (void **)&st->down_body,
+                      (void **)&st->down_d, (void **)&st->router_t, (void **)&st->bias,
+                      (void **)&st->norm};
+    for (int i = 0; i < 7; ++i) {
+        if (hipMalloc(ptrs[i], sizes[i]) != hipSuccess ||
+            hipMemsetAsync(*ptrs[i], 0, sizes[i], ctx->stream) != hipSuccess) {
+            orn_set_err(ctx, ORN_ENOMEM, "store allocation of %zu bytes failed", sizes[i]);
+            store_free(st);
+            return NULL;
+        }
+        st->bytes += sizes[i];
+    }
+    st->has_bias = (int *)calloc(L, sizeof(int));
+    float *ones = (float *)malloc(D * sizeof(float));
+    if (!st->has_bias || !ones) {
+        free(ones);
+        store_free(st);
+        return NULL;
+    }
+    for (size_t i = 0; i < D; ++i) ones[i] = 1.0f;
+    for (size_t l = 0; l < L; ++l)
+        hipMemcpyAsync(st->norm + l * D, ones, D * sizeof(float), hipMemcpyHostToDevice,
+                       ctx->stream);
+    hipStreamSynchronize(ctx->stream);
+    free(ones);
+    return st;
+}
+
+void gpu_moe_store_destroy(gpu_context *ctx, ornith_moe_store *store)
+{
+    if (ctx) hipStreamSynchronize(ctx->stream);
+    store_free(store);
+}
+
+size_t gpu_moe_store_bytes(const ornith_moe_store *store) { return store ? store->bytes : 0; }
+
+/* Permute one expert's GGUF block stream (row-major: block (k, c) at
+ * k*NBc + c) into the device's block-column-major order (c*K + k). */
+static void permute_q4k(const uint8_t *src, uint8_t *dst, int K, int NBc)
+{
+    for (int k = 0; k < K; ++k)
+        for (int c = 0; c < NBc; ++c)
+            memcpy(dst + ((size_t)c * K + k) * 144, src + ((size_t)k * NBc + c) * 144, 144);
+}
+
+static void permute_q6k(const uint8_t *src, uint8_t *body, uint16_t *dv, int K, int NBc)
+{
+    for (int k = 0; k < K; ++k)
+        for (int c = 0; c < NBc; ++c) {
+            const uint8_t *b = src + ((size_t)k * NBc + c) * ORN_Q6K_BYTES;
+            const size_t o = (size_t)c * K + k;
+            memcpy(body + o * 208, b, 208);
+            dv[o] = (uint16_t)(b[ORN_Q6K_OFF_D] | (b[ORN_Q6K_OFF_D + 1] << 8));
+        }
+}
+
+int gpu_moe_store_set_experts(gpu_context *ctx, ornith_moe_store *st, int layer, int matrix,
+                              int expert_first, int n, const void *blocks)
+{
+    if (!ctx || !st || !blocks) return ORN_EINVAL;
+    const int E1 = st->sh.n_experts + 1;
+    if (layer < 0 || layer >= st->sh.n_layers || expert_first < 0 || n < 0 ||
+        expert_first + n > E1 || matrix < 0 || matrix > 2)
+        return orn_set_err(ctx, ORN_EINVAL, "set_experts: bad layer/expert range/matrix");
+    if (n == 0) return ORN_OK;
+    const int D = st->sh.d_model, H = st->sh.hidden;
+    const size_t nb = st->blocks_per_matrix;
+    const size_t slot0 = (size_t)layer * E1 + (size_t)expert_first;
+    hipStream_t s = ctx->stream;
+    int rc = ORN_OK;
+    if (matrix != ORN_MAT_DOWN) {
+        uint8_t *tmp = (uint8_t *)malloc((size_t)n * nb * 144);
+        if (!tmp) return orn_set_err(ctx, ORN_ENOMEM, "host staging");
+        for (int i = 0; i < n; ++i)
+            permute_q4k((const uint8_t *)blocks + (size_t)i * nb * ORN_Q4K_BYTES, tmp + i * nb * 144,
+                        D, H / 256);
+        uint8_t *dst = (matrix == ORN_MAT_GATE ? st->gate : st->up) + slot0 * nb * 144;
+        rc = orn_hip_check(ctx, hipMemcpyAsync(dst, tmp, (size_t)n * nb * 144,
+                                               hipMemcpyHostToDevice, s), "upload q4k");
+        hipStreamSynchronize(s);
+        free(tmp);
+    } else {
+        uint8_t *body = (uint8_t *)malloc((size_t)n * nb * 208);
+        uint16_t *dv = (uint16_t *)malloc((size_t)n * nb * 2);
+        if (!body || !dv) {
+            free(body);
+            free(dv);
+            return orn_set_err(ctx, ORN_ENOMEM, "host staging");
+        }
+        for (int i = 0; i < n; ++i)
+            permute_q6k((const uint8_t *)blocks + (size_t)i * nb * ORN_Q6K_BYTES, body + i * nb * 208,
+                        dv + i * nb, H, D / 256);
+        rc = orn_hip_check(ctx, hipMemcpyAsync(st->down_body + slot0 * nb * 208, body,
+                                               (size_t)n * nb * 208, hipMemcpyHostToDevice, s),
+                           "upload q6k");
+        if (!rc)
+            rc = orn_hip_check(ctx, hipMemcpyAsync(st->down_d + slot0 * nb, dv, (size_t)n * nb * 2,
+                                                   hipMemcpyHostToDevice, s), "upload q6k d");
+        hipStreamSynchronize(s);
+        free(body);
+        free(dv);
+    }
+    return rc;
+}
+
+int gpu_moe_store_set_router(gpu_context *ctx, ornith_moe_store *st, int layer, const float *W,
+                             const float *bias)
+{
+    if (!ctx || !st || !W) return ORN_EINVAL;
+    if (layer < 0 || layer >= st->sh.n_layers) return orn_set_err(ctx, ORN_EINVAL, "bad layer");
+    const size_t D = (size_t)st->sh.d_model, E = (size_t)st->sh.n_experts;
+    float *t = (float *)malloc(D * E * sizeof(float));
+    if (!t) return orn_set_err(ctx, ORN_ENOMEM, "host staging");
+    for (size_t d = 0; d < D; ++d)
+        for (size_t e = 0; e < E; ++e) t[e * D + d] = W[d * E + e];
+    hipStream_t s = ctx->stream;
+    int rc = orn_hip_check(ctx, hipMemcpyAsync(st->router_t + (size_t)layer * E * D, t,
+                                               D * E * sizeof(float), hipMemcpyHostToDevice, s),
+                           "upload router");
+    if (!rc) {
+        if (bias)
+            rc = orn_hip_check(ctx, hipMemcpyAsync(st->bias + (size_t)layer * E, bias,
+                                                   E * sizeof(float), hipMemcpyHostToDevice, s),
+                               "upload bias");
+        st->has_bias[layer] = bias ? 1 : 0;
+    }
+    hipStreamSynchronize(s);
+    free(t);
+    return rc;
+}
+
+int gpu_moe_store_set_norm(gpu_context *ctx, ornith_moe_store *st, int layer, const float *w)
+{
+    if (!ctx || !st || !w) return ORN_EINVAL;
+    if (layer < 0 || layer >= st->sh.n_layers) return orn_set_err(ctx, ORN_EINVAL, "bad layer");
+    const size_t D = (size_t)st->sh.d_model;
+    int rc = orn_hip_check(ctx, hipMemcpyAsync(st->norm + (size_t)layer * D, w, D * sizeof(float),
+                                               hipMemcpyHostToDevice, ctx->stream),
+                           "upload norm");
+    hipStreamSynchronize(ctx->stream);
+    return rc;
+}
+
+int gpu_moe_store_fill_synthetic(gpu_context *ctx, ornith_moe_store *st, int layer, uint64_t seed,
+                                 float zipf_s)
+{
+    if (!ctx || !st) return ORN_EINVAL;
+    if (layer < 0 || layer >= st->sh.n_layers) return orn_set_err(ctx, ORN_EINVAL, "bad layer");
+    const int E = st->sh.n_experts, E1 = E + st->sh.has_shared;
+    const size_t nb = st->blocks_per_matrix;
+    const size_t D = (size_t)st->sh.d_model;
+    uint8_t *buf = (uint8_t *)malloc(nb * ORN_Q6K_BYTES);
+    float *W = (float *)malloc(D * (size_t)E * sizeof(float));
+    float *b = (float *)malloc((size_t)E * sizeof(float));
+    if (!buf || !W || !b) {
+        free(buf);
+        free(W);
+        free(b);
+        return orn_set_err(ctx, ORN_ENOMEM, "host staging");
+    }
+    int rc = ORN_OK;
+    for (int e = 0; e < E1 && !rc; ++e) {
+        orn_synth_q4k(seed, orn_synth_stream(layer, ORN_SYN_GATE, e), 0, nb, buf);
+        rc = gpu_moe_store_set_experts(ctx, st, layer, ORN_MAT_GATE, e, 1, buf);
+        if (rc) break;
+        orn_synth_q4k(seed, orn_synth_stream(layer, ORN_SYN_UP, e), 0, nb, buf);
+        rc = gpu_moe_store_set_experts(ctx, st, layer, ORN_MAT_UP, e, 1, buf);
+        if (rc) break;
+        orn_synth_q6k(seed, orn_synth_stream(layer, ORN_SYN_DOWN, e), 0, nb, buf);
+        rc = gpu_moe_store_set_experts(ctx, st, layer, ORN_MAT_DOWN, e, 1, buf);
+    }
+    if (!rc) {
+        orn_synth_normal(seed, orn_synth_stream(layer, ORN_SYN_ROUTER, 0), D * (size_t)E, 0.02f, W);
+        if (zipf_s > 0.0f)
+            orn_synth_zipf_bias(seed, orn_synth_stream(layer, ORN_SYN_ZIPF, 0), E, zipf_s, b);
+        rc = gpu_moe_store_set_router(ctx, st, layer, W, zipf_s > 0.0f ? b : NULL);
+    }
+    free(buf);
+    free(W);
+    free(b);
+    return rc;
+}
+
+/* ---------------------------------------------------------------------------
+ * Forward
+ * ------------------------------------------------------------------------- */
+#define ALIGN256(x) (((x) + 255u) & ~(size_t)255u)
+
+typedef struct {
+    int ks_gu, ks_dn, rows_max, items_max;
+} plan_t;
+
+static int pow2_floor(int v)
+{
+    int p = 1;
+    while (p * 2 <= v) p *= 2;
+    return p;
+}
+
+static plan_t make_plan(const ornith_moe_shape *sh, int T)
+{
+    plan_t p;
+    const int k = sh->top_k, E = sh->n_experts;
+    p.rows_max = T * k + (sh->has_shared ? T : 0);
+    const int max_slots = (T * k < E ? T * k : E) + (sh->has_shared ? 1 : 0);
+    p.items_max = max_slots + (p.rows_max + 7) / 8;
+    const int est_items = max_slots + p.rows_max / 8;
+    const int D = sh->d_model, H = sh->hidden;
+    /* gate/up: enough K-slices for ~2 blocks per CU, at least 16 rows each */
+    const int rw_gu = 64 / (16 * (H / 256));
+    int ks = pow2_floor(512 / (est_items > 0 ? est_items : 1));
+    if (ks < 1) ks = 1;
+    while (ks > 1 && (D % ks || (D / ks) % (4 * rw_gu) || D / ks < 16 * rw_gu)) ks /= 2;
+    if (ks > 64) ks = 64;
+    p.ks_gu = ks;
+    /* down: K = H rows */
+    const int crg = (8 * (D / 256)) < 64 ? 8 * (D / 256) : 64;
+    const int rw_dn = 64 / crg;
+    int kd = pow2_floor(256 / (est_items > 0 ? est_items : 1));
+    if (kd < 1) kd = 1;
+    if (kd > 8) kd = 8;
+    while (kd > 1 && (H % kd || (H / kd) % (4 * rw_dn))) kd /= 2;
+    p.ks_dn = kd;
+    return p;
+}
+
+static int check_buf(const gpu_buffer *b, size_t bytes) { return b && b->size >= bytes; }
+
+static int launch(gpu_context *ctx, const char *name, int (*fn)(const ornk_moe_args *, hipStream_t),
+                  const ornk_moe_args *a)
+{
+    int slot = orn_prof_begin(ctx, name);
+    int e = fn(a, ctx->stream);
+    orn_prof_end(ctx, slot);
+    if (e != hipSuccess)
+        return orn_set_err(ctx, ORN_EHIP, "%s: %s", name, hipGetErrorString((hipError_t)e));
+    return ORN_OK;
+}
+
+static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, const float *x,
+                           int T, const float *resid, float *out, uint32_t *idx_out, float *w_out,
+                           const ornith_moe_opts *opts)
+{
+    const ornith_moe_shape *sh = &st->sh;
+    const int D = sh->d_model, H = sh->hidden, E = sh->n_experts, k = sh->top_k;
+    const int E1 = E + 1;
+    const unsigned flags = opts ? opts->flags : 0u;
+    const int mode = opts ? opts->route_mode : ORN_ROUTE_RENORM;
+    if (mode != ORN_ROUTE_RENORM && mode != ORN_ROUTE_LITERAL)
+        return orn_set_err(ctx, ORN_EINVAL, "bad route mode");
+    plan_t p = make_plan(sh, T);
+
+    size_t off = 0;
+#define CARVE(name, bytes)       \
+    size_t name = off;           \
+    off += ALIGN256((size_t)(bytes))
+    CARVE(o_xn, (flags & ORN_MOE_NORM) ? (size_t)T * D * 4 : 0);
+    CARVE(o_logits, (size_t)T * E * 4);
+    CARVE(o_rpart, (size_t)T * E * (D / 128) * 16);
+    CARVE(o_idx, (size_t)T * k * 4);
+    CARVE(o_w, (size_t)T * k * 4);
+    CARVE(o_ctl, 64);
+    CARVE(o_slot_e, (size_t)E1 * 4);
+    CARVE(o_slot_off, (size_t)E1 * 4);
+    CARVE(o_slot_cnt, (size_t)E1 * 4);
+    CARVE(o_row_tok, (size_t)p.rows_max * 4);
+    CARVE(o_pair_row, (size_t)T * k * 4);
+    CARVE(o_items, (size_t)p.items_max * 16);
+    CARVE(o_gu, (size_t)p.ks_gu * p.rows_max * 2 * H * 4);
+    CARVE(o_mid, (size_t)p.rows_max * H * 4);
+    CARVE(o_dn, (size_t)p.ks_dn * p.rows_max * D * 4);
+#undef CARVE
+    uint8_t *ws = (uint8_t *)orn_ws_get(ctx, off);
+    if (!ws) return ORN_ENOMEM;
+
+    const size_t E1nb = (size_t)E1 * st->blocks_per_matrix;
+    ornk_moe_args a;
+    memset(&a, 0, sizeof a);
+    a.T = T;
+    a.D = D;
+    a.H = H;
+    a.E = E;
+    a.k = k;
+    a.has_shared = sh->has_shared;
+    a.mode = mode;
+    a.apply_norm = (flags & ORN_MOE_NORM) ? 1 : 0;
+    a.ks_gu = p.ks_gu;
+    a.ks_dn = p.ks_dn;
+    a.rows_max = p.rows_max;
+    a.items_max = p.items_max;
+    a.gate = st->gate + (size_t)layer * E1nb * 144;
+    a.up = st->up + (size_t)layer * E1nb * 144;
+    a.down_body = st->down_body + (size_t)layer * E1nb * 208;
+    a.down_d = st->down_d + (size_t)layer * E1nb;
+    a.router = st->router_t + (size_t)layer * E * D;
+    a.bias = st->has_bias[layer] ? st->bias + (size_t)layer * E : NULL;
+    a.norm_w = st->norm + (size_t)layer * D;
+    a.x = x;
+    a.resid = resid;
+    a.out = out;
+    a.xn = a.apply_norm ? (float *)(ws + o_xn) : (float *)x;
+    a.logits = (float *)(ws + o_logits);
+    a.rpart = (double *)(ws + o_rpart);
+    a.idx = (uint32_t *)(ws + o_idx);
+    a.w = (float *)(ws + o_w);
+    a.ctl = (int *)(ws + o_ctl);
+    a.slot_expert = (int *)(ws + o_slot_e);
+    a.slot_off = (int *)(ws + o_slot_off);
+    a.slot_cnt = (int *)(ws + o_slot_cnt);
+    a.row_token = (int *)(ws + o_row_tok);
+    a.pair_row = (int *)(ws + o_pair_row);
+    a.items = (int *)(ws + o_items);
+    a.gu_part = (float *)(ws + o_gu);
+    a.mid = (float *)(ws + o_mid);
+    a.dn_part = (float *)(ws + o_dn);
+
+    int rc;
+    if ((rc = launch(ctx, "moe_norm", ornk_moe_norm, &a))) return rc;
+    if ((rc = launch(ctx, "moe_route", ornk_moe_route, &a))) return rc;
+    if ((rc = launch(ctx, "moe_dispatch", ornk_moe_dispatch, &a))) return rc;
+    if ((rc = launch(ctx, "moe_gateup", ornk_moe_gateup, &a))) return rc;
+    if ((rc = launch(ctx, "moe_mid", ornk_moe_mid, &a))) return rc;
+    if ((rc = launch(ctx, "moe_down", ornk_moe_down, &a))) return rc;
+    if ((rc = launch(ctx, "moe_combine", ornk_moe_combine, &a))) return rc;
+
+    hipStream_t s = ctx->stream;
+    if (idx_out)
+        hipMemcpyAsync(idx_out, a.idx, (size_t)T * k * 4, hipMemcpyDeviceToDevice, s);
+    if (w_out) hipMemcpyAsync(w_out, a.w, (size_t)T * k * 4, hipMemcpyDeviceToDevice, s);
+    hipMemcpyAsync(ctx->ctl_host, a.ctl, 16 * sizeof(int), hipMemcpyDeviceToHost, s);
+    if (!(flags & ORN_MOE_ASYNC))
+        return orn_hip_check(ctx, hipStreamSynchronize(s), "moe forward");
+    return ORN_OK;
+}
+
+int gpu_moe_forward(gpu_context *ctx, ornith_moe_store *st, int layer, const gpu_buffer *x,
+                    int n_tokens, const gpu_buffer *resid, gpu_buffer *out, gpu_buffer *idx_out,
+                    gpu_buffer *w_out, const ornith_moe_opts *opts)
+{
+    if (!ctx) return ORN_EINVAL;
+    if (!st || !x || !out || n_tokens < 0)
+        return orn_set_err(ctx, ORN_EINVAL, "gpu_moe_forward: NULL argument or negative T");
+    if (layer < 0 || layer >= st->sh.n_layers)
+        return orn_set_err(ctx, ORN_EINVAL, "gpu_moe_forward: bad layer");
+    if (n_tokens == 0) return ORN_OK;
+    const size_t act = (size_t)n_tokens * st->sh.d_model * 4;
+    const size_t sel = (size_t)n_tokens * st->sh.top_k * 4;
+    if (!check_buf(x, act) || !check_buf(out, act) || (resid && !check_buf(resid, act)) ||
+        (idx_out && !check_buf(idx_out, sel)) || (w_out && !check_buf(w_out, sel)))
+        return orn_set_err(ctx, ORN_EINVAL, "gpu_moe_forward: buffer too small");
+    if (out == x || out == resid)
+        return orn_set_err(ctx, ORN_EINVAL, "gpu_moe_forward: out aliases an input");
+    return moe_forward_dev(ctx, st, layer, (const float *)x->dev, n_tokens,
+                           resid ? (const float *)resid->dev : NULL, (float *)out->dev,
+                           idx_out ? (uint32_t *)idx_out->dev : NULL,
+                           w_out ? (float *)w_out->dev : NULL, opts);
+}
+
+int gpu_moe_forward_stack(gpu_context *ctx, ornith_moe_store *st, int first_layer, int n_layers,
+                          gpu_buffer *x, gpu_buffer *tmp, int n_tokens, const ornith_moe_opts *opts)
+{
+    if (!ctx) return ORN_EINVAL;
+    if (!st || !x || !tmp || n_tokens < 0 || n_layers < 0 || first_layer < 0 ||
+        first_layer + n_layers > st->sh.n_layers)
+        return orn_set_err(ctx, ORN_EINVAL, "gpu_moe_forward_stack: bad arguments");
+    const size_t act = (size_t)n_tokens * st->sh.d_model * 4;
+    if (!check_buf(x, act) || !check_buf(tmp, act) || x == tmp)
+        return orn_set_err(ctx, ORN_EINVAL, "gpu_moe_forward_stack: buffer too small");
+    if (n_tokens == 0 || n_layers == 0) return ORN_OK;
+    ornith_moe_opts o = {opts ? opts->route_mode : ORN_ROUTE_RENORM,
+                         (opts ? opts->flags : 0u) | ORN_MOE_NORM | ORN_MOE_ASYNC};
+    float *a = (float *)x->dev, *b = (float *)tmp->dev;
+    for (int l = 0; l < n_layers; ++l) {
+        int rc = moe_forward_dev(ctx, st, first_layer + l, a, n_tokens, a, b, NULL, NULL, &o);
+        if (rc) return rc;
+        float *t = a;
+        a = b;
+        b = t;
+    }
+    if (a != (float *)x->dev)
+        hipMemcpyAsync(x->dev, a, act, hipMemcpyDeviceToDevice, ctx->stream);
+    if (!(opts && (opts->flags & ORN_MOE_ASYNC)))
+        return orn_hip_check(ctx, hipStreamSynchronize(ctx->stream), "moe stack");
+    return ORN_OK;
+}
+
+int gpu_moe_last_stats(gpu_context *ctx, int *n_slots, int *n_rows, int *n_exact)
+{
+    if (!ctx) return ORN_EINVAL;
+    hipStreamSynchronize(ctx->stream);
+    if (n_slots) *n_slots = ctx->ctl_host[0];
+    if (n_rows) *n_rows = ctx->ctl_host[2];
+    if (n_exact) *n_exact = ctx->ctl_host[3];
+    return ORN_OK;
+}

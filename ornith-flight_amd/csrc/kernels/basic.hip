@@ -1,0 +1,122 @@
+// SPDX-License-Identifier: MIT
+//
+// fp32 element-wise and small dense kernels behind the gpu.h backend API.
+// Compiled with -ffp-contract=off: every mul/add below rounds separately, in
+// the order written, like the reference CPU backend (gpu.c:104-238).
+#include "common.h"
+#include "launch.h"
+
+namespace {
+
+__global__ void k_fill(float *p, float v, size_t n)
+{
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) p[i] = v;
+}
+
+// gpu.c:104-115: C[i][j] = sum_k A[i][k] * B[k][j], k ascending from 0.0f.
+// One thread per output keeps the reference's summation order, so results
+// are bit-identical to the CPU backend.  B reads are coalesced over j.
+__global__ void k_matmul(float *C, const float *A, const float *B, int M, int N, int K)
+{
+    int j = blockIdx.x * blockDim.x + threadIdx.x;
+    int i = blockIdx.y;
+    if (j >= N || i >= M) return;
+    const float *a = A + (size_t)i * K;
+    float sum = 0.0f;
+    for (int k = 0; k < K; ++k) sum += a[k] * B[(size_t)k * N + j];
+    C[(size_t)i * N + j] = sum;
+}
+
+// gpu.c:144-156 per row: ss is the reference's sequential sum (one lane, so
+// the roundings match), then out = w * (x * inv_rms).
+__global__ void k_rmsnorm(float *out, const float *x, const float *w, int dim)
+{
+    __shared__ float inv_s;
+    const float *xr = x + (size_t)blockIdx.x * dim;
+    float *orow = out + (size_t)blockIdx.x * dim;
+    if (threadIdx.x == 0) {
+        float ss = 0.0f;
+        for (int i = 0; i < dim; ++i) ss += xr[i] * xr[i];
+        inv_s = 1.0f / sqrtf(ss / (float)dim + 1e-6f);
+    }
+    __syncthreads();
+    const float inv = inv_s;
+    for (int i = threadIdx.x; i < dim; i += blockDim.x) orow[i] = w[i] * (xr[i] * inv);
+}
+
+__global__ void k_silu(float *out, const float *x, int n)
+{
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        float v = x[i];
+        out[i] = v / (1.0f + expf(-v));
+    }
+}
+
+__global__ void k_silu_mul(float *out, const float *g, const float *u, int n)
+{
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        float v = g[i];
+        out[i] = (v / (1.0f + expf(-v))) * u[i];
+    }
+}
+
+__global__ void k_add(float *out, const float *a, const float *b, int n)
+{
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = a[i] + b[i];
+}
+
+inline int blocks_for(size_t n, int bs) { return (int)((n + (size_t)bs - 1) / (size_t)bs); }
+
+}  // namespace
+
+extern "C" int ornk_fill_f32(float *p, float v, size_t n, hipStream_t s)
+{
+    if (n == 0) return hipSuccess;
+    size_t nb = (n + 255) / 256;
+    int grid = nb > 65536 ? 65536 : (int)nb;
+    hipLaunchKernelGGL(k_fill, dim3(grid), dim3(256), 0, s, p, v, n);
+    return hipGetLastError();
+}
+
+extern "C" int ornk_matmul_f32(float *C, const float *A, const float *B, int M, int N, int K,
+                               hipStream_t s)
+{
+    if (M <= 0 || N <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_matmul, dim3(blocks_for((size_t)N, 256), M), dim3(256), 0, s, C, A, B, M,
+                       N, K);
+    return hipGetLastError();
+}
+
+extern "C" int ornk_rmsnorm(float *out, const float *x, const float *w, int rows, int dim,
+                            hipStream_t s)
+{
+    if (rows <= 0 || dim <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_rmsnorm, dim3(rows), dim3(256), 0, s, out, x, w, dim);
+    return hipGetLastError();
+}
+
+extern "C" int ornk_silu(float *out, const float *x, int n, hipStream_t s)
+{
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_silu, dim3(blocks_for((size_t)n, 256)), dim3(256), 0, s, out, x, n);
+    return hipGetLastError();
+}
+
+extern "C" int ornk_silu_mul(float *out, const float *g, const float *u, int n, hipStream_t s)
+{
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_silu_mul, dim3(blocks_for((size_t)n, 256)), dim3(256), 0, s, out, g, u, n);
+    return hipGetLastError();
+}
+
+extern "C" int ornk_add(float *out, const float *a, const float *b, int n, hipStream_t s)
+{
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_add, dim3(blocks_for((size_t)n, 256)), dim3(256), 0, s, out, a, b, n);
+    return hipGetLastError();
+}

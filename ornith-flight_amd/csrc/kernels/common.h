@@ -1,0 +1,59 @@
+// SPDX-License-Identifier: MIT
+//
+// Device-side helpers shared by the gfx950 kernels: the reference's fp16
+// conversion, K-quant scale unpacking, wave reductions, and the fixed
+// super-block geometry.  Only included from .hip translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../../include/ornith/kquant.h"
+
+#define ORN_WAVE 64
+
+// gguf.c:16-26.  0x0000 -> 0; every other pattern is decoded as a normal
+// number with exponent bias 112 (0x8000 -> -2^-15, subnormal patterns ->
+// 2^-15*(1+m/1024), exp=31 -> 2^16*(1+m/1024)).  Pure integer work, so the
+// result is bit-identical to the reference on every input.
+__device__ __forceinline__ float orn_half_to_float(uint32_t h)
+{
+    h &= 0xFFFFu;
+    if (h == 0u) return 0.0f;
+    uint32_t u = ((h & 0x8000u) << 16) | ((((h & 0x7C00u) >> 10) + 112u) << 23) |
+                 ((h & 0x03FFu) << 13);
+    return __uint_as_float(u);
+}
+
+__device__ __forceinline__ uint32_t orn_byte(uint32_t w, int i) { return (w >> (8 * i)) & 0xFFu; }
+
+// gguf.c:31-40, with the 12 packed scale bytes held as three little-endian
+// dwords s0 (bytes 0-3), s1 (bytes 4-7), s2 (bytes 8-11).
+__device__ __forceinline__ void orn_scale_min_k4(int j, uint32_t s0, uint32_t s1, uint32_t s2,
+                                                 uint32_t &sc, uint32_t &m)
+{
+    if (j < 4) {
+        sc = orn_byte(s0, j) & 63u;
+        m = orn_byte(s1, j) & 63u;
+    } else {
+        uint32_t b = orn_byte(s2, j - 4);
+        sc = (b & 0xFu) | ((orn_byte(s0, j - 4) >> 6) << 4);
+        m = (b >> 4) | ((orn_byte(s1, j - 4) >> 6) << 4);
+    }
+}
+
+// Unaligned-safe little-endian byte reads (for the GGUF AoS Q6_K stream whose
+// 210-byte blocks are only 2-byte aligned).
+__device__ __forceinline__ uint32_t orn_ld_u8(const uint8_t *p) { return (uint32_t)(*p); }
+__device__ __forceinline__ uint32_t orn_ld_u16(const uint8_t *p)
+{
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8);
+}
+
+// Sum over the 64 lanes of a wave (fixed butterfly order -> deterministic).
+__device__ __forceinline__ float orn_wave_sum(float v)
+{
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, ORN_WAVE);
+    return v;
+}

@@ -1,0 +1,136 @@
+// SPDX-License-Identifier: MIT
+//
+// GGUF dequantization on the device, bit-exact with the reference:
+//   whole tensor   gguf.c:605-638  (F32 copy, F16, Q4_K, Q6_K)
+//   expert slice   gguf.c:652-711  (interleaved: slice[i] = full[i*E + e])
+//
+// Exactness: d*sc has <= 17 significant bits (Q4_K) and d*sc*q <= 24 bits
+// (Q6_K), so every product below is exact in fp32; the only rounding is
+// Q4_K's final "- dmin*m", which this code performs exactly as the reference
+// does.  The half decode is the reference's integer mapping (common.h).
+// Reads are byte-granular because GGUF Q6_K blocks (210 B) are only 2-byte
+// aligned inside a tensor.
+#include "common.h"
+#include "launch.h"
+
+namespace {
+
+__device__ __forceinline__ float q4k_elem(const uint8_t *blk, int pos)
+{
+    const int sub = pos >> 5, chunk = pos >> 6, half = (pos >> 5) & 1, l = pos & 31;
+    const uint8_t *s = blk + ORN_Q4K_OFF_SCALES;
+    uint32_t sc, m;
+    if (sub < 4) {
+        sc = s[sub] & 63u;
+        m = s[sub + 4] & 63u;
+    } else {
+        sc = (s[sub + 4] & 0xFu) | (((uint32_t)s[sub - 4] >> 6) << 4);
+        m = ((uint32_t)s[sub + 4] >> 4) | (((uint32_t)s[sub] >> 6) << 4);
+    }
+    const float d_val = orn_half_to_float(orn_ld_u16(blk + ORN_Q4K_OFF_D)) * (float)sc;
+    const float min_val = orn_half_to_float(orn_ld_u16(blk + ORN_Q4K_OFF_DMIN)) * (float)m;
+    const uint32_t b = blk[ORN_Q4K_OFF_QS + chunk * 32 + l];
+    const uint32_t q = half ? (b >> 4) : (b & 0x0Fu);
+    return d_val * (float)q - min_val;
+}
+
+__device__ __forceinline__ float q6k_elem(const uint8_t *blk, int pos)
+{
+    const int pass = pos >> 7, lane = (pos >> 5) & 3, l = pos & 31, is = l >> 4;
+    const float d = orn_half_to_float(orn_ld_u16(blk + ORN_Q6K_OFF_D));
+    const uint32_t qlb = blk[ORN_Q6K_OFF_QL + pass * 64 + ((lane & 1) ? 32 + l : l)];
+    const uint32_t qhb = blk[ORN_Q6K_OFF_QH + pass * 32 + l];
+    const uint32_t lo = (lane < 2) ? (qlb & 0x0Fu) : (qlb >> 4);
+    const int q = (int)(lo | (((qhb >> (2 * lane)) & 3u) << 4)) - 32;
+    const int sc = (int)(int8_t)blk[ORN_Q6K_OFF_SCALES + pass * 8 + lane * 2 + is];
+    return d * (float)sc * (float)q;
+}
+
+__global__ void k_dequant_q4k(const uint8_t *src, float *dst, uint64_t n_blocks)
+{
+    for (uint64_t b = blockIdx.x; b < n_blocks; b += gridDim.x)
+        dst[b * ORN_QK_K + threadIdx.x] = q4k_elem(src + b * ORN_Q4K_BYTES, (int)threadIdx.x);
+}
+
+__global__ void k_dequant_q6k(const uint8_t *src, float *dst, uint64_t n_blocks)
+{
+    for (uint64_t b = blockIdx.x; b < n_blocks; b += gridDim.x)
+        dst[b * ORN_QK_K + threadIdx.x] = q6k_elem(src + b * ORN_Q6K_BYTES, (int)threadIdx.x);
+}
+
+__global__ void k_dequant_f16(const uint8_t *src, float *dst, uint64_t n)
+{
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        dst[i] = orn_half_to_float(orn_ld_u16(src + 2 * i));
+}
+
+// One output element per thread: linear = i*E + e, then the single-element
+// extractor of the block that holds it (gguf.c:686-706).
+__global__ void k_slice(const uint8_t *src, int type, uint64_t per, uint64_t n_experts,
+                        uint64_t e, float *dst)
+{
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < per; i += stride) {
+        const uint64_t lin = i * n_experts + e;
+        float v;
+        if (type == ORN_TYPE_Q4_K)
+            v = q4k_elem(src + (lin / ORN_QK_K) * ORN_Q4K_BYTES, (int)(lin % ORN_QK_K));
+        else if (type == ORN_TYPE_Q6_K)
+            v = q6k_elem(src + (lin / ORN_QK_K) * ORN_Q6K_BYTES, (int)(lin % ORN_QK_K));
+        else if (type == ORN_TYPE_F16)
+            v = orn_half_to_float(orn_ld_u16(src + 2 * lin));
+        else
+            v = reinterpret_cast<const float *>(src)[lin];
+        dst[i] = v;
+    }
+}
+
+inline int grid_cap(uint64_t n, uint64_t per_block)
+{
+    uint64_t g = (n + per_block - 1) / per_block;
+    return g > 65536 ? 65536 : (int)(g ? g : 1);
+}
+
+}  // namespace
+
+extern "C" int ornk_dequant(const void *src, int type, uint64_t n_elems, float *dst, hipStream_t s)
+{
+    const uint8_t *p = static_cast<const uint8_t *>(src);
+    const uint64_t nb = n_elems / ORN_QK_K;
+    switch (type) {
+    case ORN_TYPE_F32:
+        if (n_elems == 0) return hipSuccess;
+        return hipMemcpyAsync(dst, src, n_elems * 4, hipMemcpyDeviceToDevice, s);
+    case ORN_TYPE_F16:
+        if (n_elems == 0) return hipSuccess;
+        hipLaunchKernelGGL(k_dequant_f16, dim3(grid_cap(n_elems, 256)), dim3(256), 0, s, p, dst,
+                           n_elems);
+        return hipGetLastError();
+    case ORN_TYPE_Q4_K:
+        if (nb == 0) return hipSuccess;
+        hipLaunchKernelGGL(k_dequant_q4k, dim3(grid_cap(nb, 1)), dim3(ORN_QK_K), 0, s, p, dst, nb);
+        return hipGetLastError();
+    case ORN_TYPE_Q6_K:
+        if (nb == 0) return hipSuccess;
+        hipLaunchKernelGGL(k_dequant_q6k, dim3(grid_cap(nb, 1)), dim3(ORN_QK_K), 0, s, p, dst, nb);
+        return hipGetLastError();
+    default:
+        return hipErrorInvalidValue;
+    }
+}
+
+extern "C" int ornk_dequant_slice(const void *src, int type, uint64_t n_elems, uint64_t n_experts,
+                                  int expert, float *dst, hipStream_t s)
+{
+    if (n_experts == 0 || expert < 0 || (uint64_t)expert >= n_experts) return hipErrorInvalidValue;
+    if (type != ORN_TYPE_F32 && type != ORN_TYPE_F16 && type != ORN_TYPE_Q4_K &&
+        type != ORN_TYPE_Q6_K)
+        return hipErrorInvalidValue;
+    const uint64_t per = n_elems / n_experts;
+    if (per == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_slice, dim3(grid_cap(per, 256)), dim3(256), 0, s,
+                       static_cast<const uint8_t *>(src), type, per, n_experts, (uint64_t)expert,
+                       dst);
+    return hipGetLastError();
+}

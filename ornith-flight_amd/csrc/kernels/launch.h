@@ -1,0 +1,93 @@
+/* SPDX-License-Identifier: MIT
+ *
+ * The thin C ABI between the C99 host code (csrc/host/) and the hand-written
+ * gfx950 kernels (csrc/kernels/ .hip files).  Plain pointers, sizes and a HIP
+ * stream; every launcher returns a hipError_t value (0 = success) and only
+ * enqueues work on the given stream.
+ */
+#ifndef ORNITH_KERNELS_LAUNCH_H
+#define ORNITH_KERNELS_LAUNCH_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifndef __HIP_PLATFORM_AMD__
+#define __HIP_PLATFORM_AMD__ 1
+#endif
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- generic fp32 ops behind gpu.h --------------------------------------- */
+int ornk_fill_f32(float *p, float v, size_t n, hipStream_t s);
+int ornk_matmul_f32(float *C, const float *A, const float *B, int M, int N, int K, hipStream_t s);
+int ornk_rmsnorm(float *out, const float *x, const float *w, int rows, int dim, hipStream_t s);
+int ornk_silu(float *out, const float *x, int n, hipStream_t s);
+int ornk_silu_mul(float *out, const float *g, const float *u, int n, hipStream_t s);
+int ornk_add(float *out, const float *a, const float *b, int n, hipStream_t s);
+
+/* ---- GGUF dequant (gguf.c:605-711 semantics) ----------------------------- */
+int ornk_dequant(const void *src, int type, uint64_t n_elems, float *dst, hipStream_t s);
+int ornk_dequant_slice(const void *src, int type, uint64_t n_elems, uint64_t n_experts,
+                       int expert, float *dst, hipStream_t s);
+
+/* ---- routing -------------------------------------------------------------- */
+/* Bit-exact sequential fp32 router logits for T tokens (model.c:1017-1025). */
+int ornk_router_exact(const float *x, const float *W, const float *bias, int T, int D, int E,
+                      float *logits, hipStream_t s);
+/* Per-token top-k with the reference's exchange-selection semantics.
+ * mode 0: exchange on logits + softmax over the top-k (model.c:301-317);
+ * mode 1: full softmax + exchange on probabilities (model.c:1027-1049).
+ * n_exact (device int, may be NULL) counts tokens that needed the exact
+ * sequential exchange simulation (ties or NaN). */
+int ornk_topk(const float *logits, int T, int E, int k, int mode, uint32_t *idx, float *w,
+              int *n_exact, hipStream_t s);
+
+/* ---- the routed-MoE layer -------------------------------------------------- */
+/* Device layout of one layer's experts (expert index E is the shared expert):
+ *   gate/up   : [E+1][H/256][D] Q4_K blocks of 144 B, block (row k, block
+ *               column c) of expert e at ((e*(H/256) + c)*D + k)*144
+ *   down_body : [E+1][D/256][H] Q6_K bodies of 208 B (ql|qh|scales)
+ *   down_d    : [E+1][D/256][H] Q6_K super-scales (fp16 bits)
+ * Work buffers are owned by the host; sizes are computed by ornk_moe_ws_size. */
+typedef struct {
+    int T, D, H, E, k, has_shared, mode, apply_norm;
+    int ks_gu, ks_dn, rows_max, items_max;
+    const uint8_t *gate, *up, *down_body;
+    const uint16_t *down_d;
+    const float *router, *bias, *norm_w;
+    const float *x, *resid;
+    float *out;
+    /* workspace */
+    float *xn;        /* [T][D]  expert input (x or rmsnorm(x)) */
+    float *logits;    /* [T][E] */
+    double *rpart;    /* [T][E][D/128][2] certified router partials */
+    uint32_t *idx;    /* [T][k] */
+    float *w;         /* [T][k] */
+    int *ctl;         /* [16] counters: 0 n_slots, 1 n_items, 2 n_rows, 3 n_exact */
+    int *slot_expert; /* [E+1] */
+    int *slot_off;    /* [E+1] */
+    int *slot_cnt;    /* [E+1] */
+    int *row_token;   /* [rows_max] */
+    int *pair_row;    /* [T*k] */
+    int *items;       /* [items_max][4]: slot, row_begin, n_rows, pad */
+    float *gu_part;   /* [ks_gu][rows_max][2H] */
+    float *mid;       /* [rows_max][H] */
+    float *dn_part;   /* [ks_dn][rows_max][D] */
+} ornk_moe_args;
+
+int ornk_moe_norm(const ornk_moe_args *a, hipStream_t s);
+int ornk_moe_route(const ornk_moe_args *a, hipStream_t s);
+int ornk_moe_dispatch(const ornk_moe_args *a, hipStream_t s);
+int ornk_moe_gateup(const ornk_moe_args *a, hipStream_t s);
+int ornk_moe_mid(const ornk_moe_args *a, hipStream_t s);
+int ornk_moe_down(const ornk_moe_args *a, hipStream_t s);
+int ornk_moe_combine(const ornk_moe_args *a, hipStream_t s);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ORNITH_KERNELS_LAUNCH_H */

@@ -1,0 +1,327 @@
+"""ctypes binding of libornith_hip.so (the C ABI in include/ornith/*.h).
+
+Host-side mirror used by tests/, bench.py and __graft_entry__.py.  The
+library is the product; this module only marshals numpy arrays to it.  If
+the shared library has not been built, importing succeeds but every call
+raises: there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libornith_hip.so")
+
+TYPE_F32, TYPE_F16, TYPE_Q4_K, TYPE_Q6_K = 0, 1, 12, 14
+MAT_GATE, MAT_UP, MAT_DOWN = 0, 1, 2
+ROUTE_RENORM, ROUTE_LITERAL = 0, 1
+MOE_ASYNC, MOE_NORM = 1, 2
+SYN_GATE, SYN_UP, SYN_DOWN, SYN_ROUTER, SYN_ACT, SYN_ZIPF = 1, 2, 3, 4, 5, 6
+GPU_BUF_DEFAULT, GPU_BUF_SHARED, GPU_BUF_CONSTANT = 0, 1, 2
+Q4K_BYTES, Q6K_BYTES = 144, 210
+
+# Every symbol the public headers declare (include/ornith/gpu.h, ornith_hip.h).
+EXPORTED = [
+    "gpu_init", "gpu_destroy", "gpu_alloc", "gpu_free", "gpu_get_cpu_ptr", "gpu_buffer_size",
+    "gpu_copy_to_device", "gpu_copy_to_host", "gpu_copy_buffer", "gpu_matmul", "gpu_matmul_int4",
+    "gpu_rmsnorm", "gpu_silu", "gpu_silu_mul", "gpu_rope", "gpu_attention", "gpu_deltanet_step",
+    "gpu_expert_mlp", "gpu_router", "gpu_topk_softmax", "gpu_add", "gpu_sync", "gpu_memory_used",
+    "gpu_print_info",
+    "gpu_last_error", "gpu_device_ptr", "gpu_device_info",
+    "gpu_dequantize_tensor_from_buf", "gpu_dequantize_expert_slice_from_buf",
+    "gpu_dequantize_tensor_buf", "gpu_dequantize_expert_slice_buf",
+    "gpu_moe_store_create", "gpu_moe_store_destroy", "gpu_moe_store_bytes",
+    "gpu_moe_store_set_experts", "gpu_moe_store_set_router", "gpu_moe_store_set_norm",
+    "gpu_moe_store_fill_synthetic", "gpu_moe_forward", "gpu_moe_forward_stack",
+    "gpu_moe_last_stats",
+    "gpu_profile_enable", "gpu_profile_reset", "gpu_profile_count", "gpu_profile_name",
+    "gpu_profile_total_ms", "gpu_profile_calls",
+    "orn_synth_stream", "orn_synth_q4k", "orn_synth_q6k", "orn_synth_normal",
+    "orn_synth_zipf_bias",
+]
+
+
+class TensorInfo(C.Structure):
+    """orn_tensor_info (layout of the reference's gguf_tensor_info, gguf.h:15-23)."""
+    _fields_ = [("name", C.c_char_p), ("type", C.c_int), ("n_dims", C.c_uint32),
+                ("dims", C.c_uint64 * 4), ("offset", C.c_size_t), ("size_bytes", C.c_size_t),
+                ("n_elems", C.c_size_t)]
+
+
+class MoEShape(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("n_layers", "d_model", "hidden", "n_experts", "top_k",
+                                       "has_shared")]
+
+
+class MoEOpts(C.Structure):
+    _fields_ = [("route_mode", C.c_int), ("flags", C.c_uint)]
+
+
+_lib = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", HERE, "-j8"], check=True)
+
+
+def lib():
+    """Load the built library; raise if it is missing (no fallback)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build()")
+    L = C.CDLL(LIB_PATH)
+    vp, sz, i, u64, f = C.c_void_p, C.c_size_t, C.c_int, C.c_uint64, C.c_float
+    sig = {
+        "gpu_init": (vp, []), "gpu_destroy": (None, [vp]),
+        "gpu_alloc": (vp, [vp, sz, i]), "gpu_free": (None, [vp, vp]),
+        "gpu_get_cpu_ptr": (vp, [vp, vp]), "gpu_buffer_size": (sz, [vp, vp]),
+        "gpu_copy_to_device": (None, [vp, vp, vp, sz]), "gpu_copy_to_host": (None, [vp, vp, vp, sz]),
+        "gpu_copy_buffer": (None, [vp, vp, vp, sz]),
+        "gpu_matmul": (None, [vp, vp, vp, vp, i, i, i, i, i]),
+        "gpu_matmul_int4": (None, [vp, vp, vp, vp, i, i, i]),
+        "gpu_rmsnorm": (None, [vp, vp, vp, vp, i, i]), "gpu_silu": (None, [vp, vp, vp, i]),
+        "gpu_silu_mul": (None, [vp, vp, vp, vp, i]),
+        "gpu_rope": (None, [vp, vp, vp, i, i, i, i, f, i]),
+        "gpu_attention": (None, [vp, vp, vp, vp, vp, i, i]),
+        "gpu_deltanet_step": (None, [vp, vp, vp, vp, vp, i]),
+        "gpu_expert_mlp": (None, [vp, vp, vp, vp, vp, vp, i, i, i]),
+        "gpu_router": (None, [vp, vp, vp, vp, i, i]),
+        "gpu_topk_softmax": (None, [vp, vp, vp, vp, i, i]),
+        "gpu_add": (None, [vp, vp, vp, vp, i]), "gpu_sync": (None, [vp]),
+        "gpu_memory_used": (sz, [vp]), "gpu_print_info": (None, [vp]),
+        "gpu_last_error": (C.c_char_p, [vp]), "gpu_device_ptr": (vp, [vp, vp]),
+        "gpu_device_info": (i, [vp, C.c_char_p, sz, C.POINTER(C.c_int), C.POINTER(C.c_size_t)]),
+        "gpu_dequantize_tensor_from_buf": (C.c_bool, [vp, vp, C.POINTER(TensorInfo), vp]),
+        "gpu_dequantize_expert_slice_from_buf": (C.c_bool, [vp, vp, C.POINTER(TensorInfo), i, vp]),
+        "gpu_dequantize_tensor_buf": (C.c_bool, [vp, vp, C.POINTER(TensorInfo), vp]),
+        "gpu_dequantize_expert_slice_buf": (C.c_bool, [vp, vp, C.POINTER(TensorInfo), i, vp]),
+        "gpu_moe_store_create": (vp, [vp, C.POINTER(MoEShape)]),
+        "gpu_moe_store_destroy": (None, [vp, vp]), "gpu_moe_store_bytes": (sz, [vp]),
+        "gpu_moe_store_set_experts": (i, [vp, vp, i, i, i, i, vp]),
+        "gpu_moe_store_set_router": (i, [vp, vp, i, vp, vp]),
+        "gpu_moe_store_set_norm": (i, [vp, vp, i, vp]),
+        "gpu_moe_store_fill_synthetic": (i, [vp, vp, i, u64, f]),
+        "gpu_moe_forward": (i, [vp, vp, i, vp, i, vp, vp, vp, vp, C.POINTER(MoEOpts)]),
+        "gpu_moe_forward_stack": (i, [vp, vp, i, i, vp, vp, i, C.POINTER(MoEOpts)]),
+        "gpu_moe_last_stats": (i, [vp, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+        "gpu_profile_enable": (i, [vp, i]), "gpu_profile_reset": (None, [vp]),
+        "gpu_profile_count": (i, [vp]), "gpu_profile_name": (C.c_char_p, [vp, i]),
+        "gpu_profile_total_ms": (C.c_double, [vp, i]), "gpu_profile_calls": (C.c_long, [vp, i]),
+        "orn_synth_stream": (u64, [i, i, i]),
+        "orn_synth_q4k": (None, [u64, u64, u64, u64, vp]),
+        "orn_synth_q6k": (None, [u64, u64, u64, u64, vp]),
+        "orn_synth_normal": (None, [u64, u64, u64, f, vp]),
+        "orn_synth_zipf_bias": (None, [u64, u64, i, f, vp]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+# ---------------------------------------------------------------- synthetic data
+def synth_stream(layer: int, kind: int, expert: int) -> int:
+    return lib().orn_synth_stream(layer, kind, expert)
+
+
+def synth_q4k(seed: int, stream: int, n_blocks: int, first: int = 0) -> np.ndarray:
+    out = np.empty(n_blocks * Q4K_BYTES, np.uint8)
+    lib().orn_synth_q4k(seed, stream, first, n_blocks, _p(out))
+    return out
+
+
+def synth_q6k(seed: int, stream: int, n_blocks: int, first: int = 0) -> np.ndarray:
+    out = np.empty(n_blocks * Q6K_BYTES, np.uint8)
+    lib().orn_synth_q6k(seed, stream, first, n_blocks, _p(out))
+    return out
+
+
+def synth_normal(seed: int, stream: int, n: int, sigma: float) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    lib().orn_synth_normal(seed, stream, n, sigma, _p(out))
+    return out
+
+
+def synth_zipf_bias(seed: int, stream: int, n_experts: int, s: float) -> np.ndarray:
+    out = np.empty(n_experts, np.float32)
+    lib().orn_synth_zipf_bias(seed, stream, n_experts, s, _p(out))
+    return out
+
+
+class SyntheticLayer:
+    """Host copy of one synthetic layer (the bytes gpu_moe_store_fill_synthetic
+    uploads), for feeding the oracle."""
+
+    def __init__(self, seed, layer, D, H, E, has_shared=True, zipf_s=0.0):
+        nb = D * H // 256
+        E1 = E + (1 if has_shared else 0)
+        self.gate = np.concatenate([synth_q4k(seed, synth_stream(layer, SYN_GATE, e), nb) for e in range(E1)])
+        self.up = np.concatenate([synth_q4k(seed, synth_stream(layer, SYN_UP, e), nb) for e in range(E1)])
+        self.down = np.concatenate([synth_q6k(seed, synth_stream(layer, SYN_DOWN, e), nb) for e in range(E1)])
+        self.router = synth_normal(seed, synth_stream(layer, SYN_ROUTER, 0), D * E, 0.02).reshape(D, E)
+        self.bias = synth_zipf_bias(seed, synth_stream(layer, SYN_ZIPF, 0), E, zipf_s) if zipf_s > 0 else None
+        self.nb, self.E, self.has_shared = nb, E, has_shared
+
+    def routed(self, which):
+        a = getattr(self, which)
+        per = self.nb * (Q6K_BYTES if which == "down" else Q4K_BYTES)
+        return a[: self.E * per]
+
+    def shared(self, which):
+        a = getattr(self, which)
+        per = self.nb * (Q6K_BYTES if which == "down" else Q4K_BYTES)
+        return a[self.E * per:(self.E + 1) * per] if self.has_shared else None
+
+
+# ---------------------------------------------------------------- device side
+class Buffer:
+    def __init__(self, ctx, ptr, size):
+        self.ctx, self.ptr, self.size = ctx, ptr, size
+
+    def free(self):
+        if self.ptr:
+            lib().gpu_free(self.ctx.ptr, self.ptr)
+            self.ptr = None
+
+
+class Context:
+    def __init__(self):
+        L = lib()
+        self.ptr = L.gpu_init()
+        if not self.ptr:
+            raise RuntimeError("gpu_init failed (no HIP device)")
+        self._bufs = []
+
+    def check(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed ({rc}): {self.last_error()}")
+
+    def last_error(self) -> str:
+        return lib().gpu_last_error(self.ptr).decode()
+
+    def alloc(self, nbytes, shared=False) -> Buffer:
+        p = lib().gpu_alloc(self.ptr, nbytes, GPU_BUF_SHARED if shared else GPU_BUF_DEFAULT)
+        if not p:
+            raise MemoryError(f"gpu_alloc({nbytes}) failed")
+        b = Buffer(self, p, nbytes)
+        self._bufs.append(b)
+        return b
+
+    def upload(self, arr: np.ndarray) -> Buffer:
+        a = np.ascontiguousarray(arr)
+        b = self.alloc(max(a.nbytes, 1))
+        lib().gpu_copy_to_device(self.ptr, b.ptr, _p(a), a.nbytes)
+        return b
+
+    def download(self, buf: Buffer, dtype, shape) -> np.ndarray:
+        out = np.empty(shape, dtype)
+        lib().gpu_copy_to_host(self.ptr, _p(out), buf.ptr, out.nbytes)
+        return out
+
+    def sync(self):
+        lib().gpu_sync(self.ptr)
+
+    def device_info(self):
+        name = C.create_string_buffer(256)
+        cus = C.c_int(0)
+        hbm = C.c_size_t(0)
+        self.check(lib().gpu_device_info(self.ptr, name, 256, C.byref(cus), C.byref(hbm)), "device_info")
+        return name.value.decode(), cus.value, hbm.value
+
+    def close(self):
+        if self.ptr:
+            for b in self._bufs:
+                b.free()
+            lib().gpu_destroy(self.ptr)
+            self.ptr = None
+
+
+class Store:
+    def __init__(self, ctx: Context, n_layers, D, H, E, k, has_shared=True):
+        self.ctx = ctx
+        self.shape = MoEShape(n_layers, D, H, E, k, 1 if has_shared else 0)
+        self.ptr = lib().gpu_moe_store_create(ctx.ptr, C.byref(self.shape))
+        if not self.ptr:
+            raise RuntimeError("gpu_moe_store_create failed: " + ctx.last_error())
+        self.D, self.H, self.E, self.k = D, H, E, k
+
+    def set_experts(self, layer, matrix, first, blocks: np.ndarray, n):
+        b = np.ascontiguousarray(blocks, np.uint8)
+        self.ctx.check(lib().gpu_moe_store_set_experts(self.ctx.ptr, self.ptr, layer, matrix, first, n, _p(b)),
+                       "set_experts")
+
+    def set_router(self, layer, W, bias=None):
+        W = np.ascontiguousarray(W, np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        self.ctx.check(lib().gpu_moe_store_set_router(self.ctx.ptr, self.ptr, layer, _p(W),
+                                                      None if b is None else _p(b)), "set_router")
+
+    def set_norm(self, layer, w):
+        w = np.ascontiguousarray(w, np.float32)
+        self.ctx.check(lib().gpu_moe_store_set_norm(self.ctx.ptr, self.ptr, layer, _p(w)), "set_norm")
+
+    def fill_synthetic(self, layer, seed, zipf_s=0.0):
+        self.ctx.check(lib().gpu_moe_store_fill_synthetic(self.ctx.ptr, self.ptr, layer, seed, zipf_s),
+                       "fill_synthetic")
+
+    def load_layer(self, layer, syn: SyntheticLayer):
+        """Upload a host SyntheticLayer (same bytes as fill_synthetic)."""
+        E1 = self.E + (1 if self.shape.has_shared else 0)
+        self.set_experts(layer, MAT_GATE, 0, syn.gate, E1)
+        self.set_experts(layer, MAT_UP, 0, syn.up, E1)
+        self.set_experts(layer, MAT_DOWN, 0, syn.down, E1)
+        self.set_router(layer, syn.router, syn.bias)
+
+    def forward(self, layer, x: Buffer, T, out: Buffer, resid=None, idx=None, w=None,
+                mode=ROUTE_RENORM, flags=0):
+        o = MoEOpts(mode, flags)
+        rc = lib().gpu_moe_forward(self.ctx.ptr, self.ptr, layer, x.ptr, T,
+                                   resid.ptr if resid else None, out.ptr,
+                                   idx.ptr if idx else None, w.ptr if w else None, C.byref(o))
+        self.ctx.check(rc, "gpu_moe_forward")
+
+    def forward_stack(self, first, n, x: Buffer, tmp: Buffer, T, mode=ROUTE_RENORM, flags=0):
+        o = MoEOpts(mode, flags)
+        self.ctx.check(lib().gpu_moe_forward_stack(self.ctx.ptr, self.ptr, first, n, x.ptr, tmp.ptr, T,
+                                                   C.byref(o)), "gpu_moe_forward_stack")
+
+    def last_stats(self):
+        a, b, c = C.c_int(), C.c_int(), C.c_int()
+        self.ctx.check(lib().gpu_moe_last_stats(self.ctx.ptr, C.byref(a), C.byref(b), C.byref(c)), "stats")
+        return {"n_slots": a.value, "n_rows": b.value, "n_exact": c.value}
+
+    def bytes(self):
+        return lib().gpu_moe_store_bytes(self.ptr)
+
+    def close(self):
+        if self.ptr:
+            lib().gpu_moe_store_destroy(self.ctx.ptr, self.ptr)
+            self.ptr = None
+
+
+def profile(ctx: Context):
+    L = lib()
+    n = L.gpu_profile_count(ctx.ptr)
+    return {L.gpu_profile_name(ctx.ptr, i).decode(): (L.gpu_profile_total_ms(ctx.ptr, i),
+                                                      L.gpu_profile_calls(ctx.ptr, i)) for i in range(n)}
+
+
+def tensor_info(typ, dims, size_bytes=None):
+    n = int(np.prod(dims)) if len(dims) else 0
+    if size_bytes is None:
+        size_bytes = {TYPE_F32: 4 * n, TYPE_F16: 2 * n, TYPE_Q4_K: n // 256 * Q4K_BYTES,
+                      TYPE_Q6_K: n // 256 * Q6K_BYTES}.get(typ, 0)
+    arr = (C.c_uint64 * 4)(*(list(dims) + [1] * (4 - len(dims))))
+    return TensorInfo(b"t", typ, len(dims), arr, 0, size_bytes, n)
