@@ -70,7 +70,7 @@ __global__ void __launch_bounds__(1024)
     __syncthreads();
     const int P = T * k;
     for (int p = tid; p < P; p += blockDim.x)
-        if (!(w[p] < 1e-6f)) atomicAdd(&cnt[idx[p] + 1], 1);
+        if (!(w[p] < 1e-6f) && idx[p] < (uint32_t)E) atomicAdd(&cnt[idx[p] + 1], 1);
     if (tid == 0) cnt[0] = has_shared ? T : 0;
     __syncthreads();
 
@@ -99,7 +99,9 @@ __global__ void __launch_bounds__(1024)
     __syncthreads();
 
     for (int p = tid; p < P; p += blockDim.x) {
-        if (w[p] < 1e-6f) {
+        // Skip rule of model.c:1066; an index outside [0, E) cannot come out
+        // of the router but is treated as skipped rather than trusted.
+        if (w[p] < 1e-6f || idx[p] >= (uint32_t)E) {
             pair_row[p] = -1;
             continue;
         }
