@@ -42,6 +42,7 @@ struct gpu_context {
     orn_workspace ws;
     /* device counters read back after a forward */
     int *ctl_host; /* pinned mirror of the last forward's counters */
+    int *last_ctl; /* device counters of the last forward (inside the workspace) */
     /* profiling */
     int prof_on;
     int prof_n_names;

@@ -36,6 +36,7 @@ void *orn_ws_get(gpu_context *ctx, size_t bytes)
     if (ctx->ws.base) hipFree(ctx->ws.base);
     ctx->ws.base = NULL;
     ctx->ws.bytes = 0;
+    ctx->last_ctl = NULL;
     size_t want = bytes + (bytes >> 3);
     if (hipMalloc(&ctx->ws.base, want) != hipSuccess) {
         orn_set_err(ctx, ORN_ENOMEM, "workspace allocation of %zu bytes failed", want);
@@ -389,7 +390,7 @@ int gpu_moe_store_fill_synthetic(gpu_context *ctx, ornith_moe_store *st, int lay
 #define ALIGN256(x) (((x) + 255u) & ~(size_t)255u)
 
 typedef struct {
-    int ks_gu, ks_dn, rows_max, items_max;
+    int ks_gu, ks_dn, rows_max, items_max, tchunk;
 } plan_t;
 
 static int pow2_floor(int v)
@@ -399,29 +400,36 @@ static int pow2_floor(int v)
     return p;
 }
 
+/* Work decomposition for T tokens.  Work items hold up to `tchunk` token rows
+ * of one expert; the gate/up and down kernels split the reduction dimension
+ * into ks slices so the grid holds ~2048 blocks (8 per CU).  Slices keep at
+ * least 32 rows (gate/up) and 32 rows (down) so the split-K partials stay a
+ * small fraction of the weight bytes. */
 static plan_t make_plan(const ornith_moe_shape *sh, int T)
 {
     plan_t p;
     const int k = sh->top_k, E = sh->n_experts;
+    const int D = sh->d_model, H = sh->hidden;
+    p.tchunk = T <= 64 ? 2 : 8;
     p.rows_max = T * k + (sh->has_shared ? T : 0);
     const int max_slots = (T * k < E ? T * k : E) + (sh->has_shared ? 1 : 0);
-    p.items_max = max_slots + (p.rows_max + 7) / 8;
-    const int est_items = max_slots + p.rows_max / 8;
-    const int D = sh->d_model, H = sh->hidden;
-    /* gate/up: enough K-slices for ~2 blocks per CU, at least 16 rows each */
+    p.items_max = max_slots + (p.rows_max + p.tchunk - 1) / p.tchunk;
+    int est_items = max_slots + p.rows_max / p.tchunk;
+    if (est_items < 1) est_items = 1;
+    /* gate/up: K = D rows; a wave covers RW rows per step, a block 4*RW */
     const int rw_gu = 64 / (16 * (H / 256));
-    int ks = pow2_floor(512 / (est_items > 0 ? est_items : 1));
+    int ks = pow2_floor(2048 / est_items);
     if (ks < 1) ks = 1;
-    while (ks > 1 && (D % ks || (D / ks) % (4 * rw_gu) || D / ks < 16 * rw_gu)) ks /= 2;
     if (ks > 64) ks = 64;
+    while (ks > 1 && (D % ks || (D / ks) % (16 * rw_gu) || D / ks < 32)) ks /= 2;
     p.ks_gu = ks;
     /* down: K = H rows */
-    const int crg = (8 * (D / 256)) < 64 ? 8 * (D / 256) : 64;
-    const int rw_dn = 64 / crg;
-    int kd = pow2_floor(256 / (est_items > 0 ? est_items : 1));
+    const int cr = 8 * (D / 256);
+    const int rw_dn = 64 / (cr < 64 ? cr : 64);
+    int kd = pow2_floor(2048 / est_items);
     if (kd < 1) kd = 1;
-    if (kd > 8) kd = 8;
-    while (kd > 1 && (H % kd || (H / kd) % (4 * rw_dn))) kd /= 2;
+    if (kd > 16) kd = 16;
+    while (kd > 1 && (H % kd || (H / kd) % (16 * rw_dn) || H / kd < 32)) kd /= 2;
     p.ks_dn = kd;
     return p;
 }
@@ -490,6 +498,7 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     a.ks_dn = p.ks_dn;
     a.rows_max = p.rows_max;
     a.items_max = p.items_max;
+    a.tchunk = p.tchunk;
     a.gate = st->gate + (size_t)layer * E1nb * 144;
     a.up = st->up + (size_t)layer * E1nb * 144;
     a.down_body = st->down_body + (size_t)layer * E1nb * 208;
@@ -529,7 +538,7 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     if (idx_out)
         hipMemcpyAsync(idx_out, a.idx, (size_t)T * k * 4, hipMemcpyDeviceToDevice, s);
     if (w_out) hipMemcpyAsync(w_out, a.w, (size_t)T * k * 4, hipMemcpyDeviceToDevice, s);
-    hipMemcpyAsync(ctx->ctl_host, a.ctl, 16 * sizeof(int), hipMemcpyDeviceToHost, s);
+    ctx->last_ctl = a.ctl;
     if (!(flags & ORN_MOE_ASYNC))
         return orn_hip_check(ctx, hipStreamSynchronize(s), "moe forward");
     return ORN_OK;
@@ -589,6 +598,13 @@ int gpu_moe_forward_stack(gpu_context *ctx, ornith_moe_store *st, int first_laye
 int gpu_moe_last_stats(gpu_context *ctx, int *n_slots, int *n_rows, int *n_exact)
 {
     if (!ctx) return ORN_EINVAL;
+    memset(ctx->ctl_host, 0, 16 * sizeof(int));
+    if (ctx->last_ctl) {
+        int rc = orn_hip_check(ctx, hipMemcpyAsync(ctx->ctl_host, ctx->last_ctl, 16 * sizeof(int),
+                                                   hipMemcpyDeviceToHost, ctx->stream),
+                               "stats copy");
+        if (rc) return rc;
+    }
     hipStreamSynchronize(ctx->stream);
     if (n_slots) *n_slots = ctx->ctl_host[0];
     if (n_rows) *n_rows = ctx->ctl_host[2];

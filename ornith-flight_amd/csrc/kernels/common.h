@@ -19,27 +19,27 @@
 __device__ __forceinline__ float orn_half_to_float(uint32_t h)
 {
     h &= 0xFFFFu;
-    if (h == 0u) return 0.0f;
-    uint32_t u = ((h & 0x8000u) << 16) | ((((h & 0x7C00u) >> 10) + 112u) << 23) |
-                 ((h & 0x03FFu) << 13);
-    return __uint_as_float(u);
+    const uint32_t u = ((h & 0x8000u) << 16) | ((((h & 0x7C00u) >> 10) + 112u) << 23) |
+                       ((h & 0x03FFu) << 13);
+    return h == 0u ? 0.0f : __uint_as_float(u);  // select, no branch
 }
 
 __device__ __forceinline__ uint32_t orn_byte(uint32_t w, int i) { return (w >> (8 * i)) & 0xFFu; }
 
 // gguf.c:31-40, with the 12 packed scale bytes held as three little-endian
-// dwords s0 (bytes 0-3), s1 (bytes 4-7), s2 (bytes 8-11).
+// dwords s0 (bytes 0-3), s1 (bytes 4-7), s2 (bytes 8-11).  Both encodings
+// are computed and selected, so a wave whose lanes need different sub-blocks
+// does not diverge.
 __device__ __forceinline__ void orn_scale_min_k4(int j, uint32_t s0, uint32_t s1, uint32_t s2,
                                                  uint32_t &sc, uint32_t &m)
 {
-    if (j < 4) {
-        sc = orn_byte(s0, j) & 63u;
-        m = orn_byte(s1, j) & 63u;
-    } else {
-        uint32_t b = orn_byte(s2, j - 4);
-        sc = (b & 0xFu) | ((orn_byte(s0, j - 4) >> 6) << 4);
-        m = (b >> 4) | ((orn_byte(s1, j - 4) >> 6) << 4);
-    }
+    const int i = j & 3;
+    const uint32_t b0 = orn_byte(s0, i), b1 = orn_byte(s1, i), b2 = orn_byte(s2, i);
+    const uint32_t sc_lo = b0 & 63u, m_lo = b1 & 63u;
+    const uint32_t sc_hi = (b2 & 0xFu) | ((b0 >> 6) << 4);
+    const uint32_t m_hi = (b2 >> 4) | ((b1 >> 6) << 4);
+    sc = j < 4 ? sc_lo : sc_hi;
+    m = j < 4 ? m_lo : m_hi;
 }
 
 // Unaligned-safe little-endian byte reads (for the GGUF AoS Q6_K stream whose

@@ -20,21 +20,13 @@
 #include "common.h"
 #include "launch.h"
 
-#define ORN_TCHUNK 8   // token rows per work item
-#define ORN_TG_MAX 4   // token rows processed together in registers
 
 namespace {
 
 // ---------------------------------------------------------------------------
-__global__ void k_reset_ctl(int *ctl)
-{
-    if (threadIdx.x < 16) ctl[threadIdx.x] = 0;
-}
-
-// ---------------------------------------------------------------------------
 // Dispatch: one block.  List position j: 0 = shared expert (expert id E),
 // j >= 1 = routed expert j-1.  Produces the active slots (shared first, then
-// experts in ascending id), their row ranges, the work items (<= ORN_TCHUNK
+// experts in ascending id), their row ranges, the work items (<= tchunk
 // rows each) and the row <-> (token, selection slot) maps.
 // ---------------------------------------------------------------------------
 __device__ int block_excl_scan(int v, int *buf, int *total)
@@ -57,7 +49,7 @@ __device__ int block_excl_scan(int v, int *buf, int *total)
 __global__ void __launch_bounds__(1024)
     k_dispatch(const uint32_t *__restrict__ idx, const float *__restrict__ w, int T, int k, int E,
                int has_shared, int *ctl, int *slot_expert, int *slot_off, int *slot_cnt,
-               int *row_token, int *pair_row, int4 *items, int items_max)
+               int *row_token, int *pair_row, int4 *items, int items_max, int tchunk)
 {
     __shared__ int cnt[1024];
     __shared__ int cursor[1024];
@@ -76,7 +68,7 @@ __global__ void __launch_bounds__(1024)
 
     const int c = tid < NJ ? cnt[tid] : 0;
     const int flag = c > 0 ? 1 : 0;
-    const int nit = (c + ORN_TCHUNK - 1) / ORN_TCHUNK;
+    const int nit = (c + tchunk - 1) / tchunk;
     int n_slots, n_rows, n_items;
     const int slot = block_excl_scan(flag, scanbuf, &n_slots);
     const int roff = block_excl_scan(c, scanbuf, &n_rows);
@@ -87,8 +79,8 @@ __global__ void __launch_bounds__(1024)
         slot_off[slot] = roff;
         slot_cnt[slot] = c;
         for (int q = 0; q < nit && ioff + q < items_max; ++q) {
-            const int r0 = q * ORN_TCHUNK;
-            items[ioff + q] = make_int4(slot, roff + r0, min(ORN_TCHUNK, c - r0), tid == 0);
+            const int r0 = q * tchunk;
+            items[ioff + q] = make_int4(slot, roff + r0, min(tchunk, c - r0), tid == 0);
         }
     }
     if (tid == 0) {
@@ -115,126 +107,73 @@ __global__ void __launch_bounds__(1024)
 }
 
 // ---------------------------------------------------------------------------
-// Gate+up: split-K over the D input rows.  Block = 4 waves; item = up to
-// ORN_TCHUNK rows (tokens) of one expert; blockIdx.x = item*ks + kslice.
-// Lane layout inside a wave: ch = lane % CR picks (matrix m, block column
-// bc, 16-byte qs chunk j) with CR = 16*(H/256) chunks per input row, and
-// rr = lane / CR picks one of RW = 64/CR rows handled side by side.
+// Gate+up: split-K over the D input rows.  Block = 4 waves; work item = up
+// to `tchunk` token rows of one expert; blockIdx.x = item*ks + kslice.  The
+// item's tokens are processed one at a time (weights re-read from L1/L2 for
+// the second token), which keeps the register budget near 100 VGPRs.
 //
-// Q4_K chunk j of a block holds bytes 16j..16j+15 of qs: low nibbles are
-// outputs 64*(j/2) + 16*(j%2) + u of sub-block 2*(j/2), high nibbles the same
-// + 32 of sub-block 2*(j/2)+1 (gguf.c:43-61).  With D1 = d*sc, M1 = dmin*m
-// the contribution of row k is x_k*(D1*q - M1); the M1 term is constant over
-// the 16 outputs, so it is accumulated once per row and subtracted at the end.
+// Lane layout: ch = lane % CR picks (matrix m, block column bc, 16-byte qs
+// chunk j) with CR = 16*(H/256) chunks per input row, and rr = lane / CR one
+// of RW = 64/CR rows handled side by side.  Chunk j holds qs bytes
+// 16j..16j+15: low nibbles are outputs 64*(j/2) + 16*(j%2) + u of sub-block
+// 2*(j/2), high nibbles the same + 32 of sub-block 2*(j/2)+1 (gguf.c:43-61).
+// With D = d*sc and M = dmin*m a row contributes x_k*(D*q - M); the M part is
+// constant over a sub-block, so it is accumulated once per row and
+// subtracted at the end.
+//
+// Memory pipelining: each lane keeps NPF rows of loads in flight in a ring
+// of register sets that is fully unrolled (static register indices), and
+// the prefetch row index is clamped at the slice end so the loop body has no
+// branches.
 // ---------------------------------------------------------------------------
-template <int TG>
-__device__ void gateup_group(const uint8_t *__restrict__ gate, const uint8_t *__restrict__ up,
-                             const float *__restrict__ xn, const int *__restrict__ row_token,
-                             float *__restrict__ gu_part, int D, int H, int e, int row_g,
-                             int kslice, int RK, int rows_max, float *xs, float *red)
+#define ORN_NPF 4
+
+__device__ __forceinline__ void q4_nibbles(uint32_t w, float *lo, float *hi)
 {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int NB = H >> 8;
-    const int CR = 16 * NB;
-    const int RW = 64 / CR;
-    const int rr = lane / CR, ch = lane % CR;
-    const int m = ch / (8 * NB), bc = (ch >> 3) % NB, j = ch & 7;
-    const int c = j >> 1;
-    const int k_start = kslice * RK;
-    const int H2 = 2 * H;
+    const uint32_t l = w & 0x0F0F0F0Fu;
+    const uint32_t h = (w >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        lo[b] = (float)((l >> (8 * b)) & 0xFFu);
+        hi[b] = (float)((h >> (8 * b)) & 0xFFu);
+    }
+}
 
-    // Stage this group's activations for the K-slice.
-    for (int i = tid; i < TG * RK; i += blockDim.x) {
-        const int tt = i / RK, kk = i - tt * RK;
-        xs[tt * RK + kk] = xn[(size_t)row_token[row_g + tt] * D + k_start + kk];
-    }
-    __syncthreads();
+struct Q4Row {
+    uint4 hd, q;
+};
 
-    float acc[TG][32];
-    float macc[TG][2];
+__device__ __forceinline__ void load_q4(const uint8_t *base, int krow, int j, Q4Row &r)
+{
+    const uint8_t *blk = base + (size_t)krow * ORN_Q4K_BYTES;
+    r.hd = *reinterpret_cast<const uint4 *>(blk);
+    r.q = *reinterpret_cast<const uint4 *>(blk + ORN_Q4K_OFF_QS + 16 * j);
+}
+
+// One row of one lane chunk: 32 outputs (16 of sub-block 2c, 16 of 2c+1).
+__device__ __forceinline__ void q4_row(const Q4Row &r, int c, float xv, float *acc, float &macc0,
+                                       float &macc1)
+{
+    const float d = orn_half_to_float(r.hd.x & 0xFFFFu);
+    const float dmin = orn_half_to_float(r.hd.x >> 16);
+    uint32_t sc1, m1, sc2, m2;
+    orn_scale_min_k4(2 * c, r.hd.y, r.hd.z, r.hd.w, sc1, m1);
+    orn_scale_min_k4(2 * c + 1, r.hd.y, r.hd.z, r.hd.w, sc2, m2);
+    const float a1 = xv * (d * (float)sc1);
+    const float a2 = xv * (d * (float)sc2);
+    macc0 = fmaf(xv, dmin * (float)m1, macc0);
+    macc1 = fmaf(xv, dmin * (float)m2, macc1);
+    const uint32_t qw[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
 #pragma unroll
-    for (int tt = 0; tt < TG; ++tt) {
+    for (int dw = 0; dw < 4; ++dw) {
+        float lo[4], hi[4];
+        q4_nibbles(qw[dw], lo, hi);
 #pragma unroll
-        for (int u = 0; u < 32; ++u) acc[tt][u] = 0.0f;
-        macc[tt][0] = 0.0f;
-        macc[tt][1] = 0.0f;
-    }
-    const uint8_t *base = (m ? up : gate) + (size_t)(e * NB + bc) * (size_t)D * ORN_Q4K_BYTES;
-    const int n_it = RK / (4 * RW);
-#pragma unroll 2
-    for (int it = 0; it < n_it; ++it) {
-        const int rho = (it * 4 + wave) * RW + rr;
-        const uint8_t *blk = base + (size_t)(k_start + rho) * ORN_Q4K_BYTES;
-        const uint4 hd = *reinterpret_cast<const uint4 *>(blk);
-        const uint4 qv = *reinterpret_cast<const uint4 *>(blk + ORN_Q4K_OFF_QS + 16 * j);
-        const float d = orn_half_to_float(hd.x & 0xFFFFu);
-        const float dmin = orn_half_to_float(hd.x >> 16);
-        uint32_t sc1, m1, sc2, m2;
-        orn_scale_min_k4(2 * c, hd.y, hd.z, hd.w, sc1, m1);
-        orn_scale_min_k4(2 * c + 1, hd.y, hd.z, hd.w, sc2, m2);
-        const float D1 = d * (float)sc1, M1 = dmin * (float)m1;
-        const float D2 = d * (float)sc2, M2 = dmin * (float)m2;
-        const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
-        float qlo[16], qhi[16];
-#pragma unroll
-        for (int dw = 0; dw < 4; ++dw) {
-            const uint32_t lo = qw[dw] & 0x0F0F0F0Fu;
-            const uint32_t hi = (qw[dw] >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                qlo[dw * 4 + b] = (float)((lo >> (8 * b)) & 0xFFu);
-                qhi[dw * 4 + b] = (float)((hi >> (8 * b)) & 0xFFu);
-            }
-        }
-#pragma unroll
-        for (int tt = 0; tt < TG; ++tt) {
-            const float xv = xs[tt * RK + rho];
-            const float a1 = xv * D1, a2 = xv * D2;
-            macc[tt][0] = fmaf(xv, M1, macc[tt][0]);
-            macc[tt][1] = fmaf(xv, M2, macc[tt][1]);
-#pragma unroll
-            for (int u = 0; u < 16; ++u) {
-                acc[tt][u] = fmaf(a1, qlo[u], acc[tt][u]);
-                acc[tt][16 + u] = fmaf(a2, qhi[u], acc[tt][16 + u]);
-            }
+        for (int bb = 0; bb < 4; ++bb) {
+            acc[dw * 4 + bb] = fmaf(a1, lo[bb], acc[dw * 4 + bb]);
+            acc[16 + dw * 4 + bb] = fmaf(a2, hi[bb], acc[16 + dw * 4 + bb]);
         }
     }
-    // Finish per lane, then reduce over the RW rows of the wave (butterfly)
-    // and over the 4 waves in a fixed order through LDS.
-#pragma unroll
-    for (int tt = 0; tt < TG; ++tt) {
-#pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            acc[tt][u] -= macc[tt][0];
-            acc[tt][16 + u] -= macc[tt][1];
-        }
-    }
-    for (int off = CR; off < 64; off <<= 1) {
-#pragma unroll
-        for (int tt = 0; tt < TG; ++tt)
-#pragma unroll
-            for (int u = 0; u < 32; ++u) acc[tt][u] += __shfl_xor(acc[tt][u], off, 64);
-    }
-    const int col0 = m * H + bc * 256 + 64 * c + 16 * (j & 1);
-    for (int wv = 0; wv < 4; ++wv) {
-        if (wave == wv && rr == 0) {
-#pragma unroll
-            for (int tt = 0; tt < TG; ++tt)
-#pragma unroll
-                for (int u = 0; u < 16; ++u) {
-                    float *p0 = red + tt * H2 + col0 + u;
-                    float *p1 = p0 + 32;
-                    if (wv == 0) { *p0 = acc[tt][u]; *p1 = acc[tt][16 + u]; }
-                    else { *p0 += acc[tt][u]; *p1 += acc[tt][16 + u]; }
-                }
-        }
-        __syncthreads();
-    }
-    for (int i = tid; i < TG * H2; i += blockDim.x) {
-        const int tt = i / H2, col = i - tt * H2;
-        gu_part[((size_t)kslice * rows_max + row_g + tt) * H2 + col] = red[i];
-    }
-    __syncthreads();
 }
 
 __global__ void __launch_bounds__(256)
@@ -247,33 +186,77 @@ __global__ void __launch_bounds__(256)
     extern __shared__ float smem[];
     const int item = blockIdx.x / ks, kslice = blockIdx.x - item * ks;
     if (item >= ctl[1]) return;
-    const int4 it = items[item];
-    const int e = slot_expert[it.x];
+    const int4 itm = items[item];
+    const int e = slot_expert[itm.x];
     const int RK = D / ks;
-    float *xs = smem;
-    float *red = smem + ORN_TG_MAX * RK;
-    int g = 0;
-    while (g < it.z) {
-        const int left = it.z - g;
-        if (left >= 4) {
-            gateup_group<4>(gate, up, xn, row_token, gu_part, D, H, e, it.y + g, kslice, RK,
-                            rows_max, xs, red);
-            g += 4;
-        } else if (left >= 2) {
-            gateup_group<2>(gate, up, xn, row_token, gu_part, D, H, e, it.y + g, kslice, RK,
-                            rows_max, xs, red);
-            g += 2;
-        } else {
-            gateup_group<1>(gate, up, xn, row_token, gu_part, D, H, e, it.y + g, kslice, RK,
-                            rows_max, xs, red);
-            g += 1;
+    float *xs = smem;       // [RK]
+    float *red = smem + RK; // [2H]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int NB = H >> 8;
+    const int CR = 16 * NB;
+    const int RW = 64 / CR;
+    const int rr = lane / CR, ch = lane % CR;
+    const int j = ch & 7, bc = (ch >> 3) % NB, m = ch / (8 * NB);
+    const int c = j >> 1;
+    const int k_start = kslice * RK;
+    const int H2 = 2 * H;
+    const uint8_t *base =
+        (m ? up : gate) + ((size_t)(e * NB + bc) * (size_t)D + (size_t)k_start) * ORN_Q4K_BYTES;
+    const int n_it = RK / (4 * RW);  // multiple of ORN_NPF (checked by the launcher)
+    const int last = n_it - 1;
+    const int col0 = m * H + bc * 256 + 64 * c + 16 * (j & 1);
+
+    for (int r = 0; r < itm.z; ++r) {
+        const int row = itm.y + r;
+        const float *xr = xn + (size_t)row_token[row] * D + k_start;
+        for (int i = tid; i < RK; i += blockDim.x) xs[i] = xr[i];
+        __syncthreads();
+
+        float acc[32];
+#pragma unroll
+        for (int u = 0; u < 32; ++u) acc[u] = 0.0f;
+        float macc0 = 0.0f, macc1 = 0.0f;
+        Q4Row rs[ORN_NPF];
+#pragma unroll
+        for (int p = 0; p < ORN_NPF; ++p) load_q4(base, (min(p, last) * 4 + wave) * RW + rr, j, rs[p]);
+        for (int it = 0; it < n_it; it += ORN_NPF) {
+#pragma unroll
+            for (int p = 0; p < ORN_NPF; ++p) {
+                q4_row(rs[p], c, xs[((it + p) * 4 + wave) * RW + rr], acc, macc0, macc1);
+                load_q4(base, (min(it + p + ORN_NPF, last) * 4 + wave) * RW + rr, j, rs[p]);
+            }
         }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            acc[u] -= macc0;
+            acc[16 + u] -= macc1;
+        }
+        for (int off = CR; off < 64; off <<= 1) {
+#pragma unroll
+            for (int u = 0; u < 32; ++u) acc[u] += __shfl_xor(acc[u], off, 64);
+        }
+        for (int wv = 0; wv < 4; ++wv) {
+            if (wave == wv && rr == 0) {
+#pragma unroll
+                for (int u = 0; u < 16; ++u) {
+                    float *p0 = red + col0 + u;
+                    float *p1 = p0 + 32;
+                    *p0 = (wv == 0) ? acc[u] : *p0 + acc[u];
+                    *p1 = (wv == 0) ? acc[16 + u] : *p1 + acc[16 + u];
+                }
+            }
+            __syncthreads();
+        }
+        float *dst = gu_part + ((size_t)kslice * rows_max + row) * H2;
+        for (int i = tid; i < H2; i += blockDim.x) dst[i] = red[i];
+        __syncthreads();
     }
 }
 
 // ---------------------------------------------------------------------------
-// mid[row] = act(sum_ks gate) * sum_ks up.  Rows [0, T) are the shared
-// expert's (unclamped silu); all others are routed (clamped silu).
+// mid[row] = act(sum_ks gate) * sum_ks up.  Rows [0, shared_rows) belong to
+// the shared expert (unclamped silu, gpu.c:176-186); all others are routed
+// (clamped silu, model.c:340-344).
 // ---------------------------------------------------------------------------
 __global__ void k_mid(const float *__restrict__ gu_part, const int *__restrict__ ctl,
                       float *__restrict__ mid, int H, int ks, int rows_max, int shared_rows)
@@ -281,12 +264,22 @@ __global__ void k_mid(const float *__restrict__ gu_part, const int *__restrict__
     const int r = blockIdx.x;
     if (r >= ctl[2]) return;
     const int H2 = 2 * H;
+    const size_t kstride = (size_t)rows_max * H2;
     for (int h = threadIdx.x; h < H; h += blockDim.x) {
+        const float *p = gu_part + (size_t)r * H2 + h;
         float g = 0.0f, u = 0.0f;
-        for (int s = 0; s < ks; ++s) {
-            const float *p = gu_part + ((size_t)s * rows_max + r) * H2;
-            g += p[h];
-            u += p[H + h];
+        int s = 0;
+        for (; s + 4 <= ks; s += 4) {
+            const float g0 = p[(s + 0) * kstride], g1 = p[(s + 1) * kstride];
+            const float g2 = p[(s + 2) * kstride], g3 = p[(s + 3) * kstride];
+            const float u0 = p[(s + 0) * kstride + H], u1 = p[(s + 1) * kstride + H];
+            const float u2 = p[(s + 2) * kstride + H], u3 = p[(s + 3) * kstride + H];
+            g += g0; g += g1; g += g2; g += g3;
+            u += u0; u += u1; u += u2; u += u3;
+        }
+        for (; s < ks; ++s) {
+            g += p[s * kstride];
+            u += p[s * kstride + H];
         }
         float act;
         if (r < shared_rows) {
@@ -301,124 +294,23 @@ __global__ void k_mid(const float *__restrict__ gu_part, const int *__restrict__
 }
 
 // ---------------------------------------------------------------------------
-// Down: split-K over the H rows, block = 4 waves, columns in groups of up to
-// 8 block columns (2048 outputs).  Q6_K lane chunk lc = (n, jj, half of l):
-// ql bytes 64n + 32jj + l0 .. +15 and qh bytes 32n + l0 .. +15 give outputs
-// 128n + 32j + l0 + u for j = jj (low nibble, qh bits 2jj) and j = jj+2 (high
-// nibble, qh bits 2jj+4), scales sc[8n + l0/16 + 2j] (gguf.c:64-86).  The
-// "-32" offset is folded: sum a*(q-32) = sum a*q - 32*sum a.
+// Down: split-K over the H rows, block = 4 waves, one token per pass.  Lane
+// chunk (block column bc, half n, l0 in {0,16}, jj in {0,1}) covers the 32
+// outputs 128n + 32j + l0 + u for j in {jj, jj+2}, u = 0..15: low/high
+// nibbles of ql[64n + 32jj + l0 + u] give j = jj / jj+2, qh[32n + l0 + u]
+// bits 2j..2j+1 the top two bits, scale sc[8n + l0/16 + 2j] (gguf.c:64-86).
+// The "-32" is folded: sum a*(q-32) = sum a*q - 32*sum a.  Loads are
+// pipelined ORN_NPF rows deep as in k_gateup.
 // ---------------------------------------------------------------------------
-template <int TG>
-__device__ void down_group(const uint8_t *__restrict__ body, const uint16_t *__restrict__ dsc,
-                           const float *__restrict__ mid, float *__restrict__ dn_part, int D, int H,
-                           int e, int row_g, int kslice, int RH, int cg, int rows_max, float *ms,
-                           float *red)
+__device__ __forceinline__ void q6_decode(uint32_t ql, uint32_t qh, int jj, float *q0, float *q1)
 {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int NBD = D >> 8;
-    const int CR = 8 * NBD;
-    const int CRg = CR < 64 ? CR : 64;
-    const int RW = 64 / CRg;
-    const int rr = lane / CRg, ch = lane % CRg;
-    const int bc = cg * 8 + (ch >> 3), lc = ch & 7;
-    const int n = lc >> 2, jj = (lc >> 1) & 1, l0 = (lc & 1) * 16;
-    const int h_start = kslice * RH;
-    const int ncols = CRg * 32;  // outputs of this column group
-
-    for (int i = tid; i < TG * RH; i += blockDim.x) {
-        const int tt = i / RH, hh = i - tt * RH;
-        ms[tt * RH + hh] = mid[(size_t)(row_g + tt) * H + h_start + hh];
+    const uint32_t a0 = (ql & 0x0F0F0F0Fu) | (((qh >> (2 * jj)) & 0x03030303u) << 4);
+    const uint32_t a1 = ((ql >> 4) & 0x0F0F0F0Fu) | (((qh >> (2 * jj + 4)) & 0x03030303u) << 4);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        q0[b] = (float)((a0 >> (8 * b)) & 0xFFu);
+        q1[b] = (float)((a1 >> (8 * b)) & 0xFFu);
     }
-    __syncthreads();
-
-    float acc[TG][32];
-    float csum[TG][2];
-#pragma unroll
-    for (int tt = 0; tt < TG; ++tt) {
-#pragma unroll
-        for (int u = 0; u < 32; ++u) acc[tt][u] = 0.0f;
-        csum[tt][0] = 0.0f;
-        csum[tt][1] = 0.0f;
-    }
-    const size_t bcol = (size_t)(e * NBD + bc) * (size_t)H;
-    const int pos = (l0 >> 4) + 2 * jj;
-    const int n_it = RH / (4 * RW);
-#pragma unroll 2
-    for (int it = 0; it < n_it; ++it) {
-        const int rho = (it * 4 + wave) * RW + rr;
-        const size_t bi = bcol + (size_t)(h_start + rho);
-        const uint8_t *b = body + bi * 208;
-        const uint4 qlv = *reinterpret_cast<const uint4 *>(b + 64 * n + 32 * jj + l0);
-        const uint4 qhv = *reinterpret_cast<const uint4 *>(b + 128 + 32 * n + l0);
-        const uint4 scv = *reinterpret_cast<const uint4 *>(b + 192);
-        const float d = orn_half_to_float(dsc[bi]);
-        const uint32_t scw[4] = {scv.x, scv.y, scv.z, scv.w};
-        const int sa = (int)(int8_t)orn_byte(scw[2 * n], pos);
-        const int sb = (int)(int8_t)orn_byte(scw[2 * n + 1], pos);
-        const float da = d * (float)sa, db = d * (float)sb;
-        const uint32_t lw[4] = {qlv.x, qlv.y, qlv.z, qlv.w};
-        const uint32_t hw[4] = {qhv.x, qhv.y, qhv.z, qhv.w};
-        float q0[16], q1[16];
-#pragma unroll
-        for (int dw = 0; dw < 4; ++dw) {
-            const uint32_t a0 = (lw[dw] & 0x0F0F0F0Fu) | (((hw[dw] >> (2 * jj)) & 0x03030303u) << 4);
-            const uint32_t a1 =
-                ((lw[dw] >> 4) & 0x0F0F0F0Fu) | (((hw[dw] >> (2 * jj + 4)) & 0x03030303u) << 4);
-#pragma unroll
-            for (int bb = 0; bb < 4; ++bb) {
-                q0[dw * 4 + bb] = (float)((a0 >> (8 * bb)) & 0xFFu);
-                q1[dw * 4 + bb] = (float)((a1 >> (8 * bb)) & 0xFFu);
-            }
-        }
-#pragma unroll
-        for (int tt = 0; tt < TG; ++tt) {
-            const float xv = ms[tt * RH + rho];
-            const float aa = xv * da, ab = xv * db;
-            csum[tt][0] += aa;
-            csum[tt][1] += ab;
-#pragma unroll
-            for (int u = 0; u < 16; ++u) {
-                acc[tt][u] = fmaf(aa, q0[u], acc[tt][u]);
-                acc[tt][16 + u] = fmaf(ab, q1[u], acc[tt][16 + u]);
-            }
-        }
-    }
-#pragma unroll
-    for (int tt = 0; tt < TG; ++tt) {
-#pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            acc[tt][u] = fmaf(-32.0f, csum[tt][0], acc[tt][u]);
-            acc[tt][16 + u] = fmaf(-32.0f, csum[tt][1], acc[tt][16 + u]);
-        }
-    }
-    for (int off = CRg; off < 64; off <<= 1) {
-#pragma unroll
-        for (int tt = 0; tt < TG; ++tt)
-#pragma unroll
-            for (int u = 0; u < 32; ++u) acc[tt][u] += __shfl_xor(acc[tt][u], off, 64);
-    }
-    // Local column of output (n, j, l0+u) inside this column group.
-    const int lcol0 = (bc - cg * 8) * 256 + 128 * n + 32 * jj + l0;
-    for (int wv = 0; wv < 4; ++wv) {
-        if (wave == wv && rr == 0) {
-#pragma unroll
-            for (int tt = 0; tt < TG; ++tt)
-#pragma unroll
-                for (int u = 0; u < 16; ++u) {
-                    float *p0 = red + tt * ncols + lcol0 + u;
-                    float *p1 = p0 + 64;
-                    if (wv == 0) { *p0 = acc[tt][u]; *p1 = acc[tt][16 + u]; }
-                    else { *p0 += acc[tt][u]; *p1 += acc[tt][16 + u]; }
-                }
-        }
-        __syncthreads();
-    }
-    const int colbase = cg * 2048;
-    for (int i = tid; i < TG * ncols; i += blockDim.x) {
-        const int tt = i / ncols, col = i - tt * ncols;
-        dn_part[((size_t)kslice * rows_max + row_g + tt) * D + colbase + col] = red[i];
-    }
-    __syncthreads();
 }
 
 __global__ void __launch_bounds__(256)
@@ -432,27 +324,105 @@ __global__ void __launch_bounds__(256)
     const int rest = blockIdx.x / ncg;
     const int item = rest / ks, kslice = rest - item * ks;
     if (item >= ctl[1]) return;
-    const int4 it = items[item];
-    const int e = slot_expert[it.x];
+    const int4 itm = items[item];
+    const int e = slot_expert[itm.x];
     const int RH = H / ks;
-    float *ms = smem;
-    float *red = smem + ORN_TG_MAX * RH;
-    int g = 0;
-    while (g < it.z) {
-        const int left = it.z - g;
-        if (left >= 4) {
-            down_group<4>(body, dsc, mid, dn_part, D, H, e, it.y + g, kslice, RH, cg, rows_max, ms,
-                          red);
-            g += 4;
-        } else if (left >= 2) {
-            down_group<2>(body, dsc, mid, dn_part, D, H, e, it.y + g, kslice, RH, cg, rows_max, ms,
-                          red);
-            g += 2;
-        } else {
-            down_group<1>(body, dsc, mid, dn_part, D, H, e, it.y + g, kslice, RH, cg, rows_max, ms,
-                          red);
-            g += 1;
+    const int NBD = D >> 8;
+    const int CR = 8 * NBD;
+    const int CRg = CR < 64 ? CR : 64;
+    const int RW = 64 / CRg;
+    const int ncols = CRg * 32;   // outputs of this column group
+    float *ms = smem;             // [RH]
+    float *red = smem + RH;       // [ncols]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int rr = lane / CRg, ch = lane % CRg;
+    const int bc = cg * 8 + (ch >> 3), lc = ch & 7;
+    const int n = lc >> 2, jj = (lc >> 1) & 1, l0 = (lc & 1) * 16;
+    const int h_start = kslice * RH;
+    const size_t bcol = (size_t)(e * NBD + bc) * (size_t)H + (size_t)h_start;
+    const uint8_t *bbase = body + bcol * 208;
+    const uint16_t *dbase = dsc + bcol;
+    const int n_it = RH / (4 * RW);  // multiple of ORN_NPF (checked by the launcher)
+    const int last = n_it - 1;
+    const int pos = (l0 >> 4) + 2 * jj;  // byte of the scale dwords 2n (j=jj) and 2n+1 (j=jj+2)
+    const int lcol0 = (bc - cg * 8) * 256 + 128 * n + 32 * jj + l0;
+
+    for (int r = 0; r < itm.z; ++r) {
+        const int row = itm.y + r;
+        const float *mr = mid + (size_t)row * H + h_start;
+        for (int i = tid; i < RH; i += blockDim.x) ms[i] = mr[i];
+        __syncthreads();
+
+        float acc[32];
+#pragma unroll
+        for (int u = 0; u < 32; ++u) acc[u] = 0.0f;
+        float cs0 = 0.0f, cs1 = 0.0f;
+        uint4 qlr[ORN_NPF], qhr[ORN_NPF];
+        uint2 scr[ORN_NPF];
+        uint32_t dr[ORN_NPF];
+#pragma unroll
+        for (int p = 0; p < ORN_NPF; ++p) {
+            const int h = (min(p, last) * 4 + wave) * RW + rr;
+            const uint8_t *b = bbase + (size_t)h * 208;
+            qlr[p] = *reinterpret_cast<const uint4 *>(b + 64 * n + 32 * jj + l0);
+            qhr[p] = *reinterpret_cast<const uint4 *>(b + 128 + 32 * n + l0);
+            scr[p] = *reinterpret_cast<const uint2 *>(b + 192 + 8 * n);
+            dr[p] = dbase[h];
         }
+        for (int it = 0; it < n_it; it += ORN_NPF) {
+#pragma unroll
+            for (int p = 0; p < ORN_NPF; ++p) {
+                const int rho = ((it + p) * 4 + wave) * RW + rr;
+                const float d = orn_half_to_float(dr[p]);
+                const float xv = ms[rho];
+                const float a0 = xv * (d * (float)(int)(int8_t)orn_byte(scr[p].x, pos));
+                const float a1 = xv * (d * (float)(int)(int8_t)orn_byte(scr[p].y, pos));
+                cs0 += a0;
+                cs1 += a1;
+                const uint32_t qlw[4] = {qlr[p].x, qlr[p].y, qlr[p].z, qlr[p].w};
+                const uint32_t qhw[4] = {qhr[p].x, qhr[p].y, qhr[p].z, qhr[p].w};
+#pragma unroll
+                for (int dw = 0; dw < 4; ++dw) {
+                    float q0[4], q1[4];
+                    q6_decode(qlw[dw], qhw[dw], jj, q0, q1);
+#pragma unroll
+                    for (int bb = 0; bb < 4; ++bb) {
+                        acc[dw * 4 + bb] = fmaf(a0, q0[bb], acc[dw * 4 + bb]);
+                        acc[16 + dw * 4 + bb] = fmaf(a1, q1[bb], acc[16 + dw * 4 + bb]);
+                    }
+                }
+                const int h = (min(it + p + ORN_NPF, last) * 4 + wave) * RW + rr;
+                const uint8_t *b = bbase + (size_t)h * 208;
+                qlr[p] = *reinterpret_cast<const uint4 *>(b + 64 * n + 32 * jj + l0);
+                qhr[p] = *reinterpret_cast<const uint4 *>(b + 128 + 32 * n + l0);
+                scr[p] = *reinterpret_cast<const uint2 *>(b + 192 + 8 * n);
+                dr[p] = dbase[h];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            acc[u] = fmaf(-32.0f, cs0, acc[u]);
+            acc[16 + u] = fmaf(-32.0f, cs1, acc[16 + u]);
+        }
+        for (int off = CRg; off < 64; off <<= 1) {
+#pragma unroll
+            for (int u = 0; u < 32; ++u) acc[u] += __shfl_xor(acc[u], off, 64);
+        }
+        for (int wv = 0; wv < 4; ++wv) {
+            if (wave == wv && rr == 0) {
+#pragma unroll
+                for (int u = 0; u < 16; ++u) {
+                    float *p0 = red + lcol0 + u;
+                    float *p1 = p0 + 64;
+                    *p0 = (wv == 0) ? acc[u] : *p0 + acc[u];
+                    *p1 = (wv == 0) ? acc[16 + u] : *p1 + acc[16 + u];
+                }
+            }
+            __syncthreads();
+        }
+        float *dst = dn_part + ((size_t)kslice * rows_max + row) * D + cg * 2048;
+        for (int i = tid; i < ncols; i += blockDim.x) dst[i] = red[i];
+        __syncthreads();
     }
 }
 
@@ -461,6 +431,19 @@ __global__ void __launch_bounds__(256)
 //   out = (resid + y_shared) + sum_a w_a * y_a   (selection order, skipped
 //   pairs excluded), each y the fixed-order sum of its split-K partials.
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ float sum_parts(const float *p, size_t kstride, int ks)
+{
+    float y = 0.0f;
+    int s = 0;
+    for (; s + 4 <= ks; s += 4) {
+        const float v0 = p[(s + 0) * kstride], v1 = p[(s + 1) * kstride];
+        const float v2 = p[(s + 2) * kstride], v3 = p[(s + 3) * kstride];
+        y += v0; y += v1; y += v2; y += v3;
+    }
+    for (; s < ks; ++s) y += p[s * kstride];
+    return y;
+}
+
 __global__ void k_combine(const float *__restrict__ dn_part, const int *__restrict__ pair_row,
                           const float *__restrict__ w, const float *__restrict__ resid,
                           float *__restrict__ out, int T, int D, int k, int ks, int rows_max,
@@ -469,19 +452,14 @@ __global__ void k_combine(const float *__restrict__ dn_part, const int *__restri
     const int t = blockIdx.x;
     const int c = blockIdx.y * blockDim.x + threadIdx.x;
     if (t >= T || c >= D) return;
+    const size_t kstride = (size_t)rows_max * D;
     float acc = resid ? resid[(size_t)t * D + c] : 0.0f;
-    if (has_shared) {
-        float y = 0.0f;
-        for (int s = 0; s < ks; ++s) y += dn_part[((size_t)s * rows_max + t) * D + c];
-        acc = acc + y;
-    }
+    if (has_shared) acc = acc + sum_parts(dn_part + (size_t)t * D + c, kstride, ks);
     float routed = 0.0f;
     for (int a = 0; a < k; ++a) {
         const int r = pair_row[t * k + a];
         if (r < 0) continue;
-        float y = 0.0f;
-        for (int s = 0; s < ks; ++s) y += dn_part[((size_t)s * rows_max + r) * D + c];
-        routed += w[t * k + a] * y;
+        routed += w[t * k + a] * sum_parts(dn_part + (size_t)r * D + c, kstride, ks);
     }
     out[(size_t)t * D + c] = acc + routed;
 }
@@ -491,9 +469,7 @@ __global__ void k_combine(const float *__restrict__ dn_part, const int *__restri
 // ---------------------------------------------------------------------------
 extern "C" int ornk_moe_norm(const ornk_moe_args *a, hipStream_t s)
 {
-    hipLaunchKernelGGL(k_reset_ctl, dim3(1), dim3(64), 0, s, a->ctl);
-    hipError_t err = hipGetLastError();
-    if (err != hipSuccess || !a->apply_norm) return err;
+    if (!a->apply_norm) return hipSuccess;
     return ornk_rmsnorm(a->xn, a->x, a->norm_w, a->T, a->D, s);
 }
 
@@ -503,7 +479,7 @@ extern "C" int ornk_moe_dispatch(const ornk_moe_args *a, hipStream_t s)
     hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), 0, s, a->idx, a->w, a->T, a->k, a->E,
                        a->has_shared, a->ctl, a->slot_expert, a->slot_off, a->slot_cnt,
                        a->row_token, a->pair_row, reinterpret_cast<int4 *>(a->items),
-                       a->items_max);
+                       a->items_max, a->tchunk);
     return hipGetLastError();
 }
 
@@ -513,9 +489,9 @@ extern "C" int ornk_moe_gateup(const ornk_moe_args *a, hipStream_t s)
     if (a->H % 256 || NB < 1 || 16 * NB > 64) return hipErrorInvalidValue;
     const int RW = 64 / (16 * NB);
     const int RK = a->D / a->ks_gu;
-    if (a->D % a->ks_gu || RK % (4 * RW)) return hipErrorInvalidValue;
-    const size_t shmem = sizeof(float) * (size_t)ORN_TG_MAX * (RK + 2 * a->H);
-    if (shmem > 160 * 1024) return hipErrorInvalidValue;
+    if (a->D % a->ks_gu || RK % (4 * RW * ORN_NPF)) return hipErrorInvalidValue;
+    const size_t shmem = sizeof(float) * (size_t)(RK + 2 * a->H);
+    if (shmem > 64 * 1024) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_gateup, dim3(a->items_max * a->ks_gu), dim3(256), shmem, s, a->gate, a->up,
                        a->xn, a->ctl, reinterpret_cast<const int4 *>(a->items), a->slot_expert,
                        a->row_token, a->gu_part, a->D, a->H, a->ks_gu, a->rows_max);
@@ -539,9 +515,9 @@ extern "C" int ornk_moe_down(const ornk_moe_args *a, hipStream_t s)
     const int ncg = CR > 64 ? CR / 64 : 1;
     const int RW = 64 / CRg;
     const int RH = a->H / a->ks_dn;
-    if (a->H % a->ks_dn || RH % (4 * RW)) return hipErrorInvalidValue;
-    const size_t shmem = sizeof(float) * (size_t)ORN_TG_MAX * (RH + CRg * 32);
-    if (shmem > 160 * 1024) return hipErrorInvalidValue;
+    if (a->H % a->ks_dn || RH % (4 * RW * ORN_NPF)) return hipErrorInvalidValue;
+    const size_t shmem = sizeof(float) * (size_t)(RH + CRg * 32);
+    if (shmem > 64 * 1024) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_down, dim3(a->items_max * a->ks_dn * ncg), dim3(256), shmem, s,
                        a->down_body, a->down_d, a->mid, a->ctl,
                        reinterpret_cast<const int4 *>(a->items), a->slot_expert, a->dn_part, a->D,

@@ -54,7 +54,7 @@ int ornk_topk(const float *logits, int T, int E, int k, int mode, uint32_t *idx,
  * Work buffers are owned by the host; sizes are computed by ornk_moe_ws_size. */
 typedef struct {
     int T, D, H, E, k, has_shared, mode, apply_norm;
-    int ks_gu, ks_dn, rows_max, items_max;
+    int ks_gu, ks_dn, rows_max, items_max, tchunk;
     const uint8_t *gate, *up, *down_body;
     const uint16_t *down_d;
     const float *router, *bias, *norm_w;
@@ -66,7 +66,8 @@ typedef struct {
     double *rpart;    /* [T][E][D/128][2] certified router partials */
     uint32_t *idx;    /* [T][k] */
     float *w;         /* [T][k] */
-    int *ctl;         /* [16] counters: 0 n_slots, 1 n_items, 2 n_rows, 3 n_exact */
+    int *ctl;         /* [16] counters: 0 n_slots, 1 n_items, 2 n_rows, 3 n_exact;
+                         zeroed by the routing step */
     int *slot_expert; /* [E+1] */
     int *slot_off;    /* [E+1] */
     int *slot_cnt;    /* [E+1] */

@@ -63,25 +63,38 @@ __global__ void k_router_exact(const float *x, const float *W, long long sd, lon
 // ---------------------------------------------------------------------------
 template <int TB>
 __global__ void k_router_part(const float *__restrict__ x, const float *__restrict__ Wt, int T,
-                              int D, int E, int cpb, double2 *__restrict__ part)
+                              int D, int E, int cpb, double2 *__restrict__ part, int *ctl)
 {
-    __shared__ double s_sum[16][TB][64];
-    __shared__ double s_q[16][TB][64];
+    __shared__ double s_sum[4][TB][64];
+    __shared__ double s_q[4][TB][64];
+    __shared__ float xs[TB][4 * ORN_RCHUNK];
     const int lane = threadIdx.x & 63;
     const int c = threadIdx.x >> 6;           // chunk within group
     const int e = blockIdx.x * 64 + lane;
     const int g = blockIdx.y;
     const int n_groups = gridDim.y;
     const int t0 = blockIdx.z * TB;
-    const int d0 = (g * cpb + c) * ORN_RCHUNK;
+    const int rows = cpb * ORN_RCHUNK;
+    const int dg = g * rows;
     const bool live = e < E;
+
+    // The first block clears the per-forward counters (routing is the
+    // first step of every forward).
+    if (ctl && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x < 16)
+        ctl[threadIdx.x] = 0;
+    for (int i = threadIdx.x; i < TB * rows; i += blockDim.x) {
+        const int tt = i / rows, r = i - tt * rows;
+        xs[tt][r] = (t0 + tt < T) ? x[(size_t)(t0 + tt) * D + dg + r] : 0.0f;
+    }
+    __syncthreads();
 
     double S[TB], Q[TB];
 #pragma unroll
     for (int tt = 0; tt < TB; ++tt) { S[tt] = 0.0; Q[tt] = 0.0; }
 
     if (live) {
-        const float4 *wp = reinterpret_cast<const float4 *>(Wt + (size_t)e * D + d0);
+        const float4 *wp = reinterpret_cast<const float4 *>(Wt + (size_t)e * D + dg + c * ORN_RCHUNK);
+        const float *xc = &xs[0][c * ORN_RCHUNK];
         for (int i0 = 0; i0 < ORN_RCHUNK / 4; i0 += 8) {
             float4 wv[8];
 #pragma unroll
@@ -91,14 +104,12 @@ __global__ void k_router_part(const float *__restrict__ x, const float *__restri
                 const float wr[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int d = d0 + (i0 + u) * 4 + r;
+                    const int d = (i0 + u) * 4 + r;
 #pragma unroll
                     for (int tt = 0; tt < TB; ++tt) {
-                        if (t0 + tt < T) {
-                            const float p = x[(size_t)(t0 + tt) * D + d] * wr[r];
-                            S[tt] += (double)p;
-                            Q[tt] += fabs(S[tt]);
-                        }
+                        const float p = xc[tt * 4 * ORN_RCHUNK + d] * wr[r];
+                        S[tt] += (double)p;
+                        Q[tt] += fabs(S[tt]);
                     }
                 }
             }
@@ -227,13 +238,69 @@ __device__ void renorm_weights(const float *sel_v, int k, float *w)
 }
 
 // ---------------------------------------------------------------------------
+// The reference's sequential logits (model.c:1017-1025) for the experts in
+// list[0..n): products rounded to fp32, added in d order from 0.0f, then the
+// optional bias; results in lf[e].  The weight rows of up to `cb` experts at
+// a time are first copied into LDS by the whole block (every load in
+// flight at once), then one thread per expert runs its dependent chain out
+// of LDS.  xs holds x (D floats); rows has room for cb*D floats.
+// ---------------------------------------------------------------------------
+__device__ void exact_logits(const int *list, int n, const float *xs, float *rows, int cb,
+                             const float *__restrict__ Wt, const float *bias, int D, float *lf)
+{
+    const int q = D / 4;
+    for (int b0 = 0; b0 < n; b0 += cb) {
+        const int nb = min(cb, n - b0);
+        float4 *r4 = reinterpret_cast<float4 *>(rows);
+        for (int i = threadIdx.x; i < nb * q; i += blockDim.x) {
+            const int r = i / q, c = i - r * q;
+            r4[i] = reinterpret_cast<const float4 *>(Wt + (size_t)list[b0 + r] * D)[c];
+        }
+        __syncthreads();
+        if ((int)threadIdx.x < nb) {
+            const int e = list[b0 + threadIdx.x];
+            const float4 *w = r4 + (size_t)threadIdx.x * q;
+            const float4 *x4 = reinterpret_cast<const float4 *>(xs);
+            float acc = 0.0f;
+            for (int i = 0; i < q; ++i) {
+                const float4 wv = w[i], xv = x4[i];
+                acc += xv.x * wv.x;
+                acc += xv.y * wv.y;
+                acc += xv.z * wv.z;
+                acc += xv.w * wv.w;
+            }
+            if (bias) acc += bias[e];
+            lf[e] = acc;
+        }
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Certified top-k, one block per token (E <= 256).
+//
+//  1. Every reference logit lies in [v - B, v + B] (v = P~ + bias).
+//  2. If the k best intervals are disjoint from each other and from all
+//     other intervals, the reference's ordered top-k is ours: done.
+//  3. Otherwise only experts whose interval reaches tau = min over our top-k
+//     of (v - B) can be in the reference's top-k (k experts provably have
+//     reference values >= tau).  Their exact sequential logits are computed;
+//     if the best k+1 of those are pairwise distinct, the reference's top-k
+//     is their order by value (exchange selection sorts when there are no
+//     ties), since every other expert is strictly below tau.
+//  4. Exact ties (or NaN/Inf) are resolved by computing every expert's exact
+//     logit and running the literal exchange selection.
+// In the literal mode (selection on softmax probabilities) step 3 also
+// requires the candidates' logits to be at least 1e-5 apart: probabilities
+// then differ by a relative 1e-5, far more than the few ulps by which expf
+// and the division can move them, so they cannot round to equal values;
+// otherwise step 4 runs, with this device's expf.
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(ORN_TOPK_THREADS)
     k_topk_cert(const double2 *__restrict__ part, int n_groups, int rows_per_group,
                 const float *__restrict__ x, const float *__restrict__ Wt,
                 const float *__restrict__ bias, int D, int E, int k, int mode, uint32_t *idx_out,
-                float *w_out, int *n_exact)
+                float *w_out, int *n_exact, int cb)
 {
     constexpr int NW = ORN_TOPK_THREADS / 64;
     __shared__ double sv[NW + 1];
@@ -246,6 +313,12 @@ __global__ void __launch_bounds__(ORN_TOPK_THREADS)
     __shared__ float red[NW];
     __shared__ int flag_s, cert_s;
     __shared__ float w_s[16];
+    __shared__ float lg_s[ORN_TOPK_THREADS];
+    __shared__ float lf_s[ORN_TOPK_THREADS];
+    __shared__ int list_s[ORN_TOPK_THREADS];
+    __shared__ int n_list_s;
+    __shared__ float sum_s;
+    extern __shared__ float dyn[];  // x (D floats) then cb weight rows
 
     const int t = blockIdx.x;
     const int e = threadIdx.x;
@@ -274,11 +347,15 @@ __global__ void __launch_bounds__(ORN_TOPK_THREADS)
     __syncthreads();
     if (!finite) flag_s = 1;
     __syncthreads();
+    const bool all_finite = (flag_s == 0);
 
-    bool certified = (flag_s == 0);
-    if (certified) {
-        // 2. top-k by (v desc, e asc).
-        bool taken = false;
+    double wv = v;         // value used for the literal-mode weights
+    bool cand_s = false;   // this expert's exact logit was computed (step 3)
+
+    // 2. top-k by (v desc, e asc) and the certification test.
+    bool taken = false;
+    bool certified = all_finite;
+    if (all_finite) {
         for (int r = 0; r < k; ++r) {
             double bv;
             int bi;
@@ -287,14 +364,13 @@ __global__ void __launch_bounds__(ORN_TOPK_THREADS)
             if (e == bi) { taken = true; top_v[r] = v; top_b[r] = B; sel_i[r] = e; }
         }
         __syncthreads();
-        // 3. highest upper bound among the rest.
         double hi_rest;
-        int dummy;
+        int who;
         block_argmax<NW>((valid && !taken) ? v + B : -HUGE_VAL, (valid && !taken) ? e : INT_MAX, sv,
-                         si, hi_rest, dummy);
+                         si, hi_rest, who);
         if (threadIdx.x == 0) {
             bool ok = true;
-            double m = (dummy == INT_MAX) ? -HUGE_VAL : hi_rest;
+            double m = (who == INT_MAX) ? -HUGE_VAL : hi_rest;
             for (int r = k - 1; r >= 0 && ok; --r) {
                 if (!(top_v[r] - top_b[r] > m)) ok = false;
                 m = fmax(m, top_v[r] + top_b[r]);
@@ -306,70 +382,98 @@ __global__ void __launch_bounds__(ORN_TOPK_THREADS)
     }
 
     if (certified) {
-        if (mode == 0) {
-            if (threadIdx.x == 0) {
-                for (int r = 0; r < k; ++r) sel_v[r] = (float)top_v[r];
-                renorm_weights(sel_v, k, w_s);
+        if (threadIdx.x < k) sel_v[threadIdx.x] = (float)top_v[threadIdx.x];
+        __syncthreads();
+    } else {
+        if (threadIdx.x == 0 && n_exact) atomicAdd(n_exact, 1);
+        float *xs = dyn;
+        float *rows = dyn + D;
+        for (int i = threadIdx.x; i < D; i += blockDim.x) xs[i] = x[(size_t)t * D + i];
+        if (threadIdx.x == 0) { flag_s = all_finite ? 0 : 1; n_list_s = 0; }
+        __syncthreads();
+        bool resolved = false;
+        if (all_finite) {
+            // 3. Exact logits for the candidate set only.
+            double tau = HUGE_VAL;
+            for (int r = 0; r < k; ++r) tau = fmin(tau, top_v[r] - top_b[r]);
+            const bool cand = valid && (v + B >= tau);
+            cand_s = cand;
+            if (cand) list_s[atomicAdd(&n_list_s, 1)] = e;
+            __syncthreads();
+            exact_logits(list_s, n_list_s, xs, rows, cb, Wt, bias, D, lf_s);
+            const float lf = cand ? lf_s[e] : 0.0f;
+            if (cand && !isfinite(lf)) flag_s = 1;
+            __syncthreads();
+            if (flag_s == 0) {
+                bool tk = false, tie = false;
+                double prev = 0.0;
+                for (int r = 0; r <= k; ++r) {
+                    double bv;
+                    int bi;
+                    block_argmax<NW>((cand && !tk) ? (double)lf : -HUGE_VAL,
+                                     (cand && !tk) ? e : INT_MAX, sv, si, bv, bi);
+                    if (bi == INT_MAX) break;  // fewer than k+1 candidates
+                    if (e == bi) tk = true;
+                    if (r > 0) {
+                        const double gap = prev - bv;
+                        if (!(gap > 0.0)) tie = true;
+                        if (mode == 1 && !(gap > 1e-5)) tie = true;
+                    }
+                    if (r < k && threadIdx.x == 0) { sel_i[r] = bi; sel_v[r] = (float)bv; }
+                    prev = bv;
+                }
+                resolved = !tie;
             }
             __syncthreads();
-        } else {
-            // Literal: p = softmax over all E of the (certified) logits.
-            const float mx = (float)top_v[0];
-            float ex = valid ? expf((float)v - mx) : 0.0f;
-            float sum = block_sum_f(ex, red);
-            if (valid) vals_s[e] = ex / sum;
-            __syncthreads();
-            if (threadIdx.x < k) w_s[threadIdx.x] = vals_s[sel_i[threadIdx.x]];
-            __syncthreads();
+            if (resolved && cand) wv = (double)lf;
         }
-        if (threadIdx.x < k) {
-            idx_out[(size_t)t * k + threadIdx.x] = (uint32_t)sel_i[threadIdx.x];
-            w_out[(size_t)t * k + threadIdx.x] = w_s[threadIdx.x];
+        if (!resolved) {
+            // 4. Every expert's exact logit, literal exchange selection.
+            if (threadIdx.x == 0) n_list_s = E;
+            if (valid) list_s[e] = e;
+            __syncthreads();
+            exact_logits(list_s, E, xs, rows, cb, Wt, bias, D, lf_s);
+            const float lf = valid ? lf_s[e] : 0.0f;
+            wv = (double)lf;
+            float sel_val = lf;
+            if (mode == 1) {
+                if (threadIdx.x == 0) {
+                    float mx = lf_s[0];
+                    for (int j = 1; j < E; ++j) if (lf_s[j] > mx) mx = lf_s[j];
+                    float sacc = 0.0f;
+                    for (int j = 0; j < E; ++j) { lg_s[j] = expf(lf_s[j] - mx); sacc += lg_s[j]; }
+                    sum_s = sacc;
+                }
+                __syncthreads();
+                if (valid) sel_val = lg_s[e] / sum_s;
+                __syncthreads();
+            }
+            exact_select<NW>(sel_val, E, k, vals_s, idx_s, sv, si, sel_i, sel_v, &flag_s);
+            if (mode == 1) {
+                // Selection ran on the probabilities, which are the weights.
+                if (threadIdx.x < k) {
+                    idx_out[(size_t)t * k + threadIdx.x] = (uint32_t)sel_i[threadIdx.x];
+                    w_out[(size_t)t * k + threadIdx.x] = sel_v[threadIdx.x];
+                }
+                return;
+            }
         }
-        return;
     }
 
-    // 4. Exact fallback: the reference's sequential chain for every expert.
-    if (threadIdx.x == 0 && n_exact) atomicAdd(n_exact, 1);
-    float lf = 0.0f;
-    if (valid) {
-        const float *xr = x + (size_t)t * D;
-        const float4 *wp = reinterpret_cast<const float4 *>(Wt + (size_t)e * D);
-        float acc = 0.0f;
-        for (int i = 0; i < D / 4; ++i) {
-            const float4 wv = wp[i];
-            acc += xr[4 * i + 0] * wv.x;
-            acc += xr[4 * i + 1] * wv.y;
-            acc += xr[4 * i + 2] * wv.z;
-            acc += xr[4 * i + 3] * wv.w;
-        }
-        if (bias) acc += bias[e];
-        lf = acc;
-    }
-    float sel_val = lf;
-    if (mode == 1) {
-        // model.c:1028-1035: max by strict '>', expf, sequential sum, divide.
-        __shared__ float lg_s[ORN_TOPK_THREADS];
-        __shared__ float sum_s;
-        if (valid) lg_s[e] = lf;
+    // Weights.  Renormalised mode: softmax over the k selected logits
+    // (model.c:307-317).  Literal mode: full softmax probabilities.
+    if (mode == 0) {
+        if (threadIdx.x == 0) renorm_weights(sel_v, k, w_s);
         __syncthreads();
-        if (threadIdx.x == 0) {
-            float mx = lg_s[0];
-            for (int j = 1; j < E; ++j) if (lg_s[j] > mx) mx = lg_s[j];
-            float s = 0.0f;
-            for (int j = 0; j < E; ++j) { lg_s[j] = expf(lg_s[j] - mx); s += lg_s[j]; }
-            sum_s = s;
-        }
+    } else {
+        const float mx = sel_v[0];
+        float ex = valid ? expf((float)wv - mx) : 0.0f;
+        float sum = block_sum_f(ex, red);
+        if (valid) vals_s[e] = ex / sum;
         __syncthreads();
-        if (valid) sel_val = lg_s[e] / sum_s;
+        if (threadIdx.x < k) w_s[threadIdx.x] = vals_s[sel_i[threadIdx.x]];
         __syncthreads();
     }
-    exact_select<NW>(sel_val, E, k, vals_s, idx_s, sv, si, sel_i, sel_v, &flag_s);
-    if (threadIdx.x == 0) {
-        if (mode == 0) renorm_weights(sel_v, k, w_s);
-        else for (int r = 0; r < k; ++r) w_s[r] = sel_v[r];
-    }
-    __syncthreads();
     if (threadIdx.x < k) {
         idx_out[(size_t)t * k + threadIdx.x] = (uint32_t)sel_i[threadIdx.x];
         w_out[(size_t)t * k + threadIdx.x] = w_s[threadIdx.x];
@@ -459,27 +563,32 @@ extern "C" int ornk_moe_route(const ornk_moe_args *a, hipStream_t s)
 {
     const int T = a->T, D = a->D, E = a->E;
     if (T <= 0) return hipSuccess;
-    if (E > ORN_TOPK_THREADS || a->k > 16 || D % ORN_RCHUNK != 0) return hipErrorInvalidValue;
+    if (E > ORN_TOPK_THREADS || a->k > 16 || D % 64 != 0 || D % ORN_RCHUNK != 0)
+        return hipErrorInvalidValue;
     const int n_chunks = D / ORN_RCHUNK;
     int cpb = (T <= 32 || n_chunks % 4 != 0) ? 1 : 4;
-    if (cpb > 16) cpb = 16;
     const int n_groups = n_chunks / cpb;
     double2 *part = reinterpret_cast<double2 *>(a->rpart);
     const float *xin = a->apply_norm ? a->xn : a->x;
     if (T <= 2) {
         hipLaunchKernelGGL(k_router_part<1>, dim3((E + 63) / 64, n_groups, T), dim3(64 * cpb), 0, s,
-                           xin, a->router, T, D, E, cpb, part);
+                           xin, a->router, T, D, E, cpb, part, a->ctl);
     } else if (T <= 16) {
         hipLaunchKernelGGL(k_router_part<2>, dim3((E + 63) / 64, n_groups, (T + 1) / 2),
-                           dim3(64 * cpb), 0, s, xin, a->router, T, D, E, cpb, part);
+                           dim3(64 * cpb), 0, s, xin, a->router, T, D, E, cpb, part, a->ctl);
     } else {
         hipLaunchKernelGGL(k_router_part<4>, dim3((E + 63) / 64, n_groups, (T + 3) / 4),
-                           dim3(64 * cpb), 0, s, xin, a->router, T, D, E, cpb, part);
+                           dim3(64 * cpb), 0, s, xin, a->router, T, D, E, cpb, part, a->ctl);
     }
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
-    hipLaunchKernelGGL(k_topk_cert, dim3(T), dim3(ORN_TOPK_THREADS), 0, s, part, n_groups,
+    // Dynamic LDS: x plus cb weight rows for the exact fallback, within 56 KB.
+    int cb = (56 * 1024) / (4 * D) - 1;
+    if (cb > 8) cb = 8;
+    if (cb < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_topk_cert, dim3(T), dim3(ORN_TOPK_THREADS),
+                       sizeof(float) * (size_t)D * (size_t)(cb + 1), s, part, n_groups,
                        cpb * ORN_RCHUNK, xin, a->router, a->bias, D, E, a->k, a->mode, a->idx, a->w,
-                       a->ctl + 3);
+                       a->ctl + 3, cb);
     return hipGetLastError();
 }
