@@ -167,6 +167,9 @@ def main():
     ap.add_argument("--stack", action="store_true", help="also time the 40-layer stack (21 GB)")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="first copy MIB MiB device-to-device once: a kernel of known traffic "
+                         "against which hardware byte counters are scaled")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no "
@@ -176,6 +179,14 @@ def main():
     ctx = om.Context()
     name, cus, hbm = ctx.device_info()
     log("device:", name, cus, "CUs", hbm >> 30, "GiB")
+    if args.copy_probe:
+        n = args.copy_probe << 20
+        src, dst = ctx.alloc(n), ctx.alloc(n)
+        om.lib().gpu_copy_buffer(ctx.ptr, dst.ptr, src.ptr, n)
+        ctx.sync()
+        src.free()
+        dst.free()
+        log(f"copy probe: {args.copy_probe} MiB device-to-device")
     store = om.Store(ctx, 2, D, H, E, K, True)
     t0 = time.perf_counter()
     store.fill_synthetic(0, SEED)

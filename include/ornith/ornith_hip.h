@@ -148,9 +148,9 @@ int gpu_moe_forward_stack(gpu_context *ctx, ornith_moe_store *store, int first_l
                           const ornith_moe_opts *opts);
 
 /* Counters of the last forward: number of active expert slots (incl. the
- * shared expert), token rows, and tokens whose top-k needed the exact
- * sequential fallback. */
-int gpu_moe_last_stats(gpu_context *ctx, int *n_slots, int *n_rows, int *n_exact);
+ * shared expert), token rows, and tokens whose top-k ran the literal
+ * exchange selection (tied or non-finite logits among the top k+1). */
+int gpu_moe_last_stats(gpu_context *ctx, int *n_slots, int *n_rows, int *n_literal);
 
 /* ---------------------------------------------------------------------------
  * Kernel timing with HIP events recorded on the context's stream around every

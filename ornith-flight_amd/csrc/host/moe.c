@@ -3,7 +3,7 @@
  * Resident routed-MoE layers and the per-layer forward (C99 host side).
  *
  * The forward replaces model.c:992-1144 for a batch of tokens:
- *   norm/reset -> certified router + top-k -> dispatch -> gate/up -> mid ->
+ *   norm -> exact router logits + top-k -> dispatch -> gate/up -> mid ->
  *   down -> combine,
  * all enqueued on the context's stream; no host round trip between steps.
  */
@@ -19,7 +19,7 @@ struct ornith_moe_store {
     uint8_t *gate, *up;       /* [L][E+1][H/256][D] * 144 B */
     uint8_t *down_body;       /* [L][E+1][D/256][H] * 208 B */
     uint16_t *down_d;         /* [L][E+1][D/256][H] */
-    float *router_t;          /* [L][E][D] */
+    float *router_q;          /* [L][D/4][E][4]: W(d, e) at ((d/4)*E + e)*4 + d%4 */
     float *bias;              /* [L][E] */
     int *has_bias;            /* host [L] */
     float *norm;              /* [L][D] */
@@ -178,7 +178,7 @@ static void store_free(ornith_moe_store *st)
     hipFree(st->up);
     hipFree(st->down_body);
     hipFree(st->down_d);
-    hipFree(st->router_t);
+    hipFree(st->router_q);
     hipFree(st->bias);
     hipFree(st->norm);
     free(st->has_bias);
@@ -202,7 +202,7 @@ ornith_moe_store *gpu_moe_store_create(gpu_context *ctx, const ornith_moe_shape 
     const size_t nb = L * E1 * st->blocks_per_matrix;
     size_t sizes[7] = {nb * 144, nb * 144, nb * 208, nb * 2, L * E * D * 4, L * E * 4, L * D * 4};
     void **ptrs[7] = {(void **)&st->gate, (void **)&st->up, (void **)&st->down_body,
-                      (void **)&st->down_d, (void **)&st->router_t, (void **)&st->bias,
+                      (void **)&st->down_d, (void **)&st->router_q, (void **)&st->bias,
                       (void **)&st->norm};
     for (int i = 0; i < 7; ++i) {
         if (hipMalloc(ptrs[i], sizes[i]) != hipSuccess ||
@@ -315,9 +315,9 @@ int gpu_moe_store_set_router(gpu_context *ctx, ornith_moe_store *st, int layer, 
     float *t = (float *)malloc(D * E * sizeof(float));
     if (!t) return orn_set_err(ctx, ORN_ENOMEM, "host staging");
     for (size_t d = 0; d < D; ++d)
-        for (size_t e = 0; e < E; ++e) t[e * D + d] = W[d * E + e];
+        for (size_t e = 0; e < E; ++e) t[((d >> 2) * E + e) * 4 + (d & 3)] = W[d * E + e];
     hipStream_t s = ctx->stream;
-    int rc = orn_hip_check(ctx, hipMemcpyAsync(st->router_t + (size_t)layer * E * D, t,
+    int rc = orn_hip_check(ctx, hipMemcpyAsync(st->router_q + (size_t)layer * E * D, t,
                                                D * E * sizeof(float), hipMemcpyHostToDevice, s),
                            "upload router");
     if (!rc) {
@@ -466,7 +466,6 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     off += ALIGN256((size_t)(bytes))
     CARVE(o_xn, (flags & ORN_MOE_NORM) ? (size_t)T * D * 4 : 0);
     CARVE(o_logits, (size_t)T * E * 4);
-    CARVE(o_rpart, (size_t)T * E * (D / 128) * 16);
     CARVE(o_idx, (size_t)T * k * 4);
     CARVE(o_w, (size_t)T * k * 4);
     CARVE(o_ctl, 64);
@@ -503,7 +502,7 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     a.up = st->up + (size_t)layer * E1nb * 144;
     a.down_body = st->down_body + (size_t)layer * E1nb * 208;
     a.down_d = st->down_d + (size_t)layer * E1nb;
-    a.router = st->router_t + (size_t)layer * E * D;
+    a.router = st->router_q + (size_t)layer * E * D;
     a.bias = st->has_bias[layer] ? st->bias + (size_t)layer * E : NULL;
     a.norm_w = st->norm + (size_t)layer * D;
     a.x = x;
@@ -511,7 +510,6 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     a.out = out;
     a.xn = a.apply_norm ? (float *)(ws + o_xn) : (float *)x;
     a.logits = (float *)(ws + o_logits);
-    a.rpart = (double *)(ws + o_rpart);
     a.idx = (uint32_t *)(ws + o_idx);
     a.w = (float *)(ws + o_w);
     a.ctl = (int *)(ws + o_ctl);
@@ -595,7 +593,7 @@ int gpu_moe_forward_stack(gpu_context *ctx, ornith_moe_store *st, int first_laye
     return ORN_OK;
 }
 
-int gpu_moe_last_stats(gpu_context *ctx, int *n_slots, int *n_rows, int *n_exact)
+int gpu_moe_last_stats(gpu_context *ctx, int *n_slots, int *n_rows, int *n_literal)
 {
     if (!ctx) return ORN_EINVAL;
     memset(ctx->ctl_host, 0, 16 * sizeof(int));
@@ -608,6 +606,6 @@ int gpu_moe_last_stats(gpu_context *ctx, int *n_slots, int *n_rows, int *n_exact
     hipStreamSynchronize(ctx->stream);
     if (n_slots) *n_slots = ctx->ctl_host[0];
     if (n_rows) *n_rows = ctx->ctl_host[2];
-    if (n_exact) *n_exact = ctx->ctl_host[3];
+    if (n_literal) *n_literal = ctx->ctl_host[3];
     return ORN_OK;
 }

@@ -12,6 +12,11 @@
 
 #define ORN_WAVE 64
 
+// Native 4-wide vector.  Loads through it are single vector loads; copying
+// HIP's float4 struct from global memory lowers to a memcpy, which keeps
+// register arrays of it in scratch memory.
+typedef float v4f __attribute__((ext_vector_type(4)));
+
 // gguf.c:16-26.  0x0000 -> 0; every other pattern is decoded as a normal
 // number with exponent bias 112 (0x8000 -> -2^-15, subnormal patterns ->
 // 2^-15*(1+m/1024), exp=31 -> 2^16*(1+m/1024)).  Pure integer work, so the
@@ -21,7 +26,42 @@ __device__ __forceinline__ float orn_half_to_float(uint32_t h)
     h &= 0xFFFFu;
     const uint32_t u = ((h & 0x8000u) << 16) | ((((h & 0x7C00u) >> 10) + 112u) << 23) |
                        ((h & 0x03FFu) << 13);
-    return h == 0u ? 0.0f : __uint_as_float(u);  // select, no branch
+    // Zero via a mask (all ones iff h != 0), not a select: the compiler
+    // turns the select into a branch, which splits the callers' loops.
+    const uint32_t nz = 0u - ((h + 0xFFFFu) >> 16);
+    return __uint_as_float(u & nz);
+}
+
+// Empty volatile asm that reads and writes v[0..7] and clobbers memory: every
+// computation of these values is ordered before it, and no load or store
+// moves across it.  Used to keep a ring slot's refill after the slot's last
+// use, so the refill can write the slot's own registers.
+__device__ __forceinline__ void orn_pin8(float *v)
+{
+    asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
+                 "+v"(v[6]), "+v"(v[7])::"memory");
+}
+
+__device__ __forceinline__ void orn_pin2(float &a, float &b)
+{
+    asm volatile("" : "+v"(a), "+v"(b)::"memory");
+}
+
+// Marks the point where a ring slot's loaded registers are first used: the
+// wait for the slot's loads lands here, and no use of them moves above it.
+__device__ __forceinline__ void orn_pin_u4(uint4 &a)
+{
+    asm volatile("" : "+v"(a.x), "+v"(a.y), "+v"(a.z), "+v"(a.w));
+}
+
+// Byte i (0..3) of w as a float: one v_cvt_f32_ubyte<i>.  The word passes
+// through an empty asm first, so the compiler cannot fold an earlier mask
+// into a per-byte bit-field extract (two instructions per byte).
+__device__ __forceinline__ void orn_bytes_to_float(uint32_t w, float *f)
+{
+    asm("" : "+v"(w));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f[i] = (float)((w >> (8 * i)) & 0xFFu);
 }
 
 __device__ __forceinline__ uint32_t orn_byte(uint32_t w, int i) { return (w >> (8 * i)) & 0xFFu; }

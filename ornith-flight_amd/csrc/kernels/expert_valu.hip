@@ -130,22 +130,16 @@ __global__ void __launch_bounds__(1024)
 
 __device__ __forceinline__ void q4_nibbles(uint32_t w, float *lo, float *hi)
 {
-    const uint32_t l = w & 0x0F0F0F0Fu;
-    const uint32_t h = (w >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-        lo[b] = (float)((l >> (8 * b)) & 0xFFu);
-        hi[b] = (float)((h >> (8 * b)) & 0xFFu);
-    }
+    orn_bytes_to_float(w & 0x0F0F0F0Fu, lo);
+    orn_bytes_to_float((w >> 4) & 0x0F0F0F0Fu, hi);
 }
 
 struct Q4Row {
     uint4 hd, q;
 };
 
-__device__ __forceinline__ void load_q4(const uint8_t *base, int krow, int j, Q4Row &r)
+__device__ __forceinline__ void load_q4(const uint8_t *blk, int j, Q4Row &r)
 {
-    const uint8_t *blk = base + (size_t)krow * ORN_Q4K_BYTES;
     r.hd = *reinterpret_cast<const uint4 *>(blk);
     r.q = *reinterpret_cast<const uint4 *>(blk + ORN_Q4K_OFF_QS + 16 * j);
 }
@@ -176,6 +170,7 @@ __device__ __forceinline__ void q4_row(const Q4Row &r, int c, float xv, float *a
     }
 }
 
+template <int NIT, int RWT>
 __global__ void __launch_bounds__(256)
     k_gateup(const uint8_t *__restrict__ gate, const uint8_t *__restrict__ up,
              const float *__restrict__ xn, const int *__restrict__ ctl,
@@ -194,7 +189,7 @@ __global__ void __launch_bounds__(256)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int NB = H >> 8;
     const int CR = 16 * NB;
-    const int RW = 64 / CR;
+    const int RW = RWT > 0 ? RWT : 64 / CR;  // RWT == 64 / CR when given (launcher)
     const int rr = lane / CR, ch = lane % CR;
     const int j = ch & 7, bc = (ch >> 3) % NB, m = ch / (8 * NB);
     const int c = j >> 1;
@@ -202,9 +197,14 @@ __global__ void __launch_bounds__(256)
     const int H2 = 2 * H;
     const uint8_t *base =
         (m ? up : gate) + ((size_t)(e * NB + bc) * (size_t)D + (size_t)k_start) * ORN_Q4K_BYTES;
-    const int n_it = RK / (4 * RW);  // multiple of ORN_NPF (checked by the launcher)
+    // Rows per wave, a multiple of ORN_NPF (checked by the launcher).  With
+    // compile-time NIT and RWT the ring loop unrolls into straight-line code
+    // whose loads are one base address plus immediate offsets.
+    const int n_it = NIT > 0 ? NIT : RK / (4 * RW);
     const int last = n_it - 1;
     const int col0 = m * H + bc * 256 + 64 * c + 16 * (j & 1);
+    const int h0 = wave * RW + rr;      // this lane's first row; row i is h0 + 4*RW*i
+    const size_t rstep = (size_t)4 * RW * ORN_Q4K_BYTES;
 
     for (int r = 0; r < itm.z; ++r) {
         const int row = itm.y + r;
@@ -212,18 +212,40 @@ __global__ void __launch_bounds__(256)
         for (int i = tid; i < RK; i += blockDim.x) xs[i] = xr[i];
         __syncthreads();
 
+        // Opaque zero: keeps the ring's first loads inside this token's pass
+        // instead of hoisted (and held in extra registers) across all passes.
+        int z = 0;
+        asm volatile("" : "+v"(z));
+        const uint8_t *lb = base + (size_t)(h0 + z) * ORN_Q4K_BYTES;
+        const float *xl = xs + h0;
+
         float acc[32];
 #pragma unroll
         for (int u = 0; u < 32; ++u) acc[u] = 0.0f;
         float macc0 = 0.0f, macc1 = 0.0f;
         Q4Row rs[ORN_NPF];
 #pragma unroll
-        for (int p = 0; p < ORN_NPF; ++p) load_q4(base, (min(p, last) * 4 + wave) * RW + rr, j, rs[p]);
+        for (int p = 0; p < ORN_NPF; ++p) {
+            load_q4(lb + (size_t)min(p, last) * rstep, j, rs[p]);
+            __builtin_amdgcn_sched_barrier(0);  // issue order = consumption order
+        }
+#pragma unroll
         for (int it = 0; it < n_it; it += ORN_NPF) {
+            float xv[ORN_NPF];
+#pragma unroll
+            for (int p = 0; p < ORN_NPF; ++p) xv[p] = xl[(it + p) * 4 * RW];
 #pragma unroll
             for (int p = 0; p < ORN_NPF; ++p) {
-                q4_row(rs[p], c, xs[((it + p) * 4 + wave) * RW + rr], acc, macc0, macc1);
-                load_q4(base, (min(it + p + ORN_NPF, last) * 4 + wave) * RW + rr, j, rs[p]);
+                // Use the slot, then refill it in place (the pins keep the
+                // refill after the use), ORN_NPF rows ahead.
+                orn_pin_u4(rs[p].hd);
+                orn_pin_u4(rs[p].q);
+                q4_row(rs[p], c, xv[p], acc, macc0, macc1);
+#pragma unroll
+                for (int u = 0; u < 32; u += 8) orn_pin8(acc + u);
+                orn_pin2(macc0, macc1);
+                load_q4(lb + (size_t)min(it + p + ORN_NPF, last) * rstep, j, rs[p]);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
 #pragma unroll
@@ -306,13 +328,11 @@ __device__ __forceinline__ void q6_decode(uint32_t ql, uint32_t qh, int jj, floa
 {
     const uint32_t a0 = (ql & 0x0F0F0F0Fu) | (((qh >> (2 * jj)) & 0x03030303u) << 4);
     const uint32_t a1 = ((ql >> 4) & 0x0F0F0F0Fu) | (((qh >> (2 * jj + 4)) & 0x03030303u) << 4);
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-        q0[b] = (float)((a0 >> (8 * b)) & 0xFFu);
-        q1[b] = (float)((a1 >> (8 * b)) & 0xFFu);
-    }
+    orn_bytes_to_float(a0, q0);
+    orn_bytes_to_float(a1, q1);
 }
 
+template <int NIT, int RWT>
 __global__ void __launch_bounds__(256)
     k_down(const uint8_t *__restrict__ body, const uint16_t *__restrict__ dsc,
            const float *__restrict__ mid, const int *__restrict__ ctl,
@@ -330,7 +350,7 @@ __global__ void __launch_bounds__(256)
     const int NBD = D >> 8;
     const int CR = 8 * NBD;
     const int CRg = CR < 64 ? CR : 64;
-    const int RW = 64 / CRg;
+    const int RW = RWT > 0 ? RWT : 64 / CRg;  // RWT == 64 / CRg when given (launcher)
     const int ncols = CRg * 32;   // outputs of this column group
     float *ms = smem;             // [RH]
     float *red = smem + RH;       // [ncols]
@@ -342,16 +362,26 @@ __global__ void __launch_bounds__(256)
     const size_t bcol = (size_t)(e * NBD + bc) * (size_t)H + (size_t)h_start;
     const uint8_t *bbase = body + bcol * 208;
     const uint16_t *dbase = dsc + bcol;
-    const int n_it = RH / (4 * RW);  // multiple of ORN_NPF (checked by the launcher)
+    const int n_it = NIT > 0 ? NIT : RH / (4 * RW);  // as in k_gateup
     const int last = n_it - 1;
     const int pos = (l0 >> 4) + 2 * jj;  // byte of the scale dwords 2n (j=jj) and 2n+1 (j=jj+2)
     const int lcol0 = (bc - cg * 8) * 256 + 128 * n + 32 * jj + l0;
+
+    const int h0 = wave * RW + rr;  // this lane's first row; row i is h0 + 4*RW*i
+    const int hstep = 4 * RW;
 
     for (int r = 0; r < itm.z; ++r) {
         const int row = itm.y + r;
         const float *mr = mid + (size_t)row * H + h_start;
         for (int i = tid; i < RH; i += blockDim.x) ms[i] = mr[i];
         __syncthreads();
+
+        // Opaque zero, as in k_gateup: the ring's first loads stay in this pass.
+        int z = 0;
+        asm volatile("" : "+v"(z));
+        const uint8_t *lb = bbase + (size_t)(h0 + z) * 208;
+        const uint16_t *ld = dbase + h0 + z;
+        const float *ml = ms + h0;
 
         float acc[32];
 #pragma unroll
@@ -362,19 +392,26 @@ __global__ void __launch_bounds__(256)
         uint32_t dr[ORN_NPF];
 #pragma unroll
         for (int p = 0; p < ORN_NPF; ++p) {
-            const int h = (min(p, last) * 4 + wave) * RW + rr;
-            const uint8_t *b = bbase + (size_t)h * 208;
+            const int hi = min(p, last) * hstep;
+            const uint8_t *b = lb + (size_t)hi * 208;
             qlr[p] = *reinterpret_cast<const uint4 *>(b + 64 * n + 32 * jj + l0);
             qhr[p] = *reinterpret_cast<const uint4 *>(b + 128 + 32 * n + l0);
             scr[p] = *reinterpret_cast<const uint2 *>(b + 192 + 8 * n);
-            dr[p] = dbase[h];
+            dr[p] = ld[hi];
+            __builtin_amdgcn_sched_barrier(0);  // issue order = consumption order
         }
+#pragma unroll
         for (int it = 0; it < n_it; it += ORN_NPF) {
+            float mv[ORN_NPF];
+#pragma unroll
+            for (int p = 0; p < ORN_NPF; ++p) mv[p] = ml[(it + p) * hstep];
 #pragma unroll
             for (int p = 0; p < ORN_NPF; ++p) {
-                const int rho = ((it + p) * 4 + wave) * RW + rr;
+                orn_pin_u4(qlr[p]);
+                orn_pin_u4(qhr[p]);
+                asm volatile("" : "+v"(scr[p].x), "+v"(scr[p].y), "+v"(dr[p]));
                 const float d = orn_half_to_float(dr[p]);
-                const float xv = ms[rho];
+                const float xv = mv[p];
                 const float a0 = xv * (d * (float)(int)(int8_t)orn_byte(scr[p].x, pos));
                 const float a1 = xv * (d * (float)(int)(int8_t)orn_byte(scr[p].y, pos));
                 cs0 += a0;
@@ -391,12 +428,16 @@ __global__ void __launch_bounds__(256)
                         acc[16 + dw * 4 + bb] = fmaf(a1, q1[bb], acc[16 + dw * 4 + bb]);
                     }
                 }
-                const int h = (min(it + p + ORN_NPF, last) * 4 + wave) * RW + rr;
-                const uint8_t *b = bbase + (size_t)h * 208;
+#pragma unroll
+                for (int u = 0; u < 32; u += 8) orn_pin8(acc + u);
+                orn_pin2(cs0, cs1);
+                const int hi = min(it + p + ORN_NPF, last) * hstep;
+                const uint8_t *b = lb + (size_t)hi * 208;
                 qlr[p] = *reinterpret_cast<const uint4 *>(b + 64 * n + 32 * jj + l0);
                 qhr[p] = *reinterpret_cast<const uint4 *>(b + 128 + 32 * n + l0);
                 scr[p] = *reinterpret_cast<const uint2 *>(b + 192 + 8 * n);
-                dr[p] = dbase[h];
+                dr[p] = ld[hi];
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
 #pragma unroll
@@ -492,9 +533,19 @@ extern "C" int ornk_moe_gateup(const ornk_moe_args *a, hipStream_t s)
     if (a->D % a->ks_gu || RK % (4 * RW * ORN_NPF)) return hipErrorInvalidValue;
     const size_t shmem = sizeof(float) * (size_t)(RK + 2 * a->H);
     if (shmem > 64 * 1024) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_gateup, dim3(a->items_max * a->ks_gu), dim3(256), shmem, s, a->gate, a->up,
-                       a->xn, a->ctl, reinterpret_cast<const int4 *>(a->items), a->slot_expert,
-                       a->row_token, a->gu_part, a->D, a->H, a->ks_gu, a->rows_max);
+    const int n_it = RK / (4 * RW);
+#define ORN_GU(N, R)                                                                            \
+    hipLaunchKernelGGL((k_gateup<N, R>), dim3(a->items_max * a->ks_gu), dim3(256), shmem, s, a->gate, \
+                       a->up, a->xn, a->ctl, reinterpret_cast<const int4 *>(a->items),          \
+                       a->slot_expert, a->row_token, a->gu_part, a->D, a->H, a->ks_gu,          \
+                       a->rows_max)
+    // Straight-line instances for the Ornith shape (H = 512: RW = 2).
+    if (RW == 2 && n_it == 4) ORN_GU(4, 2);
+    else if (RW == 2 && n_it == 8) ORN_GU(8, 2);
+    else if (RW == 2 && n_it == 16) ORN_GU(16, 2);
+    else if (RW == 2 && n_it == 32) ORN_GU(32, 2);
+    else ORN_GU(0, 0);
+#undef ORN_GU
     return hipGetLastError();
 }
 
@@ -518,10 +569,19 @@ extern "C" int ornk_moe_down(const ornk_moe_args *a, hipStream_t s)
     if (a->H % a->ks_dn || RH % (4 * RW * ORN_NPF)) return hipErrorInvalidValue;
     const size_t shmem = sizeof(float) * (size_t)(RH + CRg * 32);
     if (shmem > 64 * 1024) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_down, dim3(a->items_max * a->ks_dn * ncg), dim3(256), shmem, s,
-                       a->down_body, a->down_d, a->mid, a->ctl,
-                       reinterpret_cast<const int4 *>(a->items), a->slot_expert, a->dn_part, a->D,
-                       a->H, a->ks_dn, ncg, a->rows_max);
+    const int n_it = RH / (4 * RW);
+#define ORN_DN(N, R)                                                                             \
+    hipLaunchKernelGGL((k_down<N, R>), dim3(a->items_max * a->ks_dn * ncg), dim3(256), shmem, s,       \
+                       a->down_body, a->down_d, a->mid, a->ctl,                                  \
+                       reinterpret_cast<const int4 *>(a->items), a->slot_expert, a->dn_part,     \
+                       a->D, a->H, a->ks_dn, ncg, a->rows_max)
+    // Straight-line instances for the Ornith shape (D = 2048: RW = 1).
+    if (RW == 1 && n_it == 4) ORN_DN(4, 1);
+    else if (RW == 1 && n_it == 8) ORN_DN(8, 1);
+    else if (RW == 1 && n_it == 16) ORN_DN(16, 1);
+    else if (RW == 1 && n_it == 32) ORN_DN(32, 1);
+    else ORN_DN(0, 0);
+#undef ORN_DN
     return hipGetLastError();
 }
 

@@ -40,8 +40,8 @@ int ornk_router_exact(const float *x, const float *W, const float *bias, int T, 
 /* Per-token top-k with the reference's exchange-selection semantics.
  * mode 0: exchange on logits + softmax over the top-k (model.c:301-317);
  * mode 1: full softmax + exchange on probabilities (model.c:1027-1049).
- * n_exact (device int, may be NULL) counts tokens that needed the exact
- * sequential exchange simulation (ties or NaN). */
+ * n_exact (device int, may be NULL) counts tokens whose selection ran the
+ * literal exchange simulation (ties or NaN). */
 int ornk_topk(const float *logits, int T, int E, int k, int mode, uint32_t *idx, float *w,
               int *n_exact, hipStream_t s);
 
@@ -51,6 +51,7 @@ int ornk_topk(const float *logits, int T, int E, int k, int mode, uint32_t *idx,
  *               column c) of expert e at ((e*(H/256) + c)*D + k)*144
  *   down_body : [E+1][D/256][H] Q6_K bodies of 208 B (ql|qh|scales)
  *   down_d    : [E+1][D/256][H] Q6_K super-scales (fp16 bits)
+ *   router    : [D/4][E][4] fp32, W(d, e) at ((d/4)*E + e)*4 + d%4
  * Work buffers are owned by the host; sizes are computed by ornk_moe_ws_size. */
 typedef struct {
     int T, D, H, E, k, has_shared, mode, apply_norm;
@@ -63,10 +64,9 @@ typedef struct {
     /* workspace */
     float *xn;        /* [T][D]  expert input (x or rmsnorm(x)) */
     float *logits;    /* [T][E] */
-    double *rpart;    /* [T][E][D/128][2] certified router partials */
     uint32_t *idx;    /* [T][k] */
     float *w;         /* [T][k] */
-    int *ctl;         /* [16] counters: 0 n_slots, 1 n_items, 2 n_rows, 3 n_exact;
+    int *ctl;         /* [16] counters: 0 n_slots, 1 n_items, 2 n_rows, 3 n_literal;
                          zeroed by the routing step */
     int *slot_expert; /* [E+1] */
     int *slot_off;    /* [E+1] */

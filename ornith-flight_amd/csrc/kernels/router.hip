@@ -6,35 +6,20 @@
 // from 0.0f, of the fp32 products x[d]*W[d*E+e], d ascending.  Selection is
 // exchange selection with strict '>' (model.c:301-305 / 1040-1048).
 //
-// A sequential 2048-long dependent chain per logit is too slow to be the
-// default path, so the MoE path runs a CERTIFIED parallel computation:
-//
-//   * k_router_part: the same fp32 products, summed in fp64 over chunks of
-//     ORN_RCHUNK rows, plus Q = sum over the chunk of |local prefix sum|.
-//   * k_topk_cert:   combines chunks into P~ (~exact sum of the products) and
-//     A' >= sum_k |P_k| (exact prefix sums, by the triangle inequality over
-//     chunk carries).  The reference's sequential result differs from the
-//     exact sum by at most u*sum_k|S_k| <= u*A/(1-n*u) (u = 2^-24), so every
-//     reference logit lies in [P~ - B, P~ + B] with B = 1.01*u*A' (+ the bias
-//     add's rounding).  If the top-k intervals are pairwise disjoint and lie
-//     above every other interval, the reference's ordered top-k equals ours
-//     and it has no ties, so exchange selection equals sorting.
-//   * otherwise (near-ties, NaN/Inf) the block recomputes the token's logits
-//     with the reference's sequential chain and selects on them exactly,
-//     falling back to a literal exchange-selection simulation when ties are
-//     present.
+// The MoE path computes every logit with exactly that arithmetic: one lane
+// per (token, expert) chain, all chains in parallel (k_router_seq), so the
+// logits are bit-identical to the reference's by construction.  Selection
+// (k_select) takes the top k+1 by (value desc, index asc); when those values
+// are pairwise distinct, exchange selection returns exactly that order, and
+// otherwise (ties, NaN/Inf) one lane runs the literal exchange selection.
 #include "common.h"
 #include "launch.h"
 
 #include <float.h>
 #include <limits.h>
 
-#define ORN_RCHUNK 128  // rows per certified chunk
-#define ORN_TOPK_THREADS 256
 
 namespace {
-
-constexpr double kU = 5.9604644775390625e-08;  // 2^-24
 
 // ---------------------------------------------------------------------------
 // Exact sequential logits (reference arithmetic); W(d, e) = W[d*sd + e*se].
@@ -51,85 +36,6 @@ __global__ void k_router_exact(const float *x, const float *W, long long sd, lon
     for (int d = 0; d < D; ++d) acc += xr[d] * w[(long long)d * sd];
     if (bias) acc += bias[e];
     logits[(size_t)t * E + e] = acc;
-}
-
-// ---------------------------------------------------------------------------
-// Certified partial sums.  Wt is the router transposed, [E][D] (d fastest), so
-// each lane streams its expert's column with 16-byte loads.  grid: (E/64,
-// n_groups, ceil(T/TB)); block: 64*cpb threads, one wave per chunk of the
-// group.  Output part[(t*E + e)*n_groups + g] = (sum, A_group) in fp64, where
-// A_group bounds sum_{k in group} |prefix_k| with prefixes restarted at the
-// group start.
-// ---------------------------------------------------------------------------
-template <int TB>
-__global__ void k_router_part(const float *__restrict__ x, const float *__restrict__ Wt, int T,
-                              int D, int E, int cpb, double2 *__restrict__ part, int *ctl)
-{
-    __shared__ double s_sum[4][TB][64];
-    __shared__ double s_q[4][TB][64];
-    __shared__ float xs[TB][4 * ORN_RCHUNK];
-    const int lane = threadIdx.x & 63;
-    const int c = threadIdx.x >> 6;           // chunk within group
-    const int e = blockIdx.x * 64 + lane;
-    const int g = blockIdx.y;
-    const int n_groups = gridDim.y;
-    const int t0 = blockIdx.z * TB;
-    const int rows = cpb * ORN_RCHUNK;
-    const int dg = g * rows;
-    const bool live = e < E;
-
-    // The first block clears the per-forward counters (routing is the
-    // first step of every forward).
-    if (ctl && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x < 16)
-        ctl[threadIdx.x] = 0;
-    for (int i = threadIdx.x; i < TB * rows; i += blockDim.x) {
-        const int tt = i / rows, r = i - tt * rows;
-        xs[tt][r] = (t0 + tt < T) ? x[(size_t)(t0 + tt) * D + dg + r] : 0.0f;
-    }
-    __syncthreads();
-
-    double S[TB], Q[TB];
-#pragma unroll
-    for (int tt = 0; tt < TB; ++tt) { S[tt] = 0.0; Q[tt] = 0.0; }
-
-    if (live) {
-        const float4 *wp = reinterpret_cast<const float4 *>(Wt + (size_t)e * D + dg + c * ORN_RCHUNK);
-        const float *xc = &xs[0][c * ORN_RCHUNK];
-        for (int i0 = 0; i0 < ORN_RCHUNK / 4; i0 += 8) {
-            float4 wv[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) wv[u] = wp[i0 + u];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const float wr[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int d = (i0 + u) * 4 + r;
-#pragma unroll
-                    for (int tt = 0; tt < TB; ++tt) {
-                        const float p = xc[tt * 4 * ORN_RCHUNK + d] * wr[r];
-                        S[tt] += (double)p;
-                        Q[tt] += fabs(S[tt]);
-                    }
-                }
-            }
-        }
-    }
-#pragma unroll
-    for (int tt = 0; tt < TB; ++tt) { s_sum[c][tt][lane] = S[tt]; s_q[c][tt][lane] = Q[tt]; }
-    __syncthreads();
-    if (c == 0 && live) {
-#pragma unroll
-        for (int tt = 0; tt < TB; ++tt) {
-            if (t0 + tt >= T) continue;
-            double carry = 0.0, A = 0.0;
-            for (int cc = 0; cc < cpb; ++cc) {
-                A += (double)ORN_RCHUNK * fabs(carry) + s_q[cc][tt][lane];
-                carry += s_sum[cc][tt][lane];
-            }
-            part[((size_t)(t0 + tt) * E + e) * n_groups + g] = make_double2(carry, A);
-        }
-    }
 }
 
 // ---------------------------------------------------------------------------
@@ -227,256 +133,343 @@ __device__ void exact_select(float val, int n, int k, float *vals_s, int *idx_s,
     }
 }
 
-// Renormalised weights over the selected logits (model.c:307-317).
-__device__ void renorm_weights(const float *sel_v, int k, float *w)
-{
-    const float mx = sel_v[0];
-    float s[64];
-    float sum = 0.0f;
-    for (int i = 0; i < k; ++i) { s[i] = expf(sel_v[i] - mx); sum += s[i]; }
-    for (int i = 0; i < k; ++i) w[i] = s[i] / sum;
-}
+// ---------------------------------------------------------------------------
+// MoE router logits, many tokens (prefill).  Lane = expert e0 + lane; wave w
+// = tokens t0 + w*TPW .. t0 + w*TPW + TPW-1 (TPW independent chains per
+// lane).  The block's 64 weight columns and its tokens' activations stream
+// through LDS in chunks of ORN_RDC values of d, so every weight byte read
+// from L2 serves 4*TPW tokens: each thread keeps its share of the next
+// ORN_RPF chunks in flight in registers, copies chunk c into one of two LDS
+// slots, and every chain then consumes the chunk in d order.
+// ---------------------------------------------------------------------------
+#define ORN_RDC 32                 // d values per chunk
+#define ORN_RPF 8                  // chunks in flight
+#define ORN_RWS4 (ORN_RDC / 4 + 1) // LDS row stride of a weight row, in float4 (padded)
 
-// ---------------------------------------------------------------------------
-// The reference's sequential logits (model.c:1017-1025) for the experts in
-// list[0..n): products rounded to fp32, added in d order from 0.0f, then the
-// optional bias; results in lf[e].  The weight rows of up to `cb` experts at
-// a time are first copied into LDS by the whole block (every load in
-// flight at once), then one thread per expert runs its dependent chain out
-// of LDS.  xs holds x (D floats); rows has room for cb*D floats.
-// ---------------------------------------------------------------------------
-__device__ void exact_logits(const int *list, int n, const float *xs, float *rows, int cb,
-                             const float *__restrict__ Wt, const float *bias, int D, float *lf)
+template <int TPW>
+__global__ void __launch_bounds__(256)
+    k_router_seq(const float *__restrict__ x, const float *__restrict__ Wq,
+                 const float *__restrict__ bias, int T, int D, int E,
+                 float *__restrict__ logits, int *ctl)
 {
-    const int q = D / 4;
-    for (int b0 = 0; b0 < n; b0 += cb) {
-        const int nb = min(cb, n - b0);
-        float4 *r4 = reinterpret_cast<float4 *>(rows);
-        for (int i = threadIdx.x; i < nb * q; i += blockDim.x) {
-            const int r = i / q, c = i - r * q;
-            r4[i] = reinterpret_cast<const float4 *>(Wt + (size_t)list[b0 + r] * D)[c];
-        }
-        __syncthreads();
-        if ((int)threadIdx.x < nb) {
-            const int e = list[b0 + threadIdx.x];
-            const float4 *w = r4 + (size_t)threadIdx.x * q;
-            const float4 *x4 = reinterpret_cast<const float4 *>(xs);
-            float acc = 0.0f;
-            for (int i = 0; i < q; ++i) {
-                const float4 wv = w[i], xv = x4[i];
-                acc += xv.x * wv.x;
-                acc += xv.y * wv.y;
-                acc += xv.z * wv.z;
-                acc += xv.w * wv.w;
-            }
-            if (bias) acc += bias[e];
-            lf[e] = acc;
-        }
-        __syncthreads();
+    constexpr int TB = 4 * TPW;               // tokens per block
+    constexpr int XF4 = TB * ORN_RDC / 4;     // activation float4 per chunk
+    constexpr int XPT = (XF4 + 255) / 256;    // ... per thread
+    constexpr int WF4 = 64 * ORN_RDC / 4;     // weight float4 per chunk
+    constexpr int WPT = WF4 / 256;            // ... per thread
+    static_assert(WF4 % 256 == 0, "chunk must split evenly over the block");
+    __shared__ v4f wl[2][64 * ORN_RWS4];
+    __shared__ v4f xl[2][XF4];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int e0 = blockIdx.x * 64, t0 = blockIdx.y * TB;
+    // The routing step is the first of every forward: clear its counters.
+    if (ctl && blockIdx.x == 0 && blockIdx.y == 0 && tid < 16) ctl[tid] = 0;
+    const int nc = D / ORN_RDC;
+
+    // Weights in the d-quad layout Wq[D/4][E][4]: the 64 experts of one
+    // quad are 1 KB contiguous.  Chunk c holds quads 8c..8c+7.
+    const float *wsrc[WPT];
+    int wdst[WPT];
+#pragma unroll
+    for (int i = 0; i < WPT; ++i) {
+        const int q = tid + 256 * i, d4 = q / 64, r = q % 64;
+        const int e = min(e0 + r, E - 1);  // rows past E load a valid row, never used
+        wsrc[i] = Wq + ((size_t)d4 * E + e) * 4;
+        wdst[i] = r * ORN_RWS4 + d4;
     }
-}
-
-// ---------------------------------------------------------------------------
-// Certified top-k, one block per token (E <= 256).
-//
-//  1. Every reference logit lies in [v - B, v + B] (v = P~ + bias).
-//  2. If the k best intervals are disjoint from each other and from all
-//     other intervals, the reference's ordered top-k is ours: done.
-//  3. Otherwise only experts whose interval reaches tau = min over our top-k
-//     of (v - B) can be in the reference's top-k (k experts provably have
-//     reference values >= tau).  Their exact sequential logits are computed;
-//     if the best k+1 of those are pairwise distinct, the reference's top-k
-//     is their order by value (exchange selection sorts when there are no
-//     ties), since every other expert is strictly below tau.
-//  4. Exact ties (or NaN/Inf) are resolved by computing every expert's exact
-//     logit and running the literal exchange selection.
-// In the literal mode (selection on softmax probabilities) step 3 also
-// requires the candidates' logits to be at least 1e-5 apart: probabilities
-// then differ by a relative 1e-5, far more than the few ulps by which expf
-// and the division can move them, so they cannot round to equal values;
-// otherwise step 4 runs, with this device's expf.
-// ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(ORN_TOPK_THREADS)
-    k_topk_cert(const double2 *__restrict__ part, int n_groups, int rows_per_group,
-                const float *__restrict__ x, const float *__restrict__ Wt,
-                const float *__restrict__ bias, int D, int E, int k, int mode, uint32_t *idx_out,
-                float *w_out, int *n_exact, int cb)
-{
-    constexpr int NW = ORN_TOPK_THREADS / 64;
-    __shared__ double sv[NW + 1];
-    __shared__ int si[NW + 1];
-    __shared__ double top_v[17], top_b[17];
-    __shared__ int sel_i[16];
-    __shared__ float sel_v[16];
-    __shared__ float vals_s[ORN_TOPK_THREADS];
-    __shared__ int idx_s[ORN_TOPK_THREADS];
-    __shared__ float red[NW];
-    __shared__ int flag_s, cert_s;
-    __shared__ float w_s[16];
-    __shared__ float lg_s[ORN_TOPK_THREADS];
-    __shared__ float lf_s[ORN_TOPK_THREADS];
-    __shared__ int list_s[ORN_TOPK_THREADS];
-    __shared__ int n_list_s;
-    __shared__ float sum_s;
-    extern __shared__ float dyn[];  // x (D floats) then cb weight rows
-
-    const int t = blockIdx.x;
-    const int e = threadIdx.x;
-    const bool valid = e < E;
-
-    // 1. Combine chunk groups: value v = P~ (+bias), bound B.
-    double v = -HUGE_VAL, B = 0.0;
-    bool finite = true;
-    if (valid) {
-        double carry = 0.0, A = 0.0;
-        const double2 *pp = part + ((size_t)t * E + e) * n_groups;
-        for (int g = 0; g < n_groups; ++g) {
-            const double2 q = pp[g];
-            A += (double)rows_per_group * fabs(carry) + q.y;
-            carry += q.x;
-        }
-        B = 1.01 * kU * A + 1e-37;
-        v = carry;
-        if (bias) {
-            v = carry + (double)bias[e];
-            B = B * (1.0 + kU) + 1.01 * kU * (fabs(v) + B);
-        }
-        finite = isfinite(v) && isfinite(B);
-    }
-    if (threadIdx.x == 0) { flag_s = 0; cert_s = 1; }
-    __syncthreads();
-    if (!finite) flag_s = 1;
-    __syncthreads();
-    const bool all_finite = (flag_s == 0);
-
-    double wv = v;         // value used for the literal-mode weights
-    bool cand_s = false;   // this expert's exact logit was computed (step 3)
-
-    // 2. top-k by (v desc, e asc) and the certification test.
-    bool taken = false;
-    bool certified = all_finite;
-    if (all_finite) {
-        for (int r = 0; r < k; ++r) {
-            double bv;
-            int bi;
-            block_argmax<NW>((valid && !taken) ? v : -HUGE_VAL, (valid && !taken) ? e : INT_MAX, sv,
-                             si, bv, bi);
-            if (e == bi) { taken = true; top_v[r] = v; top_b[r] = B; sel_i[r] = e; }
-        }
-        __syncthreads();
-        double hi_rest;
-        int who;
-        block_argmax<NW>((valid && !taken) ? v + B : -HUGE_VAL, (valid && !taken) ? e : INT_MAX, sv,
-                         si, hi_rest, who);
-        if (threadIdx.x == 0) {
-            bool ok = true;
-            double m = (who == INT_MAX) ? -HUGE_VAL : hi_rest;
-            for (int r = k - 1; r >= 0 && ok; --r) {
-                if (!(top_v[r] - top_b[r] > m)) ok = false;
-                m = fmax(m, top_v[r] + top_b[r]);
-            }
-            cert_s = ok ? 1 : 0;
-        }
-        __syncthreads();
-        certified = cert_s != 0;
+    const size_t wstep = (size_t)(ORN_RDC / 4) * E * 4;  // floats per chunk
+    const float *xsrc[XPT];
+    bool xon[XPT];
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+        const int q = tid + 256 * i, tt = q / (ORN_RDC / 4), d4 = q % (ORN_RDC / 4);
+        xon[i] = q < XF4;
+        const int t = min(t0 + min(tt, TB - 1), T - 1);
+        xsrc[i] = x + (size_t)t * D + 4 * d4;
     }
 
-    if (certified) {
-        if (threadIdx.x < k) sel_v[threadIdx.x] = (float)top_v[threadIdx.x];
-        __syncthreads();
-    } else {
-        if (threadIdx.x == 0 && n_exact) atomicAdd(n_exact, 1);
-        float *xs = dyn;
-        float *rows = dyn + D;
-        for (int i = threadIdx.x; i < D; i += blockDim.x) xs[i] = x[(size_t)t * D + i];
-        if (threadIdx.x == 0) { flag_s = all_finite ? 0 : 1; n_list_s = 0; }
-        __syncthreads();
-        bool resolved = false;
-        if (all_finite) {
-            // 3. Exact logits for the candidate set only.
-            double tau = HUGE_VAL;
-            for (int r = 0; r < k; ++r) tau = fmin(tau, top_v[r] - top_b[r]);
-            const bool cand = valid && (v + B >= tau);
-            cand_s = cand;
-            if (cand) list_s[atomicAdd(&n_list_s, 1)] = e;
-            __syncthreads();
-            exact_logits(list_s, n_list_s, xs, rows, cb, Wt, bias, D, lf_s);
-            const float lf = cand ? lf_s[e] : 0.0f;
-            if (cand && !isfinite(lf)) flag_s = 1;
-            __syncthreads();
-            if (flag_s == 0) {
-                bool tk = false, tie = false;
-                double prev = 0.0;
-                for (int r = 0; r <= k; ++r) {
-                    double bv;
-                    int bi;
-                    block_argmax<NW>((cand && !tk) ? (double)lf : -HUGE_VAL,
-                                     (cand && !tk) ? e : INT_MAX, sv, si, bv, bi);
-                    if (bi == INT_MAX) break;  // fewer than k+1 candidates
-                    if (e == bi) tk = true;
-                    if (r > 0) {
-                        const double gap = prev - bv;
-                        if (!(gap > 0.0)) tie = true;
-                        if (mode == 1 && !(gap > 1e-5)) tie = true;
+    v4f rw[ORN_RPF * WPT], rx[ORN_RPF * XPT];
+#pragma unroll
+    for (int p = 0; p < ORN_RPF; ++p) {
+        const int c = min(p, nc - 1);
+#pragma unroll
+        for (int i = 0; i < WPT; ++i)
+            rw[p * WPT + i] = *reinterpret_cast<const v4f *>(wsrc[i] + (size_t)c * wstep);
+#pragma unroll
+        for (int i = 0; i < XPT; ++i)
+            rx[p * XPT + i] = *reinterpret_cast<const v4f *>(xsrc[i] + (size_t)c * ORN_RDC);
+    }
+
+    float acc[TPW];
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) acc[j] = 0.0f;
+
+    for (int c0 = 0; c0 < nc; c0 += ORN_RPF) {
+#pragma unroll
+        for (int p = 0; p < ORN_RPF; ++p) {
+            const int c = c0 + p;
+            if (c < nc) {  // uniform over the block
+                const int sl = c & 1;
+#pragma unroll
+                for (int i = 0; i < WPT; ++i) wl[sl][wdst[i]] = rw[p * WPT + i];
+#pragma unroll
+                for (int i = 0; i < XPT; ++i)
+                    if (xon[i]) xl[sl][tid + 256 * i] = rx[p * XPT + i];
+                const int cn = min(c + ORN_RPF, nc - 1);
+#pragma unroll
+                for (int i = 0; i < WPT; ++i)
+                    rw[p * WPT + i] = *reinterpret_cast<const v4f *>(wsrc[i] + (size_t)cn * wstep);
+#pragma unroll
+                for (int i = 0; i < XPT; ++i)
+                    rx[p * XPT + i] = *reinterpret_cast<const v4f *>(xsrc[i] + (size_t)cn * ORN_RDC);
+                __syncthreads();
+                const v4f *wr = &wl[sl][lane * ORN_RWS4];
+                const v4f *xr = &xl[sl][wave * TPW * (ORN_RDC / 4)];
+#pragma unroll
+                for (int d4 = 0; d4 < ORN_RDC / 4; ++d4) {
+                    const v4f wv = wr[d4];
+#pragma unroll
+                    for (int j = 0; j < TPW; ++j) {
+                        const v4f xv = xr[j * (ORN_RDC / 4) + d4];
+                        acc[j] = acc[j] + xv.x * wv.x;
+                        acc[j] = acc[j] + xv.y * wv.y;
+                        acc[j] = acc[j] + xv.z * wv.z;
+                        acc[j] = acc[j] + xv.w * wv.w;
                     }
-                    if (r < k && threadIdx.x == 0) { sel_i[r] = bi; sel_v[r] = (float)bv; }
-                    prev = bv;
                 }
-                resolved = !tie;
             }
-            __syncthreads();
-            if (resolved && cand) wv = (double)lf;
         }
-        if (!resolved) {
-            // 4. Every expert's exact logit, literal exchange selection.
-            if (threadIdx.x == 0) n_list_s = E;
-            if (valid) list_s[e] = e;
-            __syncthreads();
-            exact_logits(list_s, E, xs, rows, cb, Wt, bias, D, lf_s);
-            const float lf = valid ? lf_s[e] : 0.0f;
-            wv = (double)lf;
-            float sel_val = lf;
-            if (mode == 1) {
-                if (threadIdx.x == 0) {
-                    float mx = lf_s[0];
-                    for (int j = 1; j < E; ++j) if (lf_s[j] > mx) mx = lf_s[j];
-                    float sacc = 0.0f;
-                    for (int j = 0; j < E; ++j) { lg_s[j] = expf(lf_s[j] - mx); sacc += lg_s[j]; }
-                    sum_s = sacc;
-                }
-                __syncthreads();
-                if (valid) sel_val = lg_s[e] / sum_s;
-                __syncthreads();
+    }
+    const int e = e0 + lane;
+    if (e < E) {
+        const float b = bias ? bias[e] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < TPW; ++j) {
+            const int t = t0 + wave * TPW + j;
+            if (t < T) logits[(size_t)t * E + e] = bias ? acc[j] + b : acc[j];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// MoE router logits, few tokens (decode).  Block = 4 waves = 4 tokens over
+// the same 64 experts (their weight loads hit L1 after the first wave); lane
+// = expert.  A lane's weights for quad d4 are the 16 bytes at
+// Wq[d4][e][0..3], so one wave load instruction reads 1 KB contiguous.  The
+// loads run ORN_DPF quads ahead in a register ring (branch-free, fully
+// unrolled); the wave's activation row sits in LDS and is read as a
+// broadcast.  No block-wide barrier: every wave touches only its own LDS row.
+// ---------------------------------------------------------------------------
+#define ORN_DPF 8  // weight quads in flight per lane
+
+// Orders LDS accesses of the lanes of one wave across this point (the wave's
+// LDS operations execute in issue order; this keeps the compiler from
+// moving them).
+__device__ __forceinline__ void wave_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__global__ void __launch_bounds__(256)
+    k_router_dec(const float *__restrict__ x, const float *__restrict__ Wq,
+                 const float *__restrict__ bias, int T, int D, int E,
+                 float *__restrict__ logits, int *ctl)
+{
+    extern __shared__ v4f xsh[];  // [4][D/4]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int e0 = blockIdx.x * 64;
+    const int t = blockIdx.y * 4 + wave;
+    // The routing step is the first of every forward: clear its counters.
+    if (ctl && blockIdx.x == 0 && blockIdx.y == 0 && tid < 16) ctl[tid] = 0;
+    if (t >= T) return;
+    const int nd4 = D / 4;  // a multiple of ORN_DPF (checked by the launcher)
+    v4f *xw = xsh + (size_t)wave * nd4;
+    const v4f *xg = reinterpret_cast<const v4f *>(x + (size_t)t * D);
+    for (int i = lane; i < nd4; i += 64) xw[i] = xg[i];
+    wave_sync();
+
+    const int e = min(e0 + lane, E - 1);  // lanes past E compute a copy, never stored
+    const v4f *wp = reinterpret_cast<const v4f *>(Wq) + e;  // quad d4 at wp[d4*E]
+    v4f r[ORN_DPF];
+#pragma unroll
+    for (int p = 0; p < ORN_DPF; ++p) r[p] = wp[(size_t)p * E];
+    float acc = 0.0f;
+    for (int i0 = 0; i0 < nd4; i0 += ORN_DPF) {
+        v4f xv4[ORN_DPF];  // this iteration's activations, read up front
+#pragma unroll
+        for (int p = 0; p < ORN_DPF; ++p) xv4[p] = xw[i0 + p];
+#pragma unroll
+        for (int p = 0; p < ORN_DPF; ++p) {
+            // Use the slot, then refill it: the refill reuses its registers.
+            const v4f xv = xv4[p];
+            acc = acc + xv.x * r[p].x;
+            acc = acc + xv.y * r[p].y;
+            acc = acc + xv.z * r[p].z;
+            acc = acc + xv.w * r[p].w;
+            r[p] = wp[(size_t)min(i0 + p + ORN_DPF, nd4 - 1) * E];
+            __builtin_amdgcn_sched_barrier(0);  // keep the refill here, ORN_DPF quads ahead
+        }
+    }
+    if (e0 + lane < E) logits[(size_t)t * E + e0 + lane] = bias ? acc + bias[e0 + lane] : acc;
+}
+
+// ---------------------------------------------------------------------------
+// Top-k selection, one wave per token, E <= 256 (lane holds experts
+// lane + 64*i).  Keys order (value desc, index asc) for non-NaN values.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t sel_key(float v, int e)
+{
+    uint32_t u = __float_as_uint(v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)u << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)e);
+}
+
+__device__ __forceinline__ float key_value(uint64_t k)
+{
+    uint32_t u = (uint32_t)(k >> 32);
+    u = (u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u;
+    return __uint_as_float(u);
+}
+
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t k)
+{
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)k, off, 64);
+        const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(k >> 32), off, 64);
+        const uint64_t o = ((uint64_t)hi << 32) | lo;
+        k = o > k ? o : k;
+    }
+    return k;
+}
+
+__device__ __forceinline__ float wave_sum(float v)
+{
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Renormalised mode (model.c:301-317): exchange selection on the logits,
+// softmax over the k selected with the first as max.  Literal mode
+// (model.c:1027-1049): softmax over all E, exchange selection on the
+// probabilities, weights = those probabilities.
+//
+// Fast path: the top k+1 logits are finite and pairwise distinct, so
+// exchange selection yields them in value order; in the literal mode they
+// must also be more than 1e-5 apart, so that their probabilities (relative
+// gaps >= 1e-5, far above the few ulps expf and the division can move them)
+// keep that order and cannot round to equal values.  Otherwise lane 0
+// runs the reference's selection literally on this device's values.
+__global__ void __launch_bounds__(256)
+    k_select(const float *__restrict__ logits, int T, int E, int k, int mode,
+             uint32_t *__restrict__ idx_out, float *__restrict__ w_out, int *n_slow)
+{
+    __shared__ float sv[4][256];
+    __shared__ int si[4][256];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t = blockIdx.x * 4 + wave;
+    if (t >= T) return;  // a wave is a token: no block-wide barrier below
+    const float *lg = logits + (size_t)t * E;
+    uint32_t *io = idx_out + (size_t)t * k;
+    float *wo = w_out + (size_t)t * k;
+
+    float v[4];
+    uint64_t key[4];
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = lane + 64 * i;
+        const bool valid = e < E;
+        v[i] = valid ? lg[e] : 0.0f;
+        if (valid && !isfinite(v[i])) bad = true;
+        key[i] = valid ? sel_key(v[i], e) : 0ull;  // 0: below every valid key
+    }
+    bool slow = __ballot(bad) != 0ull;
+
+    // Lane r < k ends up holding the r-th selected (value, index).
+    float my_v = 0.0f, mx = 0.0f;
+    int my_e = 0;
+    if (!slow) {
+        float prev = 0.0f;
+        const int rounds = k < E ? k + 1 : k;
+        for (int r = 0; r < rounds; ++r) {
+            uint64_t best = key[0];
+#pragma unroll
+            for (int i = 1; i < 4; ++i) best = key[i] > best ? key[i] : best;
+            const uint64_t wb = wave_max_key(best);
+            const float val = key_value(wb);
+            const int e = (int)(0xFFFFFFFFu - (uint32_t)wb);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (key[i] == wb) key[i] = 0ull;
+            if (r == 0) mx = val;
+            if (r > 0) {
+                if (!(prev > val)) slow = true;
+                if (mode == 1 && !((double)prev - (double)val > 1e-5)) slow = true;
             }
-            exact_select<NW>(sel_val, E, k, vals_s, idx_s, sv, si, sel_i, sel_v, &flag_s);
-            if (mode == 1) {
-                // Selection ran on the probabilities, which are the weights.
-                if (threadIdx.x < k) {
-                    idx_out[(size_t)t * k + threadIdx.x] = (uint32_t)sel_i[threadIdx.x];
-                    w_out[(size_t)t * k + threadIdx.x] = sel_v[threadIdx.x];
-                }
-                return;
-            }
+            if (lane == r) { my_v = val; my_e = e; }
+            prev = val;
         }
     }
 
-    // Weights.  Renormalised mode: softmax over the k selected logits
-    // (model.c:307-317).  Literal mode: full softmax probabilities.
-    if (mode == 0) {
-        if (threadIdx.x == 0) renorm_weights(sel_v, k, w_s);
-        __syncthreads();
-    } else {
-        const float mx = sel_v[0];
-        float ex = valid ? expf((float)wv - mx) : 0.0f;
-        float sum = block_sum_f(ex, red);
-        if (valid) vals_s[e] = ex / sum;
-        __syncthreads();
-        if (threadIdx.x < k) w_s[threadIdx.x] = vals_s[sel_i[threadIdx.x]];
-        __syncthreads();
+    if (!slow) {
+        float w;
+        if (mode == 0) {
+            // model.c:307-317: s_i = expf(v_i - v_0), sequential sum, divide.
+            const float s_i = expf(my_v - mx);
+            float sum = 0.0f;
+            for (int i = 0; i < k; ++i) sum += __shfl(s_i, i, 64);
+            w = s_i / sum;
+        } else {
+            float s = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (lane + 64 * i < E) s += expf(v[i] - mx);
+            w = expf(my_v - mx) / wave_sum(s);
+        }
+        if (lane < k) { io[lane] = (uint32_t)my_e; wo[lane] = w; }
+        return;
     }
-    if (threadIdx.x < k) {
-        idx_out[(size_t)t * k + threadIdx.x] = (uint32_t)sel_i[threadIdx.x];
-        w_out[(size_t)t * k + threadIdx.x] = w_s[threadIdx.x];
+
+    // Literal path: the reference's selection, run by lane 0 on this
+    // device's values.
+    if (lane == 0 && n_slow) atomicAdd(n_slow, 1);
+    float *val = sv[wave];
+    int *ix = si[wave];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = lane + 64 * i;
+        if (e < E) { val[e] = v[i]; ix[e] = e; }
+    }
+    wave_sync();
+    if (lane == 0) {
+        if (mode == 1) {
+            // model.c:1027-1036: max by strict '>', expf, sequential sum, divide.
+            float m = val[0];
+            for (int e = 1; e < E; ++e) if (val[e] > m) m = val[e];
+            float sum = 0.0f;
+            for (int e = 0; e < E; ++e) { val[e] = expf(val[e] - m); sum += val[e]; }
+            for (int e = 0; e < E; ++e) val[e] = val[e] / sum;
+        }
+        // k passes of exchange selection (model.c:301-305 / 1040-1048).
+        for (int i = 0; i < k && i < E - 1; ++i)
+            for (int j = i + 1; j < E; ++j)
+                if (val[j] > val[i]) {
+                    const float ft = val[i]; val[i] = val[j]; val[j] = ft;
+                    const int it = ix[i]; ix[i] = ix[j]; ix[j] = it;
+                }
+        if (mode == 0) {
+            const float m = val[0];
+            float sum = 0.0f;
+            for (int i = 0; i < k; ++i) sum += expf(val[i] - m);
+            for (int i = 0; i < k; ++i) { io[i] = (uint32_t)ix[i]; wo[i] = expf(val[i] - m) / sum; }
+        } else {
+            for (int i = 0; i < k; ++i) { io[i] = (uint32_t)ix[i]; wo[i] = val[i]; }
+        }
     }
 }
 
@@ -557,38 +550,27 @@ extern "C" int ornk_topk(const float *logits, int T, int E, int k, int mode, uin
 }
 
 // ---------------------------------------------------------------------------
-// MoE routing step: certified logits + top-k into a->idx / a->w.
+// MoE routing step: exact logits into a->logits, then top-k into a->idx/a->w.
 // ---------------------------------------------------------------------------
 extern "C" int ornk_moe_route(const ornk_moe_args *a, hipStream_t s)
 {
     const int T = a->T, D = a->D, E = a->E;
     if (T <= 0) return hipSuccess;
-    if (E > ORN_TOPK_THREADS || a->k > 16 || D % 64 != 0 || D % ORN_RCHUNK != 0)
+    if (E < 1 || E > 256 || a->k < 1 || a->k > 16 || a->k > E || D % (4 * ORN_DPF) ||
+        D % ORN_RDC || D > 4096)
         return hipErrorInvalidValue;
-    const int n_chunks = D / ORN_RCHUNK;
-    int cpb = (T <= 32 || n_chunks % 4 != 0) ? 1 : 4;
-    const int n_groups = n_chunks / cpb;
-    double2 *part = reinterpret_cast<double2 *>(a->rpart);
     const float *xin = a->apply_norm ? a->xn : a->x;
-    if (T <= 2) {
-        hipLaunchKernelGGL(k_router_part<1>, dim3((E + 63) / 64, n_groups, T), dim3(64 * cpb), 0, s,
-                           xin, a->router, T, D, E, cpb, part, a->ctl);
-    } else if (T <= 16) {
-        hipLaunchKernelGGL(k_router_part<2>, dim3((E + 63) / 64, n_groups, (T + 1) / 2),
-                           dim3(64 * cpb), 0, s, xin, a->router, T, D, E, cpb, part, a->ctl);
+    if (T >= 1024) {
+        hipLaunchKernelGGL(k_router_seq<4>, dim3((E + 63) / 64, (T + 15) / 16), dim3(256), 0, s,
+                           xin, a->router, a->bias, T, D, E, a->logits, a->ctl);
     } else {
-        hipLaunchKernelGGL(k_router_part<4>, dim3((E + 63) / 64, n_groups, (T + 3) / 4),
-                           dim3(64 * cpb), 0, s, xin, a->router, T, D, E, cpb, part, a->ctl);
+        hipLaunchKernelGGL(k_router_dec, dim3((E + 63) / 64, (T + 3) / 4), dim3(256),
+                           sizeof(float) * 4 * (size_t)D, s, xin, a->router, a->bias, T, D, E,
+                           a->logits, a->ctl);
     }
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
-    // Dynamic LDS: x plus cb weight rows for the exact fallback, within 56 KB.
-    int cb = (56 * 1024) / (4 * D) - 1;
-    if (cb > 8) cb = 8;
-    if (cb < 1) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_topk_cert, dim3(T), dim3(ORN_TOPK_THREADS),
-                       sizeof(float) * (size_t)D * (size_t)(cb + 1), s, part, n_groups,
-                       cpb * ORN_RCHUNK, xin, a->router, a->bias, D, E, a->k, a->mode, a->idx, a->w,
-                       a->ctl + 3, cb);
+    hipLaunchKernelGGL(k_select, dim3((T + 3) / 4), dim3(256), 0, s, a->logits, T, E, a->k,
+                       a->mode, a->idx, a->w, a->ctl + 3);
     return hipGetLastError();
 }

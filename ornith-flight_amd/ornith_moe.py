@@ -300,7 +300,7 @@ class Store:
     def last_stats(self):
         a, b, c = C.c_int(), C.c_int(), C.c_int()
         self.ctx.check(lib().gpu_moe_last_stats(self.ctx.ptr, C.byref(a), C.byref(b), C.byref(c)), "stats")
-        return {"n_slots": a.value, "n_rows": b.value, "n_exact": c.value}
+        return {"n_slots": a.value, "n_rows": b.value, "n_literal": c.value}
 
     def bytes(self):
         return lib().gpu_moe_store_bytes(self.ptr)
