@@ -90,6 +90,8 @@ typedef struct {
     int n_experts;  /* E = 256 (<= 256) */
     int top_k;      /* k = 8 (<= 16) */
     int has_shared; /* 1: one always-on shared expert (model.c:1001-1007) */
+    int prefill_layout; /* 1: also keep the MFMA (prefill) layouts of every expert,
+                           about 1.2x the quantized bytes more; 0: decode layout only */
 } ornith_moe_shape;
 
 enum { ORN_MAT_GATE = 0, ORN_MAT_UP = 1, ORN_MAT_DOWN = 2 };
@@ -125,6 +127,13 @@ int gpu_moe_store_fill_synthetic(gpu_context *ctx, ornith_moe_store *store, int 
 enum { ORN_ROUTE_RENORM = 0, ORN_ROUTE_LITERAL = 1 };
 #define ORN_MOE_ASYNC 1u /* return without synchronising the stream */
 #define ORN_MOE_NORM 2u  /* expert input = rmsnorm(x, layer norm weights) */
+/* Expert-product kernels.  Default: the MFMA grouped GEMM (prefill layout,
+ * fp16 hi+lo activations, fp32 accumulate) when the batch has at least
+ * ORN_MOE_MFMA_MIN_TOKENS tokens and the store keeps the prefill layouts,
+ * else the VALU matvec kernels (fp32 throughout). */
+#define ORN_MOE_PATH_VALU 4u /* force the VALU kernels */
+#define ORN_MOE_PATH_MFMA 8u /* force the MFMA kernels (EUNSUPPORTED if unavailable) */
+#define ORN_MOE_MFMA_MIN_TOKENS 128
 
 typedef struct {
     int route_mode; /* ORN_ROUTE_RENORM (default, model_get_routing) or ORN_ROUTE_LITERAL */

@@ -23,8 +23,33 @@ struct ornith_moe_store {
     float *bias;              /* [L][E] */
     int *has_bias;            /* host [L] */
     float *norm;              /* [L][D] */
+    /* Prefill (MFMA) layouts, present when sh.prefill_layout is set (built
+     * by prefill_pack.c; per layer and expert slot):
+     *   pq[m]  gate/up nibbles [D/32][H/256][16][64] u32     (D*H/2 bytes)
+     *   psc[m] sub-block scales [D/32][H/256][8][32] fp16      (D*H/16)
+     *   pmn[m] sub-block mins, same shape                       (D*H/16)
+     *   pd[m], pdm[m]  d and dmin [H/256][D] fp32               (D*H/64 each)
+     *   dq     down q + 32 [H/32][D/256][16][64][8] u8           (D*H)
+     *   dsc    down sub-block scales [H/32][D/256][16][32] fp16   (D*H/8)
+     *   dd     down d [D/256][H] fp32                             (D*H/64)
+     *   dmax   [3]: max |d|,|dmin| of gate and of up, max |d| of down */
+    uint32_t *pq[2];
+    uint16_t *psc[2], *pmn[2];
+    float *pd[2], *pdm[2];
+    uint8_t *dq;
+    uint16_t *dsc;
+    float *dd;
+    float *dmax;
+    float *dmax_host;         /* host mirror of dmax, [L][E+1][3] */
+    int *q6_scmax;            /* host [L]: largest |Q6_K sub-scale| uploaded */
     size_t bytes;
 };
+
+/* prefill_pack.c */
+void orn_pack_q4k_prefill(const uint8_t *blocks, int K, int M, uint32_t *qn, uint16_t *sc,
+                          uint16_t *mn, float *d, float *dm, float *dmax);
+int orn_pack_q6k_prefill(const uint8_t *blocks, int K, int M, uint8_t *qb, uint16_t *sc, float *d,
+                         float *dmax);
 
 /* ---------------------------------------------------------------------------
  * Workspace (grow-only device scratch owned by the context)
@@ -168,7 +193,8 @@ static int shape_ok(const ornith_moe_shape *s)
     return s && s->n_layers > 0 && s->d_model > 0 && s->d_model % 256 == 0 && s->hidden > 0 &&
            s->hidden % 256 == 0 && s->hidden <= 1024 && s->n_experts > 0 &&
            s->n_experts <= 256 && s->top_k > 0 && s->top_k <= 16 && s->top_k <= s->n_experts &&
-           (s->has_shared == 0 || s->has_shared == 1) && s->d_model % 128 == 0;
+           (s->has_shared == 0 || s->has_shared == 1) && s->d_model % 128 == 0 &&
+           (s->prefill_layout == 0 || s->prefill_layout == 1);
 }
 
 static void store_free(ornith_moe_store *st)
@@ -181,6 +207,19 @@ static void store_free(ornith_moe_store *st)
     hipFree(st->router_q);
     hipFree(st->bias);
     hipFree(st->norm);
+    for (int m = 0; m < 2; ++m) {
+        hipFree(st->pq[m]);
+        hipFree(st->psc[m]);
+        hipFree(st->pmn[m]);
+        hipFree(st->pd[m]);
+        hipFree(st->pdm[m]);
+    }
+    hipFree(st->dq);
+    hipFree(st->dsc);
+    hipFree(st->dd);
+    hipFree(st->dmax);
+    free(st->dmax_host);
+    free(st->q6_scmax);
     free(st->has_bias);
     free(st);
 }
@@ -212,6 +251,32 @@ ornith_moe_store *gpu_moe_store_create(gpu_context *ctx, const ornith_moe_shape 
             return NULL;
         }
         st->bytes += sizes[i];
+    }
+    if (shape->prefill_layout) {
+        const size_t LE = L * E1, DH = D * H;
+        size_t psz[14] = {LE * DH / 2, LE * DH / 2, LE * DH / 16, LE * DH / 16, LE * DH / 16,
+                          LE * DH / 16, LE * DH / 64, LE * DH / 64, LE * DH / 64, LE * DH / 64,
+                          LE * DH, LE * DH / 8, LE * DH / 64, LE * 3 * sizeof(float)};
+        void **pp[14] = {(void **)&st->pq[0], (void **)&st->pq[1], (void **)&st->psc[0],
+                         (void **)&st->psc[1], (void **)&st->pmn[0], (void **)&st->pmn[1],
+                         (void **)&st->pd[0], (void **)&st->pd[1], (void **)&st->pdm[0],
+                         (void **)&st->pdm[1], (void **)&st->dq, (void **)&st->dsc,
+                         (void **)&st->dd, (void **)&st->dmax};
+        for (int i = 0; i < 14; ++i) {
+            if (hipMalloc(pp[i], psz[i]) != hipSuccess ||
+                hipMemsetAsync(*pp[i], 0, psz[i], ctx->stream) != hipSuccess) {
+                orn_set_err(ctx, ORN_ENOMEM, "store allocation of %zu bytes failed", psz[i]);
+                store_free(st);
+                return NULL;
+            }
+            st->bytes += psz[i];
+        }
+        st->dmax_host = (float *)calloc(LE * 3, sizeof(float));
+        st->q6_scmax = (int *)calloc(L, sizeof(int));
+        if (!st->dmax_host || !st->q6_scmax) {
+            store_free(st);
+            return NULL;
+        }
     }
     st->has_bias = (int *)calloc(L, sizeof(int));
     float *ones = (float *)malloc(D * sizeof(float));
@@ -257,6 +322,98 @@ static void permute_q6k(const uint8_t *src, uint8_t *body, uint16_t *dv, int K, 
         }
 }
 
+/* Pack and upload the prefill layouts of n experts (one matrix). */
+static int upload_q4k_prefill(gpu_context *ctx, ornith_moe_store *st, int layer, int matrix,
+                              int first, int n, const void *blocks)
+{
+    const size_t D = (size_t)st->sh.d_model, H = (size_t)st->sh.hidden, DH = D * H;
+    const size_t E1 = (size_t)st->sh.n_experts + 1, nb = st->blocks_per_matrix;
+    const int m = matrix == ORN_MAT_GATE ? 0 : 1;
+    uint32_t *qn = (uint32_t *)malloc(DH / 2);
+    uint16_t *sc = (uint16_t *)malloc(DH / 16), *mn = (uint16_t *)malloc(DH / 16);
+    float *d = (float *)malloc(DH / 64), *dm = (float *)malloc(DH / 64);
+    int rc = ORN_OK;
+    if (!qn || !sc || !mn || !d || !dm) rc = orn_set_err(ctx, ORN_ENOMEM, "host staging");
+    hipStream_t s = ctx->stream;
+    for (int i = 0; i < n && !rc; ++i) {
+        const size_t slot = (size_t)layer * E1 + (size_t)(first + i);
+        float dmax;
+        orn_pack_q4k_prefill((const uint8_t *)blocks + (size_t)i * nb * ORN_Q4K_BYTES, (int)D,
+                             (int)H, qn, sc, mn, d, dm, &dmax);
+        st->dmax_host[slot * 3 + m] = dmax;
+        rc = orn_hip_check(ctx, hipMemcpyAsync((uint8_t *)st->pq[m] + slot * (DH / 2), qn, DH / 2,
+                                               hipMemcpyHostToDevice, s), "upload prefill q4k");
+        if (!rc)
+            rc = orn_hip_check(ctx, hipMemcpyAsync((uint8_t *)st->psc[m] + slot * (DH / 16), sc,
+                                                   DH / 16, hipMemcpyHostToDevice, s), "upload sc");
+        if (!rc)
+            rc = orn_hip_check(ctx, hipMemcpyAsync((uint8_t *)st->pmn[m] + slot * (DH / 16), mn,
+                                                   DH / 16, hipMemcpyHostToDevice, s), "upload mn");
+        if (!rc)
+            rc = orn_hip_check(ctx, hipMemcpyAsync((uint8_t *)st->pd[m] + slot * (DH / 64), d,
+                                                   DH / 64, hipMemcpyHostToDevice, s), "upload d");
+        if (!rc)
+            rc = orn_hip_check(ctx, hipMemcpyAsync((uint8_t *)st->pdm[m] + slot * (DH / 64), dm,
+                                                   DH / 64, hipMemcpyHostToDevice, s), "upload dm");
+        hipStreamSynchronize(s);
+    }
+    if (!rc) {
+        const size_t slot0 = (size_t)layer * E1 + (size_t)first;
+        rc = orn_hip_check(ctx, hipMemcpyAsync(st->dmax + slot0 * 3, st->dmax_host + slot0 * 3,
+                                               (size_t)n * 3 * sizeof(float),
+                                               hipMemcpyHostToDevice, s), "upload dmax");
+        hipStreamSynchronize(s);
+    }
+    free(qn);
+    free(sc);
+    free(mn);
+    free(d);
+    free(dm);
+    return rc;
+}
+
+static int upload_q6k_prefill(gpu_context *ctx, ornith_moe_store *st, int layer, int first, int n,
+                              const void *blocks)
+{
+    const size_t D = (size_t)st->sh.d_model, H = (size_t)st->sh.hidden, DH = D * H;
+    const size_t E1 = (size_t)st->sh.n_experts + 1, nb = st->blocks_per_matrix;
+    uint8_t *qb = (uint8_t *)malloc(DH);
+    uint16_t *sc = (uint16_t *)malloc(DH / 8);
+    float *d = (float *)malloc(DH / 64);
+    int rc = ORN_OK;
+    if (!qb || !sc || !d) rc = orn_set_err(ctx, ORN_ENOMEM, "host staging");
+    hipStream_t s = ctx->stream;
+    for (int i = 0; i < n && !rc; ++i) {
+        const size_t slot = (size_t)layer * E1 + (size_t)(first + i);
+        float dmax;
+        const int scmax = orn_pack_q6k_prefill((const uint8_t *)blocks +
+                                                   (size_t)i * nb * ORN_Q6K_BYTES,
+                                               (int)H, (int)D, qb, sc, d, &dmax);
+        if (scmax > st->q6_scmax[layer]) st->q6_scmax[layer] = scmax;
+        st->dmax_host[slot * 3 + 2] = dmax;
+        rc = orn_hip_check(ctx, hipMemcpyAsync(st->dq + slot * DH, qb, DH, hipMemcpyHostToDevice,
+                                               s), "upload prefill q6k");
+        if (!rc)
+            rc = orn_hip_check(ctx, hipMemcpyAsync((uint8_t *)st->dsc + slot * (DH / 8), sc, DH / 8,
+                                                   hipMemcpyHostToDevice, s), "upload q6k sc");
+        if (!rc)
+            rc = orn_hip_check(ctx, hipMemcpyAsync((uint8_t *)st->dd + slot * (DH / 64), d, DH / 64,
+                                                   hipMemcpyHostToDevice, s), "upload q6k d");
+        hipStreamSynchronize(s);
+    }
+    if (!rc) {
+        const size_t slot0 = (size_t)layer * E1 + (size_t)first;
+        rc = orn_hip_check(ctx, hipMemcpyAsync(st->dmax + slot0 * 3, st->dmax_host + slot0 * 3,
+                                               (size_t)n * 3 * sizeof(float),
+                                               hipMemcpyHostToDevice, s), "upload dmax");
+        hipStreamSynchronize(s);
+    }
+    free(qb);
+    free(sc);
+    free(d);
+    return rc;
+}
+
 int gpu_moe_store_set_experts(gpu_context *ctx, ornith_moe_store *st, int layer, int matrix,
                               int expert_first, int n, const void *blocks)
 {
@@ -282,6 +439,8 @@ int gpu_moe_store_set_experts(gpu_context *ctx, ornith_moe_store *st, int layer,
                                                hipMemcpyHostToDevice, s), "upload q4k");
         hipStreamSynchronize(s);
         free(tmp);
+        if (!rc && st->sh.prefill_layout) rc = upload_q4k_prefill(ctx, st, layer, matrix,
+                                                                  expert_first, n, blocks);
     } else {
         uint8_t *body = (uint8_t *)malloc((size_t)n * nb * 208);
         uint16_t *dv = (uint16_t *)malloc((size_t)n * nb * 2);
@@ -302,6 +461,8 @@ int gpu_moe_store_set_experts(gpu_context *ctx, ornith_moe_store *st, int layer,
         hipStreamSynchronize(s);
         free(body);
         free(dv);
+        if (!rc && st->sh.prefill_layout)
+            rc = upload_q6k_prefill(ctx, st, layer, expert_first, n, blocks);
     }
     return rc;
 }
@@ -405,12 +566,12 @@ static int pow2_floor(int v)
  * into ks slices so the grid holds ~2048 blocks (8 per CU).  Slices keep at
  * least 32 rows (gate/up) and 32 rows (down) so the split-K partials stay a
  * small fraction of the weight bytes. */
-static plan_t make_plan(const ornith_moe_shape *sh, int T)
+static plan_t make_plan(const ornith_moe_shape *sh, int T, int use_mfma)
 {
     plan_t p;
     const int k = sh->top_k, E = sh->n_experts;
     const int D = sh->d_model, H = sh->hidden;
-    p.tchunk = T <= 64 ? 2 : 8;
+    p.tchunk = use_mfma ? 64 : (T <= 64 ? 2 : 8);
     p.rows_max = T * k + (sh->has_shared ? T : 0);
     const int max_slots = (T * k < E ? T * k : E) + (sh->has_shared ? 1 : 0);
     p.items_max = max_slots + (p.rows_max + p.tchunk - 1) / p.tchunk;
@@ -431,6 +592,7 @@ static plan_t make_plan(const ornith_moe_shape *sh, int T)
     if (kd > 16) kd = 16;
     while (kd > 1 && (H % kd || (H / kd) % (16 * rw_dn) || H / kd < 32)) kd /= 2;
     p.ks_dn = kd;
+    if (use_mfma) p.ks_gu = p.ks_dn = 1;  /* the MFMA kernels reduce the full K */
     return p;
 }
 
@@ -458,7 +620,20 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     const int mode = opts ? opts->route_mode : ORN_ROUTE_RENORM;
     if (mode != ORN_ROUTE_RENORM && mode != ORN_ROUTE_LITERAL)
         return orn_set_err(ctx, ORN_EINVAL, "bad route mode");
-    plan_t p = make_plan(sh, T);
+    if ((flags & ORN_MOE_PATH_VALU) && (flags & ORN_MOE_PATH_MFMA))
+        return orn_set_err(ctx, ORN_EINVAL, "both expert paths forced");
+    /* The MFMA path needs the prefill layouts and Q6_K sub-scales with
+     * |sc| <= 64 (so that sc * q is exact in fp16). */
+    const int mfma_ok = sh->prefill_layout && st->q6_scmax[layer] <= 64;
+    int use_mfma = mfma_ok && T >= ORN_MOE_MFMA_MIN_TOKENS;
+    if (flags & ORN_MOE_PATH_VALU) use_mfma = 0;
+    if (flags & ORN_MOE_PATH_MFMA) {
+        if (!mfma_ok)
+            return orn_set_err(ctx, ORN_EUNSUPPORTED,
+                               "MFMA path needs the prefill layout and |Q6_K scale| <= 64");
+        use_mfma = 1;
+    }
+    plan_t p = make_plan(sh, T, use_mfma);
 
     size_t off = 0;
 #define CARVE(name, bytes)       \
@@ -478,6 +653,8 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     CARVE(o_gu, (size_t)p.ks_gu * p.rows_max * 2 * H * 4);
     CARVE(o_mid, (size_t)p.rows_max * H * 4);
     CARVE(o_dn, (size_t)p.ks_dn * p.rows_max * D * 4);
+    CARVE(o_xamax, use_mfma ? (size_t)T * 4 : 0);
+    CARVE(o_midamax, use_mfma ? (size_t)p.rows_max * 4 : 0);
 #undef CARVE
     uint8_t *ws = (uint8_t *)orn_ws_get(ctx, off);
     if (!ws) return ORN_ENOMEM;
@@ -522,14 +699,40 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     a.gu_part = (float *)(ws + o_gu);
     a.mid = (float *)(ws + o_mid);
     a.dn_part = (float *)(ws + o_dn);
+    a.use_mfma = use_mfma;
+    if (use_mfma) {
+        const size_t slot0 = (size_t)layer * E1, DH = (size_t)D * H;
+        for (int m = 0; m < 2; ++m) {
+            a.gu_pf.pq[m] = (const uint32_t *)((const uint8_t *)st->pq[m] + slot0 * (DH / 2));
+            a.gu_pf.psc[m] = (const uint16_t *)((const uint8_t *)st->psc[m] + slot0 * (DH / 16));
+            a.gu_pf.pmn[m] = (const uint16_t *)((const uint8_t *)st->pmn[m] + slot0 * (DH / 16));
+            a.gu_pf.pd[m] = (const float *)((const uint8_t *)st->pd[m] + slot0 * (DH / 64));
+            a.gu_pf.pdm[m] = (const float *)((const uint8_t *)st->pdm[m] + slot0 * (DH / 64));
+        }
+        a.gu_pf.dmax = st->dmax + slot0 * 3;
+        a.dn_pf.dq = st->dq + slot0 * DH;
+        a.dn_pf.dsc = (const uint16_t *)((const uint8_t *)st->dsc + slot0 * (DH / 8));
+        a.dn_pf.dd = (const float *)((const uint8_t *)st->dd + slot0 * (DH / 64));
+        a.dn_pf.dmax = st->dmax + slot0 * 3;
+        a.x_amax = (float *)(ws + o_xamax);
+        a.mid_amax = (float *)(ws + o_midamax);
+    }
 
     int rc;
     if ((rc = launch(ctx, "moe_norm", ornk_moe_norm, &a))) return rc;
     if ((rc = launch(ctx, "moe_route", ornk_moe_route, &a))) return rc;
     if ((rc = launch(ctx, "moe_dispatch", ornk_moe_dispatch, &a))) return rc;
-    if ((rc = launch(ctx, "moe_gateup", ornk_moe_gateup, &a))) return rc;
+    if (use_mfma) {
+        if ((rc = launch(ctx, "moe_gateup_mfma", ornk_moe_gateup_mfma, &a))) return rc;
+    } else {
+        if ((rc = launch(ctx, "moe_gateup", ornk_moe_gateup, &a))) return rc;
+    }
     if ((rc = launch(ctx, "moe_mid", ornk_moe_mid, &a))) return rc;
-    if ((rc = launch(ctx, "moe_down", ornk_moe_down, &a))) return rc;
+    if (use_mfma) {
+        if ((rc = launch(ctx, "moe_down_mfma", ornk_moe_down_mfma, &a))) return rc;
+    } else {
+        if ((rc = launch(ctx, "moe_down", ornk_moe_down, &a))) return rc;
+    }
     if ((rc = launch(ctx, "moe_combine", ornk_moe_combine, &a))) return rc;
 
     hipStream_t s = ctx->stream;

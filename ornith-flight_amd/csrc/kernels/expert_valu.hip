@@ -281,10 +281,13 @@ __global__ void __launch_bounds__(256)
 // (clamped silu, model.c:340-344).
 // ---------------------------------------------------------------------------
 __global__ void k_mid(const float *__restrict__ gu_part, const int *__restrict__ ctl,
-                      float *__restrict__ mid, int H, int ks, int rows_max, int shared_rows)
+                      float *__restrict__ mid, int H, int ks, int rows_max, int shared_rows,
+                      float *__restrict__ row_amax)
 {
+    __shared__ float red[4];
     const int r = blockIdx.x;
     if (r >= ctl[2]) return;
+    float amax = 0.0f;
     const int H2 = 2 * H;
     const size_t kstride = (size_t)rows_max * H2;
     for (int h = threadIdx.x; h < H; h += blockDim.x) {
@@ -311,7 +314,17 @@ __global__ void k_mid(const float *__restrict__ gu_part, const int *__restrict__
             else if (g > 50.0f) act = g;
             else act = g / (1.0f + expf(-g));
         }
-        mid[(size_t)r * H + h] = act * u;
+        const float v = act * u;
+        mid[(size_t)r * H + h] = v;
+        amax = fmaxf(amax, fabsf(v));
+    }
+    if (row_amax) {  // max |mid| of the row, for the MFMA down step's scaling
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+        __syncthreads();
+        if (threadIdx.x == 0)
+            row_amax[r] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     }
 }
 
@@ -552,7 +565,8 @@ extern "C" int ornk_moe_gateup(const ornk_moe_args *a, hipStream_t s)
 extern "C" int ornk_moe_mid(const ornk_moe_args *a, hipStream_t s)
 {
     hipLaunchKernelGGL(k_mid, dim3(a->rows_max), dim3(256), 0, s, a->gu_part, a->ctl, a->mid, a->H,
-                       a->ks_gu, a->rows_max, a->has_shared ? a->T : 0);
+                       a->ks_gu, a->rows_max, a->has_shared ? a->T : 0,
+                       a->use_mfma ? a->mid_amax : nullptr);
     return hipGetLastError();
 }
 

@@ -52,7 +52,23 @@ int ornk_topk(const float *logits, int T, int E, int k, int mode, uint32_t *idx,
  *   down_body : [E+1][D/256][H] Q6_K bodies of 208 B (ql|qh|scales)
  *   down_d    : [E+1][D/256][H] Q6_K super-scales (fp16 bits)
  *   router    : [D/4][E][4] fp32, W(d, e) at ((d/4)*E + e)*4 + d%4
- * Work buffers are owned by the host; sizes are computed by ornk_moe_ws_size. */
+ * Work buffers are owned by the host.
+ *
+ * Prefill (MFMA) layouts of one layer, per expert slot (prefill_pack.c): */
+typedef struct {
+    const uint32_t *pq[2];         /* gate, up nibbles [D/32][H/256][16][64] */
+    const uint16_t *psc[2], *pmn[2]; /* [D/32][H/256][8][32] fp16 scales, mins */
+    const float *pd[2], *pdm[2];   /* [H/256][D] d, dmin */
+    const float *dmax;             /* [E+1][3] */
+} ornk_gu_prefill;
+
+typedef struct {
+    const uint8_t *dq;   /* [H/32][D/256][16][64][8] q + 32 */
+    const uint16_t *dsc; /* [H/32][D/256][16][32] fp16 sub-block scales */
+    const float *dd;     /* [D/256][H] d */
+    const float *dmax;   /* [E+1][3] */
+} ornk_dn_prefill;
+
 typedef struct {
     int T, D, H, E, k, has_shared, mode, apply_norm;
     int ks_gu, ks_dn, rows_max, items_max, tchunk;
@@ -77,6 +93,12 @@ typedef struct {
     float *gu_part;   /* [ks_gu][rows_max][2H] */
     float *mid;       /* [rows_max][H] */
     float *dn_part;   /* [ks_dn][rows_max][D] */
+    /* MFMA path (ks_gu = ks_dn = 1, tchunk <= 64) */
+    int use_mfma;
+    ornk_gu_prefill gu_pf;
+    ornk_dn_prefill dn_pf;
+    float *x_amax;    /* [T] max |xin| per token */
+    float *mid_amax;  /* [rows_max] max |mid| per row (written by the mid step) */
 } ornk_moe_args;
 
 int ornk_moe_norm(const ornk_moe_args *a, hipStream_t s);
@@ -85,6 +107,8 @@ int ornk_moe_dispatch(const ornk_moe_args *a, hipStream_t s);
 int ornk_moe_gateup(const ornk_moe_args *a, hipStream_t s);
 int ornk_moe_mid(const ornk_moe_args *a, hipStream_t s);
 int ornk_moe_down(const ornk_moe_args *a, hipStream_t s);
+int ornk_moe_gateup_mfma(const ornk_moe_args *a, hipStream_t s);
+int ornk_moe_down_mfma(const ornk_moe_args *a, hipStream_t s);
 int ornk_moe_combine(const ornk_moe_args *a, hipStream_t s);
 
 #ifdef __cplusplus

@@ -20,6 +20,7 @@ TYPE_F32, TYPE_F16, TYPE_Q4_K, TYPE_Q6_K = 0, 1, 12, 14
 MAT_GATE, MAT_UP, MAT_DOWN = 0, 1, 2
 ROUTE_RENORM, ROUTE_LITERAL = 0, 1
 MOE_ASYNC, MOE_NORM = 1, 2
+MOE_PATH_VALU, MOE_PATH_MFMA = 4, 8
 SYN_GATE, SYN_UP, SYN_DOWN, SYN_ROUTER, SYN_ACT, SYN_ZIPF = 1, 2, 3, 4, 5, 6
 GPU_BUF_DEFAULT, GPU_BUF_SHARED, GPU_BUF_CONSTANT = 0, 1, 2
 Q4K_BYTES, Q6K_BYTES = 144, 210
@@ -54,7 +55,7 @@ class TensorInfo(C.Structure):
 
 class MoEShape(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("n_layers", "d_model", "hidden", "n_experts", "top_k",
-                                       "has_shared")]
+                                       "has_shared", "prefill_layout")]
 
 
 class MoEOpts(C.Structure):
@@ -249,9 +250,10 @@ class Context:
 
 
 class Store:
-    def __init__(self, ctx: Context, n_layers, D, H, E, k, has_shared=True):
+    def __init__(self, ctx: Context, n_layers, D, H, E, k, has_shared=True, prefill_layout=True):
         self.ctx = ctx
-        self.shape = MoEShape(n_layers, D, H, E, k, 1 if has_shared else 0)
+        self.shape = MoEShape(n_layers, D, H, E, k, 1 if has_shared else 0,
+                              1 if prefill_layout else 0)
         self.ptr = lib().gpu_moe_store_create(ctx.ptr, C.byref(self.shape))
         if not self.ptr:
             raise RuntimeError("gpu_moe_store_create failed: " + ctx.last_error())

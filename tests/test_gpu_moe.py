@@ -52,9 +52,10 @@ def row_err(out, ref):
 class Layer:
     """One synthetic layer resident on the GPU plus its host copy."""
 
-    def __init__(self, om, ctx, D, H, E, k, seed, zipf_s=0.0, has_shared=True, n_layers=1):
+    def __init__(self, om, ctx, D, H, E, k, seed, zipf_s=0.0, has_shared=True, n_layers=1,
+                 prefill_layout=True):
         self.D, self.H, self.E, self.k = D, H, E, k
-        self.store = om.Store(ctx, n_layers, D, H, E, k, has_shared)
+        self.store = om.Store(ctx, n_layers, D, H, E, k, has_shared, prefill_layout)
         self.syn = []
         for l in range(n_layers):
             s = om.SyntheticLayer(seed, l, D, H, E, has_shared, zipf_s)
@@ -119,6 +120,70 @@ def test_small_layer_parity(om, ctx, small, T, mode):
     err = row_err(out, ref)
     say("  max row err", err.max())
     assert err.max() <= TOL
+
+
+@pytest.mark.parametrize("T", [1, 5, 37, 150])
+@pytest.mark.parametrize("mode", [O.MODE_RENORM, O.MODE_LITERAL])
+def test_small_layer_mfma_parity(om, ctx, small, T, mode):
+    """The MFMA grouped-GEMM path (fp16 hi+lo activations, exact sc*q
+    weights, fp32 accumulate) forced at every batch size."""
+    say(f"small layer MFMA T={T} mode={mode}")
+    x = act(om, 300 + T, T, small.D)
+    out, idx, w = run(ctx, small, x, mode=mode, flags=om.MOE_PATH_MFMA)
+    ref, ridx, rw = small.oracle(x, mode=mode)
+    assert np.array_equal(idx, ridx)
+    err = row_err(out, ref)
+    say("  max row err", err.max())
+    assert err.max() <= TOL
+
+
+def test_mfma_residual_norm_and_row_independence(om, ctx, small):
+    T = 70
+    x = act(om, 17, T, small.D)
+    out, idx, _ = run(ctx, small, x, resid=x, flags=om.MOE_NORM | om.MOE_PATH_MFMA)
+    ref, ridx, _ = small.oracle(x, resid=x, norm_w=np.ones(small.D, np.float32))
+    assert np.array_equal(idx, ridx)
+    assert row_err(out, ref).max() <= TOL
+    a, _, _ = run(ctx, small, x, flags=om.MOE_PATH_MFMA)
+    b, _, _ = run(ctx, small, x, flags=om.MOE_PATH_MFMA)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    perm = np.random.default_rng(2).permutation(T)
+    c, _, _ = run(ctx, small, x[perm], flags=om.MOE_PATH_MFMA)
+    assert row_err(c, a[perm].astype(np.float64)).max() <= 1e-6
+
+
+def test_mfma_needs_prefill_layout(om, ctx):
+    """Without the prefill layouts a large batch takes the VALU path, and
+    forcing the MFMA path is refused."""
+    L = Layer(om, ctx, 256, 256, 16, 8, seed=21, prefill_layout=False)
+    x = act(om, 22, 150, 256)
+    out, idx, _ = run(ctx, L, x)
+    ref, ridx, _ = L.oracle(x)
+    assert np.array_equal(idx, ridx)
+    assert row_err(out, ref).max() <= TOL
+    with pytest.raises(RuntimeError):
+        run(ctx, L, x[:4], flags=om.MOE_PATH_MFMA)
+    L.store.close()
+
+
+def test_q6_scale_above_64_uses_valu(om, ctx):
+    """A Q6_K sub-scale with |sc| > 64 makes sc*q inexact in fp16: the layer
+    then routes every batch to the VALU kernels (and refuses a forced MFMA)."""
+    D, H, E, k = 256, 256, 16, 8
+    L = Layer(om, ctx, D, H, E, k, seed=23)
+    s = L.syn[0]
+    down = s.down.reshape(-1, 210).copy()
+    down[5, 192 + 3] = np.uint8(90)
+    s.down = down.reshape(-1)
+    L.store.set_experts(0, om.MAT_DOWN, 0, s.routed("down"), E)
+    x = act(om, 24, 150, D)
+    out, idx, _ = run(ctx, L, x)
+    ref, ridx, _ = L.oracle(x)
+    assert np.array_equal(idx, ridx)
+    assert row_err(out, ref).max() <= TOL
+    with pytest.raises(RuntimeError):
+        run(ctx, L, x[:4], flags=om.MOE_PATH_MFMA)
+    L.store.close()
 
 
 def test_small_layer_residual_and_norm(om, ctx, small):
@@ -192,6 +257,25 @@ def test_ornith_decode_parity(om, ctx, ornith, T):
     err = row_err(out, ref)
     say("  max row err", err.max(), "stats", ornith.store.last_stats())
     assert err.max() <= TOL
+
+
+def test_ornith_mfma_decode_and_valu_prefill(om, ctx, ornith):
+    """Each expert path outside its default range: MFMA at T=16, VALU at
+    T=256 (tokens subset checked against the oracle)."""
+    x = act(om, 2100, 16, 2048)
+    out, idx, _ = run(ctx, ornith, x, flags=om.MOE_PATH_MFMA)
+    ref, ridx, _ = ornith.oracle(x)
+    assert np.array_equal(idx, ridx)
+    err = row_err(out, ref)
+    say("  MFMA T=16 max row err", err.max())
+    assert err.max() <= TOL
+    x = act(om, 2101, 256, 2048)
+    out, idx, _ = run(ctx, ornith, x, flags=om.MOE_PATH_VALU)
+    ridx, _ = ornith.oracle_routing(x)
+    assert np.array_equal(idx, ridx)
+    sub = np.arange(0, 256, 32)
+    ref, _, _ = ornith.oracle(x[sub])
+    assert row_err(out[sub], ref).max() <= TOL
 
 
 def test_ornith_literal_mode(om, ctx, ornith):

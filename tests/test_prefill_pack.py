@@ -1,0 +1,116 @@
+"""CPU checks of the prefill (MFMA) layouts built by prefill_pack.c.
+
+Every weight W[k][n] of an expert matrix is rebuilt from the packed arrays
+exactly as the MFMA kernels use them (d * (sc*q) - dmin * m for Q4_K,
+d * (sc*q) for Q6_K, with q taken from the lane-ordered words) and compared
+bit for bit with the oracle's dequantization of the original GGUF blocks
+(gguf.c:43-86).  The packers are internal symbols of libornith_hip (not part
+of the C API); no GPU is needed.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+Q4, Q6 = 12, 14  # ggml type ids
+
+
+@pytest.fixture(scope="module")
+def L():
+    import ornith_moe
+    lib = ornith_moe.lib()
+    f = lib.orn_pack_q4k_prefill
+    f.restype = None
+    f.argtypes = [C.c_void_p, C.c_int, C.c_int] + [C.c_void_p] * 6
+    g = lib.orn_pack_q6k_prefill
+    g.restype = C.c_int
+    g.argtypes = [C.c_void_p, C.c_int, C.c_int] + [C.c_void_p] * 4
+    return lib
+
+
+def _p(a):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def f16(u16):
+    return u16.view(np.float16).astype(np.float64)
+
+
+def test_q4k_prefill_layout_rebuilds_weights(L):
+    import ornith_moe as om
+    K, M = 64, 512
+    nb = K * M // 256
+    blocks = om.synth_q4k(5, om.synth_stream(0, om.SYN_GATE, 3), nb)
+    # exercise the fp16 quirk and zero scales too
+    blocks = blocks.reshape(nb, 144).copy()
+    blocks[0, 0:2] = [0x00, 0x00]          # d = 0
+    blocks[1, 2:4] = [0x01, 0x00]          # dmin: a subnormal pattern (quirk: 2^-15*(1+1/1024))
+    blocks[2, 4:16] = 0                    # all sub-block scales and mins 0
+    blocks = blocks.reshape(-1)
+    KT, NB = K // 32, M // 256
+    qn = np.zeros(KT * NB * 16 * 64, np.uint32)
+    sc = np.zeros(KT * NB * 8 * 32, np.uint16)
+    mn = np.zeros_like(sc)
+    d = np.zeros(NB * K, np.float32)
+    dm = np.zeros_like(d)
+    dmax = np.zeros(1, np.float32)
+    L.orn_pack_q4k_prefill(_p(blocks), K, M, _p(qn), _p(sc), _p(mn), _p(d), _p(dm), _p(dmax))
+
+    ok, ref = O.dequant_tensor(blocks, Q4, K * M)
+    assert ok
+    ref = ref.reshape(K, M)
+    W = np.zeros((K, M), np.float64)
+    qn4 = qn.reshape(KT, NB, 16, 64)
+    sc4 = f16(sc).reshape(KT, NB, 8, 32)
+    mn4 = f16(mn).reshape(KT, NB, 8, 32)
+    d2, dm2 = d.reshape(NB, K).astype(np.float64), dm.reshape(NB, K).astype(np.float64)
+    for k in range(K):
+        kt, kk = divmod(k, 32)
+        g, e = divmod(kk, 8)
+        shift = 4 * (e // 2) + 16 * (e % 2)
+        for n in range(M):
+            b, p = divmod(n, 256)
+            nt, c = divmod(p, 16)
+            q = (int(qn4[kt, b, nt, 16 * g + c]) >> shift) & 15
+            s = p // 32
+            W[k, n] = d2[b, k] * (sc4[kt, b, s, kk] * q) - dm2[b, k] * mn4[kt, b, s, kk]
+    assert np.array_equal(W.astype(np.float32).view(np.uint32), ref.view(np.uint32))
+    assert dmax[0] == max(np.abs(d).max(), np.abs(dm).max())
+    # the B operand values sc*q are integers <= 945 (exact in fp16)
+    assert sc4.max() <= 63 and mn4.max() <= 63
+
+
+def test_q6k_prefill_layout_rebuilds_weights(L):
+    import ornith_moe as om
+    K, M = 64, 512
+    nb = K * M // 256
+    blocks = om.synth_q6k(6, om.synth_stream(0, om.SYN_DOWN, 2), nb).reshape(nb, 210).copy()
+    blocks[3, 192 + 5] = np.uint8(100)       # one sub-scale above 64 -> reported
+    blocks[4, 208:210] = [0x00, 0x00]        # d = 0
+    blocks = blocks.reshape(-1)
+    KT, NB = K // 32, M // 256
+    qb = np.zeros(KT * NB * 16 * 64 * 8, np.uint8)
+    sc = np.zeros(KT * NB * 16 * 32, np.uint16)
+    d = np.zeros(NB * K, np.float32)
+    dmax = np.zeros(1, np.float32)
+    scmax = L.orn_pack_q6k_prefill(_p(blocks), K, M, _p(qb), _p(sc), _p(d), _p(dmax))
+    assert scmax == 100
+
+    ok, ref = O.dequant_tensor(blocks, Q6, K * M)
+    assert ok
+    ref = ref.reshape(K, M)
+    qb5 = qb.reshape(KT, NB, 16, 64, 8)
+    sc4 = f16(sc).reshape(KT, NB, 16, 32)
+    d2 = d.reshape(NB, K).astype(np.float64)
+    W = np.zeros((K, M), np.float64)
+    for k in range(K):
+        kt, kk = divmod(k, 32)
+        g, e = divmod(kk, 8)
+        for n in range(M):
+            b, p = divmod(n, 256)
+            nt, c = divmod(p, 16)
+            q = int(qb5[kt, b, nt, 16 * g + c, e]) - 32
+            W[k, n] = d2[b, k] * (sc4[kt, b, nt, kk] * q)
+    assert np.array_equal(W.astype(np.float32).view(np.uint32), ref.view(np.uint32))
