@@ -133,7 +133,7 @@ enum { ORN_ROUTE_RENORM = 0, ORN_ROUTE_LITERAL = 1 };
  * else the VALU matvec kernels (fp32 throughout). */
 #define ORN_MOE_PATH_VALU 4u /* force the VALU kernels */
 #define ORN_MOE_PATH_MFMA 8u /* force the MFMA kernels (EUNSUPPORTED if unavailable) */
-#define ORN_MOE_MFMA_MIN_TOKENS 128
+#define ORN_MOE_MFMA_MIN_TOKENS 64
 
 typedef struct {
     int route_mode; /* ORN_ROUTE_RENORM (default, model_get_routing) or ORN_ROUTE_LITERAL */

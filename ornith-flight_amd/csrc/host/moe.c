@@ -578,7 +578,7 @@ static plan_t make_plan(const ornith_moe_shape *sh, int T, int use_mfma)
     int est_items = max_slots + p.rows_max / p.tchunk;
     if (est_items < 1) est_items = 1;
     /* gate/up: K = D rows; a wave covers RW rows per step, a block 4*RW */
-    const int rw_gu = 64 / (16 * (H / 256));
+    const int rw_gu = 64 / (8 * (H / 256));
     int ks = pow2_floor(2048 / est_items);
     if (ks < 1) ks = 1;
     if (ks > 64) ks = 64;

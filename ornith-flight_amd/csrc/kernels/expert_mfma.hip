@@ -16,13 +16,13 @@
 // per tile give fp32-class products; the sums accumulate in fp32 and the
 // result is scaled back by 1/s_r (exact).
 //
-// Work group: 4 waves, 64 token rows x 256 outputs (one block column of one
-// matrix), reduction in steps of 32.  Per step every thread prepares 8
-// activation values of one row into LDS (double buffered); every wave builds
-// the B operands of its 4 output tiles (64 columns) in registers from the
-// prefill layout (prefill_pack.c) and runs 4 row tiles x 4 column tiles x
-// (hi, lo) MFMAs, plus (Q4_K) one 16-column tile holding the 8 sub-block mins
-// for the dmin term of its own row tile.
+// Work group: 4 waves, up to 64 token rows x 256 outputs (one block column of
+// one matrix), reduction in steps of 32.  Per step every thread prepares 8
+// activation values of one row into LDS (double buffered); wave w builds the
+// B operands of output tiles 4w..4w+3 in registers from the prefill layout
+// (prefill_pack.c) and runs (live row tiles) x 4 x (hi, lo) MFMAs, plus
+// (Q4_K) one 16-column tile holding the 8 sub-block mins for the dmin term of
+// row tile w.  Each converted B operand feeds up to 8 MFMAs.
 #include "common.h"
 #include "launch.h"
 
@@ -31,7 +31,7 @@ namespace {
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
-#define ORN_MT 64   // token rows per work group
+#define ORN_MT 64   // token rows per work group (4 row tiles)
 #define ORN_AST 40  // LDS row stride of an activation tile, in halves (32 + 8 padding)
 
 // Power of two s with amax*dmax*s in [2^13, 2^14); 1 when that product is 0,
@@ -48,13 +48,26 @@ __device__ __forceinline__ float row_scale(float amax, float dmax)
 __device__ __forceinline__ v2h as_v2h(uint32_t u) { return __builtin_bit_cast(v2h, u); }
 __device__ __forceinline__ uint32_t as_u32(v2h v) { return __builtin_bit_cast(uint32_t, v); }
 
-// (a0, a1) -> hi = rtz fp16, lo = rtz fp16 of the exact remainder.
+// (a0, a1) -> hi = rtz fp16, lo = rtz fp16 of the exact remainder a - hi
+// (formed as fma(hi, -1, a), one mixed-precision fma per value).
 __device__ __forceinline__ void split2(float a0, float a1, uint32_t &hi, uint32_t &lo)
 {
     const v2h h = __builtin_bit_cast(v2h, __builtin_amdgcn_cvt_pkrtz(a0, a1));
-    const float r0 = a0 - (float)h[0], r1 = a1 - (float)h[1];
+    const float r0 = __builtin_fmaf((float)h[0], -1.0f, a0);
+    const float r1 = __builtin_fmaf((float)h[1], -1.0f, a1);
     hi = as_u32(h);
     lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(r0, r1));
+}
+
+// Work-group id i < n -> logical tile index, a bijection on [0, n) such that
+// each XCD (work groups are dealt to the 8 XCDs round-robin) runs one
+// contiguous range of tiles: the tiles of one item, and the items of one
+// expert, then share an L2.  n is the number of live tiles, so every XCD
+// gets an equal share of them.
+__device__ __forceinline__ int xcd_remap(int i, int n)
+{
+    const int q = n >> 3, r = n & 7, x = i & 7, pos = i >> 3;
+    return x < r ? x * (q + 1) + pos : r * (q + 1) + (x - r) * q + pos;
 }
 
 __device__ __forceinline__ v8h to_v8h(uint32_t a, uint32_t b, uint32_t c, uint32_t d)
@@ -66,13 +79,20 @@ __device__ __forceinline__ v8h to_v8h(uint32_t a, uint32_t b, uint32_t c, uint32
 // Q4_K B operand: word w holds q for k = 0..7 at bits 4*(e/2) + 16*(e%2);
 // sc = the 8 sub-block scales (fp16, k order).  B = sc * q, exactly:
 // fma(1024 + q, sc, -1024 sc).
+__device__ __forceinline__ uint32_t magic_pair(uint32_t w)
+{
+    uint32_t r;  // (w & 0x000F000F) | 0x64006400 in one instruction
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(0x000F000Fu), "v"(w), "v"(0x64006400u));
+    return r;
+}
+
 __device__ __forceinline__ v8h q4_b(uint32_t w, uint4 sc)
 {
     const uint32_t s[4] = {sc.x, sc.y, sc.z, sc.w};
     uint32_t o[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const v2h q = as_v2h(((w >> (4 * i)) & 0x000F000Fu) | 0x64006400u);
+        const v2h q = as_v2h(magic_pair(w >> (4 * i)));
         const v2h sv = as_v2h(s[i]);
         const v2h ns = sv * (v2h){(_Float16)-1024.0f, (_Float16)-1024.0f};
         o[i] = as_u32(__builtin_elementwise_fma(q, sv, ns));
@@ -104,18 +124,18 @@ __device__ __forceinline__ v4f mfma(v8h a, v8h b, v4f c)
 }
 
 // Activation tile rows: thread t prepares row t/4, reduction values
-// 8*(t%4) .. +7 of the current step, for one or two scale vectors.
+// 8*(t%4) .. +7 of the current step, for one or two scale vectors.  Rows
+// past the item's end read a valid row and are zeroed by a zero row scale.
 struct ARaw {
     v4f x0, x1, d0, d1, m0, m1;
 };
 
 template <bool MINS>
-__device__ __forceinline__ void a_load(ARaw &r, const float *xrow, bool live, const float *dv,
+__device__ __forceinline__ void a_load(ARaw &r, const float *xrow, const float *dv,
                                        const float *dmv, int k)
 {
-    const v4f z = {0.0f, 0.0f, 0.0f, 0.0f};
-    r.x0 = live ? *reinterpret_cast<const v4f *>(xrow + k) : z;
-    r.x1 = live ? *reinterpret_cast<const v4f *>(xrow + k + 4) : z;
+    r.x0 = *reinterpret_cast<const v4f *>(xrow + k);
+    r.x1 = *reinterpret_cast<const v4f *>(xrow + k + 4);
     r.d0 = *reinterpret_cast<const v4f *>(dv + k);
     r.d1 = *reinterpret_cast<const v4f *>(dv + k + 4);
     if (MINS) {
@@ -124,8 +144,7 @@ __device__ __forceinline__ void a_load(ARaw &r, const float *xrow, bool live, co
     }
 }
 
-// Writes hi/lo of x*s*d (and of x*s*dmin) as 16 bytes each at off in the
-// tiles base[0], base[1] (and base[2], base[3]).
+// Writes hi/lo of x*s*d (and of x*s*dmin) as 16 bytes each into t0, t1 (t2, t3).
 template <bool MINS>
 __device__ __forceinline__ void a_store(const ARaw &r, float s, _Float16 *t0, _Float16 *t1,
                                         _Float16 *t2, _Float16 *t3)
@@ -148,260 +167,295 @@ __device__ __forceinline__ void a_store(const ARaw &r, float s, _Float16 *t0, _F
     }
 }
 
+typedef _Float16 ATile[4][ORN_MT * ORN_AST];  // hi, lo, mins hi, mins lo of one step
+typedef _Float16 ATile2[2][ORN_MT * ORN_AST];  // hi, lo
+
+// Row tiles 0..NTT-1 x this wave's 4 column tiles: acc[tt][j] += A[tt] * B[j]
+// for the hi and lo halves of A.
+template <int NTT>
+__device__ __forceinline__ void mma_step(const _Float16 *Ahi, const _Float16 *Alo,
+                                         const v8h (&bq)[4], v4f (&acc)[NTT][4], int c, int g)
+{
+#pragma unroll
+    for (int tt = 0; tt < NTT; ++tt) {
+        const int ro = (16 * tt + c) * ORN_AST + 8 * g;
+        const v8h ahi = *reinterpret_cast<const v8h *>(Ahi + ro);
+        const v8h alo = *reinterpret_cast<const v8h *>(Alo + ro);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            acc[tt][j] = mfma(ahi, bq[j], acc[tt][j]);
+            acc[tt][j] = mfma(alo, bq[j], acc[tt][j]);
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
-// Gate/up.  blockIdx.x = (item * 2 + m) * (H/256) + b; output gu[row][m*H + n].
+// Gate/up.  Logical tile = (item * 2 + m) * (H/256) + b; output gu[row][m*H + n].
 // ---------------------------------------------------------------------------
+struct GuBlock {
+    const uint32_t *qn;
+    const uint16_t *sc, *mn;
+    const float *xrow, *dva, *dmva;
+    float ascale;
+    int aoff, NB, b, KT;
+};
+
+template <int NTT>
+__device__ __forceinline__ void gateup_tile(const GuBlock &B, ATile *As, float (*Mt)[8],
+                                            const float *s_inv, float *gu_row0, int H2, int col0,
+                                            int nrows)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const int NB = B.NB, b = B.b;
+    auto b_load = [&](int kt, uint32_t (&qw)[4], uint4 (&sw)[2], uint4 &mw) {
+        const size_t base = (size_t)kt * NB + b;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) qw[j] = B.qn[(base * 16 + 4 * wave + j) * 64 + lane];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            sw[h] = *reinterpret_cast<const uint4 *>(B.sc + (base * 8 + 2 * wave + h) * 32 + 8 * g);
+        const uint4 t = *reinterpret_cast<const uint4 *>(B.mn + (base * 8 + (c & 7)) * 32 + 8 * g);
+        mw = c < 8 ? t : make_uint4(0, 0, 0, 0);  // columns 8..15 of the mins tile are zero
+    };
+
+    v4f acc[NTT][4];
+#pragma unroll
+    for (int i = 0; i < NTT; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+    v4f accm = {0.0f, 0.0f, 0.0f, 0.0f};
+
+    ARaw ar;
+    uint32_t qw[4];
+    uint4 sw[2], mw;
+    v8h bq[4], bm;
+    a_load<true>(ar, B.xrow, B.dva, B.dmva, 0);
+    b_load(0, qw, sw, mw);
+    a_store<true>(ar, B.ascale, &As[0][0][B.aoff], &As[0][1][B.aoff], &As[0][2][B.aoff],
+                  &As[0][3][B.aoff]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bq[j] = q4_b(qw[j], sw[j >> 1]);
+    bm = __builtin_bit_cast(v8h, mw);
+    __syncthreads();
+
+    const int mro = (16 * wave + c) * ORN_AST + 8 * g;  // row tile `wave`, for the mins
+    for (int kt = 0; kt < B.KT - 1; ++kt) {
+        const ATile &A = As[kt & 1];
+        a_load<true>(ar, B.xrow, B.dva, B.dmva, 32 * (kt + 1));
+        b_load(kt + 1, qw, sw, mw);
+        mma_step<NTT>(A[0], A[1], bq, acc, c, g);
+        accm = mfma(*reinterpret_cast<const v8h *>(&A[2][mro]), bm, accm);
+        accm = mfma(*reinterpret_cast<const v8h *>(&A[3][mro]), bm, accm);
+        ATile &N = As[(kt + 1) & 1];
+        a_store<true>(ar, B.ascale, &N[0][B.aoff], &N[1][B.aoff], &N[2][B.aoff], &N[3][B.aoff]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bq[j] = q4_b(qw[j], sw[j >> 1]);
+        bm = __builtin_bit_cast(v8h, mw);
+        __syncthreads();
+    }
+    {
+        const ATile &A = As[(B.KT - 1) & 1];
+        mma_step<NTT>(A[0], A[1], bq, acc, c, g);
+        accm = mfma(*reinterpret_cast<const v8h *>(&A[2][mro]), bm, accm);
+        accm = mfma(*reinterpret_cast<const v8h *>(&A[3][mro]), bm, accm);
+    }
+
+    // dmin term of row tile `wave`: rows 16*wave + 4g + r, sub-block c.
+    if (c < 8) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) Mt[16 * wave + 4 * g + r][c] = accm[r];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int tt = 0; tt < NTT; ++tt) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int nt = 4 * wave + j, sb = nt >> 1;
+            const int col = col0 + 16 * nt + c;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = 16 * tt + 4 * g + r;
+                if (row < nrows)
+                    gu_row0[(size_t)row * H2 + col] = (acc[tt][j][r] - Mt[row][sb]) * s_inv[row];
+            }
+        }
+    }
+}
+
 __global__ void __launch_bounds__(256)
     k_gateup_mfma(ornk_gu_prefill P, const float *__restrict__ xn,
                   const float *__restrict__ x_amax, const int *__restrict__ ctl,
                   const int4 *__restrict__ items, const int *__restrict__ slot_expert,
                   const int *__restrict__ row_token, float *__restrict__ gu, int D, int H)
 {
-    __shared__ __align__(16) _Float16 As[2][4][ORN_MT * ORN_AST];
+    __shared__ __align__(16) ATile As[2];
     __shared__ float Mt[ORN_MT][8];
     __shared__ float s_scale[ORN_MT], s_inv[ORN_MT];
     __shared__ int s_tok[ORN_MT];
 
     const int NB = H >> 8;
-    const int b = blockIdx.x % NB;
-    const int m = (blockIdx.x / NB) & 1;
-    const int item = blockIdx.x / (2 * NB);
-    if (item >= ctl[1]) return;
+    const int n_live = ctl[1] * 2 * NB;  // tiles of the items dispatch produced
+    if ((int)blockIdx.x >= n_live) return;
+    const int tile = xcd_remap(blockIdx.x, n_live);
+    const int b = tile % NB;
+    const int m = (tile / NB) & 1;
+    const int item = tile / (2 * NB);
     const int4 itm = items[item];
-    const int e = slot_expert[itm.x];
-    const int nrows = itm.z;  // <= ORN_MT (plan)
+    const int e = itm.w;  // expert slot index (E = the shared expert)
+    const int nrows = itm.z;  // 1..ORN_MT (plan)
     const size_t DH = (size_t)D * H;
-    const uint32_t *qn = P.pq[m] + (size_t)e * (DH / 8);
-    const uint16_t *sc = P.psc[m] + (size_t)e * (DH / 32);
-    const uint16_t *mn = P.pmn[m] + (size_t)e * (DH / 32);
-    const float *dv = P.pd[m] + (size_t)e * (DH / 256) + (size_t)b * D;
-    const float *dmv = P.pdm[m] + (size_t)e * (DH / 256) + (size_t)b * D;
-    const float dmx = P.dmax[e * 3 + m];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int g = lane >> 4, c = lane & 15;
+    const int tid = threadIdx.x;
 
     if (tid < ORN_MT) {
-        const int tok = tid < nrows ? row_token[itm.y + tid] : -1;
-        const float s = tok >= 0 ? row_scale(x_amax[tok], dmx) : 1.0f;
+        const int tok = row_token[itm.y + (tid < nrows ? tid : 0)];
+        const float s = tid < nrows ? row_scale(x_amax[tok], P.dmax[e * 3 + m]) : 0.0f;
         s_tok[tid] = tok;
         s_scale[tid] = s;
-        s_inv[tid] = 1.0f / s;
+        s_inv[tid] = s != 0.0f ? 1.0f / s : 0.0f;
     }
     __syncthreads();
 
+    GuBlock B;
+    B.qn = P.pq[m] + (size_t)e * (DH / 8);
+    B.sc = P.psc[m] + (size_t)e * (DH / 32);
+    B.mn = P.pmn[m] + (size_t)e * (DH / 32);
     const int ar = tid >> 2, ao = tid & 3;
-    const int atok = s_tok[ar];
-    const float ascale = s_scale[ar];
-    const float *xrow = xn + (size_t)(atok < 0 ? 0 : atok) * D + 8 * ao;
-    const float *dva = dv + 8 * ao, *dmva = dmv + 8 * ao;
-    const int aoff = ar * ORN_AST + 8 * ao;
-    const int n_tt = (nrows + 15) >> 4;  // live row tiles
-
-    auto b_load = [&](int kt, uint32_t (&qw)[4], uint4 (&sw)[2], uint4 &mw) {
-        const size_t base = (size_t)kt * NB + b;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) qw[j] = qn[(base * 16 + 4 * wave + j) * 64 + lane];
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-            sw[h] = *reinterpret_cast<const uint4 *>(sc + (base * 8 + 2 * wave + h) * 32 + 8 * g);
-        mw = c < 8 ? *reinterpret_cast<const uint4 *>(mn + (base * 8 + c) * 32 + 8 * g)
-                   : make_uint4(0, 0, 0, 0);
-    };
-
-    v4f acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
-    v4f accm = {0.0f, 0.0f, 0.0f, 0.0f};
-
-    ARaw ar_raw;
-    uint32_t qw[4];
-    uint4 sw[2], mw;
-    v8h bq[4], bm;
-    a_load<true>(ar_raw, xrow, atok >= 0, dva, dmva, 0);
-    b_load(0, qw, sw, mw);
-    a_store<true>(ar_raw, ascale, &As[0][0][aoff], &As[0][1][aoff], &As[0][2][aoff],
-                  &As[0][3][aoff]);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) bq[j] = q4_b(qw[j], sw[j >> 1]);
-    bm = __builtin_bit_cast(v8h, mw);
-    __syncthreads();
-
-    const int KT = D / 32;
-    for (int kt = 0; kt < KT; ++kt) {
-        const int buf = kt & 1;
-        const bool more = kt + 1 < KT;
-        if (more) {
-            a_load<true>(ar_raw, xrow, atok >= 0, dva, dmva, 32 * (kt + 1));
-            b_load(kt + 1, qw, sw, mw);
-        }
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-            if (tt < n_tt) {
-                const int ro = (16 * tt + c) * ORN_AST + 8 * g;
-                const v8h ahi = *reinterpret_cast<const v8h *>(&As[buf][0][ro]);
-                const v8h alo = *reinterpret_cast<const v8h *>(&As[buf][1][ro]);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    acc[tt][j] = mfma(ahi, bq[j], acc[tt][j]);
-                    acc[tt][j] = mfma(alo, bq[j], acc[tt][j]);
-                }
-            }
-        }
-        if (wave < n_tt) {
-            const int ro = (16 * wave + c) * ORN_AST + 8 * g;
-            const v8h mhi = *reinterpret_cast<const v8h *>(&As[buf][2][ro]);
-            const v8h mlo = *reinterpret_cast<const v8h *>(&As[buf][3][ro]);
-            accm = mfma(mhi, bm, accm);
-            accm = mfma(mlo, bm, accm);
-        }
-        if (more) {
-            const int nb = buf ^ 1;
-            a_store<true>(ar_raw, ascale, &As[nb][0][aoff], &As[nb][1][aoff], &As[nb][2][aoff],
-                          &As[nb][3][aoff]);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) bq[j] = q4_b(qw[j], sw[j >> 1]);
-            bm = __builtin_bit_cast(v8h, mw);
-        }
-        __syncthreads();
+    B.xrow = xn + (size_t)s_tok[ar] * D + 8 * ao;
+    B.dva = P.pd[m] + (size_t)e * (DH / 256) + (size_t)b * D + 8 * ao;
+    B.dmva = P.pdm[m] + (size_t)e * (DH / 256) + (size_t)b * D + 8 * ao;
+    B.ascale = s_scale[ar];
+    B.aoff = ar * ORN_AST + 8 * ao;
+    B.NB = NB;
+    B.b = b;
+    B.KT = D / 32;
+    float *row0 = gu + (size_t)itm.y * (2 * H);
+    const int col0 = m * H + 256 * b;
+    switch ((nrows + 15) >> 4) {
+    case 1: gateup_tile<1>(B, As, Mt, s_inv, row0, 2 * H, col0, nrows); break;
+    case 2: gateup_tile<2>(B, As, Mt, s_inv, row0, 2 * H, col0, nrows); break;
+    case 3: gateup_tile<3>(B, As, Mt, s_inv, row0, 2 * H, col0, nrows); break;
+    default: gateup_tile<4>(B, As, Mt, s_inv, row0, 2 * H, col0, nrows); break;
     }
+}
 
-    // dmin term of this wave's row tile: rows 16*wave + 4g + r, sub-block c.
-    if (c < 8) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) Mt[16 * wave + 4 * g + r][c] = accm[r];
-    }
-    __syncthreads();
-    const int H2 = 2 * H;
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-        if (tt >= n_tt) continue;
+// ---------------------------------------------------------------------------
+// Down (Q6_K).  Logical tile = item * (D/256) + b; output dn[row][n].
+// ---------------------------------------------------------------------------
+struct DnBlock {
+    const uint2 *qb;
+    const uint16_t *sc;
+    const float *mrow, *dva;
+    float ascale;
+    int aoff, NBD, b, KT;
+};
+
+template <int NTT>
+__device__ __forceinline__ void down_tile(const DnBlock &B, ATile2 *As, const float *s_inv,
+                                          float *dn_row0, int D, int col0, int nrows)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const int NBD = B.NBD, b = B.b;
+    auto b_load = [&](int kt, uint2 (&qv)[4], uint4 (&sv)[4]) {
+        const size_t base = (size_t)kt * NBD + b;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int nt = 4 * wave + j, s = nt >> 1;
-            const int col = m * H + 256 * b + 16 * nt + c;
+            const size_t t = base * 16 + 4 * wave + j;
+            qv[j] = B.qb[t * 64 + lane];
+            sv[j] = *reinterpret_cast<const uint4 *>(B.sc + t * 32 + 8 * g);
+        }
+    };
+
+    v4f acc[NTT][4];
+#pragma unroll
+    for (int i = 0; i < NTT; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+
+    ARaw ar;
+    uint2 qv[4];
+    uint4 sv[4];
+    v8h bq[4];
+    a_load<false>(ar, B.mrow, B.dva, nullptr, 0);
+    b_load(0, qv, sv);
+    a_store<false>(ar, B.ascale, &As[0][0][B.aoff], &As[0][1][B.aoff], nullptr, nullptr);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bq[j] = q6_b(qv[j], sv[j]);
+    __syncthreads();
+
+    for (int kt = 0; kt < B.KT - 1; ++kt) {
+        a_load<false>(ar, B.mrow, B.dva, nullptr, 32 * (kt + 1));
+        b_load(kt + 1, qv, sv);
+        mma_step<NTT>(As[kt & 1][0], As[kt & 1][1], bq, acc, c, g);
+        ATile2 &N = As[(kt + 1) & 1];
+        a_store<false>(ar, B.ascale, &N[0][B.aoff], &N[1][B.aoff], nullptr, nullptr);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bq[j] = q6_b(qv[j], sv[j]);
+        __syncthreads();
+    }
+    mma_step<NTT>(As[(B.KT - 1) & 1][0], As[(B.KT - 1) & 1][1], bq, acc, c, g);
+
+#pragma unroll
+    for (int tt = 0; tt < NTT; ++tt) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int col = col0 + 16 * (4 * wave + j) + c;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row = 16 * tt + 4 * g + r;
-                if (row < nrows)
-                    gu[(size_t)(itm.y + row) * H2 + col] = (acc[tt][j][r] - Mt[row][s]) * s_inv[row];
+                if (row < nrows) dn_row0[(size_t)row * D + col] = acc[tt][j][r] * s_inv[row];
             }
         }
     }
 }
 
-// ---------------------------------------------------------------------------
-// Down (Q6_K).  blockIdx.x = item * (D/256) + b; output dn[row][n].
-// ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256)
     k_down_mfma(ornk_dn_prefill P, const float *__restrict__ mid,
                 const float *__restrict__ mid_amax, const int *__restrict__ ctl,
                 const int4 *__restrict__ items, const int *__restrict__ slot_expert,
                 float *__restrict__ dn, int D, int H)
 {
-    __shared__ __align__(16) _Float16 As[2][2][ORN_MT * ORN_AST];
+    __shared__ __align__(16) ATile2 As[2];
     __shared__ float s_scale[ORN_MT], s_inv[ORN_MT];
 
     const int NBD = D >> 8;
-    const int b = blockIdx.x % NBD;
-    const int item = blockIdx.x / NBD;
-    if (item >= ctl[1]) return;
+    const int n_live = ctl[1] * NBD;
+    if ((int)blockIdx.x >= n_live) return;
+    const int tile = xcd_remap(blockIdx.x, n_live);
+    const int b = tile % NBD;
+    const int item = tile / NBD;
     const int4 itm = items[item];
-    const int e = slot_expert[itm.x];
+    const int e = itm.w;  // expert slot index (E = the shared expert)
     const int nrows = itm.z;
     const size_t DH = (size_t)D * H;
-    const uint2 *qb = reinterpret_cast<const uint2 *>(P.dq + (size_t)e * DH);
-    const uint16_t *sc = P.dsc + (size_t)e * (DH / 16);
-    const float *dv = P.dd + (size_t)e * (DH / 256) + (size_t)b * H;
-    const float dmx = P.dmax[e * 3 + 2];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int g = lane >> 4, c = lane & 15;
+    const int tid = threadIdx.x;
 
     if (tid < ORN_MT) {
-        const float s = tid < nrows ? row_scale(mid_amax[itm.y + tid], dmx) : 1.0f;
+        const float s = tid < nrows ? row_scale(mid_amax[itm.y + tid], P.dmax[e * 3 + 2]) : 0.0f;
         s_scale[tid] = s;
-        s_inv[tid] = 1.0f / s;
+        s_inv[tid] = s != 0.0f ? 1.0f / s : 0.0f;
     }
     __syncthreads();
 
+    DnBlock B;
+    B.qb = reinterpret_cast<const uint2 *>(P.dq + (size_t)e * DH);
+    B.sc = P.dsc + (size_t)e * (DH / 16);
     const int ar = tid >> 2, ao = tid & 3;
-    const bool alive = ar < nrows;
-    const float ascale = s_scale[ar];
-    const float *mrow = mid + (size_t)(itm.y + (alive ? ar : 0)) * H + 8 * ao;
-    const float *dva = dv + 8 * ao;
-    const int aoff = ar * ORN_AST + 8 * ao;
-    const int n_tt = (nrows + 15) >> 4;
-
-    auto b_load = [&](int kt, uint2 (&qv)[4], uint4 (&sv)[4]) {
-        const size_t base = (size_t)kt * NBD + b;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const size_t t = base * 16 + 4 * wave + j;
-            qv[j] = qb[t * 64 + lane];
-            sv[j] = *reinterpret_cast<const uint4 *>(sc + t * 32 + 8 * g);
-        }
-    };
-
-    v4f acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
-
-    ARaw ar_raw;
-    uint2 qv[4];
-    uint4 sv[4];
-    v8h bq[4];
-    a_load<false>(ar_raw, mrow, alive, dva, nullptr, 0);
-    b_load(0, qv, sv);
-    a_store<false>(ar_raw, ascale, &As[0][0][aoff], &As[0][1][aoff], nullptr, nullptr);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) bq[j] = q6_b(qv[j], sv[j]);
-    __syncthreads();
-
-    const int KT = H / 32;
-    for (int kt = 0; kt < KT; ++kt) {
-        const int buf = kt & 1;
-        const bool more = kt + 1 < KT;
-        if (more) {
-            a_load<false>(ar_raw, mrow, alive, dva, nullptr, 32 * (kt + 1));
-            b_load(kt + 1, qv, sv);
-        }
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-            if (tt < n_tt) {
-                const int ro = (16 * tt + c) * ORN_AST + 8 * g;
-                const v8h ahi = *reinterpret_cast<const v8h *>(&As[buf][0][ro]);
-                const v8h alo = *reinterpret_cast<const v8h *>(&As[buf][1][ro]);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    acc[tt][j] = mfma(ahi, bq[j], acc[tt][j]);
-                    acc[tt][j] = mfma(alo, bq[j], acc[tt][j]);
-                }
-            }
-        }
-        if (more) {
-            const int nb = buf ^ 1;
-            a_store<false>(ar_raw, ascale, &As[nb][0][aoff], &As[nb][1][aoff], nullptr, nullptr);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) bq[j] = q6_b(qv[j], sv[j]);
-        }
-        __syncthreads();
-    }
-
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-        if (tt >= n_tt) continue;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int col = 256 * b + 16 * (4 * wave + j) + c;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = 16 * tt + 4 * g + r;
-                if (row < nrows) dn[(size_t)(itm.y + row) * D + col] = acc[tt][j][r] * s_inv[row];
-            }
-        }
+    B.mrow = mid + (size_t)(itm.y + (ar < nrows ? ar : 0)) * H + 8 * ao;
+    B.dva = P.dd + (size_t)e * (DH / 256) + (size_t)b * H + 8 * ao;
+    B.ascale = s_scale[ar];
+    B.aoff = ar * ORN_AST + 8 * ao;
+    B.NBD = NBD;
+    B.b = b;
+    B.KT = H / 32;
+    float *row0 = dn + (size_t)itm.y * D;
+    const int col0 = 256 * b;
+    switch ((nrows + 15) >> 4) {
+    case 1: down_tile<1>(B, As, s_inv, row0, D, col0, nrows); break;
+    case 2: down_tile<2>(B, As, s_inv, row0, D, col0, nrows); break;
+    case 3: down_tile<3>(B, As, s_inv, row0, D, col0, nrows); break;
+    default: down_tile<4>(B, As, s_inv, row0, D, col0, nrows); break;
     }
 }
 

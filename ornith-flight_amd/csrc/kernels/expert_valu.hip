@@ -80,7 +80,7 @@ __global__ void __launch_bounds__(1024)
         slot_cnt[slot] = c;
         for (int q = 0; q < nit && ioff + q < items_max; ++q) {
             const int r0 = q * tchunk;
-            items[ioff + q] = make_int4(slot, roff + r0, min(tchunk, c - r0), tid == 0);
+            items[ioff + q] = make_int4(slot, roff + r0, min(tchunk, c - r0), tid == 0 ? E : tid - 1);
         }
     }
     if (tid == 0) {
@@ -112,11 +112,12 @@ __global__ void __launch_bounds__(1024)
 // item's tokens are processed one at a time (weights re-read from L1/L2 for
 // the second token), which keeps the register budget near 100 VGPRs.
 //
-// Lane layout: ch = lane % CR picks (matrix m, block column bc, 16-byte qs
-// chunk j) with CR = 16*(H/256) chunks per input row, and rr = lane / CR one
-// of RW = 64/CR rows handled side by side.  Chunk j holds qs bytes
-// 16j..16j+15: low nibbles are outputs 64*(j/2) + 16*(j%2) + u of sub-block
-// 2*(j/2), high nibbles the same + 32 of sub-block 2*(j/2)+1 (gguf.c:43-61).
+// Lane layout: ch = lane % CR picks (matrix m, block column bc, 32-byte qs
+// chunk c) with CR = 8*(H/256) chunks per input row, and rr = lane / CR one
+// of RW = 64/CR rows handled side by side.  Chunk c holds qs bytes
+// 32c..32c+31: low nibbles are outputs 64c + l of sub-block 2c, high nibbles
+// 64c + 32 + l of sub-block 2c+1 (gguf.c:43-61), so the per-row scale work is
+// shared by 64 weights.
 // With D = d*sc and M = dmin*m a row contributes x_k*(D*q - M); the M part is
 // constant over a sub-block, so it is accumulated once per row and
 // subtracted at the end.
@@ -135,16 +136,19 @@ __device__ __forceinline__ void q4_nibbles(uint32_t w, float *lo, float *hi)
 }
 
 struct Q4Row {
-    uint4 hd, q;
+    uint4 hd, q0, q1;  // header (d, dmin, scales) and the lane's 32 qs bytes
 };
 
-__device__ __forceinline__ void load_q4(const uint8_t *blk, int j, Q4Row &r)
+__device__ __forceinline__ void load_q4(const uint8_t *blk, int c, Q4Row &r)
 {
     r.hd = *reinterpret_cast<const uint4 *>(blk);
-    r.q = *reinterpret_cast<const uint4 *>(blk + ORN_Q4K_OFF_QS + 16 * j);
+    r.q0 = *reinterpret_cast<const uint4 *>(blk + ORN_Q4K_OFF_QS + 32 * c);
+    r.q1 = *reinterpret_cast<const uint4 *>(blk + ORN_Q4K_OFF_QS + 32 * c + 16);
 }
 
-// One row of one lane chunk: 32 outputs (16 of sub-block 2c, 16 of 2c+1).
+// One row of one lane chunk c: qs bytes 32c..32c+31, i.e. the 64 outputs
+// 64c + l (low nibbles, sub-block 2c) and 64c + 32 + l (high nibbles,
+// sub-block 2c+1), l = 0..31 (gguf.c:43-61).
 __device__ __forceinline__ void q4_row(const Q4Row &r, int c, float xv, float *acc, float &macc0,
                                        float &macc1)
 {
@@ -157,15 +161,15 @@ __device__ __forceinline__ void q4_row(const Q4Row &r, int c, float xv, float *a
     const float a2 = xv * (d * (float)sc2);
     macc0 = fmaf(xv, dmin * (float)m1, macc0);
     macc1 = fmaf(xv, dmin * (float)m2, macc1);
-    const uint32_t qw[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+    const uint32_t qw[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
 #pragma unroll
-    for (int dw = 0; dw < 4; ++dw) {
+    for (int dw = 0; dw < 8; ++dw) {
         float lo[4], hi[4];
         q4_nibbles(qw[dw], lo, hi);
 #pragma unroll
         for (int bb = 0; bb < 4; ++bb) {
             acc[dw * 4 + bb] = fmaf(a1, lo[bb], acc[dw * 4 + bb]);
-            acc[16 + dw * 4 + bb] = fmaf(a2, hi[bb], acc[16 + dw * 4 + bb]);
+            acc[32 + dw * 4 + bb] = fmaf(a2, hi[bb], acc[32 + dw * 4 + bb]);
         }
     }
 }
@@ -182,17 +186,16 @@ __global__ void __launch_bounds__(256)
     const int item = blockIdx.x / ks, kslice = blockIdx.x - item * ks;
     if (item >= ctl[1]) return;
     const int4 itm = items[item];
-    const int e = slot_expert[itm.x];
+    const int e = itm.w;  // expert slot index (E = the shared expert)
     const int RK = D / ks;
     float *xs = smem;       // [RK]
     float *red = smem + RK; // [2H]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int NB = H >> 8;
-    const int CR = 16 * NB;
+    const int CR = 8 * NB;
     const int RW = RWT > 0 ? RWT : 64 / CR;  // RWT == 64 / CR when given (launcher)
     const int rr = lane / CR, ch = lane % CR;
-    const int j = ch & 7, bc = (ch >> 3) % NB, m = ch / (8 * NB);
-    const int c = j >> 1;
+    const int c = ch & 3, bc = (ch >> 2) % NB, m = ch / (4 * NB);
     const int k_start = kslice * RK;
     const int H2 = 2 * H;
     const uint8_t *base =
@@ -202,33 +205,35 @@ __global__ void __launch_bounds__(256)
     // whose loads are one base address plus immediate offsets.
     const int n_it = NIT > 0 ? NIT : RK / (4 * RW);
     const int last = n_it - 1;
-    const int col0 = m * H + bc * 256 + 64 * c + 16 * (j & 1);
+    const int col0 = m * H + bc * 256 + 64 * c;
     const int h0 = wave * RW + rr;      // this lane's first row; row i is h0 + 4*RW*i
     const size_t rstep = (size_t)4 * RW * ORN_Q4K_BYTES;
 
     for (int r = 0; r < itm.z; ++r) {
-        const int row = itm.y + r;
-        const float *xr = xn + (size_t)row_token[row] * D + k_start;
-        for (int i = tid; i < RK; i += blockDim.x) xs[i] = xr[i];
-        __syncthreads();
-
         // Opaque zero: keeps the ring's first loads inside this token's pass
         // instead of hoisted (and held in extra registers) across all passes.
         int z = 0;
         asm volatile("" : "+v"(z));
         const uint8_t *lb = base + (size_t)(h0 + z) * ORN_Q4K_BYTES;
         const float *xl = xs + h0;
-
-        float acc[32];
-#pragma unroll
-        for (int u = 0; u < 32; ++u) acc[u] = 0.0f;
-        float macc0 = 0.0f, macc1 = 0.0f;
+        // The weights do not depend on the token: start their loads before
+        // the activation slice is staged.
         Q4Row rs[ORN_NPF];
 #pragma unroll
         for (int p = 0; p < ORN_NPF; ++p) {
-            load_q4(lb + (size_t)min(p, last) * rstep, j, rs[p]);
+            load_q4(lb + (size_t)min(p, last) * rstep, c, rs[p]);
             __builtin_amdgcn_sched_barrier(0);  // issue order = consumption order
         }
+
+        const int row = itm.y + r;
+        const float *xr = xn + (size_t)row_token[row] * D + k_start;
+        for (int i = tid; i < RK; i += blockDim.x) xs[i] = xr[i];
+        __syncthreads();
+
+        float acc[64];
+#pragma unroll
+        for (int u = 0; u < 64; ++u) acc[u] = 0.0f;
+        float macc0 = 0.0f, macc1 = 0.0f;
 #pragma unroll
         for (int it = 0; it < n_it; it += ORN_NPF) {
             float xv[ORN_NPF];
@@ -239,32 +244,31 @@ __global__ void __launch_bounds__(256)
                 // Use the slot, then refill it in place (the pins keep the
                 // refill after the use), ORN_NPF rows ahead.
                 orn_pin_u4(rs[p].hd);
-                orn_pin_u4(rs[p].q);
+                orn_pin_u4(rs[p].q0);
+                orn_pin_u4(rs[p].q1);
                 q4_row(rs[p], c, xv[p], acc, macc0, macc1);
 #pragma unroll
-                for (int u = 0; u < 32; u += 8) orn_pin8(acc + u);
+                for (int u = 0; u < 64; u += 8) orn_pin8(acc + u);
                 orn_pin2(macc0, macc1);
-                load_q4(lb + (size_t)min(it + p + ORN_NPF, last) * rstep, j, rs[p]);
+                load_q4(lb + (size_t)min(it + p + ORN_NPF, last) * rstep, c, rs[p]);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
+        for (int u = 0; u < 32; ++u) {
             acc[u] -= macc0;
-            acc[16 + u] -= macc1;
+            acc[32 + u] -= macc1;
         }
         for (int off = CR; off < 64; off <<= 1) {
 #pragma unroll
-            for (int u = 0; u < 32; ++u) acc[u] += __shfl_xor(acc[u], off, 64);
+            for (int u = 0; u < 64; ++u) acc[u] += __shfl_xor(acc[u], off, 64);
         }
         for (int wv = 0; wv < 4; ++wv) {
             if (wave == wv && rr == 0) {
 #pragma unroll
-                for (int u = 0; u < 16; ++u) {
+                for (int u = 0; u < 64; ++u) {
                     float *p0 = red + col0 + u;
-                    float *p1 = p0 + 32;
                     *p0 = (wv == 0) ? acc[u] : *p0 + acc[u];
-                    *p1 = (wv == 0) ? acc[16 + u] : *p1 + acc[16 + u];
                 }
             }
             __syncthreads();
@@ -358,7 +362,7 @@ __global__ void __launch_bounds__(256)
     const int item = rest / ks, kslice = rest - item * ks;
     if (item >= ctl[1]) return;
     const int4 itm = items[item];
-    const int e = slot_expert[itm.x];
+    const int e = itm.w;  // expert slot index (E = the shared expert)
     const int RH = H / ks;
     const int NBD = D >> 8;
     const int CR = 8 * NBD;
@@ -384,27 +388,17 @@ __global__ void __launch_bounds__(256)
     const int hstep = 4 * RW;
 
     for (int r = 0; r < itm.z; ++r) {
-        const int row = itm.y + r;
-        const float *mr = mid + (size_t)row * H + h_start;
-        for (int i = tid; i < RH; i += blockDim.x) ms[i] = mr[i];
-        __syncthreads();
-
         // Opaque zero, as in k_gateup: the ring's first loads stay in this pass.
         int z = 0;
         asm volatile("" : "+v"(z));
         const uint8_t *lb = bbase + (size_t)(h0 + z) * 208;
         const uint16_t *ld = dbase + h0 + z;
         const float *ml = ms + h0;
-
-        float acc[32];
-#pragma unroll
-        for (int u = 0; u < 32; ++u) acc[u] = 0.0f;
-        float cs0 = 0.0f, cs1 = 0.0f;
         uint4 qlr[ORN_NPF], qhr[ORN_NPF];
         uint2 scr[ORN_NPF];
         uint32_t dr[ORN_NPF];
 #pragma unroll
-        for (int p = 0; p < ORN_NPF; ++p) {
+        for (int p = 0; p < ORN_NPF; ++p) {  // weight loads before the activation staging
             const int hi = min(p, last) * hstep;
             const uint8_t *b = lb + (size_t)hi * 208;
             qlr[p] = *reinterpret_cast<const uint4 *>(b + 64 * n + 32 * jj + l0);
@@ -413,6 +407,16 @@ __global__ void __launch_bounds__(256)
             dr[p] = ld[hi];
             __builtin_amdgcn_sched_barrier(0);  // issue order = consumption order
         }
+
+        const int row = itm.y + r;
+        const float *mr = mid + (size_t)row * H + h_start;
+        for (int i = tid; i < RH; i += blockDim.x) ms[i] = mr[i];
+        __syncthreads();
+
+        float acc[32];
+#pragma unroll
+        for (int u = 0; u < 32; ++u) acc[u] = 0.0f;
+        float cs0 = 0.0f, cs1 = 0.0f;
 #pragma unroll
         for (int it = 0; it < n_it; it += ORN_NPF) {
             float mv[ORN_NPF];
@@ -507,14 +511,52 @@ __global__ void k_combine(const float *__restrict__ dn_part, const int *__restri
     const int c = blockIdx.y * blockDim.x + threadIdx.x;
     if (t >= T || c >= D) return;
     const size_t kstride = (size_t)rows_max * D;
-    float acc = resid ? resid[(size_t)t * D + c] : 0.0f;
-    if (has_shared) acc = acc + sum_parts(dn_part + (size_t)t * D + c, kstride, ks);
-    float routed = 0.0f;
-    for (int a = 0; a < k; ++a) {
-        const int r = pair_row[t * k + a];
-        if (r < 0) continue;
-        routed += w[t * k + a] * sum_parts(dn_part + (size_t)r * D + c, kstride, ks);
+    // Row indices and weights first, then every partial of every row in
+    // flight at once (excluded pairs read row 0 and are dropped below).
+    int rr[16];
+    float ww[16], y[16];
+#pragma unroll
+    for (int a = 0; a < 16; ++a) {
+        const int r = a < k ? pair_row[t * k + a] : -1;
+        rr[a] = r;
+        ww[a] = a < k ? w[t * k + a] : 0.0f;
+        y[a] = 0.0f;
     }
+    int ro[16];
+#pragma unroll
+    for (int a = 0; a < 16; ++a) ro[a] = rr[a] < 0 ? 0 : rr[a];
+    float ysh = 0.0f;
+    int sidx = 0;
+    // Split-K partials in fixed order, four steps of loads in flight at once.
+    for (; sidx + 4 <= ks; sidx += 4) {
+        float vs[4], v[4][16];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float *base = dn_part + (sidx + u) * kstride + c;
+            vs[u] = has_shared ? base[(size_t)t * D] : 0.0f;
+#pragma unroll
+            for (int a = 0; a < 16; ++a) v[u][a] = a < k ? base[(size_t)ro[a] * D] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            ysh += vs[u];
+#pragma unroll
+            for (int a = 0; a < 16; ++a) y[a] += v[u][a];
+        }
+    }
+    for (; sidx < ks; ++sidx) {
+        const float *base = dn_part + sidx * kstride + c;
+        if (has_shared) ysh += base[(size_t)t * D];
+#pragma unroll
+        for (int a = 0; a < 16; ++a)
+            if (a < k) y[a] += base[(size_t)ro[a] * D];
+    }
+    float acc = resid ? resid[(size_t)t * D + c] : 0.0f;
+    if (has_shared) acc = acc + ysh;
+    float routed = 0.0f;
+#pragma unroll
+    for (int a = 0; a < 16; ++a)
+        if (a < k && rr[a] >= 0) routed += ww[a] * y[a];
     out[(size_t)t * D + c] = acc + routed;
 }
 
@@ -540,8 +582,8 @@ extern "C" int ornk_moe_dispatch(const ornk_moe_args *a, hipStream_t s)
 extern "C" int ornk_moe_gateup(const ornk_moe_args *a, hipStream_t s)
 {
     const int NB = a->H / 256;
-    if (a->H % 256 || NB < 1 || 16 * NB > 64) return hipErrorInvalidValue;
-    const int RW = 64 / (16 * NB);
+    if (a->H % 256 || NB < 1 || 8 * NB > 64) return hipErrorInvalidValue;
+    const int RW = 64 / (8 * NB);
     const int RK = a->D / a->ks_gu;
     if (a->D % a->ks_gu || RK % (4 * RW * ORN_NPF)) return hipErrorInvalidValue;
     const size_t shmem = sizeof(float) * (size_t)(RK + 2 * a->H);
@@ -552,11 +594,11 @@ extern "C" int ornk_moe_gateup(const ornk_moe_args *a, hipStream_t s)
                        a->up, a->xn, a->ctl, reinterpret_cast<const int4 *>(a->items),          \
                        a->slot_expert, a->row_token, a->gu_part, a->D, a->H, a->ks_gu,          \
                        a->rows_max)
-    // Straight-line instances for the Ornith shape (H = 512: RW = 2).
-    if (RW == 2 && n_it == 4) ORN_GU(4, 2);
-    else if (RW == 2 && n_it == 8) ORN_GU(8, 2);
-    else if (RW == 2 && n_it == 16) ORN_GU(16, 2);
-    else if (RW == 2 && n_it == 32) ORN_GU(32, 2);
+    // Straight-line instances for the Ornith shape (H = 512: RW = 4).
+    if (RW == 4 && n_it == 4) ORN_GU(4, 4);
+    else if (RW == 4 && n_it == 8) ORN_GU(8, 4);
+    else if (RW == 4 && n_it == 16) ORN_GU(16, 4);
+    else if (RW == 4 && n_it == 32) ORN_GU(32, 4);
     else ORN_GU(0, 0);
 #undef ORN_GU
     return hipGetLastError();

@@ -89,7 +89,7 @@ typedef struct {
     int *slot_cnt;    /* [E+1] */
     int *row_token;   /* [rows_max] */
     int *pair_row;    /* [T*k] */
-    int *items;       /* [items_max][4]: slot, row_begin, n_rows, pad */
+    int *items;       /* [items_max][4]: slot, row_begin, n_rows, expert (E = shared) */
     float *gu_part;   /* [ks_gu][rows_max][2H] */
     float *mid;       /* [rows_max][H] */
     float *dn_part;   /* [ks_dn][rows_max][D] */

@@ -253,13 +253,12 @@ __global__ void __launch_bounds__(256)
 }
 
 // ---------------------------------------------------------------------------
-// MoE router logits, few tokens (decode).  Block = 4 waves = 4 tokens over
-// the same 64 experts (their weight loads hit L1 after the first wave); lane
-// = expert.  A lane's weights for quad d4 are the 16 bytes at
-// Wq[d4][e][0..3], so one wave load instruction reads 1 KB contiguous.  The
-// loads run ORN_DPF quads ahead in a register ring (branch-free, fully
-// unrolled); the wave's activation row sits in LDS and is read as a
-// broadcast.  No block-wide barrier: every wave touches only its own LDS row.
+// MoE router logits, few tokens (decode).  Block = one wave = one token over
+// 64 experts (lane = expert), so the 2 MiB router streams through 4*T CUs.
+// A lane's weights for quad d4 are the 16 bytes at Wq[d4][e][0..3], so one
+// wave load instruction reads 1 KB contiguous.  The loads run ORN_DPF quads
+// ahead in a register ring (branch-free, fully unrolled); the token's
+// activation row sits in LDS and is read as a broadcast.
 // ---------------------------------------------------------------------------
 #define ORN_DPF 8  // weight quads in flight per lane
 
@@ -273,22 +272,30 @@ __device__ __forceinline__ void wave_sync()
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(64)
     k_router_dec(const float *__restrict__ x, const float *__restrict__ Wq,
                  const float *__restrict__ bias, int T, int D, int E,
                  float *__restrict__ logits, int *ctl)
 {
-    extern __shared__ v4f xsh[];  // [4][D/4]
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    extern __shared__ v4f xsh[];  // [D/4]
+    const int lane = threadIdx.x;
     const int e0 = blockIdx.x * 64;
-    const int t = blockIdx.y * 4 + wave;
+    const int t = blockIdx.y;
     // The routing step is the first of every forward: clear its counters.
-    if (ctl && blockIdx.x == 0 && blockIdx.y == 0 && tid < 16) ctl[tid] = 0;
-    if (t >= T) return;
+    if (ctl && blockIdx.x == 0 && blockIdx.y == 0 && lane < 16) ctl[lane] = 0;
     const int nd4 = D / 4;  // a multiple of ORN_DPF (checked by the launcher)
-    v4f *xw = xsh + (size_t)wave * nd4;
+    v4f *xw = xsh;
     const v4f *xg = reinterpret_cast<const v4f *>(x + (size_t)t * D);
-    for (int i = lane; i < nd4; i += 64) xw[i] = xg[i];
+    {
+        // All loads first, then the LDS writes (D <= 4096: at most 16 per lane).
+        v4f tmp[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            if (lane + 64 * j < nd4) tmp[j] = xg[lane + 64 * j];
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            if (lane + 64 * j < nd4) xw[lane + 64 * j] = tmp[j];
+    }
     wave_sync();
 
     const int e = min(e0 + lane, E - 1);  // lanes past E compute a copy, never stored
@@ -557,16 +564,15 @@ extern "C" int ornk_moe_route(const ornk_moe_args *a, hipStream_t s)
     const int T = a->T, D = a->D, E = a->E;
     if (T <= 0) return hipSuccess;
     if (E < 1 || E > 256 || a->k < 1 || a->k > 16 || a->k > E || D % (4 * ORN_DPF) ||
-        D % ORN_RDC || D > 4096)
+        D % (ORN_RDC * ORN_RPF) || D > 4096)
         return hipErrorInvalidValue;
     const float *xin = a->apply_norm ? a->xn : a->x;
     if (T >= 1024) {
         hipLaunchKernelGGL(k_router_seq<4>, dim3((E + 63) / 64, (T + 15) / 16), dim3(256), 0, s,
                            xin, a->router, a->bias, T, D, E, a->logits, a->ctl);
     } else {
-        hipLaunchKernelGGL(k_router_dec, dim3((E + 63) / 64, (T + 3) / 4), dim3(256),
-                           sizeof(float) * 4 * (size_t)D, s, xin, a->router, a->bias, T, D, E,
-                           a->logits, a->ctl);
+        hipLaunchKernelGGL(k_router_dec, dim3((E + 63) / 64, T), dim3(64), sizeof(float) * (size_t)D,
+                           s, xin, a->router, a->bias, T, D, E, a->logits, a->ctl);
     }
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
