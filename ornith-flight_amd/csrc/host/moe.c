@@ -571,7 +571,9 @@ static plan_t make_plan(const ornith_moe_shape *sh, int T, int use_mfma)
     plan_t p;
     const int k = sh->top_k, E = sh->n_experts;
     const int D = sh->d_model, H = sh->hidden;
-    p.tchunk = use_mfma ? 64 : (T <= 64 ? 2 : 8);
+    /* MFMA work items hold at most one 16-row tile at decode sizes (the
+     * kernel instance with a single row tile), four at prefill sizes. */
+    p.tchunk = use_mfma ? (T <= 64 ? 16 : 64) : (T <= 64 ? 2 : 8);
     p.rows_max = T * k + (sh->has_shared ? T : 0);
     const int max_slots = (T * k < E ? T * k : E) + (sh->has_shared ? 1 : 0);
     p.items_max = max_slots + (p.rows_max + p.tchunk - 1) / p.tchunk;
@@ -592,7 +594,19 @@ static plan_t make_plan(const ornith_moe_shape *sh, int T, int use_mfma)
     if (kd > 16) kd = 16;
     while (kd > 1 && (H % kd || (H / kd) % (16 * rw_dn) || H / kd < 32)) kd /= 2;
     p.ks_dn = kd;
-    if (use_mfma) p.ks_gu = p.ks_dn = 1;  /* the MFMA kernels reduce the full K */
+    if (use_mfma) {
+        /* split-K so that the grid holds ~2048 work groups: gate/up has
+         * 2*(H/256) tiles per item and slice, down D/256 */
+        int kg = pow2_floor(2048 / (est_items * 2 * (H / 256)) > 0
+                                ? 2048 / (est_items * 2 * (H / 256)) : 1);
+        while (kg > 1 && (D / 32) % kg) kg /= 2;
+        if (kg > D / 32) kg = D / 32;
+        int kdn = pow2_floor(2048 / (est_items * (D / 256)) > 0 ? 2048 / (est_items * (D / 256)) : 1);
+        while (kdn > 1 && (H / 32) % kdn) kdn /= 2;
+        if (kdn > H / 32) kdn = H / 32;
+        p.ks_gu = kg;
+        p.ks_dn = kdn;
+    }
     return p;
 }
 

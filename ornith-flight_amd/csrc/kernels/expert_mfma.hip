@@ -167,8 +167,12 @@ __device__ __forceinline__ void a_store(const ARaw &r, float s, _Float16 *t0, _F
     }
 }
 
-typedef _Float16 ATile[4][ORN_MT * ORN_AST];  // hi, lo, mins hi, mins lo of one step
-typedef _Float16 ATile2[2][ORN_MT * ORN_AST];  // hi, lo
+// LDS activation tiles of one reduction step: NARR arrays (hi, lo and, for
+// Q4_K, mins hi, mins lo) of ROWS x ORN_AST halves, two steps (double buffer).
+template <int ROWS, int NARR>
+struct ATiles {
+    _Float16 t[2][NARR][ROWS * ORN_AST];
+};
 
 // Row tiles 0..NTT-1 x this wave's 4 column tiles: acc[tt][j] += A[tt] * B[j]
 // for the hi and lo halves of A.
@@ -190,26 +194,29 @@ __device__ __forceinline__ void mma_step(const _Float16 *Ahi, const _Float16 *Al
 }
 
 // ---------------------------------------------------------------------------
-// Gate/up.  Logical tile = (item * 2 + m) * (H/256) + b; output gu[row][m*H + n].
+// Gate/up.  Logical tile = ((item * ks + kslice) * 2 + m) * (H/256) + b;
+// output gu[kslice][row][m*H + n] (split-K partial over the reduction steps
+// kslice*KT .. +KT-1).
 // ---------------------------------------------------------------------------
 struct GuBlock {
     const uint32_t *qn;
     const uint16_t *sc, *mn;
-    const float *xrow, *dva, *dmva;
+    const float *xrow, *dva, *dmva;  // already offset to this slice's first step
     float ascale;
-    int aoff, NB, b, KT;
+    int aoff, NB, b, kt0, KT;
 };
 
-template <int NTT>
-__device__ __forceinline__ void gateup_tile(const GuBlock &B, ATile *As, float (*Mt)[8],
-                                            const float *s_inv, float *gu_row0, int H2, int col0,
-                                            int nrows)
+template <int NTT, int ROWS>
+__device__ __forceinline__ void gateup_tile(const GuBlock &B, ATiles<ROWS, 4> &As,
+                                            float (*Mt)[8], const float *s_inv, float *gu_row0,
+                                            int H2, int col0, int nrows)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, c = lane & 15;
     const int NB = B.NB, b = B.b;
+    const bool a_live = wave < NTT;  // this wave's rows hold tokens (uniform)
     auto b_load = [&](int kt, uint32_t (&qw)[4], uint4 (&sw)[2], uint4 &mw) {
-        const size_t base = (size_t)kt * NB + b;
+        const size_t base = (size_t)(B.kt0 + kt) * NB + b;
 #pragma unroll
         for (int j = 0; j < 4; ++j) qw[j] = B.qn[(base * 16 + 4 * wave + j) * 64 + lane];
 #pragma unroll
@@ -230,10 +237,12 @@ __device__ __forceinline__ void gateup_tile(const GuBlock &B, ATile *As, float (
     uint32_t qw[4];
     uint4 sw[2], mw;
     v8h bq[4], bm;
-    a_load<true>(ar, B.xrow, B.dva, B.dmva, 0);
+    if (a_live) {
+        a_load<true>(ar, B.xrow, B.dva, B.dmva, 0);
+        a_store<true>(ar, B.ascale, &As.t[0][0][B.aoff], &As.t[0][1][B.aoff], &As.t[0][2][B.aoff],
+                      &As.t[0][3][B.aoff]);
+    }
     b_load(0, qw, sw, mw);
-    a_store<true>(ar, B.ascale, &As[0][0][B.aoff], &As[0][1][B.aoff], &As[0][2][B.aoff],
-                  &As[0][3][B.aoff]);
 #pragma unroll
     for (int j = 0; j < 4; ++j) bq[j] = q4_b(qw[j], sw[j >> 1]);
     bm = __builtin_bit_cast(v8h, mw);
@@ -241,28 +250,32 @@ __device__ __forceinline__ void gateup_tile(const GuBlock &B, ATile *As, float (
 
     const int mro = (16 * wave + c) * ORN_AST + 8 * g;  // row tile `wave`, for the mins
     for (int kt = 0; kt < B.KT - 1; ++kt) {
-        const ATile &A = As[kt & 1];
-        a_load<true>(ar, B.xrow, B.dva, B.dmva, 32 * (kt + 1));
+        const int cur = kt & 1, nxt = cur ^ 1;
+        if (a_live) a_load<true>(ar, B.xrow, B.dva, B.dmva, 32 * (kt + 1));
         b_load(kt + 1, qw, sw, mw);
-        mma_step<NTT>(A[0], A[1], bq, acc, c, g);
-        accm = mfma(*reinterpret_cast<const v8h *>(&A[2][mro]), bm, accm);
-        accm = mfma(*reinterpret_cast<const v8h *>(&A[3][mro]), bm, accm);
-        ATile &N = As[(kt + 1) & 1];
-        a_store<true>(ar, B.ascale, &N[0][B.aoff], &N[1][B.aoff], &N[2][B.aoff], &N[3][B.aoff]);
+        mma_step<NTT>(As.t[cur][0], As.t[cur][1], bq, acc, c, g);
+        if (a_live) {
+            accm = mfma(*reinterpret_cast<const v8h *>(&As.t[cur][2][mro]), bm, accm);
+            accm = mfma(*reinterpret_cast<const v8h *>(&As.t[cur][3][mro]), bm, accm);
+            a_store<true>(ar, B.ascale, &As.t[nxt][0][B.aoff], &As.t[nxt][1][B.aoff],
+                          &As.t[nxt][2][B.aoff], &As.t[nxt][3][B.aoff]);
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) bq[j] = q4_b(qw[j], sw[j >> 1]);
         bm = __builtin_bit_cast(v8h, mw);
         __syncthreads();
     }
     {
-        const ATile &A = As[(B.KT - 1) & 1];
-        mma_step<NTT>(A[0], A[1], bq, acc, c, g);
-        accm = mfma(*reinterpret_cast<const v8h *>(&A[2][mro]), bm, accm);
-        accm = mfma(*reinterpret_cast<const v8h *>(&A[3][mro]), bm, accm);
+        const int cur = (B.KT - 1) & 1;
+        mma_step<NTT>(As.t[cur][0], As.t[cur][1], bq, acc, c, g);
+        if (a_live) {
+            accm = mfma(*reinterpret_cast<const v8h *>(&As.t[cur][2][mro]), bm, accm);
+            accm = mfma(*reinterpret_cast<const v8h *>(&As.t[cur][3][mro]), bm, accm);
+        }
     }
 
     // dmin term of row tile `wave`: rows 16*wave + 4g + r, sub-block c.
-    if (c < 8) {
+    if (a_live && c < 8) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) Mt[16 * wave + 4 * g + r][c] = accm[r];
     }
@@ -283,31 +296,37 @@ __device__ __forceinline__ void gateup_tile(const GuBlock &B, ATile *As, float (
     }
 }
 
+// NTTMAX = 1: items of at most 16 rows (decode), one row tile, small LDS.
+// NTTMAX = 4: items of at most 64 rows (prefill), 1..4 row tiles.
+template <int NTTMAX>
 __global__ void __launch_bounds__(256)
     k_gateup_mfma(ornk_gu_prefill P, const float *__restrict__ xn,
                   const float *__restrict__ x_amax, const int *__restrict__ ctl,
-                  const int4 *__restrict__ items, const int *__restrict__ slot_expert,
-                  const int *__restrict__ row_token, float *__restrict__ gu, int D, int H)
+                  const int4 *__restrict__ items, const int *__restrict__ row_token,
+                  float *__restrict__ gu, int D, int H, int ks, int rows_max)
 {
-    __shared__ __align__(16) ATile As[2];
-    __shared__ float Mt[ORN_MT][8];
-    __shared__ float s_scale[ORN_MT], s_inv[ORN_MT];
-    __shared__ int s_tok[ORN_MT];
+    constexpr int ROWS = 16 * NTTMAX;
+    __shared__ __align__(16) ATiles<ROWS, 4> As;
+    __shared__ float Mt[ROWS][8];
+    __shared__ float s_scale[ROWS], s_inv[ROWS];
+    __shared__ int s_tok[ROWS];
 
     const int NB = H >> 8;
-    const int n_live = ctl[1] * 2 * NB;  // tiles of the items dispatch produced
+    const int per_item = 2 * NB * ks;
+    const int n_live = ctl[1] * per_item;  // tiles of the items dispatch produced
     if ((int)blockIdx.x >= n_live) return;
     const int tile = xcd_remap(blockIdx.x, n_live);
     const int b = tile % NB;
     const int m = (tile / NB) & 1;
-    const int item = tile / (2 * NB);
+    const int kslice = (tile / (2 * NB)) % ks;
+    const int item = tile / per_item;
     const int4 itm = items[item];
     const int e = itm.w;  // expert slot index (E = the shared expert)
-    const int nrows = itm.z;  // 1..ORN_MT (plan)
+    const int nrows = itm.z;  // 1..ROWS (plan)
     const size_t DH = (size_t)D * H;
     const int tid = threadIdx.x;
 
-    if (tid < ORN_MT) {
+    if (tid < ROWS) {
         const int tok = row_token[itm.y + (tid < nrows ? tid : 0)];
         const float s = tid < nrows ? row_scale(x_amax[tok], P.dmax[e * 3 + m]) : 0.0f;
         s_tok[tid] = tok;
@@ -317,48 +336,56 @@ __global__ void __launch_bounds__(256)
     __syncthreads();
 
     GuBlock B;
+    B.KT = D / 32 / ks;
+    B.kt0 = kslice * B.KT;
+    const int k0 = 32 * B.kt0;
     B.qn = P.pq[m] + (size_t)e * (DH / 8);
     B.sc = P.psc[m] + (size_t)e * (DH / 32);
     B.mn = P.pmn[m] + (size_t)e * (DH / 32);
-    const int ar = tid >> 2, ao = tid & 3;
-    B.xrow = xn + (size_t)s_tok[ar] * D + 8 * ao;
-    B.dva = P.pd[m] + (size_t)e * (DH / 256) + (size_t)b * D + 8 * ao;
-    B.dmva = P.pdm[m] + (size_t)e * (DH / 256) + (size_t)b * D + 8 * ao;
+    const int ar = (tid >> 2) & (ROWS - 1), ao = tid & 3;  // rows >= ROWS belong to dead waves
+    B.xrow = xn + (size_t)s_tok[ar] * D + k0 + 8 * ao;
+    B.dva = P.pd[m] + (size_t)e * (DH / 256) + (size_t)b * D + k0 + 8 * ao;
+    B.dmva = P.pdm[m] + (size_t)e * (DH / 256) + (size_t)b * D + k0 + 8 * ao;
     B.ascale = s_scale[ar];
     B.aoff = ar * ORN_AST + 8 * ao;
     B.NB = NB;
     B.b = b;
-    B.KT = D / 32;
-    float *row0 = gu + (size_t)itm.y * (2 * H);
+    float *row0 = gu + ((size_t)kslice * rows_max + itm.y) * (2 * H);
     const int col0 = m * H + 256 * b;
-    switch ((nrows + 15) >> 4) {
-    case 1: gateup_tile<1>(B, As, Mt, s_inv, row0, 2 * H, col0, nrows); break;
-    case 2: gateup_tile<2>(B, As, Mt, s_inv, row0, 2 * H, col0, nrows); break;
-    case 3: gateup_tile<3>(B, As, Mt, s_inv, row0, 2 * H, col0, nrows); break;
-    default: gateup_tile<4>(B, As, Mt, s_inv, row0, 2 * H, col0, nrows); break;
+    if (NTTMAX == 1) {
+        gateup_tile<1, ROWS>(B, As, Mt, s_inv, row0, 2 * H, col0, nrows);
+    } else {
+        switch ((nrows + 15) >> 4) {
+        case 1: gateup_tile<1, ROWS>(B, As, Mt, s_inv, row0, 2 * H, col0, nrows); break;
+        case 2: gateup_tile<2, ROWS>(B, As, Mt, s_inv, row0, 2 * H, col0, nrows); break;
+        case 3: gateup_tile<3, ROWS>(B, As, Mt, s_inv, row0, 2 * H, col0, nrows); break;
+        default: gateup_tile<4, ROWS>(B, As, Mt, s_inv, row0, 2 * H, col0, nrows); break;
+        }
     }
 }
 
 // ---------------------------------------------------------------------------
-// Down (Q6_K).  Logical tile = item * (D/256) + b; output dn[row][n].
+// Down (Q6_K).  Logical tile = (item * ks + kslice) * (D/256) + b; output
+// dn[kslice][row][n].
 // ---------------------------------------------------------------------------
 struct DnBlock {
     const uint2 *qb;
     const uint16_t *sc;
-    const float *mrow, *dva;
+    const float *mrow, *dva;  // already offset to this slice's first step
     float ascale;
-    int aoff, NBD, b, KT;
+    int aoff, NBD, b, kt0, KT;
 };
 
-template <int NTT>
-__device__ __forceinline__ void down_tile(const DnBlock &B, ATile2 *As, const float *s_inv,
+template <int NTT, int ROWS>
+__device__ __forceinline__ void down_tile(const DnBlock &B, ATiles<ROWS, 2> &As, const float *s_inv,
                                           float *dn_row0, int D, int col0, int nrows)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, c = lane & 15;
     const int NBD = B.NBD, b = B.b;
+    const bool a_live = wave < NTT;
     auto b_load = [&](int kt, uint2 (&qv)[4], uint4 (&sv)[4]) {
-        const size_t base = (size_t)kt * NBD + b;
+        const size_t base = (size_t)(B.kt0 + kt) * NBD + b;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const size_t t = base * 16 + 4 * wave + j;
@@ -377,24 +404,31 @@ __device__ __forceinline__ void down_tile(const DnBlock &B, ATile2 *As, const fl
     uint2 qv[4];
     uint4 sv[4];
     v8h bq[4];
-    a_load<false>(ar, B.mrow, B.dva, nullptr, 0);
+    if (a_live) {
+        a_load<false>(ar, B.mrow, B.dva, nullptr, 0);
+        a_store<false>(ar, B.ascale, &As.t[0][0][B.aoff], &As.t[0][1][B.aoff], nullptr, nullptr);
+    }
     b_load(0, qv, sv);
-    a_store<false>(ar, B.ascale, &As[0][0][B.aoff], &As[0][1][B.aoff], nullptr, nullptr);
 #pragma unroll
     for (int j = 0; j < 4; ++j) bq[j] = q6_b(qv[j], sv[j]);
     __syncthreads();
 
     for (int kt = 0; kt < B.KT - 1; ++kt) {
-        a_load<false>(ar, B.mrow, B.dva, nullptr, 32 * (kt + 1));
+        const int cur = kt & 1, nxt = cur ^ 1;
+        if (a_live) a_load<false>(ar, B.mrow, B.dva, nullptr, 32 * (kt + 1));
         b_load(kt + 1, qv, sv);
-        mma_step<NTT>(As[kt & 1][0], As[kt & 1][1], bq, acc, c, g);
-        ATile2 &N = As[(kt + 1) & 1];
-        a_store<false>(ar, B.ascale, &N[0][B.aoff], &N[1][B.aoff], nullptr, nullptr);
+        mma_step<NTT>(As.t[cur][0], As.t[cur][1], bq, acc, c, g);
+        if (a_live)
+            a_store<false>(ar, B.ascale, &As.t[nxt][0][B.aoff], &As.t[nxt][1][B.aoff], nullptr,
+                           nullptr);
 #pragma unroll
         for (int j = 0; j < 4; ++j) bq[j] = q6_b(qv[j], sv[j]);
         __syncthreads();
     }
-    mma_step<NTT>(As[(B.KT - 1) & 1][0], As[(B.KT - 1) & 1][1], bq, acc, c, g);
+    {
+        const int cur = (B.KT - 1) & 1;
+        mma_step<NTT>(As.t[cur][0], As.t[cur][1], bq, acc, c, g);
+    }
 
 #pragma unroll
     for (int tt = 0; tt < NTT; ++tt) {
@@ -410,28 +444,32 @@ __device__ __forceinline__ void down_tile(const DnBlock &B, ATile2 *As, const fl
     }
 }
 
+template <int NTTMAX>
 __global__ void __launch_bounds__(256)
     k_down_mfma(ornk_dn_prefill P, const float *__restrict__ mid,
                 const float *__restrict__ mid_amax, const int *__restrict__ ctl,
-                const int4 *__restrict__ items, const int *__restrict__ slot_expert,
-                float *__restrict__ dn, int D, int H)
+                const int4 *__restrict__ items, float *__restrict__ dn, int D, int H, int ks,
+                int rows_max)
 {
-    __shared__ __align__(16) ATile2 As[2];
-    __shared__ float s_scale[ORN_MT], s_inv[ORN_MT];
+    constexpr int ROWS = 16 * NTTMAX;
+    __shared__ __align__(16) ATiles<ROWS, 2> As;
+    __shared__ float s_scale[ROWS], s_inv[ROWS];
 
     const int NBD = D >> 8;
-    const int n_live = ctl[1] * NBD;
+    const int per_item = NBD * ks;
+    const int n_live = ctl[1] * per_item;
     if ((int)blockIdx.x >= n_live) return;
     const int tile = xcd_remap(blockIdx.x, n_live);
     const int b = tile % NBD;
-    const int item = tile / NBD;
+    const int kslice = (tile / NBD) % ks;
+    const int item = tile / per_item;
     const int4 itm = items[item];
-    const int e = itm.w;  // expert slot index (E = the shared expert)
+    const int e = itm.w;
     const int nrows = itm.z;
     const size_t DH = (size_t)D * H;
     const int tid = threadIdx.x;
 
-    if (tid < ORN_MT) {
+    if (tid < ROWS) {
         const float s = tid < nrows ? row_scale(mid_amax[itm.y + tid], P.dmax[e * 3 + 2]) : 0.0f;
         s_scale[tid] = s;
         s_inv[tid] = s != 0.0f ? 1.0f / s : 0.0f;
@@ -439,23 +477,29 @@ __global__ void __launch_bounds__(256)
     __syncthreads();
 
     DnBlock B;
+    B.KT = H / 32 / ks;
+    B.kt0 = kslice * B.KT;
+    const int k0 = 32 * B.kt0;
     B.qb = reinterpret_cast<const uint2 *>(P.dq + (size_t)e * DH);
     B.sc = P.dsc + (size_t)e * (DH / 16);
-    const int ar = tid >> 2, ao = tid & 3;
-    B.mrow = mid + (size_t)(itm.y + (ar < nrows ? ar : 0)) * H + 8 * ao;
-    B.dva = P.dd + (size_t)e * (DH / 256) + (size_t)b * H + 8 * ao;
+    const int ar = (tid >> 2) & (ROWS - 1), ao = tid & 3;
+    B.mrow = mid + (size_t)(itm.y + (ar < nrows ? ar : 0)) * H + k0 + 8 * ao;
+    B.dva = P.dd + (size_t)e * (DH / 256) + (size_t)b * H + k0 + 8 * ao;
     B.ascale = s_scale[ar];
     B.aoff = ar * ORN_AST + 8 * ao;
     B.NBD = NBD;
     B.b = b;
-    B.KT = H / 32;
-    float *row0 = dn + (size_t)itm.y * D;
+    float *row0 = dn + ((size_t)kslice * rows_max + itm.y) * D;
     const int col0 = 256 * b;
-    switch ((nrows + 15) >> 4) {
-    case 1: down_tile<1>(B, As, s_inv, row0, D, col0, nrows); break;
-    case 2: down_tile<2>(B, As, s_inv, row0, D, col0, nrows); break;
-    case 3: down_tile<3>(B, As, s_inv, row0, D, col0, nrows); break;
-    default: down_tile<4>(B, As, s_inv, row0, D, col0, nrows); break;
+    if (NTTMAX == 1) {
+        down_tile<1, ROWS>(B, As, s_inv, row0, D, col0, nrows);
+    } else {
+        switch ((nrows + 15) >> 4) {
+        case 1: down_tile<1, ROWS>(B, As, s_inv, row0, D, col0, nrows); break;
+        case 2: down_tile<2, ROWS>(B, As, s_inv, row0, D, col0, nrows); break;
+        case 3: down_tile<3, ROWS>(B, As, s_inv, row0, D, col0, nrows); break;
+        default: down_tile<4, ROWS>(B, As, s_inv, row0, D, col0, nrows); break;
+        }
     }
 }
 
@@ -478,21 +522,37 @@ __global__ void __launch_bounds__(256)
 
 extern "C" int ornk_moe_gateup_mfma(const ornk_moe_args *a, hipStream_t s)
 {
-    if (a->D % 32 || a->H % 256 || a->tchunk > ORN_MT) return hipErrorInvalidValue;
+    const int ks = a->ks_gu;
+    if (a->D % 32 || a->H % 256 || ks < 1 || (a->D / 32) % ks || a->tchunk > ORN_MT)
+        return hipErrorInvalidValue;
     const float *xin = a->apply_norm ? a->xn : a->x;
     hipLaunchKernelGGL(k_rowmax, dim3((a->T + 3) / 4), dim3(256), 0, s, xin, a->T, a->D,
                        a->x_amax);
-    hipLaunchKernelGGL(k_gateup_mfma, dim3(a->items_max * 2 * (a->H / 256)), dim3(256), 0, s,
-                       a->gu_pf, xin, a->x_amax, a->ctl, reinterpret_cast<const int4 *>(a->items),
-                       a->slot_expert, a->row_token, a->gu_part, a->D, a->H);
+    const dim3 grid(a->items_max * 2 * (a->H / 256) * ks);
+    if (a->tchunk <= 16)
+        hipLaunchKernelGGL(k_gateup_mfma<1>, grid, dim3(256), 0, s, a->gu_pf, xin, a->x_amax,
+                           a->ctl, reinterpret_cast<const int4 *>(a->items), a->row_token,
+                           a->gu_part, a->D, a->H, ks, a->rows_max);
+    else
+        hipLaunchKernelGGL(k_gateup_mfma<4>, grid, dim3(256), 0, s, a->gu_pf, xin, a->x_amax,
+                           a->ctl, reinterpret_cast<const int4 *>(a->items), a->row_token,
+                           a->gu_part, a->D, a->H, ks, a->rows_max);
     return hipGetLastError();
 }
 
 extern "C" int ornk_moe_down_mfma(const ornk_moe_args *a, hipStream_t s)
 {
-    if (a->H % 32 || a->D % 256 || a->tchunk > ORN_MT) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_down_mfma, dim3(a->items_max * (a->D / 256)), dim3(256), 0, s, a->dn_pf,
-                       a->mid, a->mid_amax, a->ctl, reinterpret_cast<const int4 *>(a->items),
-                       a->slot_expert, a->dn_part, a->D, a->H);
+    const int ks = a->ks_dn;
+    if (a->H % 32 || a->D % 256 || ks < 1 || (a->H / 32) % ks || a->tchunk > ORN_MT)
+        return hipErrorInvalidValue;
+    const dim3 grid(a->items_max * (a->D / 256) * ks);
+    if (a->tchunk <= 16)
+        hipLaunchKernelGGL(k_down_mfma<1>, grid, dim3(256), 0, s, a->dn_pf, a->mid, a->mid_amax,
+                           a->ctl, reinterpret_cast<const int4 *>(a->items), a->dn_part, a->D,
+                           a->H, ks, a->rows_max);
+    else
+        hipLaunchKernelGGL(k_down_mfma<4>, grid, dim3(256), 0, s, a->dn_pf, a->mid, a->mid_amax,
+                           a->ctl, reinterpret_cast<const int4 *>(a->items), a->dn_part, a->D,
+                           a->H, ks, a->rows_max);
     return hipGetLastError();
 }
