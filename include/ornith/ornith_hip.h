@@ -127,13 +127,22 @@ int gpu_moe_store_fill_synthetic(gpu_context *ctx, ornith_moe_store *store, int 
 enum { ORN_ROUTE_RENORM = 0, ORN_ROUTE_LITERAL = 1 };
 #define ORN_MOE_ASYNC 1u /* return without synchronising the stream */
 #define ORN_MOE_NORM 2u  /* expert input = rmsnorm(x, layer norm weights) */
-/* Expert-product kernels.  Default: the MFMA grouped GEMM (prefill layout,
- * fp16 hi+lo activations, fp32 accumulate) when the batch has at least
- * ORN_MOE_MFMA_MIN_TOKENS tokens and the store keeps the prefill layouts,
- * else the VALU matvec kernels (fp32 throughout). */
+/* Expert-product kernels.  Default: the MFMA kernels (prefill layout, fp16
+ * hi+lo activations, fp32 accumulate; decode-shaped instances up to 64
+ * tokens, grouped GEMMs above) when the batch has at least
+ * ORN_MOE_MFMA_MIN_TOKENS tokens, the store keeps the prefill layouts and
+ * every Q6_K sub-block scale of the layer has |sc| <= 64; else the VALU
+ * matvec kernels (fp32 throughout). */
 #define ORN_MOE_PATH_VALU 4u /* force the VALU kernels */
 #define ORN_MOE_PATH_MFMA 8u /* force the MFMA kernels (EUNSUPPORTED if unavailable) */
-#define ORN_MOE_MFMA_MIN_TOKENS 64
+#define ORN_MOE_MFMA_MIN_TOKENS 1
+/* Replay as a HIP graph: the first call with a given (layer(s), token
+ * count, route mode, flags, buffer addresses) runs normally and records its
+ * kernel sequence; later identical calls launch the recorded graph (one
+ * host call for the whole forward).  Buffer contents may change between
+ * calls, their addresses may not.  Uploading to the store drops the
+ * recordings.  Ignored while kernel profiling is on. */
+#define ORN_MOE_GRAPH 16u
 
 typedef struct {
     int route_mode; /* ORN_ROUTE_RENORM (default, model_get_routing) or ORN_ROUTE_LITERAL */

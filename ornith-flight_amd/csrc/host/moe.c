@@ -13,6 +13,24 @@
 #include <stdlib.h>
 #include <string.h>
 
+/* A forward call as a HIP graph: everything the captured kernel arguments
+ * depend on is in the key (buffers by address, the workspace base). */
+#define ORN_GRAPH_SLOTS 32
+typedef struct {
+    int layer, n_layers, T, mode;
+    unsigned flags;
+    const void *x, *resid, *out, *idx, *w;
+    void *ws;
+} orn_graph_key;
+
+typedef struct {
+    int used;
+    orn_graph_key key;
+    hipGraphExec_t exec;
+    int *ctl; /* the call's device counters (for gpu_moe_last_stats) */
+    unsigned long long tick;
+} orn_graph;
+
 struct ornith_moe_store {
     ornith_moe_shape sh;
     size_t blocks_per_matrix; /* D*H/256 */
@@ -25,11 +43,11 @@ struct ornith_moe_store {
     float *norm;              /* [L][D] */
     /* Prefill (MFMA) layouts, present when sh.prefill_layout is set (built
      * by prefill_pack.c; per layer and expert slot):
-     *   pq[m]  gate/up nibbles [D/32][H/256][16][64] u32     (D*H/2 bytes)
+     *   pq[m]  gate/up nibbles [D/32][H/256][4][64][4] u32   (D*H/2 bytes)
      *   psc[m] sub-block scales [D/32][H/256][8][32] fp16      (D*H/16)
      *   pmn[m] sub-block mins, same shape                       (D*H/16)
      *   pd[m], pdm[m]  d and dmin [H/256][D] fp32               (D*H/64 each)
-     *   dq     down q + 32 [H/32][D/256][16][64][8] u8           (D*H)
+     *   dq     down q + 32 [H/32][D/256][4][64][4][8] u8      (D*H)
      *   dsc    down sub-block scales [H/32][D/256][16][32] fp16   (D*H/8)
      *   dd     down d [D/256][H] fp32                             (D*H/64)
      *   dmax   [3]: max |d|,|dmin| of gate and of up, max |d| of down */
@@ -43,6 +61,10 @@ struct ornith_moe_store {
     float *dmax_host;         /* host mirror of dmax, [L][E+1][3] */
     int *q6_scmax;            /* host [L]: largest |Q6_K sub-scale| uploaded */
     size_t bytes;
+    /* HIP graphs of earlier calls made with ORN_MOE_GRAPH (least recently
+     * used replaced first); any upload to the store drops them all. */
+    orn_graph graphs[ORN_GRAPH_SLOTS];
+    unsigned long long graph_tick;
 };
 
 /* prefill_pack.c */
@@ -197,9 +219,18 @@ static int shape_ok(const ornith_moe_shape *s)
            (s->prefill_layout == 0 || s->prefill_layout == 1);
 }
 
+static void graphs_clear(ornith_moe_store *st)
+{
+    for (int i = 0; i < ORN_GRAPH_SLOTS; ++i) {
+        if (st->graphs[i].used) hipGraphExecDestroy(st->graphs[i].exec);
+        st->graphs[i].used = 0;
+    }
+}
+
 static void store_free(ornith_moe_store *st)
 {
     if (!st) return;
+    graphs_clear(st);
     hipFree(st->gate);
     hipFree(st->up);
     hipFree(st->down_body);
@@ -423,6 +454,7 @@ int gpu_moe_store_set_experts(gpu_context *ctx, ornith_moe_store *st, int layer,
         expert_first + n > E1 || matrix < 0 || matrix > 2)
         return orn_set_err(ctx, ORN_EINVAL, "set_experts: bad layer/expert range/matrix");
     if (n == 0) return ORN_OK;
+    graphs_clear(st);  /* the path choice depends on the uploaded scales */
     const int D = st->sh.d_model, H = st->sh.hidden;
     const size_t nb = st->blocks_per_matrix;
     const size_t slot0 = (size_t)layer * E1 + (size_t)expert_first;
@@ -472,6 +504,7 @@ int gpu_moe_store_set_router(gpu_context *ctx, ornith_moe_store *st, int layer, 
 {
     if (!ctx || !st || !W) return ORN_EINVAL;
     if (layer < 0 || layer >= st->sh.n_layers) return orn_set_err(ctx, ORN_EINVAL, "bad layer");
+    graphs_clear(st);  /* the bias pointer is a kernel argument */
     const size_t D = (size_t)st->sh.d_model, E = (size_t)st->sh.n_experts;
     float *t = (float *)malloc(D * E * sizeof(float));
     if (!t) return orn_set_err(ctx, ORN_ENOMEM, "host staging");
@@ -552,6 +585,7 @@ int gpu_moe_store_fill_synthetic(gpu_context *ctx, ornith_moe_store *st, int lay
 
 typedef struct {
     int ks_gu, ks_dn, rows_max, items_max, tchunk;
+    int use_dec; /* MFMA path with the decode-shaped kernels (items <= 16 rows) */
 } plan_t;
 
 static int pow2_floor(int v)
@@ -569,6 +603,7 @@ static int pow2_floor(int v)
 static plan_t make_plan(const ornith_moe_shape *sh, int T, int use_mfma)
 {
     plan_t p;
+    p.use_dec = 0;
     const int k = sh->top_k, E = sh->n_experts;
     const int D = sh->d_model, H = sh->hidden;
     /* MFMA work items hold at most one 16-row tile at decode sizes (the
@@ -606,6 +641,33 @@ static plan_t make_plan(const ornith_moe_shape *sh, int T, int use_mfma)
         if (kdn > H / 32) kdn = H / 32;
         p.ks_gu = kg;
         p.ks_dn = kdn;
+        if (p.tchunk <= 16) {
+            /* Decode kernels: about 4096 (gate/up) and 8192 (down) work
+             * groups over the estimated items, each slice 4..32 reduction
+             * steps (the compiled step counts); many short work groups keep
+             * the last round's tail small. */
+            int dg = pow2_floor(4096 / (est_items * 2 * (H / 256)) > 0
+                                    ? 4096 / (est_items * 2 * (H / 256)) : 1);
+            while (dg > 1 && (D / 32) % dg) dg /= 2;
+            while (dg > 1 && D / 32 / dg < 4) dg /= 2;
+            while ((D / 32) % (2 * dg) == 0 && D / 32 / dg > 32) dg *= 2;
+            int dd = pow2_floor(8192 / (est_items * (D / 256)) > 0 ? 8192 / (est_items * (D / 256)) : 1);
+            while (dd > 1 && (H / 32) % dd) dd /= 2;
+            while (dd > 1 && H / 32 / dd < 4) dd /= 2;
+            while ((H / 32) % (2 * dd) == 0 && H / 32 / dd > 32) dd *= 2;
+            {
+                const char *ev = getenv("ORN_TUNE_KSGU");
+                if (ev) dg = atoi(ev);
+                ev = getenv("ORN_TUNE_KSDN");
+                if (ev) dd = atoi(ev);
+            }
+            if ((D / 32) % dg == 0 && (H / 32) % dd == 0 &&
+                ornk_dec_supported(D / 32 / dg, H / 32 / dd)) {
+                p.use_dec = 1;
+                p.ks_gu = dg;
+                p.ks_dn = dd;
+            }
+        }
     }
     return p;
 }
@@ -701,8 +763,9 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     a.out = out;
     a.xn = a.apply_norm ? (float *)(ws + o_xn) : (float *)x;
     a.logits = (float *)(ws + o_logits);
-    a.idx = (uint32_t *)(ws + o_idx);
-    a.w = (float *)(ws + o_w);
+    /* the selection is written straight into the caller's buffers if given */
+    a.idx = idx_out ? idx_out : (uint32_t *)(ws + o_idx);
+    a.w = w_out ? w_out : (float *)(ws + o_w);
     a.ctl = (int *)(ws + o_ctl);
     a.slot_expert = (int *)(ws + o_slot_e);
     a.slot_off = (int *)(ws + o_slot_off);
@@ -729,6 +792,7 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
         a.dn_pf.dd = (const float *)((const uint8_t *)st->dd + slot0 * (DH / 64));
         a.dn_pf.dmax = st->dmax + slot0 * 3;
         a.x_amax = (float *)(ws + o_xamax);
+        a.router_amax = ornk_router_dpp_supported(T, D);
         a.mid_amax = (float *)(ws + o_midamax);
     }
 
@@ -736,27 +800,105 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     if ((rc = launch(ctx, "moe_norm", ornk_moe_norm, &a))) return rc;
     if ((rc = launch(ctx, "moe_route", ornk_moe_route, &a))) return rc;
     if ((rc = launch(ctx, "moe_dispatch", ornk_moe_dispatch, &a))) return rc;
-    if (use_mfma) {
+    if (p.use_dec) {
+        if ((rc = launch(ctx, "moe_gateup_dec", ornk_moe_gateup_dec, &a))) return rc;
+    } else if (use_mfma) {
         if ((rc = launch(ctx, "moe_gateup_mfma", ornk_moe_gateup_mfma, &a))) return rc;
     } else {
         if ((rc = launch(ctx, "moe_gateup", ornk_moe_gateup, &a))) return rc;
     }
     if ((rc = launch(ctx, "moe_mid", ornk_moe_mid, &a))) return rc;
-    if (use_mfma) {
+    if (p.use_dec) {
+        if ((rc = launch(ctx, "moe_down_dec", ornk_moe_down_dec, &a))) return rc;
+    } else if (use_mfma) {
         if ((rc = launch(ctx, "moe_down_mfma", ornk_moe_down_mfma, &a))) return rc;
     } else {
         if ((rc = launch(ctx, "moe_down", ornk_moe_down, &a))) return rc;
     }
     if ((rc = launch(ctx, "moe_combine", ornk_moe_combine, &a))) return rc;
 
-    hipStream_t s = ctx->stream;
-    if (idx_out)
-        hipMemcpyAsync(idx_out, a.idx, (size_t)T * k * 4, hipMemcpyDeviceToDevice, s);
-    if (w_out) hipMemcpyAsync(w_out, a.w, (size_t)T * k * 4, hipMemcpyDeviceToDevice, s);
     ctx->last_ctl = a.ctl;
     if (!(flags & ORN_MOE_ASYNC))
-        return orn_hip_check(ctx, hipStreamSynchronize(s), "moe forward");
+        return orn_hip_check(ctx, hipStreamSynchronize(ctx->stream), "moe forward");
     return ORN_OK;
+}
+
+/* ---------------------------------------------------------------------------
+ * HIP graphs (ORN_MOE_GRAPH): the first call with a given key runs eagerly
+ * (which also sizes the workspace), then records the same enqueue sequence
+ * into a graph without executing it; later calls with the same key launch
+ * the graph.  No memset or memcpy nodes: every step is a kernel.
+ * ------------------------------------------------------------------------- */
+typedef int (*orn_body_fn)(gpu_context *ctx, ornith_moe_store *st, const void *arg);
+
+static orn_graph *graph_lookup(ornith_moe_store *st, const orn_graph_key *key)
+{
+    for (int i = 0; i < ORN_GRAPH_SLOTS; ++i)
+        if (st->graphs[i].used && !memcmp(&st->graphs[i].key, key, sizeof *key))
+            return &st->graphs[i];
+    return NULL;
+}
+
+static int run_body(gpu_context *ctx, ornith_moe_store *st, orn_graph_key *key, orn_body_fn body,
+                    const void *arg, int sync)
+{
+    int rc;
+    if ((key->flags & ORN_MOE_GRAPH) && !ctx->prof_on) {
+        key->ws = ctx->ws.base;
+        orn_graph *g = graph_lookup(st, key);
+        if (g) {
+            g->tick = ++st->graph_tick;
+            rc = orn_hip_check(ctx, hipGraphLaunch(g->exec, ctx->stream), "graph launch");
+            if (rc) return rc;
+            ctx->last_ctl = g->ctl;
+        } else {
+            if ((rc = body(ctx, st, arg))) return rc;
+            key->ws = ctx->ws.base;
+            hipGraph_t graph = NULL;
+            rc = orn_hip_check(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal),
+                               "begin capture");
+            if (rc) return rc;
+            const int brc = body(ctx, st, arg);
+            const hipError_t ce = hipStreamEndCapture(ctx->stream, &graph);
+            hipGraphExec_t exec = NULL;
+            if (!brc && ce == hipSuccess && graph &&
+                hipGraphInstantiate(&exec, graph, NULL, NULL, 0) == hipSuccess) {
+                orn_graph *slot = &st->graphs[0];
+                for (int i = 0; i < ORN_GRAPH_SLOTS; ++i) {
+                    if (!st->graphs[i].used) { slot = &st->graphs[i]; break; }
+                    if (st->graphs[i].tick < slot->tick) slot = &st->graphs[i];
+                }
+                if (slot->used) hipGraphExecDestroy(slot->exec);
+                slot->used = 1;
+                slot->key = *key;
+                slot->exec = exec;
+                slot->ctl = ctx->last_ctl;
+                slot->tick = ++st->graph_tick;
+            }
+            if (graph) hipGraphDestroy(graph);
+            (void)hipGetLastError();  /* a failed capture leaves the eager result valid */
+        }
+    } else {
+        if ((rc = body(ctx, st, arg))) return rc;
+    }
+    if (sync) return orn_hip_check(ctx, hipStreamSynchronize(ctx->stream), "moe forward");
+    return ORN_OK;
+}
+
+typedef struct {
+    int layer, T;
+    const float *x, *resid;
+    float *out;
+    uint32_t *idx;
+    float *w;
+    ornith_moe_opts opts; /* ORN_MOE_ASYNC set */
+} fwd_arg;
+
+static int fwd_body(gpu_context *ctx, ornith_moe_store *st, const void *p)
+{
+    const fwd_arg *a = (const fwd_arg *)p;
+    return moe_forward_dev(ctx, st, a->layer, a->x, a->T, a->resid, a->out, a->idx, a->w,
+                           &a->opts);
 }
 
 int gpu_moe_forward(gpu_context *ctx, ornith_moe_store *st, int layer, const gpu_buffer *x,
@@ -776,10 +918,50 @@ int gpu_moe_forward(gpu_context *ctx, ornith_moe_store *st, int layer, const gpu
         return orn_set_err(ctx, ORN_EINVAL, "gpu_moe_forward: buffer too small");
     if (out == x || out == resid)
         return orn_set_err(ctx, ORN_EINVAL, "gpu_moe_forward: out aliases an input");
-    return moe_forward_dev(ctx, st, layer, (const float *)x->dev, n_tokens,
-                           resid ? (const float *)resid->dev : NULL, (float *)out->dev,
-                           idx_out ? (uint32_t *)idx_out->dev : NULL,
-                           w_out ? (float *)w_out->dev : NULL, opts);
+    const unsigned flags = opts ? opts->flags : 0u;
+    fwd_arg a = {layer,
+                 n_tokens,
+                 (const float *)x->dev,
+                 resid ? (const float *)resid->dev : NULL,
+                 (float *)out->dev,
+                 idx_out ? (uint32_t *)idx_out->dev : NULL,
+                 w_out ? (float *)w_out->dev : NULL,
+                 {opts ? opts->route_mode : ORN_ROUTE_RENORM, flags | ORN_MOE_ASYNC}};
+    orn_graph_key key;
+    memset(&key, 0, sizeof key);
+    key.layer = layer;
+    key.n_layers = 1;
+    key.T = n_tokens;
+    key.mode = a.opts.route_mode;
+    key.flags = flags & ~ORN_MOE_ASYNC;
+    key.x = a.x;
+    key.resid = a.resid;
+    key.out = a.out;
+    key.idx = a.idx;
+    key.w = a.w;
+    return run_body(ctx, st, &key, fwd_body, &a, !(flags & ORN_MOE_ASYNC));
+}
+
+typedef struct {
+    int first, n, T;
+    float *x, *tmp;
+    ornith_moe_opts opts; /* ORN_MOE_NORM | ORN_MOE_ASYNC set */
+} stack_arg;
+
+/* Layers ping-pong between x and tmp; the last one writes x in place, which
+ * is safe because its only reader of the residual input at the time of the
+ * write is the combine kernel itself, element by element. */
+static int stack_body(gpu_context *ctx, ornith_moe_store *st, const void *p)
+{
+    const stack_arg *a = (const stack_arg *)p;
+    float *cur = a->x;
+    for (int l = 0; l < a->n; ++l) {
+        float *dst = (l == a->n - 1) ? a->x : (cur == a->x ? a->tmp : a->x);
+        int rc = moe_forward_dev(ctx, st, a->first + l, cur, a->T, cur, dst, NULL, NULL, &a->opts);
+        if (rc) return rc;
+        cur = dst;
+    }
+    return ORN_OK;
 }
 
 int gpu_moe_forward_stack(gpu_context *ctx, ornith_moe_store *st, int first_layer, int n_layers,
@@ -793,21 +975,20 @@ int gpu_moe_forward_stack(gpu_context *ctx, ornith_moe_store *st, int first_laye
     if (!check_buf(x, act) || !check_buf(tmp, act) || x == tmp)
         return orn_set_err(ctx, ORN_EINVAL, "gpu_moe_forward_stack: buffer too small");
     if (n_tokens == 0 || n_layers == 0) return ORN_OK;
-    ornith_moe_opts o = {opts ? opts->route_mode : ORN_ROUTE_RENORM,
-                         (opts ? opts->flags : 0u) | ORN_MOE_NORM | ORN_MOE_ASYNC};
-    float *a = (float *)x->dev, *b = (float *)tmp->dev;
-    for (int l = 0; l < n_layers; ++l) {
-        int rc = moe_forward_dev(ctx, st, first_layer + l, a, n_tokens, a, b, NULL, NULL, &o);
-        if (rc) return rc;
-        float *t = a;
-        a = b;
-        b = t;
-    }
-    if (a != (float *)x->dev)
-        hipMemcpyAsync(x->dev, a, act, hipMemcpyDeviceToDevice, ctx->stream);
-    if (!(opts && (opts->flags & ORN_MOE_ASYNC)))
-        return orn_hip_check(ctx, hipStreamSynchronize(ctx->stream), "moe stack");
-    return ORN_OK;
+    const unsigned flags = opts ? opts->flags : 0u;
+    stack_arg a = {first_layer, n_layers, n_tokens, (float *)x->dev, (float *)tmp->dev,
+                   {opts ? opts->route_mode : ORN_ROUTE_RENORM,
+                    flags | ORN_MOE_NORM | ORN_MOE_ASYNC}};
+    orn_graph_key key;
+    memset(&key, 0, sizeof key);
+    key.layer = first_layer;
+    key.n_layers = n_layers;
+    key.T = n_tokens;
+    key.mode = a.opts.route_mode;
+    key.flags = (flags & ~ORN_MOE_ASYNC) | 0x80000000u; /* stack calls never match a layer call */
+    key.x = a.x;
+    key.out = a.tmp;
+    return run_body(ctx, st, &key, stack_body, &a, !(flags & ORN_MOE_ASYNC));
 }
 
 int gpu_moe_last_stats(gpu_context *ctx, int *n_slots, int *n_rows, int *n_literal)

@@ -19,6 +19,11 @@
  * column l % 16.  Q4_K words place value e at bit 4*(e/2) + 16*(e%2), so
  * ((w >> 4i) & 0x000F000F) | 0x64006400 is the fp16 pair (1024 + q_{2i},
  * 1024 + q_{2i+1}).  Q6_K stores q + 32 in one byte per value (k order).
+ *
+ * A kernel wave covers the four 16-column tiles 4w..4w+3 of a 256-column
+ * block, so the words (Q4_K) or 8-byte groups (Q6_K) of those four tiles sit
+ * side by side per lane: [K/32][M/256][4 w][64 lanes][4 tiles] -- one 16-byte
+ * load (Q4_K) or two (Q6_K) per lane and reduction step.
  */
 #include "internal.h"
 
@@ -109,7 +114,8 @@ void orn_pack_q4k_prefill(const uint8_t *blocks, int K, int M, uint32_t *qn, uin
             const uint8_t *qs = blk + ORN_Q4K_OFF_QS;
             for (int p = 0; p < 256; ++p) {
                 const int nt = p / 16, col = p % 16;
-                const size_t w = (((size_t)kt * NB + b) * 16 + nt) * 64 + 16 * g + col;
+                const size_t w =
+                    ((((size_t)kt * NB + b) * 4 + nt / 4) * 64 + 16 * g + col) * 4 + nt % 4;
                 qn[w] |= (uint32_t)q4_at(qs, p) << shift;
             }
         }
@@ -142,7 +148,8 @@ int orn_pack_q6k_prefill(const uint8_t *blocks, int K, int M, uint8_t *qb, uint1
             }
             for (int p = 0; p < 256; ++p) {
                 const int nt = p / 16, col = p % 16;
-                const size_t o = ((((size_t)kt * NB + b) * 16 + nt) * 64 + 16 * g + col) * 8 + e;
+                const size_t o =
+                    (((((size_t)kt * NB + b) * 4 + nt / 4) * 64 + 16 * g + col) * 4 + nt % 4) * 8 + e;
                 qb[o] = (uint8_t)(q6_at(ql, qh, p) + 32);
             }
         }

@@ -1,20 +1,8 @@
 // SPDX-License-Identifier: MIT
 //
 // Prefill-shaped expert products on the matrix cores: grouped GEMMs over the
-// dispatch's per-expert row groups with v_mfma_f32_16x16x32_f16.
-//
-// Arithmetic (all exact except the activation split and fp32 accumulation):
-//   Q4_K (gguf.c:43-61):  W[k][n] = d(k,b) * (sc*q)[k][n] - dmin(k,b) * m[k][n]
-//   Q6_K (gguf.c:64-86):  W[k][n] = d(k,b) * (sc*q)[k][n]
-//   y[r][n] = sum_k x[r][k] * W[k][n]
-//           = sum_k A[r][k] * B[k][n] - sum_k Am[r][k] * m[k][n]
-// with B = sc*q (an integer, |B| <= 945 for Q4_K and <= 2048 for Q6_K when
-// |sc| <= 64, so exact in fp16), A = x*d and Am = x*dmin.  A is scaled per
-// row by a power of two s_r (|A| < 2^14, no fp16 overflow) and split into
-// fp16 hi + lo (hi = A rounded toward zero, lo = the exact remainder rounded
-// toward zero): A = hi + lo to about 2^-21 relative, so two MFMAs (hi, lo)
-// per tile give fp32-class products; the sums accumulate in fp32 and the
-// result is scaled back by 1/s_r (exact).
+// dispatch's per-expert row groups with v_mfma_f32_16x16x32_f16 (operand
+// preparation and its exactness argument: mfma_ops.h).
 //
 // Work group: 4 waves, up to 64 token rows x 256 outputs (one block column of
 // one matrix), reduction in steps of 32.  Per step every thread prepares 8
@@ -25,103 +13,13 @@
 // row tile w.  Each converted B operand feeds up to 8 MFMAs.
 #include "common.h"
 #include "launch.h"
+#include "mfma_ops.h"
 
 namespace {
 
-typedef _Float16 v2h __attribute__((ext_vector_type(2)));
-typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+using namespace orn_mfma;
 
 #define ORN_MT 64   // token rows per work group (4 row tiles)
-#define ORN_AST 40  // LDS row stride of an activation tile, in halves (32 + 8 padding)
-
-// Power of two s with amax*dmax*s in [2^13, 2^14); 1 when that product is 0,
-// NaN or infinite.
-__device__ __forceinline__ float row_scale(float amax, float dmax)
-{
-    const float t = amax * dmax;
-    if (!(t > 0.0f) || !(t <= 3.0e38f)) return 1.0f;
-    int e = 13 - ilogbf(t);
-    e = e < -126 ? -126 : (e > 126 ? 126 : e);
-    return ldexpf(1.0f, e);
-}
-
-__device__ __forceinline__ v2h as_v2h(uint32_t u) { return __builtin_bit_cast(v2h, u); }
-__device__ __forceinline__ uint32_t as_u32(v2h v) { return __builtin_bit_cast(uint32_t, v); }
-
-// (a0, a1) -> hi = rtz fp16, lo = rtz fp16 of the exact remainder a - hi
-// (formed as fma(hi, -1, a), one mixed-precision fma per value).
-__device__ __forceinline__ void split2(float a0, float a1, uint32_t &hi, uint32_t &lo)
-{
-    const v2h h = __builtin_bit_cast(v2h, __builtin_amdgcn_cvt_pkrtz(a0, a1));
-    const float r0 = __builtin_fmaf((float)h[0], -1.0f, a0);
-    const float r1 = __builtin_fmaf((float)h[1], -1.0f, a1);
-    hi = as_u32(h);
-    lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(r0, r1));
-}
-
-// Work-group id i < n -> logical tile index, a bijection on [0, n) such that
-// each XCD (work groups are dealt to the 8 XCDs round-robin) runs one
-// contiguous range of tiles: the tiles of one item, and the items of one
-// expert, then share an L2.  n is the number of live tiles, so every XCD
-// gets an equal share of them.
-__device__ __forceinline__ int xcd_remap(int i, int n)
-{
-    const int q = n >> 3, r = n & 7, x = i & 7, pos = i >> 3;
-    return x < r ? x * (q + 1) + pos : r * (q + 1) + (x - r) * q + pos;
-}
-
-__device__ __forceinline__ v8h to_v8h(uint32_t a, uint32_t b, uint32_t c, uint32_t d)
-{
-    const uint4 u = make_uint4(a, b, c, d);
-    return __builtin_bit_cast(v8h, u);
-}
-
-// Q4_K B operand: word w holds q for k = 0..7 at bits 4*(e/2) + 16*(e%2);
-// sc = the 8 sub-block scales (fp16, k order).  B = sc * q, exactly:
-// fma(1024 + q, sc, -1024 sc).
-__device__ __forceinline__ uint32_t magic_pair(uint32_t w)
-{
-    uint32_t r;  // (w & 0x000F000F) | 0x64006400 in one instruction
-    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(0x000F000Fu), "v"(w), "v"(0x64006400u));
-    return r;
-}
-
-__device__ __forceinline__ v8h q4_b(uint32_t w, uint4 sc)
-{
-    const uint32_t s[4] = {sc.x, sc.y, sc.z, sc.w};
-    uint32_t o[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const v2h q = as_v2h(magic_pair(w >> (4 * i)));
-        const v2h sv = as_v2h(s[i]);
-        const v2h ns = sv * (v2h){(_Float16)-1024.0f, (_Float16)-1024.0f};
-        o[i] = as_u32(__builtin_elementwise_fma(q, sv, ns));
-    }
-    return to_v8h(o[0], o[1], o[2], o[3]);
-}
-
-// Q6_K B operand: 8 bytes q + 32 (k order), sc as above.  B = sc * q with
-// q = (1024 + (q + 32)) - 1056 exact and |sc * q| <= 2048.
-__device__ __forceinline__ v8h q6_b(uint2 q, uint4 sc)
-{
-    const uint32_t s[4] = {sc.x, sc.y, sc.z, sc.w};
-    const uint32_t p[4] = {__builtin_amdgcn_perm(0x64646464u, q.x, 0x04010400u),
-                           __builtin_amdgcn_perm(0x64646464u, q.x, 0x04030402u),
-                           __builtin_amdgcn_perm(0x64646464u, q.y, 0x04010400u),
-                           __builtin_amdgcn_perm(0x64646464u, q.y, 0x04030402u)};
-    uint32_t o[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const v2h qv = as_v2h(p[i]) + (v2h){(_Float16)-1056.0f, (_Float16)-1056.0f};
-        o[i] = as_u32(qv * as_v2h(s[i]));
-    }
-    return to_v8h(o[0], o[1], o[2], o[3]);
-}
-
-__device__ __forceinline__ v4f mfma(v8h a, v8h b, v4f c)
-{
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
 
 // Activation tile rows: thread t prepares row t/4, reduction values
 // 8*(t%4) .. +7 of the current step, for one or two scale vectors.  Rows
@@ -217,8 +115,11 @@ __device__ __forceinline__ void gateup_tile(const GuBlock &B, ATiles<ROWS, 4> &A
     const bool a_live = wave < NTT;  // this wave's rows hold tokens (uniform)
     auto b_load = [&](int kt, uint32_t (&qw)[4], uint4 (&sw)[2], uint4 &mw) {
         const size_t base = (size_t)(B.kt0 + kt) * NB + b;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) qw[j] = B.qn[(base * 16 + 4 * wave + j) * 64 + lane];
+        const uint4 q = *reinterpret_cast<const uint4 *>(B.qn + ((base * 4 + wave) * 64 + lane) * 4);
+        qw[0] = q.x;
+        qw[1] = q.y;
+        qw[2] = q.z;
+        qw[3] = q.w;
 #pragma unroll
         for (int h = 0; h < 2; ++h)
             sw[h] = *reinterpret_cast<const uint4 *>(B.sc + (base * 8 + 2 * wave + h) * 32 + 8 * g);
@@ -369,7 +270,7 @@ __global__ void __launch_bounds__(256)
 // dn[kslice][row][n].
 // ---------------------------------------------------------------------------
 struct DnBlock {
-    const uint2 *qb;
+    const uint4 *qb;
     const uint16_t *sc;
     const float *mrow, *dva;  // already offset to this slice's first step
     float ascale;
@@ -384,14 +285,14 @@ __device__ __forceinline__ void down_tile(const DnBlock &B, ATiles<ROWS, 2> &As,
     const int g = lane >> 4, c = lane & 15;
     const int NBD = B.NBD, b = B.b;
     const bool a_live = wave < NTT;
-    auto b_load = [&](int kt, uint2 (&qv)[4], uint4 (&sv)[4]) {
+    auto b_load = [&](int kt, uint4 (&qv)[2], uint4 (&sv)[4]) {
         const size_t base = (size_t)(B.kt0 + kt) * NBD + b;
+        const uint4 *qp = B.qb + ((base * 4 + wave) * 64 + lane) * 2;
+        qv[0] = qp[0];
+        qv[1] = qp[1];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const size_t t = base * 16 + 4 * wave + j;
-            qv[j] = B.qb[t * 64 + lane];
-            sv[j] = *reinterpret_cast<const uint4 *>(B.sc + t * 32 + 8 * g);
-        }
+        for (int j = 0; j < 4; ++j)
+            sv[j] = *reinterpret_cast<const uint4 *>(B.sc + (base * 16 + 4 * wave + j) * 32 + 8 * g);
     };
 
     v4f acc[NTT][4];
@@ -401,7 +302,7 @@ __device__ __forceinline__ void down_tile(const DnBlock &B, ATiles<ROWS, 2> &As,
         for (int j = 0; j < 4; ++j) acc[i][j] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
 
     ARaw ar;
-    uint2 qv[4];
+    uint4 qv[2];
     uint4 sv[4];
     v8h bq[4];
     if (a_live) {
@@ -410,7 +311,8 @@ __device__ __forceinline__ void down_tile(const DnBlock &B, ATiles<ROWS, 2> &As,
     }
     b_load(0, qv, sv);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) bq[j] = q6_b(qv[j], sv[j]);
+    for (int j = 0; j < 4; ++j) bq[j] = q6_b(j & 1 ? qv[j >> 1].z : qv[j >> 1].x,
+                                             j & 1 ? qv[j >> 1].w : qv[j >> 1].y, sv[j]);
     __syncthreads();
 
     for (int kt = 0; kt < B.KT - 1; ++kt) {
@@ -422,7 +324,8 @@ __device__ __forceinline__ void down_tile(const DnBlock &B, ATiles<ROWS, 2> &As,
             a_store<false>(ar, B.ascale, &As.t[nxt][0][B.aoff], &As.t[nxt][1][B.aoff], nullptr,
                            nullptr);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) bq[j] = q6_b(qv[j], sv[j]);
+        for (int j = 0; j < 4; ++j) bq[j] = q6_b(j & 1 ? qv[j >> 1].z : qv[j >> 1].x,
+                                                 j & 1 ? qv[j >> 1].w : qv[j >> 1].y, sv[j]);
         __syncthreads();
     }
     {
@@ -480,7 +383,7 @@ __global__ void __launch_bounds__(256)
     B.KT = H / 32 / ks;
     B.kt0 = kslice * B.KT;
     const int k0 = 32 * B.kt0;
-    B.qb = reinterpret_cast<const uint2 *>(P.dq + (size_t)e * DH);
+    B.qb = reinterpret_cast<const uint4 *>(P.dq + (size_t)e * DH);
     B.sc = P.dsc + (size_t)e * (DH / 16);
     const int ar = (tid >> 2) & (ROWS - 1), ao = tid & 3;
     B.mrow = mid + (size_t)(itm.y + (ar < nrows ? ar : 0)) * H + k0 + 8 * ao;
@@ -503,16 +406,29 @@ __global__ void __launch_bounds__(256)
     }
 }
 
-// max_k |x[r][k]| per row, one wave per row.
+// max_k |x[r][k]| per row, one wave per row; every load of a lane is issued
+// before the first use (D <= 64 * 4 * 16 per pass).
 __global__ void __launch_bounds__(256)
     k_rowmax(const float *__restrict__ x, int rows, int D, float *__restrict__ out)
 {
     const int lane = threadIdx.x & 63;
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= rows) return;
-    const float *p = x + (size_t)r * D;
+    const v4f *p = reinterpret_cast<const v4f *>(x + (size_t)r * D);
+    const int n4 = D >> 2;
     float mx = 0.0f;
-    for (int i = lane; i < D; i += 64) mx = fmaxf(mx, fabsf(p[i]));
+    for (int i0 = 0; i0 < n4; i0 += 64 * 16) {
+        v4f v[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int i = i0 + lane + 64 * j;
+            v[j] = i < n4 ? p[i] : (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)),
+                                 fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+    }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
     if (lane == 0) out[r] = mx;
@@ -520,14 +436,23 @@ __global__ void __launch_bounds__(256)
 
 }  // namespace
 
+extern "C" int ornk_rowmax(const float *x, int rows, int D, float *out, hipStream_t s)
+{
+    if (D % 4) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_rowmax, dim3((rows + 3) / 4), dim3(256), 0, s, x, rows, D, out);
+    return hipGetLastError();
+}
+
 extern "C" int ornk_moe_gateup_mfma(const ornk_moe_args *a, hipStream_t s)
 {
     const int ks = a->ks_gu;
     if (a->D % 32 || a->H % 256 || ks < 1 || (a->D / 32) % ks || a->tchunk > ORN_MT)
         return hipErrorInvalidValue;
     const float *xin = a->apply_norm ? a->xn : a->x;
-    hipLaunchKernelGGL(k_rowmax, dim3((a->T + 3) / 4), dim3(256), 0, s, xin, a->T, a->D,
-                       a->x_amax);
+    if (!a->router_amax) {
+        const int e = ornk_rowmax(xin, a->T, a->D, a->x_amax, s);
+        if (e != hipSuccess) return e;
+    }
     const dim3 grid(a->items_max * 2 * (a->H / 256) * ks);
     if (a->tchunk <= 16)
         hipLaunchKernelGGL(k_gateup_mfma<1>, grid, dim3(256), 0, s, a->gu_pf, xin, a->x_amax,

@@ -56,14 +56,14 @@ int ornk_topk(const float *logits, int T, int E, int k, int mode, uint32_t *idx,
  *
  * Prefill (MFMA) layouts of one layer, per expert slot (prefill_pack.c): */
 typedef struct {
-    const uint32_t *pq[2];         /* gate, up nibbles [D/32][H/256][16][64] */
+    const uint32_t *pq[2];         /* gate, up nibbles [D/32][H/256][4][64][4] */
     const uint16_t *psc[2], *pmn[2]; /* [D/32][H/256][8][32] fp16 scales, mins */
     const float *pd[2], *pdm[2];   /* [H/256][D] d, dmin */
     const float *dmax;             /* [E+1][3] */
 } ornk_gu_prefill;
 
 typedef struct {
-    const uint8_t *dq;   /* [H/32][D/256][16][64][8] q + 32 */
+    const uint8_t *dq;   /* [H/32][D/256][4][64][4][8] q + 32 */
     const uint16_t *dsc; /* [H/32][D/256][16][32] fp16 sub-block scales */
     const float *dd;     /* [D/256][H] d */
     const float *dmax;   /* [E+1][3] */
@@ -98,17 +98,30 @@ typedef struct {
     ornk_gu_prefill gu_pf;
     ornk_dn_prefill dn_pf;
     float *x_amax;    /* [T] max |xin| per token */
+    int router_amax;  /* 1: the routing step writes x_amax (else the MFMA launchers do) */
     float *mid_amax;  /* [rows_max] max |mid| per row (written by the mid step) */
 } ornk_moe_args;
 
 int ornk_moe_norm(const ornk_moe_args *a, hipStream_t s);
 int ornk_moe_route(const ornk_moe_args *a, hipStream_t s);
+/* Batches the one-wave-per-(token, 8 experts) router takes (and that can
+ * produce x_amax on the side). */
+#define ORN_ROUTER_DPP_MAX_T 64
+int ornk_router_dpp_supported(int T, int D);
 int ornk_moe_dispatch(const ornk_moe_args *a, hipStream_t s);
 int ornk_moe_gateup(const ornk_moe_args *a, hipStream_t s);
 int ornk_moe_mid(const ornk_moe_args *a, hipStream_t s);
 int ornk_moe_down(const ornk_moe_args *a, hipStream_t s);
+/* MFMA expert products: prefill-shaped (items of <= 64 rows) and
+ * decode-shaped (items of <= 16 rows, deeper load pipelining). */
 int ornk_moe_gateup_mfma(const ornk_moe_args *a, hipStream_t s);
 int ornk_moe_down_mfma(const ornk_moe_args *a, hipStream_t s);
+int ornk_moe_gateup_dec(const ornk_moe_args *a, hipStream_t s);
+/* 1 if the decode instances cover kt_gu (D/32/ks_gu) and kt_dn (H/32/ks_dn). */
+int ornk_dec_supported(int kt_gu, int kt_dn);
+int ornk_moe_down_dec(const ornk_moe_args *a, hipStream_t s);
+/* out[r] = max_k |x[r][k]| (D a multiple of 4). */
+int ornk_rowmax(const float *x, int rows, int D, float *out, hipStream_t s);
 int ornk_moe_combine(const ornk_moe_args *a, hipStream_t s);
 
 #ifdef __cplusplus

@@ -324,6 +324,100 @@ __global__ void __launch_bounds__(64)
 }
 
 // ---------------------------------------------------------------------------
+// Decode-sized batches: one wave per (token, 8 experts), the chain carried by
+// one lane per expert while the products come from its neighbours.
+//
+// Lane l = 8*es + q (es: expert e0+es, q = 0..7) multiplies the k quad
+// 8*it + q of x and W(., e0+es), i.e. k = 32*it + 4q + j (j = 0..3), so a
+// wave load covers 8 experts x 32 k (W's [D/4][E][4] layout: 8 runs of 128
+// contiguous bytes).  The chain lane of expert es is lane 8*es: for q =
+// 0..7, j = 0..3 it adds the product held by lane 8*es + q, fetched by the
+// add itself (v_add_f32 with a DPP row_shl:q source; lanes 8es..8es+7 lie in
+// one 16-lane DPP row).  Each logit is therefore acc = acc + fl(x[k]*W[k])
+// for k ascending, one add per element, bit-identical to model.c:1017-1025
+// (addition commutes exactly, so DPP operand order does not matter).
+//
+// ND = D/32 steps are fully unrolled, with W loads NR steps ahead in a
+// register ring.  The wave also stages x[t] in LDS and, when amax != NULL
+// (block column 0), writes max_k |x[t][k]| for the MFMA activation scaling.
+// ---------------------------------------------------------------------------
+template <int Q>
+__device__ __forceinline__ float dpp_shl(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                                 0x100 + Q, 0xF, 0xF, true));
+}
+
+template <int Q>
+__device__ __forceinline__ void chain_add4(float &acc, const float (&p)[4])
+{
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc = (Q == 0 ? p[j] : dpp_shl<Q>(p[j])) + acc;
+}
+
+template <int ND>
+__global__ void __launch_bounds__(64)
+    k_router_dpp(const float *__restrict__ x, const float *__restrict__ Wq,
+                 const float *__restrict__ bias, int T, int E, float *__restrict__ logits,
+                 int *ctl, float *__restrict__ amax)
+{
+    constexpr int D = 32 * ND, NR = ND < 16 ? ND : 16;
+    __shared__ v4f xs[D / 4];
+    const int lane = threadIdx.x;
+    const int es = lane >> 3, q = lane & 7;
+    const int e0 = blockIdx.x * 8;
+    const int t = blockIdx.y;
+    // The routing step is the first of every forward: clear its counters.
+    if (ctl && blockIdx.x == 0 && blockIdx.y == 0 && lane < 16) ctl[lane] = 0;
+    const int e = min(e0 + es, E - 1);  // lanes past E compute a copy, never stored
+    const v4f *wp = reinterpret_cast<const v4f *>(Wq) + (size_t)q * E + e;  // step it: + 8*it*E
+    v4f ring[NR];
+#pragma unroll
+    for (int i = 0; i < NR; ++i) ring[i] = wp[(size_t)8 * i * E];
+    {
+        const v4f *xg = reinterpret_cast<const v4f *>(x + (size_t)t * D);
+        constexpr int NX = D / 256;  // v4f loads per lane
+        v4f tmp[NX];
+#pragma unroll
+        for (int i = 0; i < NX; ++i) tmp[i] = xg[lane + 64 * i];
+        float mx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NX; ++i) {
+            xs[lane + 64 * i] = tmp[i];
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(tmp[i].x), fabsf(tmp[i].y)),
+                                 fmaxf(fabsf(tmp[i].z), fabsf(tmp[i].w))));
+        }
+        if (amax && blockIdx.x == 0) {
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+            if (lane == 0) amax[t] = mx;
+        }
+    }
+    __syncthreads();
+
+    float acc = 0.0f;
+#pragma unroll
+    for (int it = 0; it < ND; ++it) {
+        const v4f xv = xs[8 * it + q];
+        const v4f w = ring[it % NR];
+        const float p[4] = {xv.x * w.x, xv.y * w.y, xv.z * w.z, xv.w * w.w};
+        if (it + NR < ND) ring[it % NR] = wp[(size_t)8 * (it + NR) * E];
+        chain_add4<0>(acc, p);
+        chain_add4<1>(acc, p);
+        chain_add4<2>(acc, p);
+        chain_add4<3>(acc, p);
+        chain_add4<4>(acc, p);
+        chain_add4<5>(acc, p);
+        chain_add4<6>(acc, p);
+        chain_add4<7>(acc, p);
+        // The next step's weights pass through this point together with the
+        // chain, so its products cannot be computed ahead of this step's adds.
+        if (it + 1 < ND) asm volatile("" : "+v"(acc), "+v"(ring[(it + 1) % NR]));
+    }
+    if (q == 0 && e0 + es < E) logits[(size_t)t * E + e0 + es] = bias ? acc + bias[e0 + es] : acc;
+}
+
+// ---------------------------------------------------------------------------
 // Top-k selection, one wave per token, E <= 256 (lane holds experts
 // lane + 64*i).  Keys order (value desc, index asc) for non-NaN values.
 // ---------------------------------------------------------------------------
@@ -559,6 +653,12 @@ extern "C" int ornk_topk(const float *logits, int T, int E, int k, int mode, uin
 // ---------------------------------------------------------------------------
 // MoE routing step: exact logits into a->logits, then top-k into a->idx/a->w.
 // ---------------------------------------------------------------------------
+extern "C" int ornk_router_dpp_supported(int T, int D)
+{
+    return T >= 1 && T <= ORN_ROUTER_DPP_MAX_T &&
+           (D == 256 || D == 512 || D == 1024 || D == 2048 || D == 4096);
+}
+
 extern "C" int ornk_moe_route(const ornk_moe_args *a, hipStream_t s)
 {
     const int T = a->T, D = a->D, E = a->E;
@@ -567,7 +667,18 @@ extern "C" int ornk_moe_route(const ornk_moe_args *a, hipStream_t s)
         D % (ORN_RDC * ORN_RPF) || D > 4096)
         return hipErrorInvalidValue;
     const float *xin = a->apply_norm ? a->xn : a->x;
-    if (T >= 1024) {
+    float *amax = a->router_amax ? a->x_amax : nullptr;
+    const dim3 gd((E + 7) / 8, T);
+    if (a->router_amax && !ornk_router_dpp_supported(T, D)) return hipErrorInvalidValue;
+    if (ornk_router_dpp_supported(T, D)) {
+        switch (D) {
+        case 256: hipLaunchKernelGGL(k_router_dpp<8>, gd, dim3(64), 0, s, xin, a->router, a->bias, T, E, a->logits, a->ctl, amax); break;
+        case 512: hipLaunchKernelGGL(k_router_dpp<16>, gd, dim3(64), 0, s, xin, a->router, a->bias, T, E, a->logits, a->ctl, amax); break;
+        case 1024: hipLaunchKernelGGL(k_router_dpp<32>, gd, dim3(64), 0, s, xin, a->router, a->bias, T, E, a->logits, a->ctl, amax); break;
+        case 2048: hipLaunchKernelGGL(k_router_dpp<64>, gd, dim3(64), 0, s, xin, a->router, a->bias, T, E, a->logits, a->ctl, amax); break;
+        default: hipLaunchKernelGGL(k_router_dpp<128>, gd, dim3(64), 0, s, xin, a->router, a->bias, T, E, a->logits, a->ctl, amax); break;
+        }
+    } else if (T >= 1024) {
         hipLaunchKernelGGL(k_router_seq<4>, dim3((E + 63) / 64, (T + 15) / 16), dim3(256), 0, s,
                            xin, a->router, a->bias, T, D, E, a->logits, a->ctl);
     } else {

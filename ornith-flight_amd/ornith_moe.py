@@ -20,7 +20,7 @@ TYPE_F32, TYPE_F16, TYPE_Q4_K, TYPE_Q6_K = 0, 1, 12, 14
 MAT_GATE, MAT_UP, MAT_DOWN = 0, 1, 2
 ROUTE_RENORM, ROUTE_LITERAL = 0, 1
 MOE_ASYNC, MOE_NORM = 1, 2
-MOE_PATH_VALU, MOE_PATH_MFMA = 4, 8
+MOE_PATH_VALU, MOE_PATH_MFMA, MOE_GRAPH = 4, 8, 16
 SYN_GATE, SYN_UP, SYN_DOWN, SYN_ROUTER, SYN_ACT, SYN_ZIPF = 1, 2, 3, 4, 5, 6
 GPU_BUF_DEFAULT, GPU_BUF_SHARED, GPU_BUF_CONSTANT = 0, 1, 2
 Q4K_BYTES, Q6K_BYTES = 144, 210

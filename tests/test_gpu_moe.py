@@ -110,10 +110,11 @@ def small(om, ctx):
 
 @pytest.mark.parametrize("T", [1, 3, 16, 37])
 @pytest.mark.parametrize("mode", [O.MODE_RENORM, O.MODE_LITERAL])
-def test_small_layer_parity(om, ctx, small, T, mode):
-    say(f"small layer T={T} mode={mode}")
+def test_small_layer_valu_parity(om, ctx, small, T, mode):
+    """The VALU matvec kernels (fp32 throughout), forced."""
+    say(f"small layer VALU T={T} mode={mode}")
     x = act(om, 100 + T, T, small.D)
-    out, idx, w = run(ctx, small, x, mode=mode)
+    out, idx, w = run(ctx, small, x, mode=mode, flags=om.MOE_PATH_VALU)
     ref, ridx, rw = small.oracle(x, mode=mode)
     assert np.array_equal(idx, ridx)
     assert np.allclose(w, rw, rtol=1e-5, atol=1e-7)
@@ -125,8 +126,8 @@ def test_small_layer_parity(om, ctx, small, T, mode):
 @pytest.mark.parametrize("T", [1, 5, 37, 150])
 @pytest.mark.parametrize("mode", [O.MODE_RENORM, O.MODE_LITERAL])
 def test_small_layer_mfma_parity(om, ctx, small, T, mode):
-    """The MFMA grouped-GEMM path (fp16 hi+lo activations, exact sc*q
-    weights, fp32 accumulate) forced at every batch size."""
+    """The MFMA kernels (fp16 hi+lo activations, exact sc*q weights, fp32
+    accumulate): decode-shaped instances for T <= 64, grouped GEMMs above."""
     say(f"small layer MFMA T={T} mode={mode}")
     x = act(om, 300 + T, T, small.D)
     out, idx, w = run(ctx, small, x, mode=mode, flags=om.MOE_PATH_MFMA)
@@ -183,6 +184,61 @@ def test_q6_scale_above_64_uses_valu(om, ctx):
     assert row_err(out, ref).max() <= TOL
     with pytest.raises(RuntimeError):
         run(ctx, L, x[:4], flags=om.MOE_PATH_MFMA)
+    L.store.close()
+
+
+def write(om, ctx, buf, arr):
+    a = np.ascontiguousarray(arr)
+    om.lib().gpu_copy_to_device(ctx.ptr, buf.ptr, a.ctypes.data, a.nbytes)
+
+
+@pytest.mark.parametrize("T", [5, 150])
+def test_graph_replay_matches_eager(om, ctx, small, T):
+    """ORN_MOE_GRAPH: the first call runs and records, later calls with the
+    same buffers replay the recording.  Each replay sees new input contents,
+    with eager forwards and synchronisations in between, and must equal an
+    eager forward of the same input bit for bit (same kernels, same plan)."""
+    D, k = small.D, small.k
+    xb, ob = ctx.alloc(T * D * 4), ctx.alloc(T * D * 4)
+    ib, wb = ctx.alloc(T * k * 4), ctx.alloc(T * k * 4)
+    for i in range(4):
+        x = act(om, 500 + 10 * T + i, T, D)
+        write(om, ctx, xb, x)
+        small.store.forward(0, xb, T, ob, idx=ib, w=wb, flags=om.MOE_GRAPH)
+        g = ctx.download(ob, np.float32, (T, D))
+        gi = ctx.download(ib, np.uint32, (T, k))
+        gw = ctx.download(wb, np.float32, (T, k))
+        e, ei, ew = run(ctx, small, x)
+        say(f"  replay {i}: equal={np.array_equal(g.view(np.uint32), e.view(np.uint32))}")
+        assert np.array_equal(gi, ei) and np.array_equal(gw.view(np.uint32), ew.view(np.uint32))
+        assert np.array_equal(g.view(np.uint32), e.view(np.uint32))
+        if i == 0:
+            ref, ridx, _ = small.oracle(x)
+            assert np.array_equal(gi, ridx) and row_err(g, ref).max() <= TOL
+    for b in (xb, ob, ib, wb):
+        b.free()
+
+
+def test_graph_replay_stack(om, ctx):
+    """A recorded layer stack (odd and even depth: the last layer writes x in
+    place) equals the eager stack on every replay (the eager stack itself is
+    checked against the oracle in test_stack_teacher_forced)."""
+    D, H, E, k = 256, 256, 16, 8
+    L = Layer(om, ctx, D, H, E, k, seed=31, n_layers=3)
+    T = 4
+    xb, tb = ctx.alloc(T * D * 4), ctx.alloc(T * D * 4)
+    for n in (3, 2):
+        for i in range(3):
+            x = act(om, 600 + 10 * n + i, T, D)
+            write(om, ctx, xb, x)
+            L.store.forward_stack(0, n, xb, tb, T, flags=om.MOE_GRAPH)
+            g = ctx.download(xb, np.float32, (T, D))
+            write(om, ctx, xb, x)
+            L.store.forward_stack(0, n, xb, tb, T)
+            e = ctx.download(xb, np.float32, (T, D))
+            assert np.array_equal(g.view(np.uint32), e.view(np.uint32))
+    for b in (xb, tb):
+        b.free()
     L.store.close()
 
 
@@ -259,15 +315,15 @@ def test_ornith_decode_parity(om, ctx, ornith, T):
     assert err.max() <= TOL
 
 
-def test_ornith_mfma_decode_and_valu_prefill(om, ctx, ornith):
-    """Each expert path outside its default range: MFMA at T=16, VALU at
-    T=256 (tokens subset checked against the oracle)."""
+def test_ornith_valu_decode_and_prefill(om, ctx, ornith):
+    """The VALU kernels, forced, at T=16 and T=256 (a token subset checked
+    against the oracle at T=256)."""
     x = act(om, 2100, 16, 2048)
-    out, idx, _ = run(ctx, ornith, x, flags=om.MOE_PATH_MFMA)
+    out, idx, _ = run(ctx, ornith, x, flags=om.MOE_PATH_VALU)
     ref, ridx, _ = ornith.oracle(x)
     assert np.array_equal(idx, ridx)
     err = row_err(out, ref)
-    say("  MFMA T=16 max row err", err.max())
+    say("  VALU T=16 max row err", err.max())
     assert err.max() <= TOL
     x = act(om, 2101, 256, 2048)
     out, idx, _ = run(ctx, ornith, x, flags=om.MOE_PATH_VALU)

@@ -62,7 +62,7 @@ def test_q4k_prefill_layout_rebuilds_weights(L):
     assert ok
     ref = ref.reshape(K, M)
     W = np.zeros((K, M), np.float64)
-    qn4 = qn.reshape(KT, NB, 16, 64)
+    qn5 = qn.reshape(KT, NB, 4, 64, 4)  # [step][block column][wave][lane][tile]
     sc4 = f16(sc).reshape(KT, NB, 8, 32)
     mn4 = f16(mn).reshape(KT, NB, 8, 32)
     d2, dm2 = d.reshape(NB, K).astype(np.float64), dm.reshape(NB, K).astype(np.float64)
@@ -73,7 +73,7 @@ def test_q4k_prefill_layout_rebuilds_weights(L):
         for n in range(M):
             b, p = divmod(n, 256)
             nt, c = divmod(p, 16)
-            q = (int(qn4[kt, b, nt, 16 * g + c]) >> shift) & 15
+            q = (int(qn5[kt, b, nt // 4, 16 * g + c, nt % 4]) >> shift) & 15
             s = p // 32
             W[k, n] = d2[b, k] * (sc4[kt, b, s, kk] * q) - dm2[b, k] * mn4[kt, b, s, kk]
     assert np.array_equal(W.astype(np.float32).view(np.uint32), ref.view(np.uint32))
@@ -101,7 +101,7 @@ def test_q6k_prefill_layout_rebuilds_weights(L):
     ok, ref = O.dequant_tensor(blocks, Q6, K * M)
     assert ok
     ref = ref.reshape(K, M)
-    qb5 = qb.reshape(KT, NB, 16, 64, 8)
+    qb6 = qb.reshape(KT, NB, 4, 64, 4, 8)  # [step][block column][wave][lane][tile][k]
     sc4 = f16(sc).reshape(KT, NB, 16, 32)
     d2 = d.reshape(NB, K).astype(np.float64)
     W = np.zeros((K, M), np.float64)
@@ -111,6 +111,6 @@ def test_q6k_prefill_layout_rebuilds_weights(L):
         for n in range(M):
             b, p = divmod(n, 256)
             nt, c = divmod(p, 16)
-            q = int(qb5[kt, b, nt, 16 * g + c, e]) - 32
+            q = int(qb6[kt, b, nt // 4, 16 * g + c, nt % 4, e]) - 32
             W[k, n] = d2[b, k] * (sc4[kt, b, nt, kk] * q)
     assert np.array_equal(W.astype(np.float32).view(np.uint32), ref.view(np.uint32))
