@@ -99,35 +99,59 @@ def measure(ctx, store, layer, T, steps, warmup, x_seed=1, stack_layers=0):
     return ms, ms_events, kernels, stats
 
 
-def roofline_for(kernels, stats, T):
+def load_traffic(kernel, workload):
+    """HBM bytes per launch of `kernel` on `workload` from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE x counter scale + WRITE_SIZE), if
+    one exists: profiles/traffic_<kernel>_<workload>.txt, a line
+    'traffic_bytes_per_dispatch <N>'."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{kernel}_{workload}.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_dispatch"):
+                    return int(float(line.split()[1])), os.path.relpath(path, ROOT)
+    except OSError:
+        pass
+    return None, None
+
+
+def roofline_for(kernels, stats, T, workload):
     """Dominant expert kernel against its roofline.
 
-    VALU matvec kernels (decode): HBM-bound; achieved = algorithmic expert
-    bytes per launch (active experts x bytes per expert matrix set) / time.
-    MFMA grouped GEMMs (prefill): matrix-core bound; achieved = useful flops
-    per launch (token-expert rows x 2*K*N) / time, against the dense fp16
-    peak.  The kernels run two MFMAs (activation hi and lo halves) per useful
-    product, so their instruction rate is twice the useful rate shown.
+    Decode-shaped kernels (VALU matvec, MFMA decode instances): HBM-bound;
+    achieved = algorithmic expert bytes per launch (active experts x GGUF
+    bytes of the matrices the kernel streams: Q4_K gate+up, Q6_K down) /
+    average launch time.  Prefill MFMA grouped GEMMs: matrix-core bound;
+    achieved = useful flops per launch (token-expert rows x 2*K*N) / time,
+    against the dense fp16 peak.  The MFMA kernels run two MFMAs (activation
+    hi and lo halves) per useful product, so their instruction rate is twice
+    the useful rate shown.
     """
     slots = stats["n_slots"]  # active experts incl. the shared one
     rows = stats["n_rows"]    # token-expert pairs incl. the shared expert's
     work = {"moe_gateup": ("hbm", slots * GU_BYTES), "moe_down": ("hbm", slots * DN_BYTES),
+            "moe_gateup_dec": ("hbm", slots * GU_BYTES), "moe_down_dec": ("hbm", slots * DN_BYTES),
             "moe_gateup_mfma": ("mfma", rows * 2 * D * 2 * H), "moe_down_mfma": ("mfma", rows * 2 * H * D)}
     present = [n for n in work if n in kernels]
     name = max(present, key=lambda n: kernels[n]["avg_us"] * kernels[n]["calls_per_step"])
     bound, amount = work[name]
     avg_s = kernels[name]["avg_us"] * 1e-6
+    traffic, src = load_traffic(name, workload)
     if bound == "hbm":
         ach = amount / avg_s / 1e9
-        return name, {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
-                      "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
-                      "kernel": name, "bytes_per_launch": amount,
-                      "avg_us": round(kernels[name]["avg_us"], 2)}
-    ach = amount / avg_s / 1e12
-    return name, {"bound": "mfma", "achieved": round(ach, 1), "peak": MFMA_F16_PEAK_TFLOPS,
-                  "unit": "TFLOP/s", "frac": round(ach / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
-                  "kernel": name, "flops_per_launch": amount,
-                  "avg_us": round(kernels[name]["avg_us"], 2)}
+        out = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+               "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
+               "kernel": name, "bytes_per_launch": amount,
+               "avg_us": round(kernels[name]["avg_us"], 2)}
+    else:
+        ach = amount / avg_s / 1e12
+        out = {"bound": "mfma", "achieved": round(ach, 1), "peak": MFMA_F16_PEAK_TFLOPS,
+               "unit": "TFLOP/s", "frac": round(ach / MFMA_F16_PEAK_TFLOPS, 4), "traffic": traffic,
+               "kernel": name, "flops_per_launch": amount,
+               "avg_us": round(kernels[name]["avg_us"], 2)}
+    if src:
+        out["traffic_source"] = src
+    return name, out
 
 
 def cpu_baseline(budget_s):
@@ -214,7 +238,7 @@ def main():
 
     T = 16
     ms, ms_ev, kernels, stats = measure(ctx, store, 0, T, args.steps, args.warmup)
-    dom, roof = roofline_for(kernels, stats, T)
+    dom, roof = roofline_for(kernels, stats, T, "t16")
     U = stats["n_slots"]
     result = {
         "metric": "MoE-layer tokens/s at batch 1/16/2048; achieved HBM GB/s & MFMA % vs peak",
@@ -227,7 +251,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32 (Q4_K/Q6_K weights decoded in registers)",
+        "dtype": "f16 hi+lo MFMA, f32 accumulate (Q4_K/Q6_K weights exact as f16 sc*q)",
         "data": "synthetic (seeded Q4_K/Q6_K experts, N(0,1)-like activations)",
         "config": {"workload": "BASELINE configs[1]: single Ornith-shape MoE layer, 16-token decode",
                    "tokens": T, "d_model": D, "expert_ffn": H, "experts": E, "top_k": K,
@@ -243,7 +267,7 @@ def main():
         for label, layer, Tn in (("decode_t1", 0, 1), ("prefill_t2048", 0, 2048), ("zipf_t256", 1, 256)):
             steps = max(5, args.steps // (20 if Tn >= 256 else 1))
             ms_x, _, kern_x, st_x = measure(ctx, store, layer, Tn, steps, max(2, args.warmup // 4))
-            _, roof_x = roofline_for(kern_x, st_x, Tn)
+            _, roof_x = roofline_for(kern_x, st_x, Tn, label.split("_")[-1])
             extra[label] = {"tokens_per_s": round(Tn / (ms_x * 1e-3), 1), "ms_per_step": round(ms_x, 4),
                             "active_experts": st_x["n_slots"],
                             "layer_hbm_gbs": round(st_x["n_slots"] * EXPERT_BYTES / (ms_x * 1e-3) / 1e9, 1),

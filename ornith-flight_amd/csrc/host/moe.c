@@ -642,25 +642,16 @@ static plan_t make_plan(const ornith_moe_shape *sh, int T, int use_mfma)
         p.ks_gu = kg;
         p.ks_dn = kdn;
         if (p.tchunk <= 16) {
-            /* Decode kernels: about 4096 (gate/up) and 8192 (down) work
-             * groups over the estimated items, each slice 4..32 reduction
-             * steps (the compiled step counts); many short work groups keep
-             * the last round's tail small. */
-            int dg = pow2_floor(4096 / (est_items * 2 * (H / 256)) > 0
-                                    ? 4096 / (est_items * 2 * (H / 256)) : 1);
+            /* Decode kernels: slices of 4 or 8 reduction steps (the
+             * compiled counts).  Gate/up: about 2048 work groups over the
+             * estimated items, clamped to those counts; down: 8 steps. */
+            const int ng = 2048 / (est_items * 2 * (H / 256));
+            int dg = pow2_floor(ng > 0 ? ng : 1);
             while (dg > 1 && (D / 32) % dg) dg /= 2;
             while (dg > 1 && D / 32 / dg < 4) dg /= 2;
-            while ((D / 32) % (2 * dg) == 0 && D / 32 / dg > 32) dg *= 2;
-            int dd = pow2_floor(8192 / (est_items * (D / 256)) > 0 ? 8192 / (est_items * (D / 256)) : 1);
-            while (dd > 1 && (H / 32) % dd) dd /= 2;
-            while (dd > 1 && H / 32 / dd < 4) dd /= 2;
-            while ((H / 32) % (2 * dd) == 0 && H / 32 / dd > 32) dd *= 2;
-            {
-                const char *ev = getenv("ORN_TUNE_KSGU");
-                if (ev) dg = atoi(ev);
-                ev = getenv("ORN_TUNE_KSDN");
-                if (ev) dd = atoi(ev);
-            }
+            while ((D / 32) % (2 * dg) == 0 && D / 32 / dg > 8) dg *= 2;
+            int dd = 1;
+            while ((H / 32) % (2 * dd) == 0 && H / 32 / dd > 8) dd *= 2;
             if ((D / 32) % dg == 0 && (H / 32) % dd == 0 &&
                 ornk_dec_supported(D / 32 / dg, H / 32 / dd)) {
                 p.use_dec = 1;

@@ -1,0 +1,394 @@
+// SPDX-License-Identifier: MIT
+//
+// Top-k selection and token -> expert dispatch of the routed-MoE step.
+//
+// Selection (model.c:301-317 renormalised, model.c:1027-1049 literal) is
+// exchange selection with strict '>'.  When the top k+1 logits are finite
+// and pairwise distinct, exchange selection returns them in value order, so
+// a wave finds them with k+1 rounds of "wave max, check it is unique,
+// remove it" (DPP reductions, ballots); in the literal mode their gaps must
+// also exceed 1e-5, so that their probabilities keep that order.  Otherwise
+// (ties, NaN/Inf) one lane runs the reference's selection literally on this
+// device's values.
+//
+// Dispatch (one work group): list position j = 0 is the shared expert
+// (expert id E), j >= 1 routed expert j-1.  It produces the active slots
+// (shared first, then experts in ascending id), their row ranges, the work
+// items (<= tchunk rows each, expert id in the 4th word) and the
+// row <-> (token, selection slot) maps.  Pairs with w < 1e-6 are skipped
+// (model.c:1066).  Scans are wave-level DPP scans joined through LDS.
+//
+// Up to ORN_FUSED_SELECT_T tokens, selection and dispatch run in one work
+// group of 16 waves (one launch); above, k_select (a wave per token) then
+// k_dispatch.
+#include "common.h"
+#include "launch.h"
+
+#include <math.h>
+
+#define ORN_FUSED_SELECT_T 64
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// Wave reductions through DPP (every lane receives the result).
+// ---------------------------------------------------------------------------
+template <int CTRL, bool BC = false>
+__device__ __forceinline__ int dpp_i(int v)
+{
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, BC);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v)
+{
+    return __builtin_bit_cast(float, dpp_i<CTRL>(__builtin_bit_cast(int, v)));
+}
+__device__ __forceinline__ float readlane_f(float v, int l)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
+// quad_perm [1,0,3,2], [2,3,0,1], then row_ror 4, 8: every lane of a 16-lane
+// row holds the row's value; the four rows are joined with readlane.
+__device__ __forceinline__ float wave_max(float v)
+{
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x124>(v));
+    v = fmaxf(v, dpp_f<0x128>(v));
+    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)),
+                 fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
+
+__device__ __forceinline__ float wave_sum(float v)
+{
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x124>(v);
+    v += dpp_f<0x128>(v);
+    return (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
+}
+
+// Inclusive prefix sum over the wave: row_shr 1, 2, 4, 8 within 16-lane rows
+// (lanes before the row start read 0), then the earlier rows' totals.
+__device__ __forceinline__ int wave_incl_scan(int v)
+{
+    const int lane = threadIdx.x & 63;
+    v += dpp_i<0x111, true>(v);
+    v += dpp_i<0x112, true>(v);
+    v += dpp_i<0x114, true>(v);
+    v += dpp_i<0x118, true>(v);
+    const int r0 = __builtin_amdgcn_readlane(v, 15), r1 = __builtin_amdgcn_readlane(v, 31);
+    const int r2 = __builtin_amdgcn_readlane(v, 47);
+    const int row = lane >> 4;
+    return v + (row >= 1 ? r0 : 0) + (row >= 2 ? r1 : 0) + (row >= 3 ? r2 : 0);
+}
+
+__device__ __forceinline__ void wave_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// ---------------------------------------------------------------------------
+// Selection of one token by one wave (E <= 256: lane holds experts lane +
+// 64*i).  Writes k indices and weights to io/wo and, if given, to the LDS
+// copies lio/lwo.  val/ix: E floats/ints of LDS for the literal path.
+// ---------------------------------------------------------------------------
+__device__ void select_token(const float *__restrict__ lg, int E, int k, int mode,
+                             uint32_t *__restrict__ io, float *__restrict__ wo, int *lio,
+                             float *lwo, float *val, int *ix, int *n_slow)
+{
+    const int lane = threadIdx.x & 63;
+    float vo[4], v[4];
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = lane + 64 * i;
+        const bool valid = e < E;
+        vo[i] = valid ? lg[e] : -INFINITY;
+        if (valid && !isfinite(vo[i])) bad = true;
+        v[i] = vo[i];
+    }
+    bool slow = __ballot(bad) != 0ull;
+
+    // Lane r < k ends up holding the r-th selected (value, index).
+    float my_v = 0.0f, mx = 0.0f, prev = 0.0f;
+    int my_e = 0;
+    if (!slow) {
+        const int rounds = k < E ? k + 1 : k;
+        for (int r = 0; r < rounds; ++r) {
+            const float m = wave_max(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+            uint64_t b[4];
+            int cnt = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                b[i] = __ballot(v[i] == m);
+                cnt += __popcll(b[i]);
+            }
+            if (cnt != 1) {  // a tie (or -0 == +0): take the literal path
+                slow = true;
+                break;
+            }
+            int e = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (b[i]) e = 64 * i + __ffsll((unsigned long long)b[i]) - 1;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (lane + 64 * i == e) v[i] = -INFINITY;
+            if (r == 0) {
+                mx = m;
+            } else {
+                if (!(prev > m)) slow = true;
+                if (mode == 1 && !((double)prev - (double)m > 1e-5)) slow = true;
+            }
+            if (lane == r) {
+                my_v = m;
+                my_e = e;
+            }
+            prev = m;
+        }
+    }
+
+    if (!slow) {
+        float w;
+        if (mode == 0) {
+            // model.c:307-317: s_i = expf(v_i - v_0), sequential sum, divide.
+            const float s_i = expf(my_v - mx);
+            float sum = 0.0f;
+            for (int i = 0; i < k; ++i) sum += readlane_f(s_i, i);
+            w = s_i / sum;
+        } else {
+            float s = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s += expf(vo[i] - mx);  // -inf (no expert) -> 0
+            w = expf(my_v - mx) / wave_sum(s);
+        }
+        if (lane < k) {
+            io[lane] = (uint32_t)my_e;
+            wo[lane] = w;
+            if (lio) {
+                lio[lane] = my_e;
+                lwo[lane] = w;
+            }
+        }
+        return;
+    }
+
+    // Literal path: the reference's selection, run by lane 0 on this
+    // device's values.
+    if (lane == 0 && n_slow) atomicAdd(n_slow, 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = lane + 64 * i;
+        if (e < E) {
+            val[e] = vo[i];
+            ix[e] = e;
+        }
+    }
+    wave_sync();
+    if (lane == 0) {
+        if (mode == 1) {
+            // model.c:1027-1036: max by strict '>', expf, sequential sum, divide.
+            float m = val[0];
+            for (int e = 1; e < E; ++e)
+                if (val[e] > m) m = val[e];
+            float sum = 0.0f;
+            for (int e = 0; e < E; ++e) {
+                val[e] = expf(val[e] - m);
+                sum += val[e];
+            }
+            for (int e = 0; e < E; ++e) val[e] = val[e] / sum;
+        }
+        // k passes of exchange selection (model.c:301-305 / 1040-1048).
+        for (int i = 0; i < k && i < E - 1; ++i)
+            for (int j = i + 1; j < E; ++j)
+                if (val[j] > val[i]) {
+                    const float ft = val[i];
+                    val[i] = val[j];
+                    val[j] = ft;
+                    const int it = ix[i];
+                    ix[i] = ix[j];
+                    ix[j] = it;
+                }
+        if (mode == 0) {
+            const float m = val[0];
+            float sum = 0.0f;
+            for (int i = 0; i < k; ++i) sum += expf(val[i] - m);
+            for (int i = 0; i < k; ++i) val[i] = expf(val[i] - m) / sum;
+        }
+        for (int i = 0; i < k; ++i) {
+            io[i] = (uint32_t)ix[i];
+            wo[i] = val[i];
+            if (lio) {
+                lio[i] = ix[i];
+                lwo[i] = val[i];
+            }
+        }
+    }
+    wave_sync();
+}
+
+__global__ void __launch_bounds__(256)
+    k_select(const float *__restrict__ logits, int T, int E, int k, int mode,
+             uint32_t *__restrict__ idx_out, float *__restrict__ w_out, int *n_slow)
+{
+    __shared__ float sv[4][256];
+    __shared__ int si[4][256];
+    const int wave = threadIdx.x >> 6;
+    const int t = blockIdx.x * 4 + wave;
+    if (t >= T) return;  // a wave is a token: no block-wide barrier
+    select_token(logits + (size_t)t * E, E, k, mode, idx_out + (size_t)t * k,
+                 w_out + (size_t)t * k, nullptr, nullptr, sv[wave], si[wave], n_slow);
+}
+
+// ---------------------------------------------------------------------------
+// Dispatch core, one work group of 1024 threads; sel_idx/sel_w may live in
+// LDS or global memory (visible to the whole group on entry).
+// ---------------------------------------------------------------------------
+struct DispatchLds {
+    int cnt[1024];
+    int cursor[1024];
+    int rowoff[1024];
+    int wtot[3][16];
+};
+
+template <typename IdxT>
+__device__ void dispatch_group(DispatchLds &L, const IdxT *sel_idx, const float *sel_w, int T,
+                               int k, int E, int has_shared, int *ctl, int *slot_expert,
+                               int *slot_off, int *slot_cnt, int *row_token, int *pair_row,
+                               int4 *items, int items_max, int tchunk)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int NJ = E + 1;
+    const int P = T * k;
+    L.cnt[tid] = 0;
+    L.cursor[tid] = 0;
+    __syncthreads();
+    for (int p = tid; p < P; p += 1024) {
+        const uint32_t e = (uint32_t)sel_idx[p];
+        if (!(sel_w[p] < 1e-6f) && e < (uint32_t)E) atomicAdd(&L.cnt[e + 1], 1);
+    }
+    if (tid == 0) L.cnt[0] = has_shared ? T : 0;
+    __syncthreads();
+
+    const int c = tid < NJ ? L.cnt[tid] : 0;
+    const int flag = c > 0 ? 1 : 0;
+    const int nit = (c + tchunk - 1) / tchunk;
+    const int s_flag = wave_incl_scan(flag), s_c = wave_incl_scan(c), s_nit = wave_incl_scan(nit);
+    if (lane == 63) {
+        L.wtot[0][wave] = s_flag;
+        L.wtot[1][wave] = s_c;
+        L.wtot[2][wave] = s_nit;
+    }
+    __syncthreads();
+    int o_flag = 0, o_c = 0, o_nit = 0, n_slots = 0, n_rows = 0, n_items = 0;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) {
+        const int a = L.wtot[0][w], b = L.wtot[1][w], d = L.wtot[2][w];
+        if (w < wave) {
+            o_flag += a;
+            o_c += b;
+            o_nit += d;
+        }
+        n_slots += a;
+        n_rows += b;
+        n_items += d;
+    }
+    const int slot = o_flag + s_flag - flag;
+    const int roff = o_c + s_c - c;
+    const int ioff = o_nit + s_nit - nit;
+    L.rowoff[tid] = roff;
+    if (flag) {
+        const int ex = tid == 0 ? E : tid - 1;
+        slot_expert[slot] = ex;
+        slot_off[slot] = roff;
+        slot_cnt[slot] = c;
+        for (int q = 0; q < nit && ioff + q < items_max; ++q) {
+            const int r0 = q * tchunk;
+            items[ioff + q] = make_int4(slot, roff + r0, min(tchunk, c - r0), ex);
+        }
+    }
+    if (tid == 0) {
+        ctl[0] = n_slots;
+        ctl[1] = n_items < items_max ? n_items : items_max;
+        ctl[2] = n_rows;
+    }
+    __syncthreads();
+
+    for (int p = tid; p < P; p += 1024) {
+        const uint32_t e = (uint32_t)sel_idx[p];
+        // Skip rule of model.c:1066; an index outside [0, E) cannot come out
+        // of the router but is treated as skipped rather than trusted.
+        if (sel_w[p] < 1e-6f || e >= (uint32_t)E) {
+            pair_row[p] = -1;
+            continue;
+        }
+        const int j = (int)e + 1;
+        const int r = L.rowoff[j] + atomicAdd(&L.cursor[j], 1);
+        row_token[r] = p / k;
+        pair_row[p] = r;
+    }
+    if (has_shared)
+        for (int t = tid; t < T; t += 1024) row_token[L.rowoff[0] + t] = t;
+}
+
+__global__ void __launch_bounds__(1024)
+    k_dispatch(const uint32_t *__restrict__ idx, const float *__restrict__ w, int T, int k, int E,
+               int has_shared, int *ctl, int *slot_expert, int *slot_off, int *slot_cnt,
+               int *row_token, int *pair_row, int4 *items, int items_max, int tchunk)
+{
+    __shared__ DispatchLds L;
+    dispatch_group(L, idx, w, T, k, E, has_shared, ctl, slot_expert, slot_off, slot_cnt,
+                   row_token, pair_row, items, items_max, tchunk);
+}
+
+// Selection of T <= ORN_FUSED_SELECT_T tokens (wave w: tokens w, w+16, ...)
+// followed by the dispatch, in one work group.
+__global__ void __launch_bounds__(1024)
+    k_select_dispatch(const float *__restrict__ logits, int T, int E, int k, int mode,
+                      uint32_t *__restrict__ idx_out, float *__restrict__ w_out, int has_shared,
+                      int *ctl, int *slot_expert, int *slot_off, int *slot_cnt, int *row_token,
+                      int *pair_row, int4 *items, int items_max, int tchunk)
+{
+    __shared__ DispatchLds L;
+    __shared__ float sv[16][256];
+    __shared__ int si[16][256];
+    __shared__ int lidx[ORN_FUSED_SELECT_T * 16];
+    __shared__ float lw[ORN_FUSED_SELECT_T * 16];
+    const int wave = threadIdx.x >> 6;
+    for (int t = wave; t < T; t += 16)
+        select_token(logits + (size_t)t * E, E, k, mode, idx_out + (size_t)t * k,
+                     w_out + (size_t)t * k, lidx + t * k, lw + t * k, sv[wave], si[wave], ctl + 3);
+    __syncthreads();
+    dispatch_group(L, lidx, lw, T, k, E, has_shared, ctl, slot_expert, slot_off, slot_cnt,
+                   row_token, pair_row, items, items_max, tchunk);
+}
+
+}  // namespace
+
+// Selection + dispatch step of the MoE forward (after the router).
+extern "C" int ornk_moe_dispatch(const ornk_moe_args *a, hipStream_t s)
+{
+    const int T = a->T, E = a->E, k = a->k;
+    if (T <= 0) return hipSuccess;
+    if (E < 1 || E > 256 || k < 1 || k > 16 || k > E) return hipErrorInvalidValue;
+    int4 *items = reinterpret_cast<int4 *>(a->items);
+    if (T <= ORN_FUSED_SELECT_T) {
+        hipLaunchKernelGGL(k_select_dispatch, dim3(1), dim3(1024), 0, s, a->logits, T, E, k,
+                           a->mode, a->idx, a->w, a->has_shared, a->ctl, a->slot_expert,
+                           a->slot_off, a->slot_cnt, a->row_token, a->pair_row, items,
+                           a->items_max, a->tchunk);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL(k_select, dim3((T + 3) / 4), dim3(256), 0, s, a->logits, T, E, k, a->mode,
+                       a->idx, a->w, a->ctl + 3);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), 0, s, a->idx, a->w, T, k, E,
+                       a->has_shared, a->ctl, a->slot_expert, a->slot_off, a->slot_cnt,
+                       a->row_token, a->pair_row, items, a->items_max, a->tchunk);
+    return hipGetLastError();
+}

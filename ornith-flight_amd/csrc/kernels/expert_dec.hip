@@ -7,18 +7,17 @@
 //
 // At decode sizes the weights are read once per launch and the step is
 // bound by how many bytes are in flight, so each lane keeps NR reduction
-// steps of loads (weights, per-row scales and the activations they meet)
-// in a register ring, refilled right after a step's registers are consumed.
-// The KT steps of a slice are a compile-time count and fully unrolled: a
-// loop would carry the ring through the back edge as register copies, which
-// wait for every load in flight.
+// steps of weight loads in a register ring, refilled right after a step's
+// registers are consumed.  The KT steps of a slice are a compile-time count
+// and fully unrolled: a loop would carry the ring through the back edge as
+// register copies, which wait for every load in flight.
 //
 // Work group: 4 waves over one 256-column block of one matrix.  Wave w owns
 // column tiles 4w..4w+3 (one 16-byte weight load per lane and step for
-// Q4_K, two for Q6_K).  Each step all 256 threads prepare the 16 x 32
-// activation tile (2 values per thread, hi/lo split) into LDS (double
-// buffered, one barrier per step); every wave then runs 4 x (hi, lo) MFMAs
-// and, for Q4_K, 2 more for the dmin term of its own two sub-blocks.
+// Q4_K, two for Q6_K).  The 16 x 32*KT activation tiles of the slice are
+// prepared into LDS once (hi/lo split), so the waves never wait for each
+// other after that; every step a wave runs 4 x (hi, lo) MFMAs and, for
+// Q4_K, 2 more for the dmin term of its own two sub-blocks.
 #include "common.h"
 #include "launch.h"
 #include "mfma_ops.h"
@@ -55,38 +54,36 @@ __device__ __forceinline__ v2f bload8f(rsrc_t r, uint32_t voff, uint32_t soff)
     return __builtin_bit_cast(v2f, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
 }
 
-// LDS activation tiles: [buffer][hi, lo, mins hi, mins lo][16 rows x ORN_AST]
-// as 32-bit words (two halves).
-template <int NARR>
-struct DecTiles {
-    uint32_t w[2][NARR][16 * ORN_AST / 2];
-};
-
 // ---------------------------------------------------------------------------
 // Gate/up (Q4_K).  Logical tile = ((item * ks + kslice) * 2 + m) * (H/256) + b;
 // output gu[kslice][row][m*H + n], the split-K partial over the reduction
 // steps kslice*KT .. +KT-1.
+//
+// The slice's activation tiles (all KT steps) are prepared once into LDS:
+// thread t prepares row t/16, a run of 2*KT consecutive reduction values
+// (hi/lo of x*s*d and of x*s*dmin); after one barrier every wave streams its
+// own weights with no further synchronisation.
 // ---------------------------------------------------------------------------
-struct GuStage {
-    uint4 q;         // nibble words of column tiles 4w..4w+3
-    uint4 s0, s1;    // scales of sub-blocks 2w, 2w+1 at k = 8g..8g+7
-    uint4 mn;        // mins of sub-block 2w + (c & 1) at k = 8g..8g+7
-    v2f x, d, dm;    // activation row tid/16 at k pair 2*(tid%16), its d, dmin
+struct GuRing {
+    uint4 q;       // nibble words of column tiles 4w..4w+3
+    uint4 s0, s1;  // scales of sub-blocks 2w, 2w+1 at k = 8g..8g+7
+    uint4 mn;      // mins of sub-block 2w + (c & 1) at k = 8g..8g+7
 };
 
 template <int NR, int KT>
 __global__ void __launch_bounds__(256)
     k_gateup_dec(ornk_gu_prefill P, const float *__restrict__ xn,
-                 const float *__restrict__ x_amax, const int *__restrict__ ctl,
-                 const int4 *__restrict__ items, const int *__restrict__ row_token,
-                 float *__restrict__ gu, int T, int D, int H, int ks, int rows_max)
+                  const float *__restrict__ x_amax, const int *__restrict__ ctl,
+                  const int4 *__restrict__ items, const int *__restrict__ row_token,
+                  float *__restrict__ gu, int T, int D, int H, int ks, int rows_max)
 {
-    __shared__ __align__(16) DecTiles<4> As;
+    constexpr int L = 2 * KT, C = L < 16 ? L : 16, NCH = L / C;
+    __shared__ __align__(16) uint32_t As[KT][4][16 * ORN_AST / 2];
     __shared__ float s_inv[16];
 
     const int NB = H >> 8;
     const int per_item = 2 * NB * ks;
-    const int n_live = ctl[1] * per_item;  // tiles of the items dispatch produced
+    const int n_live = ctl[1] * per_item;
     if ((int)blockIdx.x >= n_live) return;
     const int tile = xcd_remap(blockIdx.x, n_live);
     const int b = tile % NB;
@@ -94,16 +91,14 @@ __global__ void __launch_bounds__(256)
     const int kslice = (tile / (2 * NB)) % ks;
     const int item = tile / per_item;
     const int4 itm = items[item];
-    const int e = itm.w;      // expert slot index (E = the shared expert)
-    const int nrows = itm.z;  // 1..16 (plan)
+    const int e = itm.w;
+    const int nrows = itm.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, c = lane & 15;
     const int kt0 = kslice * KT;
     const size_t DH = (size_t)D * H;
 
-    // Streams of this work group (buffer bases, wave-uniform) and this
-    // lane's fixed byte offsets; step kt adds kt * (step bytes).
-    const uint32_t EQ = (uint32_t)(DH / 2), ES = (uint32_t)(DH / 16);  // bytes per expert
+    const uint32_t EQ = (uint32_t)(DH / 2), ES = (uint32_t)(DH / 16);
     const rsrc_t rq = make_rsrc(reinterpret_cast<const uint8_t *>(P.pq[m]) + (size_t)e * EQ, EQ);
     const rsrc_t rs = make_rsrc(reinterpret_cast<const uint8_t *>(P.psc[m]) + (size_t)e * ES, ES);
     const rsrc_t rm = make_rsrc(reinterpret_cast<const uint8_t *>(P.pmn[m]) + (size_t)e * ES, ES);
@@ -111,84 +106,83 @@ __global__ void __launch_bounds__(256)
     const uint32_t q_off = (uint32_t)(((size_t)kt0 * NB + b) * 4096) + (wave * 64 + lane) * 16;
     const uint32_t s_off = (uint32_t)((((size_t)kt0 * NB + b) * 8 + 2 * wave) * 64) + 16 * g;
     const uint32_t m_off = s_off + 64 * (c & 1);
-    // Activation prep: thread row ar, k pair kp of each step.
-    const int ar = tid >> 4, kp = 2 * (tid & 15);
-    const int arow = ar < nrows ? ar : 0;  // rows past the item read a valid row, scaled by 0
-    const uint32_t ED = (uint32_t)(DH / 64);  // d (or dmin) bytes per expert
-    const rsrc_t rd = make_rsrc(reinterpret_cast<const uint8_t *>(P.pd[m]) + (size_t)e * ED, ED);
-    const rsrc_t rdm = make_rsrc(reinterpret_cast<const uint8_t *>(P.pdm[m]) + (size_t)e * ED, ED);
-    const uint32_t d_off = (uint32_t)(((size_t)b * D + 32 * kt0 + kp) * 4);
-
-    auto load_b = [&](GuStage &st, int kt) {
+    auto load_b = [&](GuRing &st, int kt) {
         st.q = bload16(rq, q_off, kt * qstep);
         st.s0 = bload16(rs, s_off, kt * sstep);
         st.s1 = bload16(rs, s_off + 64, kt * sstep);
         st.mn = bload16(rm, m_off, kt * sstep);
     };
-    const rsrc_t rx = make_rsrc(xn, (uint32_t)((size_t)T * D * 4));
-    uint32_t x_off = 0;
-    auto load_a = [&](GuStage &st, int kt) {
-        st.x = bload8f(rx, x_off, kt * 128);
-        st.d = bload8f(rd, d_off, kt * 128);
-        st.dm = bload8f(rdm, d_off, kt * 128);
-    };
 
-    // Prologue: the token index first, then the weight loads of the first NR
-    // steps (independent of the tokens), then the token-dependent loads.
+    const int ar = tid >> 4, seg = tid & 15;
+    const int arow = ar < nrows ? ar : 0;
     const int tok = row_token[itm.y + arow];
-    GuStage st[NR];
+    GuRing st[NR];
 #pragma unroll
-    for (int s = 0; s < NR; ++s) load_b(st[s], s);
+    for (int i = 0; i < NR; ++i) load_b(st[i], i);
     __builtin_amdgcn_sched_barrier(0);
-    x_off = (uint32_t)(((size_t)tok * D + 32 * kt0 + kp) * 4);
+
+    // Activation tiles: A = x*s*d and Am = x*s*dmin, hi/lo, for all KT steps.
     const float amax = x_amax[tok];
     const float dmx = P.dmax[e * 3 + m];
-#pragma unroll
-    for (int s = 0; s < NR; ++s) load_a(st[s], s);
-    __builtin_amdgcn_sched_barrier(0);
     const float ascale = ar < nrows ? row_scale(amax, dmx) : 0.0f;
-    if ((tid & 15) == 0) s_inv[ar] = ascale != 0.0f ? 1.0f / ascale : 0.0f;
+    if (seg == 0) s_inv[ar] = ascale != 0.0f ? 1.0f / ascale : 0.0f;
+    const float *xr = xn + (size_t)tok * D + 32 * kt0 + seg * L;
+    const float *dr = P.pd[m] + (size_t)e * (DH / 256) + (size_t)b * D + 32 * kt0 + seg * L;
+    const float *dmr = P.pdm[m] + (size_t)e * (DH / 256) + (size_t)b * D + 32 * kt0 + seg * L;
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+        v4f xv[C / 4], dv[C / 4], mv[C / 4];
+#pragma unroll
+        for (int i = 0; i < C / 4; ++i) {
+            xv[i] = *reinterpret_cast<const v4f *>(xr + ch * C + 4 * i);
+            dv[i] = *reinterpret_cast<const v4f *>(dr + ch * C + 4 * i);
+            mv[i] = *reinterpret_cast<const v4f *>(dmr + ch * C + 4 * i);
+        }
+#pragma unroll
+        for (int o = 0; o < C / 8; ++o) {  // groups of 8 values: one 16-byte LDS store per array
+            const int kk = seg * L + ch * C + 8 * o;  // within the slice
+            const int kt = kk >> 5, ko = kk & 31;
+            uint32_t hi[4], lo[4], mh[4], ml[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const v4f x4 = xv[2 * o + (j >> 1)], d4 = dv[2 * o + (j >> 1)], m4 = mv[2 * o + (j >> 1)];
+                const int u = 2 * (j & 1);
+                const float x0 = x4[u] * ascale, x1 = x4[u + 1] * ascale;
+                split2(x0 * d4[u], x1 * d4[u + 1], hi[j], lo[j]);
+                split2(x0 * m4[u], x1 * m4[u + 1], mh[j], ml[j]);
+            }
+            const int w0 = (ar * ORN_AST + ko) >> 1;
+            *reinterpret_cast<uint4 *>(&As[kt][0][w0]) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+            *reinterpret_cast<uint4 *>(&As[kt][1][w0]) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+            *reinterpret_cast<uint4 *>(&As[kt][2][w0]) = make_uint4(mh[0], mh[1], mh[2], mh[3]);
+            *reinterpret_cast<uint4 *>(&As[kt][3][w0]) = make_uint4(ml[0], ml[1], ml[2], ml[3]);
+        }
+    }
+    __syncthreads();
 
     v4f acc[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[j] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
     v4f accm = {0.0f, 0.0f, 0.0f, 0.0f};
-    const int aw = (ar * ORN_AST + kp) >> 1;  // this thread's LDS word
-    const int ro = c * ORN_AST + 8 * g;       // this lane's A operand (halves)
-
-    auto step = [&](GuStage &st, int buf, bool refill, int ktn) {
-        {
-            const float x0 = st.x.x * ascale, x1 = st.x.y * ascale;
-            uint32_t hi, lo, mhi, mlo;
-            split2(x0 * st.d.x, x1 * st.d.y, hi, lo);
-            split2(x0 * st.dm.x, x1 * st.dm.y, mhi, mlo);
-            As.w[buf][0][aw] = hi;
-            As.w[buf][1][aw] = lo;
-            As.w[buf][2][aw] = mhi;
-            As.w[buf][3][aw] = mlo;
-        }
+    const int ro = c * ORN_AST + 8 * g;
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+        GuRing &r = st[kt % NR];
         v8h bq[4];
-        bq[0] = q4_b(st.q.x, st.s0);
-        bq[1] = q4_b(st.q.y, st.s0);
-        bq[2] = q4_b(st.q.z, st.s1);
-        bq[3] = q4_b(st.q.w, st.s1);
-        const uint4 mz = c < 2 ? st.mn : make_uint4(0u, 0u, 0u, 0u);  // columns 2..15: zero
+        bq[0] = q4_b(r.q.x, r.s0);
+        bq[1] = q4_b(r.q.y, r.s0);
+        bq[2] = q4_b(r.q.z, r.s1);
+        bq[3] = q4_b(r.q.w, r.s1);
+        const uint4 mz = c < 2 ? r.mn : make_uint4(0u, 0u, 0u, 0u);
         const v8h bm = __builtin_bit_cast(v8h, mz);
         __builtin_amdgcn_sched_barrier(0);
-        if (refill) {
-            load_b(st, ktn);
-            load_a(st, ktn);
-        }
+        if (kt + NR < KT) load_b(r, kt + NR);
         __builtin_amdgcn_sched_barrier(0);
-        __syncthreads();
-        const _Float16 *A0 = reinterpret_cast<const _Float16 *>(As.w[buf][0]);
-        const _Float16 *A1 = reinterpret_cast<const _Float16 *>(As.w[buf][1]);
-        const _Float16 *A2 = reinterpret_cast<const _Float16 *>(As.w[buf][2]);
-        const _Float16 *A3 = reinterpret_cast<const _Float16 *>(As.w[buf][3]);
-        const v8h ahi = *reinterpret_cast<const v8h *>(A0 + ro);
-        const v8h alo = *reinterpret_cast<const v8h *>(A1 + ro);
-        const v8h mhi = *reinterpret_cast<const v8h *>(A2 + ro);
-        const v8h mlo = *reinterpret_cast<const v8h *>(A3 + ro);
+        const _Float16 *A = reinterpret_cast<const _Float16 *>(As[kt][0]);
+        const v8h ahi = *reinterpret_cast<const v8h *>(A + ro);
+        const v8h alo = *reinterpret_cast<const v8h *>(A + 16 * ORN_AST + ro);
+        const v8h mhi = *reinterpret_cast<const v8h *>(A + 32 * ORN_AST + ro);
+        const v8h mlo = *reinterpret_cast<const v8h *>(A + 48 * ORN_AST + ro);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             acc[j] = mfma(ahi, bq[j], acc[j]);
@@ -196,49 +190,44 @@ __global__ void __launch_bounds__(256)
         }
         accm = mfma(mhi, bm, accm);
         accm = mfma(mlo, bm, accm);
-    };
+    }
 
-#pragma unroll
-    for (int kt = 0; kt < KT; ++kt) step(st[kt % NR], kt & 1, kt + NR < KT, kt + NR);
-
-    // y = (acc - dmin term of the column's sub-block) / s_row.  accm of lane
-    // (g, c < 2) holds rows 4g..4g+3 of sub-block 2w + c.
     float *row0 = gu + ((size_t)kslice * rows_max + itm.y) * (2 * H);
     const int colb = m * H + 256 * b + 64 * wave + c;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int row = 4 * g + r;
+    for (int rr = 0; rr < 4; ++rr) {
+        const int row = 4 * g + rr;
         const float si = s_inv[row];
-        const float m0 = __shfl(accm[r], 16 * g, 64);
-        const float m1 = __shfl(accm[r], 16 * g + 1, 64);
+        const float m0 = __shfl(accm[rr], 16 * g, 64);
+        const float m1 = __shfl(accm[rr], 16 * g + 1, 64);
         if (row < nrows) {
             float *o = row0 + (size_t)row * (2 * H) + colb;
-            o[0] = (acc[0][r] - m0) * si;
-            o[16] = (acc[1][r] - m0) * si;
-            o[32] = (acc[2][r] - m1) * si;
-            o[48] = (acc[3][r] - m1) * si;
+            o[0] = (acc[0][rr] - m0) * si;
+            o[16] = (acc[1][rr] - m0) * si;
+            o[32] = (acc[2][rr] - m1) * si;
+            o[48] = (acc[3][rr] - m1) * si;
         }
     }
 }
 
 // ---------------------------------------------------------------------------
 // Down (Q6_K).  Logical tile = (item * ks + kslice) * (D/256) + b; output
-// dn[kslice][row][n].
+// dn[kslice][row][n].  Same structure (activation = mid row, hi/lo of
+// mid*s*d).
 // ---------------------------------------------------------------------------
-struct DnStage {
-    uint4 q0, q1;  // q + 32 of column tiles 4w..4w+3, 8 bytes per tile
-    uint4 sc[4];   // scales of tiles 4w+j at k = 8g..8g+7
-    v2f x, d;      // mid row tid/16 at k pair 2*(tid%16), its d
+struct DnRing {
+    uint4 q0, q1, sc[4];
 };
 
 template <int NR, int KT>
 __global__ void __launch_bounds__(256)
     k_down_dec(ornk_dn_prefill P, const float *__restrict__ mid,
-               const float *__restrict__ mid_amax, const int *__restrict__ ctl,
-               const int4 *__restrict__ items, float *__restrict__ dn, int D, int H, int ks,
-               int rows_max)
+                const float *__restrict__ mid_amax, const int *__restrict__ ctl,
+                const int4 *__restrict__ items, float *__restrict__ dn, int D, int H, int ks,
+                int rows_max)
 {
-    __shared__ __align__(16) DecTiles<2> As;
+    constexpr int L = 2 * KT, C = L < 16 ? L : 16, NCH = L / C;
+    __shared__ __align__(16) uint32_t As[KT][2][16 * ORN_AST / 2];
     __shared__ float s_inv[16];
 
     const int NBD = D >> 8;
@@ -257,83 +246,93 @@ __global__ void __launch_bounds__(256)
     const int kt0 = kslice * KT;
     const size_t DH = (size_t)D * H;
 
-    const uint32_t EQ = (uint32_t)DH, ES = (uint32_t)(DH / 8), ED = (uint32_t)(DH / 64);
+    const uint32_t EQ = (uint32_t)DH, ES = (uint32_t)(DH / 8);
     const rsrc_t rq = make_rsrc(P.dq + (size_t)e * EQ, EQ);
     const rsrc_t rs = make_rsrc(reinterpret_cast<const uint8_t *>(P.dsc) + (size_t)e * ES, ES);
-    const rsrc_t rd = make_rsrc(reinterpret_cast<const uint8_t *>(P.dd) + (size_t)e * ED, ED);
-    const rsrc_t rx = make_rsrc(mid, (uint32_t)((size_t)rows_max * H * 4));
     const uint32_t qstep = (uint32_t)NBD * 8192, sstep = (uint32_t)NBD * 1024;
     const uint32_t q_off = (uint32_t)(((size_t)kt0 * NBD + b) * 8192) + (wave * 64 + lane) * 32;
     const uint32_t s_off = (uint32_t)((((size_t)kt0 * NBD + b) * 16 + 4 * wave) * 64) + 16 * g;
-    const int ar = tid >> 4, kp = 2 * (tid & 15);
-    const int arow = ar < nrows ? ar : 0;
-    const uint32_t x_off = (uint32_t)(((size_t)(itm.y + arow) * H + 32 * kt0 + kp) * 4);
-    const uint32_t d_off = (uint32_t)(((size_t)b * H + 32 * kt0 + kp) * 4);
-
-    auto load = [&](DnStage &st, int kt) {
+    auto load_b = [&](DnRing &st, int kt) {
         st.q0 = bload16(rq, q_off, kt * qstep);
         st.q1 = bload16(rq, q_off + 16, kt * qstep);
 #pragma unroll
         for (int j = 0; j < 4; ++j) st.sc[j] = bload16(rs, s_off + 64 * j, kt * sstep);
-        st.x = bload8f(rx, x_off, kt * 128);
-        st.d = bload8f(rd, d_off, kt * 128);
     };
+
+    const int ar = tid >> 4, seg = tid & 15;
+    const int arow = ar < nrows ? ar : 0;
+    DnRing st[NR];
+#pragma unroll
+    for (int i = 0; i < NR; ++i) load_b(st[i], i);
+    __builtin_amdgcn_sched_barrier(0);
 
     const float amax = mid_amax[itm.y + arow];
     const float dmx = P.dmax[e * 3 + 2];
-    DnStage st[NR];
-#pragma unroll
-    for (int s = 0; s < NR; ++s) load(st[s], s);
-    __builtin_amdgcn_sched_barrier(0);
     const float ascale = ar < nrows ? row_scale(amax, dmx) : 0.0f;
-    if ((tid & 15) == 0) s_inv[ar] = ascale != 0.0f ? 1.0f / ascale : 0.0f;
+    if (seg == 0) s_inv[ar] = ascale != 0.0f ? 1.0f / ascale : 0.0f;
+    const float *xr = mid + (size_t)(itm.y + arow) * H + 32 * kt0 + seg * L;
+    const float *dr = P.dd + (size_t)e * (DH / 256) + (size_t)b * H + 32 * kt0 + seg * L;
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+        v4f xv[C / 4], dv[C / 4];
+#pragma unroll
+        for (int i = 0; i < C / 4; ++i) {
+            xv[i] = *reinterpret_cast<const v4f *>(xr + ch * C + 4 * i);
+            dv[i] = *reinterpret_cast<const v4f *>(dr + ch * C + 4 * i);
+        }
+#pragma unroll
+        for (int o = 0; o < C / 8; ++o) {
+            const int kk = seg * L + ch * C + 8 * o;
+            const int kt = kk >> 5, ko = kk & 31;
+            uint32_t hi[4], lo[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const v4f x4 = xv[2 * o + (j >> 1)], d4 = dv[2 * o + (j >> 1)];
+                const int u = 2 * (j & 1);
+                split2(x4[u] * ascale * d4[u], x4[u + 1] * ascale * d4[u + 1], hi[j], lo[j]);
+            }
+            const int w0 = (ar * ORN_AST + ko) >> 1;
+            *reinterpret_cast<uint4 *>(&As[kt][0][w0]) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+            *reinterpret_cast<uint4 *>(&As[kt][1][w0]) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+        }
+    }
+    __syncthreads();
 
     v4f acc[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[j] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
-    const int aw = (ar * ORN_AST + kp) >> 1;
     const int ro = c * ORN_AST + 8 * g;
-
-    auto step = [&](DnStage &st, int buf, bool refill, int ktn) {
-        {
-            uint32_t hi, lo;
-            split2(st.x.x * ascale * st.d.x, st.x.y * ascale * st.d.y, hi, lo);
-            As.w[buf][0][aw] = hi;
-            As.w[buf][1][aw] = lo;
-        }
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+        DnRing &r = st[kt % NR];
         v8h bq[4];
-        bq[0] = q6_b(st.q0.x, st.q0.y, st.sc[0]);
-        bq[1] = q6_b(st.q0.z, st.q0.w, st.sc[1]);
-        bq[2] = q6_b(st.q1.x, st.q1.y, st.sc[2]);
-        bq[3] = q6_b(st.q1.z, st.q1.w, st.sc[3]);
+        bq[0] = q6_b(r.q0.x, r.q0.y, r.sc[0]);
+        bq[1] = q6_b(r.q0.z, r.q0.w, r.sc[1]);
+        bq[2] = q6_b(r.q1.x, r.q1.y, r.sc[2]);
+        bq[3] = q6_b(r.q1.z, r.q1.w, r.sc[3]);
         __builtin_amdgcn_sched_barrier(0);
-        if (refill) load(st, ktn);
+        if (kt + NR < KT) load_b(r, kt + NR);
         __builtin_amdgcn_sched_barrier(0);
-        __syncthreads();
-        const v8h ahi = *reinterpret_cast<const v8h *>(
-            reinterpret_cast<const _Float16 *>(As.w[buf][0]) + ro);
-        const v8h alo = *reinterpret_cast<const v8h *>(
-            reinterpret_cast<const _Float16 *>(As.w[buf][1]) + ro);
+        const _Float16 *A = reinterpret_cast<const _Float16 *>(As[kt][0]);
+        const v8h ahi = *reinterpret_cast<const v8h *>(A + ro);
+        const v8h alo = *reinterpret_cast<const v8h *>(A + 16 * ORN_AST + ro);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             acc[j] = mfma(ahi, bq[j], acc[j]);
             acc[j] = mfma(alo, bq[j], acc[j]);
         }
-    };
-
-#pragma unroll
-    for (int kt = 0; kt < KT; ++kt) step(st[kt % NR], kt & 1, kt + NR < KT, kt + NR);
+    }
 
     float *row0 = dn + ((size_t)kslice * rows_max + itm.y) * D;
     const int colb = 256 * b + 64 * wave + c;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int row = 4 * g + r;
+    for (int rr = 0; rr < 4; ++rr) {
+        const int row = 4 * g + rr;
         const float si = s_inv[row];
         if (row < nrows) {
             float *o = row0 + (size_t)row * D + colb;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) o[16 * j] = acc[j][r] * si;
+            for (int j = 0; j < 4; ++j) o[16 * j] = acc[j][rr] * si;
         }
     }
 }
@@ -341,11 +340,11 @@ __global__ void __launch_bounds__(256)
 }  // namespace
 
 // Decode instances: work items of <= 16 rows; KT = D/32/ks (gate/up) or
-// H/32/ks (down) reduction steps per slice, one of the instantiated counts.
+// H/32/ks (down) reduction steps per slice, 4 or 8 (the LDS holds a slice's
+// activation tiles: 5 KB per step for gate/up, 2.5 KB for down).
 extern "C" int ornk_dec_supported(int kt_gu, int kt_dn)
 {
-    auto ok = [](int kt) { return kt == 4 || kt == 8 || kt == 16 || kt == 32; };
-    return ok(kt_gu) && ok(kt_dn);
+    return (kt_gu == 4 || kt_gu == 8) && (kt_dn == 4 || kt_dn == 8);
 }
 
 extern "C" int ornk_moe_gateup_dec(const ornk_moe_args *a, hipStream_t s)
@@ -365,12 +364,8 @@ extern "C" int ornk_moe_gateup_dec(const ornk_moe_args *a, hipStream_t s)
     hipLaunchKernelGGL((k_gateup_dec<ORN_DEC_NR, K>), grid, dim3(256), 0, s, a->gu_pf, xin,   \
                        a->x_amax, a->ctl, reinterpret_cast<const int4 *>(a->items),           \
                        a->row_token, a->gu_part, a->T, a->D, a->H, ks, a->rows_max)
-    switch (KT) {
-    case 4: ORN_GU_DEC(4); break;
-    case 8: ORN_GU_DEC(8); break;
-    case 16: ORN_GU_DEC(16); break;
-    default: ORN_GU_DEC(32); break;
-    }
+    if (KT == 4) ORN_GU_DEC(4);
+    else ORN_GU_DEC(8);
 #undef ORN_GU_DEC
     return hipGetLastError();
 }
@@ -387,12 +382,8 @@ extern "C" int ornk_moe_down_dec(const ornk_moe_args *a, hipStream_t s)
     hipLaunchKernelGGL((k_down_dec<ORN_DEC_NR, K>), grid, dim3(256), 0, s, a->dn_pf, a->mid, \
                        a->mid_amax, a->ctl, reinterpret_cast<const int4 *>(a->items),        \
                        a->dn_part, a->D, a->H, ks, a->rows_max)
-    switch (KT) {
-    case 4: ORN_DN_DEC(4); break;
-    case 8: ORN_DN_DEC(8); break;
-    case 16: ORN_DN_DEC(16); break;
-    default: ORN_DN_DEC(32); break;
-    }
+    if (KT == 4) ORN_DN_DEC(4);
+    else ORN_DN_DEC(8);
 #undef ORN_DN_DEC
     return hipGetLastError();
 }

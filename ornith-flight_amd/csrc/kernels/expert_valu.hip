@@ -1,7 +1,7 @@
 // SPDX-License-Identifier: MIT
 //
-// Routed-MoE expert path for decode-shaped work (few tokens per expert):
-// dispatch -> fused Q4_K dequant-matvec for gate+up -> SiLU(gate)*up ->
+// Routed-MoE expert path on the vector ALUs (few tokens per expert):
+// fused Q4_K dequant-matvec for gate+up -> SiLU(gate)*up ->
 // Q6_K dequant-matvec for down -> weighted combine.  fp32 VALU arithmetic
 // (explicit fmaf), weights decoded in registers straight from the resident
 // K-quant blocks with 128-bit loads; each output is reduced in a fixed order
@@ -22,89 +22,6 @@
 
 
 namespace {
-
-// ---------------------------------------------------------------------------
-// Dispatch: one block.  List position j: 0 = shared expert (expert id E),
-// j >= 1 = routed expert j-1.  Produces the active slots (shared first, then
-// experts in ascending id), their row ranges, the work items (<= tchunk
-// rows each) and the row <-> (token, selection slot) maps.
-// ---------------------------------------------------------------------------
-__device__ int block_excl_scan(int v, int *buf, int *total)
-{
-    const int tid = threadIdx.x, n = blockDim.x;
-    buf[tid] = v;
-    __syncthreads();
-    for (int off = 1; off < n; off <<= 1) {
-        int add = tid >= off ? buf[tid - off] : 0;
-        __syncthreads();
-        buf[tid] += add;
-        __syncthreads();
-    }
-    int incl = buf[tid];
-    if (total) *total = buf[n - 1];
-    __syncthreads();
-    return incl - v;
-}
-
-__global__ void __launch_bounds__(1024)
-    k_dispatch(const uint32_t *__restrict__ idx, const float *__restrict__ w, int T, int k, int E,
-               int has_shared, int *ctl, int *slot_expert, int *slot_off, int *slot_cnt,
-               int *row_token, int *pair_row, int4 *items, int items_max, int tchunk)
-{
-    __shared__ int cnt[1024];
-    __shared__ int cursor[1024];
-    __shared__ int rowoff[1024];
-    __shared__ int scanbuf[1024];
-    const int tid = threadIdx.x;
-    const int NJ = E + 1;
-    cnt[tid] = 0;
-    cursor[tid] = 0;
-    __syncthreads();
-    const int P = T * k;
-    for (int p = tid; p < P; p += blockDim.x)
-        if (!(w[p] < 1e-6f) && idx[p] < (uint32_t)E) atomicAdd(&cnt[idx[p] + 1], 1);
-    if (tid == 0) cnt[0] = has_shared ? T : 0;
-    __syncthreads();
-
-    const int c = tid < NJ ? cnt[tid] : 0;
-    const int flag = c > 0 ? 1 : 0;
-    const int nit = (c + tchunk - 1) / tchunk;
-    int n_slots, n_rows, n_items;
-    const int slot = block_excl_scan(flag, scanbuf, &n_slots);
-    const int roff = block_excl_scan(c, scanbuf, &n_rows);
-    const int ioff = block_excl_scan(nit, scanbuf, &n_items);
-    rowoff[tid] = roff;
-    if (flag) {
-        slot_expert[slot] = tid == 0 ? E : tid - 1;
-        slot_off[slot] = roff;
-        slot_cnt[slot] = c;
-        for (int q = 0; q < nit && ioff + q < items_max; ++q) {
-            const int r0 = q * tchunk;
-            items[ioff + q] = make_int4(slot, roff + r0, min(tchunk, c - r0), tid == 0 ? E : tid - 1);
-        }
-    }
-    if (tid == 0) {
-        ctl[0] = n_slots;
-        ctl[1] = n_items < items_max ? n_items : items_max;
-        ctl[2] = n_rows;
-    }
-    __syncthreads();
-
-    for (int p = tid; p < P; p += blockDim.x) {
-        // Skip rule of model.c:1066; an index outside [0, E) cannot come out
-        // of the router but is treated as skipped rather than trusted.
-        if (w[p] < 1e-6f || idx[p] >= (uint32_t)E) {
-            pair_row[p] = -1;
-            continue;
-        }
-        const int j = (int)idx[p] + 1;
-        const int r = rowoff[j] + atomicAdd(&cursor[j], 1);
-        row_token[r] = p / k;
-        pair_row[p] = r;
-    }
-    if (has_shared)
-        for (int t = tid; t < T; t += blockDim.x) row_token[rowoff[0] + t] = t;
-}
 
 // ---------------------------------------------------------------------------
 // Gate+up: split-K over the D input rows.  Block = 4 waves; work item = up
@@ -284,9 +201,12 @@ __global__ void __launch_bounds__(256)
 // the shared expert (unclamped silu, gpu.c:176-186); all others are routed
 // (clamped silu, model.c:340-344).
 // ---------------------------------------------------------------------------
-__global__ void k_mid(const float *__restrict__ gu_part, const int *__restrict__ ctl,
-                      float *__restrict__ mid, int H, int ks, int rows_max, int shared_rows,
-                      float *__restrict__ row_amax)
+// KMAX > 0 (= ks): the partials of a value are loaded together, one memory
+// round trip per thread; KMAX = 0: any ks, four partials at a time.
+template <int KMAX>
+__global__ void __launch_bounds__(256)
+    k_mid(const float *__restrict__ gu_part, const int *__restrict__ ctl, float *__restrict__ mid,
+          int H, int ks, int rows_max, int shared_rows, float *__restrict__ row_amax)
 {
     __shared__ float red[4];
     const int r = blockIdx.x;
@@ -297,18 +217,33 @@ __global__ void k_mid(const float *__restrict__ gu_part, const int *__restrict__
     for (int h = threadIdx.x; h < H; h += blockDim.x) {
         const float *p = gu_part + (size_t)r * H2 + h;
         float g = 0.0f, u = 0.0f;
-        int s = 0;
-        for (; s + 4 <= ks; s += 4) {
-            const float g0 = p[(s + 0) * kstride], g1 = p[(s + 1) * kstride];
-            const float g2 = p[(s + 2) * kstride], g3 = p[(s + 3) * kstride];
-            const float u0 = p[(s + 0) * kstride + H], u1 = p[(s + 1) * kstride + H];
-            const float u2 = p[(s + 2) * kstride + H], u3 = p[(s + 3) * kstride + H];
-            g += g0; g += g1; g += g2; g += g3;
-            u += u0; u += u1; u += u2; u += u3;
-        }
-        for (; s < ks; ++s) {
-            g += p[s * kstride];
-            u += p[s * kstride + H];
+        if (KMAX > 0) {
+            float gv[KMAX > 0 ? KMAX : 1], uv[KMAX > 0 ? KMAX : 1];
+#pragma unroll
+            for (int s = 0; s < KMAX; ++s) {
+                const size_t o = (size_t)(s < ks ? s : 0) * kstride;
+                gv[s] = p[o];
+                uv[s] = p[o + H];
+            }
+#pragma unroll
+            for (int s = 0; s < KMAX; ++s) {
+                g = s < ks ? g + gv[s] : g;
+                u = s < ks ? u + uv[s] : u;
+            }
+        } else {
+            int s = 0;
+            for (; s + 4 <= ks; s += 4) {
+                const float g0 = p[(s + 0) * kstride], g1 = p[(s + 1) * kstride];
+                const float g2 = p[(s + 2) * kstride], g3 = p[(s + 3) * kstride];
+                const float u0 = p[(s + 0) * kstride + H], u1 = p[(s + 1) * kstride + H];
+                const float u2 = p[(s + 2) * kstride + H], u3 = p[(s + 3) * kstride + H];
+                g += g0; g += g1; g += g2; g += g3;
+                u += u0; u += u1; u += u2; u += u3;
+            }
+            for (; s < ks; ++s) {
+                g += p[s * kstride];
+                u += p[s * kstride + H];
+            }
         }
         float act;
         if (r < shared_rows) {
@@ -489,74 +424,57 @@ __global__ void __launch_bounds__(256)
 //   out = (resid + y_shared) + sum_a w_a * y_a   (selection order, skipped
 //   pairs excluded), each y the fixed-order sum of its split-K partials.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float sum_parts(const float *p, size_t kstride, int ks)
+// KS = ks (compile time, 1..16) and K = k (8, or 0: any k <= 16): every
+// load of a thread is issued before the first add.
+template <int KS, int K>
+__global__ void __launch_bounds__(256)
+    k_combine(const float *__restrict__ dn_part, const int *__restrict__ pair_row,
+              const float *__restrict__ w, const float *__restrict__ resid,
+              float *__restrict__ out, int T, int D, int k, int rows_max, int has_shared)
 {
-    float y = 0.0f;
-    int s = 0;
-    for (; s + 4 <= ks; s += 4) {
-        const float v0 = p[(s + 0) * kstride], v1 = p[(s + 1) * kstride];
-        const float v2 = p[(s + 2) * kstride], v3 = p[(s + 3) * kstride];
-        y += v0; y += v1; y += v2; y += v3;
-    }
-    for (; s < ks; ++s) y += p[s * kstride];
-    return y;
-}
-
-__global__ void k_combine(const float *__restrict__ dn_part, const int *__restrict__ pair_row,
-                          const float *__restrict__ w, const float *__restrict__ resid,
-                          float *__restrict__ out, int T, int D, int k, int ks, int rows_max,
-                          int has_shared)
-{
+    constexpr int KK = K > 0 ? K : 16;
     const int t = blockIdx.x;
     const int c = blockIdx.y * blockDim.x + threadIdx.x;
     if (t >= T || c >= D) return;
+    const int kk = K > 0 ? K : k;
     const size_t kstride = (size_t)rows_max * D;
-    // Row indices and weights first, then every partial of every row in
-    // flight at once (excluded pairs read row 0 and are dropped below).
-    int rr[16];
-    float ww[16], y[16];
+    int rr[KK];
+    float ww[KK];
 #pragma unroll
-    for (int a = 0; a < 16; ++a) {
-        const int r = a < k ? pair_row[t * k + a] : -1;
-        rr[a] = r;
-        ww[a] = a < k ? w[t * k + a] : 0.0f;
-        y[a] = 0.0f;
+    for (int a = 0; a < KK; ++a) {
+        const int ai = a < kk ? a : 0;  // slots past k re-read slot 0, dropped below
+        rr[a] = pair_row[t * k + ai];
+        ww[a] = w[t * k + ai];
     }
-    int ro[16];
+    const float rv = resid ? resid[(size_t)t * D + c] : 0.0f;
+    float ysh = 0.0f, y[KK];
 #pragma unroll
-    for (int a = 0; a < 16; ++a) ro[a] = rr[a] < 0 ? 0 : rr[a];
-    float ysh = 0.0f;
-    int sidx = 0;
-    // Split-K partials in fixed order, four steps of loads in flight at once.
-    for (; sidx + 4 <= ks; sidx += 4) {
-        float vs[4], v[4][16];
+    for (int a = 0; a < KK; ++a) y[a] = 0.0f;
+    // Split-K partials in fixed order, up to four steps of loads at once.
+    constexpr int CH = KS < 4 ? KS : 4;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const float *base = dn_part + (sidx + u) * kstride + c;
+    for (int s0 = 0; s0 < KS; s0 += CH) {
+        float vs[CH], v[CH][KK];
+#pragma unroll
+        for (int u = 0; u < CH; ++u) {
+            const float *base = dn_part + (size_t)(s0 + u) * kstride + c;
             vs[u] = has_shared ? base[(size_t)t * D] : 0.0f;
 #pragma unroll
-            for (int a = 0; a < 16; ++a) v[u][a] = a < k ? base[(size_t)ro[a] * D] : 0.0f;
+            for (int a = 0; a < KK; ++a) v[u][a] = base[(size_t)(rr[a] < 0 ? 0 : rr[a]) * D];
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < CH; ++u) {
             ysh += vs[u];
 #pragma unroll
-            for (int a = 0; a < 16; ++a) y[a] += v[u][a];
+            for (int a = 0; a < KK; ++a) y[a] += v[u][a];
         }
     }
-    for (; sidx < ks; ++sidx) {
-        const float *base = dn_part + sidx * kstride + c;
-        if (has_shared) ysh += base[(size_t)t * D];
-#pragma unroll
-        for (int a = 0; a < 16; ++a)
-            if (a < k) y[a] += base[(size_t)ro[a] * D];
-    }
-    float acc = resid ? resid[(size_t)t * D + c] : 0.0f;
+    float acc = rv;
     if (has_shared) acc = acc + ysh;
     float routed = 0.0f;
 #pragma unroll
-    for (int a = 0; a < 16; ++a)
-        if (a < k && rr[a] >= 0) routed += ww[a] * y[a];
+    for (int a = 0; a < KK; ++a)
+        if (a < kk && rr[a] >= 0) routed += ww[a] * y[a];
     out[(size_t)t * D + c] = acc + routed;
 }
 
@@ -567,16 +485,6 @@ extern "C" int ornk_moe_norm(const ornk_moe_args *a, hipStream_t s)
 {
     if (!a->apply_norm) return hipSuccess;
     return ornk_rmsnorm(a->xn, a->x, a->norm_w, a->T, a->D, s);
-}
-
-extern "C" int ornk_moe_dispatch(const ornk_moe_args *a, hipStream_t s)
-{
-    if (a->E + 1 > 1024) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), 0, s, a->idx, a->w, a->T, a->k, a->E,
-                       a->has_shared, a->ctl, a->slot_expert, a->slot_off, a->slot_cnt,
-                       a->row_token, a->pair_row, reinterpret_cast<int4 *>(a->items),
-                       a->items_max, a->tchunk);
-    return hipGetLastError();
 }
 
 extern "C" int ornk_moe_gateup(const ornk_moe_args *a, hipStream_t s)
@@ -606,9 +514,19 @@ extern "C" int ornk_moe_gateup(const ornk_moe_args *a, hipStream_t s)
 
 extern "C" int ornk_moe_mid(const ornk_moe_args *a, hipStream_t s)
 {
-    hipLaunchKernelGGL(k_mid, dim3(a->rows_max), dim3(256), 0, s, a->gu_part, a->ctl, a->mid, a->H,
-                       a->ks_gu, a->rows_max, a->has_shared ? a->T : 0,
-                       a->use_mfma ? a->mid_amax : nullptr);
+#define ORN_MID(K)                                                                             \
+    hipLaunchKernelGGL(k_mid<K>, dim3(a->rows_max), dim3(256), 0, s, a->gu_part, a->ctl, a->mid, \
+                       a->H, a->ks_gu, a->rows_max, a->has_shared ? a->T : 0,                 \
+                       a->use_mfma ? a->mid_amax : nullptr)
+    switch (a->ks_gu) {
+    case 1: ORN_MID(1); break;
+    case 2: ORN_MID(2); break;
+    case 4: ORN_MID(4); break;
+    case 8: ORN_MID(8); break;
+    case 16: ORN_MID(16); break;
+    default: ORN_MID(0); break;
+    }
+#undef ORN_MID
     return hipGetLastError();
 }
 
@@ -643,8 +561,22 @@ extern "C" int ornk_moe_down(const ornk_moe_args *a, hipStream_t s)
 
 extern "C" int ornk_moe_combine(const ornk_moe_args *a, hipStream_t s)
 {
-    hipLaunchKernelGGL(k_combine, dim3(a->T, (a->D + 255) / 256), dim3(256), 0, s, a->dn_part,
-                       a->pair_row, a->w, a->resid, a->out, a->T, a->D, a->k, a->ks_dn, a->rows_max,
-                       a->has_shared);
+    const dim3 grid(a->T, (a->D + 255) / 256);
+#define ORN_CMB(KS, K)                                                                          \
+    hipLaunchKernelGGL((k_combine<KS, K>), grid, dim3(256), 0, s, a->dn_part, a->pair_row, a->w, \
+                       a->resid, a->out, a->T, a->D, a->k, a->rows_max, a->has_shared)
+#define ORN_CMB_K(KS)                  \
+    if (a->k == 8) ORN_CMB(KS, 8);     \
+    else ORN_CMB(KS, 0)
+    switch (a->ks_dn) {
+    case 1: ORN_CMB_K(1); break;
+    case 2: ORN_CMB_K(2); break;
+    case 4: ORN_CMB_K(4); break;
+    case 8: ORN_CMB_K(8); break;
+    case 16: ORN_CMB_K(16); break;
+    default: return hipErrorInvalidValue;
+    }
+#undef ORN_CMB_K
+#undef ORN_CMB
     return hipGetLastError();
 }

@@ -6,12 +6,11 @@
 // from 0.0f, of the fp32 products x[d]*W[d*E+e], d ascending.  Selection is
 // exchange selection with strict '>' (model.c:301-305 / 1040-1048).
 //
-// The MoE path computes every logit with exactly that arithmetic: one lane
-// per (token, expert) chain, all chains in parallel (k_router_seq), so the
-// logits are bit-identical to the reference's by construction.  Selection
-// (k_select) takes the top k+1 by (value desc, index asc); when those values
-// are pairwise distinct, exchange selection returns exactly that order, and
-// otherwise (ties, NaN/Inf) one lane runs the literal exchange selection.
+// The MoE path computes every logit with exactly that arithmetic, one chain
+// per (token, expert), all chains in parallel (k_router_dpp for decode-sized
+// batches, k_router_dec / k_router_seq above), so the logits are
+// bit-identical to the reference's by construction.  Top-k selection and
+// the dispatch that follows it: dispatch.hip.
 #include "common.h"
 #include "launch.h"
 
@@ -418,166 +417,6 @@ __global__ void __launch_bounds__(64)
 }
 
 // ---------------------------------------------------------------------------
-// Top-k selection, one wave per token, E <= 256 (lane holds experts
-// lane + 64*i).  Keys order (value desc, index asc) for non-NaN values.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ uint64_t sel_key(float v, int e)
-{
-    uint32_t u = __float_as_uint(v);
-    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return ((uint64_t)u << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)e);
-}
-
-__device__ __forceinline__ float key_value(uint64_t k)
-{
-    uint32_t u = (uint32_t)(k >> 32);
-    u = (u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u;
-    return __uint_as_float(u);
-}
-
-__device__ __forceinline__ uint64_t wave_max_key(uint64_t k)
-{
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)k, off, 64);
-        const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(k >> 32), off, 64);
-        const uint64_t o = ((uint64_t)hi << 32) | lo;
-        k = o > k ? o : k;
-    }
-    return k;
-}
-
-__device__ __forceinline__ float wave_sum(float v)
-{
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
-// Renormalised mode (model.c:301-317): exchange selection on the logits,
-// softmax over the k selected with the first as max.  Literal mode
-// (model.c:1027-1049): softmax over all E, exchange selection on the
-// probabilities, weights = those probabilities.
-//
-// Fast path: the top k+1 logits are finite and pairwise distinct, so
-// exchange selection yields them in value order; in the literal mode they
-// must also be more than 1e-5 apart, so that their probabilities (relative
-// gaps >= 1e-5, far above the few ulps expf and the division can move them)
-// keep that order and cannot round to equal values.  Otherwise lane 0
-// runs the reference's selection literally on this device's values.
-__global__ void __launch_bounds__(256)
-    k_select(const float *__restrict__ logits, int T, int E, int k, int mode,
-             uint32_t *__restrict__ idx_out, float *__restrict__ w_out, int *n_slow)
-{
-    __shared__ float sv[4][256];
-    __shared__ int si[4][256];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int t = blockIdx.x * 4 + wave;
-    if (t >= T) return;  // a wave is a token: no block-wide barrier below
-    const float *lg = logits + (size_t)t * E;
-    uint32_t *io = idx_out + (size_t)t * k;
-    float *wo = w_out + (size_t)t * k;
-
-    float v[4];
-    uint64_t key[4];
-    bool bad = false;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int e = lane + 64 * i;
-        const bool valid = e < E;
-        v[i] = valid ? lg[e] : 0.0f;
-        if (valid && !isfinite(v[i])) bad = true;
-        key[i] = valid ? sel_key(v[i], e) : 0ull;  // 0: below every valid key
-    }
-    bool slow = __ballot(bad) != 0ull;
-
-    // Lane r < k ends up holding the r-th selected (value, index).
-    float my_v = 0.0f, mx = 0.0f;
-    int my_e = 0;
-    if (!slow) {
-        float prev = 0.0f;
-        const int rounds = k < E ? k + 1 : k;
-        for (int r = 0; r < rounds; ++r) {
-            uint64_t best = key[0];
-#pragma unroll
-            for (int i = 1; i < 4; ++i) best = key[i] > best ? key[i] : best;
-            const uint64_t wb = wave_max_key(best);
-            const float val = key_value(wb);
-            const int e = (int)(0xFFFFFFFFu - (uint32_t)wb);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (key[i] == wb) key[i] = 0ull;
-            if (r == 0) mx = val;
-            if (r > 0) {
-                if (!(prev > val)) slow = true;
-                if (mode == 1 && !((double)prev - (double)val > 1e-5)) slow = true;
-            }
-            if (lane == r) { my_v = val; my_e = e; }
-            prev = val;
-        }
-    }
-
-    if (!slow) {
-        float w;
-        if (mode == 0) {
-            // model.c:307-317: s_i = expf(v_i - v_0), sequential sum, divide.
-            const float s_i = expf(my_v - mx);
-            float sum = 0.0f;
-            for (int i = 0; i < k; ++i) sum += __shfl(s_i, i, 64);
-            w = s_i / sum;
-        } else {
-            float s = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (lane + 64 * i < E) s += expf(v[i] - mx);
-            w = expf(my_v - mx) / wave_sum(s);
-        }
-        if (lane < k) { io[lane] = (uint32_t)my_e; wo[lane] = w; }
-        return;
-    }
-
-    // Literal path: the reference's selection, run by lane 0 on this
-    // device's values.
-    if (lane == 0 && n_slow) atomicAdd(n_slow, 1);
-    float *val = sv[wave];
-    int *ix = si[wave];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int e = lane + 64 * i;
-        if (e < E) { val[e] = v[i]; ix[e] = e; }
-    }
-    wave_sync();
-    if (lane == 0) {
-        if (mode == 1) {
-            // model.c:1027-1036: max by strict '>', expf, sequential sum, divide.
-            float m = val[0];
-            for (int e = 1; e < E; ++e) if (val[e] > m) m = val[e];
-            float sum = 0.0f;
-            for (int e = 0; e < E; ++e) { val[e] = expf(val[e] - m); sum += val[e]; }
-            for (int e = 0; e < E; ++e) val[e] = val[e] / sum;
-        }
-        // k passes of exchange selection (model.c:301-305 / 1040-1048).
-        for (int i = 0; i < k && i < E - 1; ++i)
-            for (int j = i + 1; j < E; ++j)
-                if (val[j] > val[i]) {
-                    const float ft = val[i]; val[i] = val[j]; val[j] = ft;
-                    const int it = ix[i]; ix[i] = ix[j]; ix[j] = it;
-                }
-        if (mode == 0) {
-            const float m = val[0];
-            float sum = 0.0f;
-            for (int i = 0; i < k; ++i) sum += expf(val[i] - m);
-            for (int i = 0; i < k; ++i) { io[i] = (uint32_t)ix[i]; wo[i] = expf(val[i] - m) / sum; }
-        } else {
-            for (int i = 0; i < k; ++i) { io[i] = (uint32_t)ix[i]; wo[i] = val[i]; }
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Exact top-k from given fp32 logits (gpu_topk_softmax and E > 256), one
-// block of 1024 threads per token, n <= 1024.
-// ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(1024)
     k_topk_exact(const float *logits, int n, int k, int mode, uint32_t *idx_out, float *w_out,
                  int *n_exact)
@@ -651,7 +490,7 @@ extern "C" int ornk_topk(const float *logits, int T, int E, int k, int mode, uin
 }
 
 // ---------------------------------------------------------------------------
-// MoE routing step: exact logits into a->logits, then top-k into a->idx/a->w.
+// MoE routing step: exact logits into a->logits (selection: dispatch.hip).
 // ---------------------------------------------------------------------------
 extern "C" int ornk_router_dpp_supported(int T, int D)
 {
@@ -685,9 +524,5 @@ extern "C" int ornk_moe_route(const ornk_moe_args *a, hipStream_t s)
         hipLaunchKernelGGL(k_router_dec, dim3((E + 63) / 64, T), dim3(64), sizeof(float) * (size_t)D,
                            s, xin, a->router, a->bias, T, D, E, a->logits, a->ctl);
     }
-    hipError_t err = hipGetLastError();
-    if (err != hipSuccess) return err;
-    hipLaunchKernelGGL(k_select, dim3((T + 3) / 4), dim3(256), 0, s, a->logits, T, E, a->k,
-                       a->mode, a->idx, a->w, a->ctl + 3);
     return hipGetLastError();
 }
