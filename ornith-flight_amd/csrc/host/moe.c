@@ -642,14 +642,15 @@ static plan_t make_plan(const ornith_moe_shape *sh, int T, int use_mfma)
         p.ks_gu = kg;
         p.ks_dn = kdn;
         if (p.tchunk <= 16) {
-            /* Decode kernels: slices of 4 or 8 reduction steps (the
-             * compiled counts).  Gate/up: about 2048 work groups over the
-             * estimated items, clamped to those counts; down: 8 steps. */
+            /* Decode kernels (slices of 4..32 reduction steps compiled).
+             * Gate/up: about 2048 work groups over the estimated items, slices
+             * of 4..16 steps (measured best: 16 at 16 tokens, 4 at 1 token);
+             * down: 8-step slices. */
             const int ng = 2048 / (est_items * 2 * (H / 256));
             int dg = pow2_floor(ng > 0 ? ng : 1);
             while (dg > 1 && (D / 32) % dg) dg /= 2;
             while (dg > 1 && D / 32 / dg < 4) dg /= 2;
-            while ((D / 32) % (2 * dg) == 0 && D / 32 / dg > 8) dg *= 2;
+            while ((D / 32) % (2 * dg) == 0 && D / 32 / dg > 16) dg *= 2;
             int dd = 1;
             while ((H / 32) % (2 * dd) == 0 && H / 32 / dd > 8) dd *= 2;
             if ((D / 32) % dg == 0 && (H / 32) % dd == 0 &&

@@ -338,7 +338,8 @@ __device__ void dispatch_group(DispatchLds &L, const IdxT *sel_idx, const float 
 __global__ void __launch_bounds__(1024)
     k_dispatch(const uint32_t *__restrict__ idx, const float *__restrict__ w, int T, int k, int E,
                int has_shared, int *ctl, int *slot_expert, int *slot_off, int *slot_cnt,
-               int *row_token, int *pair_row, int4 *items, int items_max, int tchunk)
+               int *row_token, int *pair_row, int4 *items, int items_max,
+               int tchunk)
 {
     __shared__ DispatchLds L;
     dispatch_group(L, idx, w, T, k, E, has_shared, ctl, slot_expert, slot_off, slot_cnt,

@@ -70,30 +70,34 @@ struct GuRing {
     uint4 mn;      // mins of sub-block 2w + (c & 1) at k = 8g..8g+7
 };
 
-template <int NR, int KT>
+template <int NR, int KT, int KC>
 __global__ void __launch_bounds__(256)
     k_gateup_dec(ornk_gu_prefill P, const float *__restrict__ xn,
-                  const float *__restrict__ x_amax, const int *__restrict__ ctl,
-                  const int4 *__restrict__ items, const int *__restrict__ row_token,
-                  float *__restrict__ gu, int T, int D, int H, int ks, int rows_max)
+                 const float *__restrict__ x_amax, const int *__restrict__ ctl,
+                 const int4 *__restrict__ items, const int *__restrict__ row_token,
+                 float *__restrict__ gu, int T, int D, int H, int ks, int rows_max)
 {
-    constexpr int L = 2 * KT, C = L < 16 ? L : 16, NCH = L / C;
-    __shared__ __align__(16) uint32_t As[KT][4][16 * ORN_AST / 2];
+    constexpr int NCHK = KT / KC, NBUF = NCHK > 1 ? 2 : 1;
+    constexpr int LC = 2 * KC;  // activation values a thread prepares per chunk
+    __shared__ __align__(16) uint32_t As[NBUF][KC][4][16 * ORN_AST / 2];
     __shared__ float s_inv[16];
 
+    // The item and the live item count are read together; work groups past
+    // the dispatched items then leave.
     const int NB = H >> 8;
     const int per_item = 2 * NB * ks;
-    const int n_live = ctl[1] * per_item;
-    if ((int)blockIdx.x >= n_live) return;
-    const int tile = xcd_remap(blockIdx.x, n_live);
+    const int tile = blockIdx.x;
     const int b = tile % NB;
     const int m = (tile / NB) & 1;
     const int kslice = (tile / (2 * NB)) % ks;
     const int item = tile / per_item;
+    const int tid = threadIdx.x;
+    const int n_items = ctl[1];
     const int4 itm = items[item];
+    if (item >= n_items) return;
     const int e = itm.w;
     const int nrows = itm.z;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, c = lane & 15;
     const int kt0 = kslice * KT;
     const size_t DH = (size_t)D * H;
@@ -114,34 +118,37 @@ __global__ void __launch_bounds__(256)
     };
 
     const int ar = tid >> 4, seg = tid & 15;
-    const int arow = ar < nrows ? ar : 0;
+    const int arow = ar < nrows ? ar : 0;  // rows past the item read a valid row, scaled by 0
     const int tok = row_token[itm.y + arow];
     GuRing st[NR];
 #pragma unroll
     for (int i = 0; i < NR; ++i) load_b(st[i], i);
     __builtin_amdgcn_sched_barrier(0);
 
-    // Activation tiles: A = x*s*d and Am = x*s*dmin, hi/lo, for all KT steps.
+    // Activation tiles: A = x*s*d and Am = x*s*dmin, hi/lo, one chunk of KC
+    // steps at a time (chunk ch in LDS buffer ch % 2).  Thread (ar, seg)
+    // owns the LC values seg*LC.. of row ar in every chunk.
     const float amax = x_amax[tok];
     const float dmx = P.dmax[e * 3 + m];
-    const float ascale = ar < nrows ? row_scale(amax, dmx) : 0.0f;
-    if (seg == 0) s_inv[ar] = ascale != 0.0f ? 1.0f / ascale : 0.0f;
-    const float *xr = xn + (size_t)tok * D + 32 * kt0 + seg * L;
-    const float *dr = P.pd[m] + (size_t)e * (DH / 256) + (size_t)b * D + 32 * kt0 + seg * L;
-    const float *dmr = P.pdm[m] + (size_t)e * (DH / 256) + (size_t)b * D + 32 * kt0 + seg * L;
+    const float *xr = xn + (size_t)tok * D + 32 * kt0 + seg * LC;
+    const float *dr = P.pd[m] + (size_t)e * (DH / 256) + (size_t)b * D + 32 * kt0 + seg * LC;
+    const float *dmr = P.pdm[m] + (size_t)e * (DH / 256) + (size_t)b * D + 32 * kt0 + seg * LC;
+    v4f xv[LC / 4], dv[LC / 4], mv[LC / 4];
+    auto a_load = [&](int ch) {
 #pragma unroll
-    for (int ch = 0; ch < NCH; ++ch) {
-        v4f xv[C / 4], dv[C / 4], mv[C / 4];
-#pragma unroll
-        for (int i = 0; i < C / 4; ++i) {
-            xv[i] = *reinterpret_cast<const v4f *>(xr + ch * C + 4 * i);
-            dv[i] = *reinterpret_cast<const v4f *>(dr + ch * C + 4 * i);
-            mv[i] = *reinterpret_cast<const v4f *>(dmr + ch * C + 4 * i);
+        for (int i = 0; i < LC / 4; ++i) {
+            xv[i] = *reinterpret_cast<const v4f *>(xr + 32 * KC * ch + 4 * i);
+            dv[i] = *reinterpret_cast<const v4f *>(dr + 32 * KC * ch + 4 * i);
+            mv[i] = *reinterpret_cast<const v4f *>(dmr + 32 * KC * ch + 4 * i);
         }
+    };
+    float ascale = 0.0f;
+    auto a_store = [&](int ch) {
+        const int buf = ch % NBUF;
 #pragma unroll
-        for (int o = 0; o < C / 8; ++o) {  // groups of 8 values: one 16-byte LDS store per array
-            const int kk = seg * L + ch * C + 8 * o;  // within the slice
-            const int kt = kk >> 5, ko = kk & 31;
+        for (int o = 0; o < LC / 8; ++o) {  // groups of 8 values: one 16-byte LDS store per array
+            const int kk = seg * LC + 8 * o;  // within the chunk
+            const int kl = kk >> 5, ko = kk & 31;
             uint32_t hi[4], lo[4], mh[4], ml[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -152,12 +159,17 @@ __global__ void __launch_bounds__(256)
                 split2(x0 * m4[u], x1 * m4[u + 1], mh[j], ml[j]);
             }
             const int w0 = (ar * ORN_AST + ko) >> 1;
-            *reinterpret_cast<uint4 *>(&As[kt][0][w0]) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-            *reinterpret_cast<uint4 *>(&As[kt][1][w0]) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-            *reinterpret_cast<uint4 *>(&As[kt][2][w0]) = make_uint4(mh[0], mh[1], mh[2], mh[3]);
-            *reinterpret_cast<uint4 *>(&As[kt][3][w0]) = make_uint4(ml[0], ml[1], ml[2], ml[3]);
+            *reinterpret_cast<uint4 *>(&As[buf][kl][0][w0]) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+            *reinterpret_cast<uint4 *>(&As[buf][kl][1][w0]) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+            *reinterpret_cast<uint4 *>(&As[buf][kl][2][w0]) = make_uint4(mh[0], mh[1], mh[2], mh[3]);
+            *reinterpret_cast<uint4 *>(&As[buf][kl][3][w0]) = make_uint4(ml[0], ml[1], ml[2], ml[3]);
         }
-    }
+    };
+    a_load(0);
+    ascale = ar < nrows ? row_scale(amax, dmx) : 0.0f;
+    if (seg == 0) s_inv[ar] = ascale != 0.0f ? 1.0f / ascale : 0.0f;
+    a_store(0);
+    if (NCHK > 1) a_load(1);
     __syncthreads();
 
     v4f acc[4];
@@ -167,6 +179,7 @@ __global__ void __launch_bounds__(256)
     const int ro = c * ORN_AST + 8 * g;
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
+        const int ch = kt / KC, kl = kt % KC;
         GuRing &r = st[kt % NR];
         v8h bq[4];
         bq[0] = q4_b(r.q.x, r.s0);
@@ -178,7 +191,7 @@ __global__ void __launch_bounds__(256)
         __builtin_amdgcn_sched_barrier(0);
         if (kt + NR < KT) load_b(r, kt + NR);
         __builtin_amdgcn_sched_barrier(0);
-        const _Float16 *A = reinterpret_cast<const _Float16 *>(As[kt][0]);
+        const _Float16 *A = reinterpret_cast<const _Float16 *>(As[ch % NBUF][kl][0]);
         const v8h ahi = *reinterpret_cast<const v8h *>(A + ro);
         const v8h alo = *reinterpret_cast<const v8h *>(A + 16 * ORN_AST + ro);
         const v8h mhi = *reinterpret_cast<const v8h *>(A + 32 * ORN_AST + ro);
@@ -190,6 +203,14 @@ __global__ void __launch_bounds__(256)
         }
         accm = mfma(mhi, bm, accm);
         accm = mfma(mlo, bm, accm);
+        if (kl == 0 && ch + 1 < NCHK) {
+            // Next chunk's tiles into the other buffer (last read in chunk
+            // ch-1, which every wave finished before the barrier below it),
+            // then the loads for the chunk after it.
+            a_store(ch + 1);
+            if (ch + 2 < NCHK) a_load(ch + 2);
+        }
+        if (kl == KC - 1 && ch + 1 < NCHK) __syncthreads();
     }
 
     float *row0 = gu + ((size_t)kslice * rows_max + itm.y) * (2 * H);
@@ -219,26 +240,27 @@ struct DnRing {
     uint4 q0, q1, sc[4];
 };
 
-template <int NR, int KT>
+template <int NR, int KT, int KC>
 __global__ void __launch_bounds__(256)
     k_down_dec(ornk_dn_prefill P, const float *__restrict__ mid,
-                const float *__restrict__ mid_amax, const int *__restrict__ ctl,
-                const int4 *__restrict__ items, float *__restrict__ dn, int D, int H, int ks,
-                int rows_max)
+               const float *__restrict__ mid_amax, const int *__restrict__ ctl,
+               const int4 *__restrict__ items, float *__restrict__ dn, int D, int H, int ks,
+               int rows_max)
 {
-    constexpr int L = 2 * KT, C = L < 16 ? L : 16, NCH = L / C;
-    __shared__ __align__(16) uint32_t As[KT][2][16 * ORN_AST / 2];
+    constexpr int NCHK = KT / KC, NBUF = NCHK > 1 ? 2 : 1;
+    constexpr int LC = 2 * KC;
+    __shared__ __align__(16) uint32_t As[NBUF][KC][2][16 * ORN_AST / 2];
     __shared__ float s_inv[16];
 
     const int NBD = D >> 8;
     const int per_item = NBD * ks;
-    const int n_live = ctl[1] * per_item;
-    if ((int)blockIdx.x >= n_live) return;
-    const int tile = xcd_remap(blockIdx.x, n_live);
+    const int tile = blockIdx.x;
     const int b = tile % NBD;
     const int kslice = (tile / NBD) % ks;
     const int item = tile / per_item;
+    const int n_items = ctl[1];
     const int4 itm = items[item];
+    if (item >= n_items) return;
     const int e = itm.w;
     const int nrows = itm.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -268,22 +290,23 @@ __global__ void __launch_bounds__(256)
 
     const float amax = mid_amax[itm.y + arow];
     const float dmx = P.dmax[e * 3 + 2];
-    const float ascale = ar < nrows ? row_scale(amax, dmx) : 0.0f;
-    if (seg == 0) s_inv[ar] = ascale != 0.0f ? 1.0f / ascale : 0.0f;
-    const float *xr = mid + (size_t)(itm.y + arow) * H + 32 * kt0 + seg * L;
-    const float *dr = P.dd + (size_t)e * (DH / 256) + (size_t)b * H + 32 * kt0 + seg * L;
+    const float *xr = mid + (size_t)(itm.y + arow) * H + 32 * kt0 + seg * LC;
+    const float *dr = P.dd + (size_t)e * (DH / 256) + (size_t)b * H + 32 * kt0 + seg * LC;
+    v4f xv[LC / 4], dv[LC / 4];
+    auto a_load = [&](int ch) {
 #pragma unroll
-    for (int ch = 0; ch < NCH; ++ch) {
-        v4f xv[C / 4], dv[C / 4];
-#pragma unroll
-        for (int i = 0; i < C / 4; ++i) {
-            xv[i] = *reinterpret_cast<const v4f *>(xr + ch * C + 4 * i);
-            dv[i] = *reinterpret_cast<const v4f *>(dr + ch * C + 4 * i);
+        for (int i = 0; i < LC / 4; ++i) {
+            xv[i] = *reinterpret_cast<const v4f *>(xr + 32 * KC * ch + 4 * i);
+            dv[i] = *reinterpret_cast<const v4f *>(dr + 32 * KC * ch + 4 * i);
         }
+    };
+    float ascale = 0.0f;
+    auto a_store = [&](int ch) {
+        const int buf = ch % NBUF;
 #pragma unroll
-        for (int o = 0; o < C / 8; ++o) {
-            const int kk = seg * L + ch * C + 8 * o;
-            const int kt = kk >> 5, ko = kk & 31;
+        for (int o = 0; o < LC / 8; ++o) {
+            const int kk = seg * LC + 8 * o;
+            const int kl = kk >> 5, ko = kk & 31;
             uint32_t hi[4], lo[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -292,10 +315,15 @@ __global__ void __launch_bounds__(256)
                 split2(x4[u] * ascale * d4[u], x4[u + 1] * ascale * d4[u + 1], hi[j], lo[j]);
             }
             const int w0 = (ar * ORN_AST + ko) >> 1;
-            *reinterpret_cast<uint4 *>(&As[kt][0][w0]) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-            *reinterpret_cast<uint4 *>(&As[kt][1][w0]) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+            *reinterpret_cast<uint4 *>(&As[buf][kl][0][w0]) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+            *reinterpret_cast<uint4 *>(&As[buf][kl][1][w0]) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
         }
-    }
+    };
+    a_load(0);
+    ascale = ar < nrows ? row_scale(amax, dmx) : 0.0f;
+    if (seg == 0) s_inv[ar] = ascale != 0.0f ? 1.0f / ascale : 0.0f;
+    a_store(0);
+    if (NCHK > 1) a_load(1);
     __syncthreads();
 
     v4f acc[4];
@@ -304,6 +332,7 @@ __global__ void __launch_bounds__(256)
     const int ro = c * ORN_AST + 8 * g;
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
+        const int ch = kt / KC, kl = kt % KC;
         DnRing &r = st[kt % NR];
         v8h bq[4];
         bq[0] = q6_b(r.q0.x, r.q0.y, r.sc[0]);
@@ -313,7 +342,7 @@ __global__ void __launch_bounds__(256)
         __builtin_amdgcn_sched_barrier(0);
         if (kt + NR < KT) load_b(r, kt + NR);
         __builtin_amdgcn_sched_barrier(0);
-        const _Float16 *A = reinterpret_cast<const _Float16 *>(As[kt][0]);
+        const _Float16 *A = reinterpret_cast<const _Float16 *>(As[ch % NBUF][kl][0]);
         const v8h ahi = *reinterpret_cast<const v8h *>(A + ro);
         const v8h alo = *reinterpret_cast<const v8h *>(A + 16 * ORN_AST + ro);
 #pragma unroll
@@ -321,6 +350,11 @@ __global__ void __launch_bounds__(256)
             acc[j] = mfma(ahi, bq[j], acc[j]);
             acc[j] = mfma(alo, bq[j], acc[j]);
         }
+        if (kl == 0 && ch + 1 < NCHK) {
+            a_store(ch + 1);
+            if (ch + 2 < NCHK) a_load(ch + 2);
+        }
+        if (kl == KC - 1 && ch + 1 < NCHK) __syncthreads();
     }
 
     float *row0 = dn + ((size_t)kslice * rows_max + itm.y) * D;
@@ -340,11 +374,12 @@ __global__ void __launch_bounds__(256)
 }  // namespace
 
 // Decode instances: work items of <= 16 rows; KT = D/32/ks (gate/up) or
-// H/32/ks (down) reduction steps per slice, 4 or 8 (the LDS holds a slice's
-// activation tiles: 5 KB per step for gate/up, 2.5 KB for down).
+// H/32/ks (down) reduction steps per slice, 4 to 32; activation tiles in
+// chunks of 4 steps (LDS: 2 x 20 KB for gate/up, 2 x 10 KB for down).
 extern "C" int ornk_dec_supported(int kt_gu, int kt_dn)
 {
-    return (kt_gu == 4 || kt_gu == 8) && (kt_dn == 4 || kt_dn == 8);
+    auto ok = [](int kt) { return kt == 4 || kt == 8 || kt == 16 || kt == 32; };
+    return ok(kt_gu) && ok(kt_dn);
 }
 
 extern "C" int ornk_moe_gateup_dec(const ornk_moe_args *a, hipStream_t s)
@@ -361,11 +396,15 @@ extern "C" int ornk_moe_gateup_dec(const ornk_moe_args *a, hipStream_t s)
     }
     const dim3 grid(a->items_max * 2 * (a->H / 256) * ks);
 #define ORN_GU_DEC(K)                                                                        \
-    hipLaunchKernelGGL((k_gateup_dec<ORN_DEC_NR, K>), grid, dim3(256), 0, s, a->gu_pf, xin,   \
+    hipLaunchKernelGGL((k_gateup_dec<ORN_DEC_NR, K, 4>), grid, dim3(256), 0, s, a->gu_pf, xin, \
                        a->x_amax, a->ctl, reinterpret_cast<const int4 *>(a->items),           \
                        a->row_token, a->gu_part, a->T, a->D, a->H, ks, a->rows_max)
-    if (KT == 4) ORN_GU_DEC(4);
-    else ORN_GU_DEC(8);
+    switch (KT) {
+    case 4: ORN_GU_DEC(4); break;
+    case 8: ORN_GU_DEC(8); break;
+    case 16: ORN_GU_DEC(16); break;
+    default: ORN_GU_DEC(32); break;
+    }
 #undef ORN_GU_DEC
     return hipGetLastError();
 }
@@ -379,11 +418,15 @@ extern "C" int ornk_moe_down_dec(const ornk_moe_args *a, hipStream_t s)
     if (!ornk_dec_supported(4, KT)) return hipErrorInvalidValue;
     const dim3 grid(a->items_max * (a->D / 256) * ks);
 #define ORN_DN_DEC(K)                                                                       \
-    hipLaunchKernelGGL((k_down_dec<ORN_DEC_NR, K>), grid, dim3(256), 0, s, a->dn_pf, a->mid, \
+    hipLaunchKernelGGL((k_down_dec<ORN_DEC_NR, K, 4>), grid, dim3(256), 0, s, a->dn_pf, a->mid, \
                        a->mid_amax, a->ctl, reinterpret_cast<const int4 *>(a->items),        \
                        a->dn_part, a->D, a->H, ks, a->rows_max)
-    if (KT == 4) ORN_DN_DEC(4);
-    else ORN_DN_DEC(8);
+    switch (KT) {
+    case 4: ORN_DN_DEC(4); break;
+    case 8: ORN_DN_DEC(8); break;
+    case 16: ORN_DN_DEC(16); break;
+    default: ORN_DN_DEC(32); break;
+    }
 #undef ORN_DN_DEC
     return hipGetLastError();
 }
