@@ -634,8 +634,10 @@ static plan_t make_plan(const ornith_moe_shape *sh, int T, int use_mfma)
          * 2*(H/256) tiles per item and slice, down D/256 */
         int kg = pow2_floor(2048 / (est_items * 2 * (H / 256)) > 0
                                 ? 2048 / (est_items * 2 * (H / 256)) : 1);
-        while (kg > 1 && (D / 32) % kg) kg /= 2;
-        if (kg > D / 32) kg = D / 32;
+        /* the prefill gate/up kernel pipelines 4 steps per loop turn:
+         * slices of a multiple of 4 steps, at most 64 */
+        while (kg > 1 && ((D / 32) % kg || (D / 32 / kg) % 4)) kg /= 2;
+        while (D / 32 / kg > 64) kg *= 2;
         int kdn = pow2_floor(2048 / (est_items * (D / 256)) > 0 ? 2048 / (est_items * (D / 256)) : 1);
         while (kdn > 1 && (H / 32) % kdn) kdn /= 2;
         if (kdn > H / 32) kdn = H / 32;

@@ -20,6 +20,29 @@ namespace {
 using namespace orn_mfma;
 
 #define ORN_MT 64   // token rows per work group (4 row tiles)
+#define ORN_GU_KT_MAX 64  // reduction steps per gate/up slice (D <= 2048 at ks = 1)
+
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// Weight streams are raw buffer loads: a fixed per-lane VGPR offset plus the
+// step's wave-uniform offset in an SGPR (0x00020000: 32-bit data format).
+__device__ __forceinline__ rsrc_t make_rsrc(const void *p, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
+__device__ __forceinline__ uint4 bload16(rsrc_t r, uint32_t voff, uint32_t soff)
+{
+    const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Empty asm that reads and writes a ring slot: the wait for the slot's loads
+// lands here and no use of the slot moves above it.
+__device__ __forceinline__ void pin4(uint4 &a) { asm volatile("" : "+v"(a.x), "+v"(a.y), "+v"(a.z), "+v"(a.w)); }
+__device__ __forceinline__ void pinf(v4f &a) { asm volatile("" : "+v"(a)); }
 
 // Activation tile rows: thread t prepares row t/4, reduction values
 // 8*(t%4) .. +7 of the current step, for one or two scale vectors.  Rows
@@ -97,13 +120,45 @@ __device__ __forceinline__ void mma_step(const _Float16 *Ahi, const _Float16 *Al
 // kslice*KT .. +KT-1).
 // ---------------------------------------------------------------------------
 struct GuBlock {
-    const uint32_t *qn;
-    const uint16_t *sc, *mn;
-    const float *xrow, *dva, *dmva;  // already offset to this slice's first step
+    rsrc_t rq, rs, rm;                // this expert's nibble words, scales, mins
+    uint32_t q_off, s_off, m_off;     // this lane's byte offsets at the slice's first step
+    uint32_t qstep, sstep;            // bytes per reduction step
+    const float *xrow;                // already offset to this slice's first step
+    const float *dsl;                 // LDS: d then dmin of the slice's KT*32 reduction rows
     float ascale;
-    int aoff, NB, b, kt0, KT;
+    int aoff, ko, KT;                 // ko: this thread's first reduction value in a step
 };
 
+struct XRaw {
+    v4f x0, x1;
+};
+
+// hi/lo of x*s*d and of x*s*dmin for this thread's 8 values of step kt into
+// LDS (d, dmin from the slice's LDS copy).
+__device__ __forceinline__ void a_store_l(const XRaw &r, const GuBlock &B, int kt, _Float16 *t0,
+                                          _Float16 *t1, _Float16 *t2, _Float16 *t3)
+{
+    ARaw a;
+    a.x0 = r.x0;
+    a.x1 = r.x1;
+    const float *dl = B.dsl + 32 * kt + B.ko;
+    const float *ml = dl + 32 * B.KT;
+    a.d0 = *reinterpret_cast<const v4f *>(dl);
+    a.d1 = *reinterpret_cast<const v4f *>(dl + 4);
+    a.m0 = *reinterpret_cast<const v4f *>(ml);
+    a.m1 = *reinterpret_cast<const v4f *>(ml + 4);
+    a_store<true>(a, B.ascale, t0, t1, t2, t3);
+}
+
+struct GuRingP {
+    uint4 q, s0, s1, mn;
+};
+
+// Software pipeline over the slice's KT steps (KT a multiple of 4): weight
+// loads 4 steps ahead in a register ring, activation loads 2 steps ahead;
+// the activation tile of step kt+1 is prepared into LDS (double buffer)
+// while step kt's MFMAs run, one barrier per step.  The loop is unrolled by
+// 4 so ring slots are static; loads past the slice re-read its last step.
 template <int NTT, int ROWS>
 __device__ __forceinline__ void gateup_tile(const GuBlock &B, ATiles<ROWS, 4> &As,
                                             float (*Mt)[8], const float *s_inv, float *gu_row0,
@@ -111,20 +166,23 @@ __device__ __forceinline__ void gateup_tile(const GuBlock &B, ATiles<ROWS, 4> &A
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, c = lane & 15;
-    const int NB = B.NB, b = B.b;
     const bool a_live = wave < NTT;  // this wave's rows hold tokens (uniform)
-    auto b_load = [&](int kt, uint32_t (&qw)[4], uint4 (&sw)[2], uint4 &mw) {
-        const size_t base = (size_t)(B.kt0 + kt) * NB + b;
-        const uint4 q = *reinterpret_cast<const uint4 *>(B.qn + ((base * 4 + wave) * 64 + lane) * 4);
-        qw[0] = q.x;
-        qw[1] = q.y;
-        qw[2] = q.z;
-        qw[3] = q.w;
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-            sw[h] = *reinterpret_cast<const uint4 *>(B.sc + (base * 8 + 2 * wave + h) * 32 + 8 * g);
-        const uint4 t = *reinterpret_cast<const uint4 *>(B.mn + (base * 8 + (c & 7)) * 32 + 8 * g);
-        mw = c < 8 ? t : make_uint4(0, 0, 0, 0);  // columns 8..15 of the mins tile are zero
+    const int KT = B.KT;
+    auto load_b = [&](GuRingP &st, int kt) {
+        kt = kt < KT ? kt : KT - 1;
+        st.q = bload16(B.rq, B.q_off, kt * B.qstep);
+        st.s0 = bload16(B.rs, B.s_off, kt * B.sstep);
+        st.s1 = bload16(B.rs, B.s_off + 64, kt * B.sstep);
+        st.mn = bload16(B.rm, B.m_off, kt * B.sstep);
+    };
+    auto load_a = [&](XRaw &r, int kt) {
+        kt = kt < KT ? kt : KT - 1;
+        r.x0 = *reinterpret_cast<const v4f *>(B.xrow + 32 * kt);
+        r.x1 = *reinterpret_cast<const v4f *>(B.xrow + 32 * kt + 4);
+    };
+    auto pin_a = [&](XRaw &r) {
+        pinf(r.x0);
+        pinf(r.x1);
     };
 
     v4f acc[NTT][4];
@@ -133,46 +191,59 @@ __device__ __forceinline__ void gateup_tile(const GuBlock &B, ATiles<ROWS, 4> &A
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
     v4f accm = {0.0f, 0.0f, 0.0f, 0.0f};
+    const int mro = (16 * wave + c) * ORN_AST + 8 * g;  // row tile `wave`, for the mins
 
-    ARaw ar;
-    uint32_t qw[4];
-    uint4 sw[2], mw;
-    v8h bq[4], bm;
-    if (a_live) {
-        a_load<true>(ar, B.xrow, B.dva, B.dmva, 0);
-        a_store<true>(ar, B.ascale, &As.t[0][0][B.aoff], &As.t[0][1][B.aoff], &As.t[0][2][B.aoff],
-                      &As.t[0][3][B.aoff]);
-    }
-    b_load(0, qw, sw, mw);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) bq[j] = q4_b(qw[j], sw[j >> 1]);
-    bm = __builtin_bit_cast(v8h, mw);
+    GuRingP r0, r1, r2, r3;
+    XRaw a0, a1;
+    load_b(r0, 0);
+    load_b(r1, 1);
+    load_b(r2, 2);
+    load_b(r3, 3);
+    load_a(a0, 0);
+    load_a(a1, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();  // the slice's d/dmin are in LDS
+    a_store_l(a0, B, 0, &As.t[0][0][B.aoff], &As.t[0][1][B.aoff], &As.t[0][2][B.aoff],
+              &As.t[0][3][B.aoff]);
+    __builtin_amdgcn_sched_barrier(0);
+    load_a(a0, 2);
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
 
-    const int mro = (16 * wave + c) * ORN_AST + 8 * g;  // row tile `wave`, for the mins
-    for (int kt = 0; kt < B.KT - 1; ++kt) {
-        const int cur = kt & 1, nxt = cur ^ 1;
-        if (a_live) a_load<true>(ar, B.xrow, B.dva, B.dmva, 32 * (kt + 1));
-        b_load(kt + 1, qw, sw, mw);
-        mma_step<NTT>(As.t[cur][0], As.t[cur][1], bq, acc, c, g);
+    // Step k = kt + s: weights from ring slot s, activation tile from LDS
+    // buffer k & 1; then the activation tile of step k+1 from raw slot
+    // (k+1) % 2 into buffer (k+1) & 1, whose last reader was step k-1.
+    auto sub = [&](GuRingP &rb, XRaw &ra, int k, int buf) {
+        pin4(rb.q); pin4(rb.s0); pin4(rb.s1); pin4(rb.mn);
+        v8h bq[4];
+        bq[0] = q4_b(rb.q.x, rb.s0);
+        bq[1] = q4_b(rb.q.y, rb.s0);
+        bq[2] = q4_b(rb.q.z, rb.s1);
+        bq[3] = q4_b(rb.q.w, rb.s1);
+        const uint4 mz = c < 8 ? rb.mn : make_uint4(0u, 0u, 0u, 0u);  // mins tile: 8 columns
+        const v8h bm = __builtin_bit_cast(v8h, mz);
+        __builtin_amdgcn_sched_barrier(0);
+        load_b(rb, k + 4);
+        __builtin_amdgcn_sched_barrier(0);
+        mma_step<NTT>(As.t[buf][0], As.t[buf][1], bq, acc, c, g);
         if (a_live) {
-            accm = mfma(*reinterpret_cast<const v8h *>(&As.t[cur][2][mro]), bm, accm);
-            accm = mfma(*reinterpret_cast<const v8h *>(&As.t[cur][3][mro]), bm, accm);
-            a_store<true>(ar, B.ascale, &As.t[nxt][0][B.aoff], &As.t[nxt][1][B.aoff],
-                          &As.t[nxt][2][B.aoff], &As.t[nxt][3][B.aoff]);
+            accm = mfma(*reinterpret_cast<const v8h *>(&As.t[buf][2][mro]), bm, accm);
+            accm = mfma(*reinterpret_cast<const v8h *>(&As.t[buf][3][mro]), bm, accm);
         }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) bq[j] = q4_b(qw[j], sw[j >> 1]);
-        bm = __builtin_bit_cast(v8h, mw);
+        pin_a(ra);
+        const int nb = buf ^ 1;
+        a_store_l(ra, B, k + 1 < KT ? k + 1 : KT - 1, &As.t[nb][0][B.aoff], &As.t[nb][1][B.aoff],
+                  &As.t[nb][2][B.aoff], &As.t[nb][3][B.aoff]);
+        __builtin_amdgcn_sched_barrier(0);
+        load_a(ra, k + 3);
+        __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
-    }
-    {
-        const int cur = (B.KT - 1) & 1;
-        mma_step<NTT>(As.t[cur][0], As.t[cur][1], bq, acc, c, g);
-        if (a_live) {
-            accm = mfma(*reinterpret_cast<const v8h *>(&As.t[cur][2][mro]), bm, accm);
-            accm = mfma(*reinterpret_cast<const v8h *>(&As.t[cur][3][mro]), bm, accm);
-        }
+    };
+    for (int kt = 0; kt < KT; kt += 4) {
+        sub(r0, a1, kt + 0, 0);
+        sub(r1, a0, kt + 1, 1);
+        sub(r2, a1, kt + 2, 0);
+        sub(r3, a0, kt + 3, 1);
     }
 
     // dmin term of row tile `wave`: rows 16*wave + 4g + r, sub-block c.
@@ -211,6 +282,7 @@ __global__ void __launch_bounds__(256)
     __shared__ float Mt[ROWS][8];
     __shared__ float s_scale[ROWS], s_inv[ROWS];
     __shared__ int s_tok[ROWS];
+    __shared__ __align__(16) float s_dd[2 * ORN_GU_KT_MAX * 32];  // d, then dmin, of the slice
 
     const int NB = H >> 8;
     const int per_item = 2 * NB * ks;
@@ -238,19 +310,35 @@ __global__ void __launch_bounds__(256)
 
     GuBlock B;
     B.KT = D / 32 / ks;
-    B.kt0 = kslice * B.KT;
-    const int k0 = 32 * B.kt0;
-    B.qn = P.pq[m] + (size_t)e * (DH / 8);
-    B.sc = P.psc[m] + (size_t)e * (DH / 32);
-    B.mn = P.pmn[m] + (size_t)e * (DH / 32);
+    const int kt0 = kslice * B.KT;
+    const int k0 = 32 * kt0;
+    const int lane = tid & 63, wave = tid >> 6, g = lane >> 4, c = lane & 15;
+    const uint32_t EQ = (uint32_t)(DH / 2), ES = (uint32_t)(DH / 16);  // bytes per expert
+    B.rq = make_rsrc(reinterpret_cast<const uint8_t *>(P.pq[m]) + (size_t)e * EQ, EQ);
+    B.rs = make_rsrc(reinterpret_cast<const uint8_t *>(P.psc[m]) + (size_t)e * ES, ES);
+    B.rm = make_rsrc(reinterpret_cast<const uint8_t *>(P.pmn[m]) + (size_t)e * ES, ES);
+    B.qstep = (uint32_t)NB * 4096;
+    B.sstep = (uint32_t)NB * 512;
+    B.q_off = (uint32_t)(((size_t)kt0 * NB + b) * 4096) + (wave * 64 + lane) * 16;
+    B.s_off = (uint32_t)((((size_t)kt0 * NB + b) * 8 + 2 * wave) * 64) + 16 * g;
+    B.m_off = (uint32_t)((((size_t)kt0 * NB + b) * 8 + (c & 7)) * 64) + 16 * g;
     const int ar = (tid >> 2) & (ROWS - 1), ao = tid & 3;  // rows >= ROWS belong to dead waves
     B.xrow = xn + (size_t)s_tok[ar] * D + k0 + 8 * ao;
-    B.dva = P.pd[m] + (size_t)e * (DH / 256) + (size_t)b * D + k0 + 8 * ao;
-    B.dmva = P.pdm[m] + (size_t)e * (DH / 256) + (size_t)b * D + k0 + 8 * ao;
+    {
+        // d and dmin of the slice's 32*KT reduction rows into LDS (made
+        // visible by the first barrier of the tile loop)
+        const float *dg = P.pd[m] + (size_t)e * (DH / 256) + (size_t)b * D + k0;
+        const float *mg = P.pdm[m] + (size_t)e * (DH / 256) + (size_t)b * D + k0;
+        const int n4 = 8 * B.KT;  // v4f per array
+        for (int i = tid; i < n4; i += 256) {
+            reinterpret_cast<v4f *>(s_dd)[i] = reinterpret_cast<const v4f *>(dg)[i];
+            reinterpret_cast<v4f *>(s_dd)[n4 + i] = reinterpret_cast<const v4f *>(mg)[i];
+        }
+    }
+    B.dsl = s_dd;
+    B.ko = 8 * ao;
     B.ascale = s_scale[ar];
     B.aoff = ar * ORN_AST + 8 * ao;
-    B.NB = NB;
-    B.b = b;
     float *row0 = gu + ((size_t)kslice * rows_max + itm.y) * (2 * H);
     const int col0 = m * H + 256 * b;
     if (NTTMAX == 1) {
@@ -446,7 +534,8 @@ extern "C" int ornk_rowmax(const float *x, int rows, int D, float *out, hipStrea
 extern "C" int ornk_moe_gateup_mfma(const ornk_moe_args *a, hipStream_t s)
 {
     const int ks = a->ks_gu;
-    if (a->D % 32 || a->H % 256 || ks < 1 || (a->D / 32) % ks || a->tchunk > ORN_MT)
+    if (a->D % 32 || a->H % 256 || ks < 1 || (a->D / 32) % ks || a->tchunk > ORN_MT ||
+        (a->D / 32 / ks) % 4 || a->D / 32 / ks > ORN_GU_KT_MAX)
         return hipErrorInvalidValue;
     const float *xin = a->apply_norm ? a->xn : a->x;
     if (!a->router_amax) {

@@ -45,14 +45,17 @@ __device__ __forceinline__ float row_scale(float amax, float dmax)
 __device__ __forceinline__ v2h as_v2h(uint32_t u) { return __builtin_bit_cast(v2h, u); }
 __device__ __forceinline__ uint32_t as_u32(v2h v) { return __builtin_bit_cast(uint32_t, v); }
 
-// (a0, a1) -> hi = rtz fp16, lo = rtz fp16 of the exact remainder a - hi
-// (formed as fma(hi, -1, a), one mixed-precision fma per value).
+// (a0, a1) -> hi = rtz fp16, lo = rtz fp16 of the remainder a - hi, which is
+// exact in fp32 (hi is a truncation of a).  The remainder is one
+// v_fma_mix_f32 per value: hi's fp16 half times -1 plus a (the compiler
+// would otherwise turn fma(hi, -1, a) into a convert and a subtract).
 __device__ __forceinline__ void split2(float a0, float a1, uint32_t &hi, uint32_t &lo)
 {
-    const v2h h = __builtin_bit_cast(v2h, __builtin_amdgcn_cvt_pkrtz(a0, a1));
-    const float r0 = __builtin_fmaf((float)h[0], -1.0f, a0);
-    const float r1 = __builtin_fmaf((float)h[1], -1.0f, a1);
-    hi = as_u32(h);
+    const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a0, a1));
+    float r0, r1;
+    asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r0) : "v"(h), "v"(a0));
+    asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r1) : "v"(h), "v"(a1));
+    hi = h;
     lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(r0, r1));
 }
 
