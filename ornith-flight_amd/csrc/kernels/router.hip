@@ -411,6 +411,12 @@ __global__ void __launch_bounds__(64)
         chain_add4<7>(acc, p);
         // The next step's weights pass through this point together with the
         // chain, so its products cannot be computed ahead of this step's adds.
+        // There is no pin after the last step on purpose: the final adds then
+        // sink into the conditional store below, which keeps the compiler
+        // from folding the row shifts into v_add_f32_dpp anywhere.  A folded
+        // add needs two wait states after the previous add of the chain, so
+        // the chain (the critical path) is shorter with separate DPP moves,
+        // which issue off it.
         if (it + 1 < ND) asm volatile("" : "+v"(acc), "+v"(ring[(it + 1) % NR]));
     }
     if (q == 0 && e0 + es < E) logits[(size_t)t * E + e0 + es] = bias ? acc + bias[e0 + es] : acc;
