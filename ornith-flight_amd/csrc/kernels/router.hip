@@ -395,9 +395,14 @@ __global__ void __launch_bounds__(64)
     __syncthreads();
 
     float acc = 0.0f;
+    // x of step it+1 is read from LDS during step it, so its latency is
+    // hidden behind a step of the chain.
+    v4f xnext = xs[q];
 #pragma unroll
     for (int it = 0; it < ND; ++it) {
-        const v4f xv = xs[8 * it + q];
+        const v4f xv = xnext;
+        if (it + 1 < ND) xnext = xs[8 * (it + 1) + q];
+        __builtin_amdgcn_sched_barrier(0);  // the read is issued before the chain
         const v4f w = ring[it % NR];
         const float p[4] = {xv.x * w.x, xv.y * w.y, xv.z * w.z, xv.w * w.w};
         if (it + NR < ND) ring[it % NR] = wp[(size_t)8 * (it + NR) * E];
@@ -417,7 +422,7 @@ __global__ void __launch_bounds__(64)
         // add needs two wait states after the previous add of the chain, so
         // the chain (the critical path) is shorter with separate DPP moves,
         // which issue off it.
-        if (it + 1 < ND) asm volatile("" : "+v"(acc), "+v"(ring[(it + 1) % NR]));
+        if (it + 1 < ND) asm volatile("" : "+v"(acc), "+v"(ring[(it + 1) % NR]), "+v"(xnext));
     }
     if (q == 0 && e0 + es < E) logits[(size_t)t * E + e0 + es] = bias ? acc + bias[e0 + es] : acc;
 }
