@@ -71,7 +71,7 @@ struct GuRing {
 };
 
 template <int NR, int KT, int KC>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
     k_gateup_dec(ornk_gu_prefill P, const float *__restrict__ xn,
                  const float *__restrict__ x_amax, const int *__restrict__ ctl,
                  const int4 *__restrict__ items, const int *__restrict__ row_token,
@@ -133,8 +133,14 @@ __global__ void __launch_bounds__(256)
     const float *xr = xn + (size_t)tok * D + 32 * kt0 + seg * LC;
     const float *dr = P.pd[m] + (size_t)e * (DH / 256) + (size_t)b * D + 32 * kt0 + seg * LC;
     const float *dmr = P.pdm[m] + (size_t)e * (DH / 256) + (size_t)b * D + 32 * kt0 + seg * LC;
+    // Wave w prepares rows 4w..4w+3.  A wave whose rows all lie past the
+    // item (most waves at decode sizes, where items hold one or a few rows)
+    // zeroes its rows of both buffers once and then skips the loads and the
+    // arithmetic (uniform per wave).
+    const bool rows_live = __builtin_amdgcn_readfirstlane(4 * (tid >> 6)) < nrows;
     v4f xv[LC / 4], dv[LC / 4], mv[LC / 4];
     auto a_load = [&](int ch) {
+        if (!rows_live) return;
 #pragma unroll
         for (int i = 0; i < LC / 4; ++i) {
             xv[i] = *reinterpret_cast<const v4f *>(xr + 32 * KC * ch + 4 * i);
@@ -143,7 +149,20 @@ __global__ void __launch_bounds__(256)
         }
     };
     float ascale = 0.0f;
+    if (!rows_live) {
+#pragma unroll
+        for (int buf = 0; buf < NBUF; ++buf)
+#pragma unroll
+            for (int o = 0; o < LC / 8; ++o) {
+                const int kk = seg * LC + 8 * o, kl = kk >> 5, ko = kk & 31;
+                const int w0 = (ar * ORN_AST + ko) >> 1;
+#pragma unroll
+                for (int a = 0; a < 4; ++a)
+                    *reinterpret_cast<uint4 *>(&As[buf][kl][a][w0]) = make_uint4(0u, 0u, 0u, 0u);
+            }
+    }
     auto a_store = [&](int ch) {
+        if (!rows_live) return;
         const int buf = ch % NBUF;
 #pragma unroll
         for (int o = 0; o < LC / 8; ++o) {  // groups of 8 values: one 16-byte LDS store per array
@@ -241,7 +260,7 @@ struct DnRing {
 };
 
 template <int NR, int KT, int KC>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
     k_down_dec(ornk_dn_prefill P, const float *__restrict__ mid,
                const float *__restrict__ mid_amax, const int *__restrict__ ctl,
                const int4 *__restrict__ items, float *__restrict__ dn, int D, int H, int ks,
@@ -292,8 +311,12 @@ __global__ void __launch_bounds__(256)
     const float dmx = P.dmax[e * 3 + 2];
     const float *xr = mid + (size_t)(itm.y + arow) * H + 32 * kt0 + seg * LC;
     const float *dr = P.dd + (size_t)e * (DH / 256) + (size_t)b * H + 32 * kt0 + seg * LC;
+    // Waves whose rows all lie past the item zero them once and skip the
+    // loads and the arithmetic, as in the gate/up kernel.
+    const bool rows_live = __builtin_amdgcn_readfirstlane(4 * (tid >> 6)) < nrows;
     v4f xv[LC / 4], dv[LC / 4];
     auto a_load = [&](int ch) {
+        if (!rows_live) return;
 #pragma unroll
         for (int i = 0; i < LC / 4; ++i) {
             xv[i] = *reinterpret_cast<const v4f *>(xr + 32 * KC * ch + 4 * i);
@@ -301,7 +324,19 @@ __global__ void __launch_bounds__(256)
         }
     };
     float ascale = 0.0f;
+    if (!rows_live) {
+#pragma unroll
+        for (int buf = 0; buf < NBUF; ++buf)
+#pragma unroll
+            for (int o = 0; o < LC / 8; ++o) {
+                const int kk = seg * LC + 8 * o, kl = kk >> 5, ko = kk & 31;
+                const int w0 = (ar * ORN_AST + ko) >> 1;
+                *reinterpret_cast<uint4 *>(&As[buf][kl][0][w0]) = make_uint4(0u, 0u, 0u, 0u);
+                *reinterpret_cast<uint4 *>(&As[buf][kl][1][w0]) = make_uint4(0u, 0u, 0u, 0u);
+            }
+    }
     auto a_store = [&](int ch) {
+        if (!rows_live) return;
         const int buf = ch % NBUF;
 #pragma unroll
         for (int o = 0; o < LC / 8; ++o) {
