@@ -29,21 +29,95 @@ __global__ void k_matmul(float *C, const float *A, const float *B, int M, int N,
     C[(size_t)i * N + j] = sum;
 }
 
-// gpu.c:144-156 per row: ss is the reference's sequential sum (one lane, so
-// the roundings match), then out = w * (x * inv_rms).
-__global__ void k_rmsnorm(float *out, const float *x, const float *w, int dim)
+// gpu.c:144-156 per row: ss is the reference's sequential fp32 sum of the
+// fp32 products x[i]*x[i], i ascending, then out = w * (x * inv_rms).  The
+// products are formed by all threads into LDS (dim floats of dynamic shared
+// memory); one lane then adds them in order, reading four at a time with
+// eight reads in flight, so only the chain of adds is serial and the
+// roundings are the reference's.
+__global__ void __launch_bounds__(256) k_rmsnorm(float *out, const float *x, const float *w, int dim)
 {
+    extern __shared__ __align__(16) float s_p[];
     __shared__ float inv_s;
     const float *xr = x + (size_t)blockIdx.x * dim;
     float *orow = out + (size_t)blockIdx.x * dim;
+    // Vector path (dim a multiple of 4, at most 16384): a thread's x and w
+    // are loaded in one round trip, before the first product.
+    const bool vec = (dim & 3) == 0 && dim <= 16 * 1024;
+    const int n4 = dim >> 2;
+    v4f xv[16], wv[16];
+    if (vec) {
+        const v4f *x4 = reinterpret_cast<const v4f *>(xr);
+        const v4f *w4 = reinterpret_cast<const v4f *>(w);
+        v4f *p4 = reinterpret_cast<v4f *>(s_p);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int i = (int)threadIdx.x + 256 * j;
+            if (i < n4) {
+                xv[j] = x4[i];
+                wv[j] = w4[i];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int i = (int)threadIdx.x + 256 * j;
+            if (i < n4) p4[i] = xv[j] * xv[j];
+        }
+    } else {
+        for (int i = threadIdx.x; i < dim; i += blockDim.x) {
+            const float v = xr[i];
+            s_p[i] = v * v;
+        }
+    }
+    __syncthreads();
     if (threadIdx.x == 0) {
+        // Batches of 32 products in two register buffers A, B: the reads of
+        // one batch are issued before the adds of the other, so they arrive
+        // while the chain runs.  Batches past the end re-read the last one
+        // (never added).
         float ss = 0.0f;
-        for (int i = 0; i < dim; ++i) ss += xr[i] * xr[i];
+        const int nb = dim >> 5;
+        const v4f *p4 = reinterpret_cast<const v4f *>(s_p);
+        v4f A[8], B[8];
+        auto rd = [&](v4f(&r)[8], int bt) {
+            const int b = bt < nb ? bt : nb - 1;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) r[i] = p4[8 * b + i];
+        };
+        auto add = [&](const v4f(&r)[8]) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                ss += r[i].x;
+                ss += r[i].y;
+                ss += r[i].z;
+                ss += r[i].w;
+            }
+        };
+        if (nb > 0) rd(A, 0);
+        for (int bt = 0; bt < nb; bt += 2) {
+            rd(B, bt + 1);
+            __builtin_amdgcn_sched_barrier(0);
+            add(A);
+            if (bt + 1 >= nb) break;
+            rd(A, bt + 2);
+            __builtin_amdgcn_sched_barrier(0);
+            add(B);
+        }
+        for (int i = 32 * nb; i < dim; ++i) ss += s_p[i];
         inv_s = 1.0f / sqrtf(ss / (float)dim + 1e-6f);
     }
     __syncthreads();
     const float inv = inv_s;
-    for (int i = threadIdx.x; i < dim; i += blockDim.x) orow[i] = w[i] * (xr[i] * inv);
+    if (vec) {
+        v4f *o4 = reinterpret_cast<v4f *>(orow);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int i = (int)threadIdx.x + 256 * j;
+            if (i < n4) o4[i] = wv[j] * (xv[j] * inv);
+        }
+    } else {
+        for (int i = threadIdx.x; i < dim; i += blockDim.x) orow[i] = w[i] * (xr[i] * inv);
+    }
 }
 
 __global__ void k_silu(float *out, const float *x, int n)
@@ -96,7 +170,9 @@ extern "C" int ornk_rmsnorm(float *out, const float *x, const float *w, int rows
                             hipStream_t s)
 {
     if (rows <= 0 || dim <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_rmsnorm, dim3(rows), dim3(256), 0, s, out, x, w, dim);
+    if (dim > 16384) return hipErrorInvalidValue;  // the products live in LDS
+    hipLaunchKernelGGL(k_rmsnorm, dim3(rows), dim3(256), (size_t)dim * sizeof(float), s, out, x,
+                       w, dim);
     return hipGetLastError();
 }
 
