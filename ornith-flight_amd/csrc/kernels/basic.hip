@@ -32,9 +32,8 @@ __global__ void k_matmul(float *C, const float *A, const float *B, int M, int N,
 // gpu.c:144-156 per row: ss is the reference's sequential fp32 sum of the
 // fp32 products x[i]*x[i], i ascending, then out = w * (x * inv_rms).  The
 // products are formed by all threads into LDS (dim floats of dynamic shared
-// memory); one lane then adds them in order, reading four at a time with
-// eight reads in flight, so only the chain of adds is serial and the
-// roundings are the reference's.
+// memory); one lane then adds them in order (orn_lds_seq_sum32), so only the
+// chain of adds is serial and the roundings are the reference's.
 __global__ void __launch_bounds__(256) k_rmsnorm(float *out, const float *x, const float *w, int dim)
 {
     extern __shared__ __align__(16) float s_p[];
@@ -71,38 +70,8 @@ __global__ void __launch_bounds__(256) k_rmsnorm(float *out, const float *x, con
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        // Batches of 32 products in two register buffers A, B: the reads of
-        // one batch are issued before the adds of the other, so they arrive
-        // while the chain runs.  Batches past the end re-read the last one
-        // (never added).
-        float ss = 0.0f;
         const int nb = dim >> 5;
-        const v4f *p4 = reinterpret_cast<const v4f *>(s_p);
-        v4f A[8], B[8];
-        auto rd = [&](v4f(&r)[8], int bt) {
-            const int b = bt < nb ? bt : nb - 1;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) r[i] = p4[8 * b + i];
-        };
-        auto add = [&](const v4f(&r)[8]) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                ss += r[i].x;
-                ss += r[i].y;
-                ss += r[i].z;
-                ss += r[i].w;
-            }
-        };
-        if (nb > 0) rd(A, 0);
-        for (int bt = 0; bt < nb; bt += 2) {
-            rd(B, bt + 1);
-            __builtin_amdgcn_sched_barrier(0);
-            add(A);
-            if (bt + 1 >= nb) break;
-            rd(A, bt + 2);
-            __builtin_amdgcn_sched_barrier(0);
-            add(B);
-        }
+        float ss = orn_lds_seq_sum32(reinterpret_cast<const v4f *>(s_p), nb);
         for (int i = 32 * nb; i < dim; ++i) ss += s_p[i];
         inv_s = 1.0f / sqrtf(ss / (float)dim + 1e-6f);
     }

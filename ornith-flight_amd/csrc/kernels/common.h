@@ -32,6 +32,41 @@ __device__ __forceinline__ float orn_half_to_float(uint32_t h)
     return __uint_as_float(u & nz);
 }
 
+// Sequential fp32 sum ((0 + p[0]) + p[1]) + ... of the 32 * nb floats at p4
+// (LDS), for one lane: batches of 32 in two register buffers, the reads of one
+// batch issued before the adds of the other, so only the chain of adds is
+// serial.  (The order and roundings of a plain loop over p.)
+__device__ __forceinline__ float orn_lds_seq_sum32(const v4f *p4, int nb)
+{
+    float ss = 0.0f;
+    v4f A[8], B[8];
+    auto rd = [&](v4f(&r)[8], int bt) {
+        const int b = bt < nb ? bt : nb - 1;  // past the end: re-read the last batch, unused
+#pragma unroll
+        for (int i = 0; i < 8; ++i) r[i] = p4[8 * b + i];
+    };
+    auto add = [&](const v4f(&r)[8]) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            ss += r[i].x;
+            ss += r[i].y;
+            ss += r[i].z;
+            ss += r[i].w;
+        }
+    };
+    if (nb > 0) rd(A, 0);
+    for (int bt = 0; bt < nb; bt += 2) {
+        rd(B, bt + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        add(A);
+        if (bt + 1 >= nb) break;
+        rd(A, bt + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        add(B);
+    }
+    return ss;
+}
+
 // Empty volatile asm that reads and writes v[0..7] and clobbers memory: every
 // computation of these values is ordered before it, and no load or store
 // moves across it.  Used to keep a ring slot's refill after the slot's last

@@ -339,6 +339,9 @@ __global__ void __launch_bounds__(64)
 // ND = D/32 steps are fully unrolled, with W loads NR steps ahead in a
 // register ring.  The wave also stages x[t] in LDS and, when amax != NULL
 // (block column 0), writes max_k |x[t][k]| for the MFMA activation scaling.
+// With norm_w the input is first replaced by its rmsnorm (each wave runs the
+// norm's sequential sum while its first weight loads are in flight; block
+// column 0 writes the normalised rows to xn_out).
 // ---------------------------------------------------------------------------
 template <int Q>
 __device__ __forceinline__ float dpp_shl(float v)
@@ -358,10 +361,13 @@ template <int ND>
 __global__ void __launch_bounds__(64)
     k_router_dpp(const float *__restrict__ x, const float *__restrict__ Wq,
                  const float *__restrict__ bias, int T, int E, float *__restrict__ logits,
-                 int *ctl, float *__restrict__ amax)
+                 int *ctl, float *__restrict__ amax, const float *__restrict__ norm_w,
+                 float *__restrict__ xn_out)
 {
     constexpr int D = 32 * ND, NR = ND < 16 ? ND : 16;
     __shared__ v4f xs[D / 4];
+    __shared__ v4f ps[D / 4];  // x*x, with norm_w
+    __shared__ float inv_s;
     const int lane = threadIdx.x;
     const int es = lane >> 3, q = lane & 7;
     const int e0 = blockIdx.x * 8;
@@ -376,9 +382,34 @@ __global__ void __launch_bounds__(64)
     {
         const v4f *xg = reinterpret_cast<const v4f *>(x + (size_t)t * D);
         constexpr int NX = D / 256;  // v4f loads per lane
-        v4f tmp[NX];
+        v4f tmp[NX], wn[NX];
 #pragma unroll
         for (int i = 0; i < NX; ++i) tmp[i] = xg[lane + 64 * i];
+        if (norm_w) {
+            // The layer's rmsnorm (gpu.c:144-156) on the fly: x*x into LDS,
+            // lane 0 sums the products in order (the reference's roundings),
+            // then x <- w * (x * inv_rms).  Block column 0 also writes the
+            // normalised row out for the expert steps.
+            const v4f *wg = reinterpret_cast<const v4f *>(norm_w);
+#pragma unroll
+            for (int i = 0; i < NX; ++i) wn[i] = wg[lane + 64 * i];
+#pragma unroll
+            for (int i = 0; i < NX; ++i) ps[lane + 64 * i] = tmp[i] * tmp[i];
+            __syncthreads();
+            if (lane == 0) {
+                const float ss = orn_lds_seq_sum32(ps, D / 32);
+                inv_s = 1.0f / sqrtf(ss / (float)D + 1e-6f);
+            }
+            __syncthreads();
+            const float inv = inv_s;
+#pragma unroll
+            for (int i = 0; i < NX; ++i) tmp[i] = wn[i] * (tmp[i] * inv);
+            if (blockIdx.x == 0) {
+                v4f *xo = reinterpret_cast<v4f *>(xn_out + (size_t)t * D);
+#pragma unroll
+                for (int i = 0; i < NX; ++i) xo[lane + 64 * i] = tmp[i];
+            }
+        }
         float mx = 0.0f;
 #pragma unroll
         for (int i = 0; i < NX; ++i) {
@@ -521,13 +552,21 @@ extern "C" int ornk_moe_route(const ornk_moe_args *a, hipStream_t s)
     const dim3 gd((E + 7) / 8, T);
     if (a->router_amax && !ornk_router_dpp_supported(T, D)) return hipErrorInvalidValue;
     if (ornk_router_dpp_supported(T, D)) {
+        // the norm runs inside the router here (ornk_moe_norm launches nothing)
+        const float *xr = a->apply_norm ? a->x : xin;
+        const float *nw = a->apply_norm ? a->norm_w : nullptr;
+        float *xo = a->apply_norm ? a->xn : nullptr;
+#define ORN_RDPP(N)                                                                              \
+    hipLaunchKernelGGL(k_router_dpp<N>, gd, dim3(64), 0, s, xr, a->router, a->bias, T, E,        \
+                       a->logits, a->ctl, amax, nw, xo)
         switch (D) {
-        case 256: hipLaunchKernelGGL(k_router_dpp<8>, gd, dim3(64), 0, s, xin, a->router, a->bias, T, E, a->logits, a->ctl, amax); break;
-        case 512: hipLaunchKernelGGL(k_router_dpp<16>, gd, dim3(64), 0, s, xin, a->router, a->bias, T, E, a->logits, a->ctl, amax); break;
-        case 1024: hipLaunchKernelGGL(k_router_dpp<32>, gd, dim3(64), 0, s, xin, a->router, a->bias, T, E, a->logits, a->ctl, amax); break;
-        case 2048: hipLaunchKernelGGL(k_router_dpp<64>, gd, dim3(64), 0, s, xin, a->router, a->bias, T, E, a->logits, a->ctl, amax); break;
-        default: hipLaunchKernelGGL(k_router_dpp<128>, gd, dim3(64), 0, s, xin, a->router, a->bias, T, E, a->logits, a->ctl, amax); break;
+        case 256: ORN_RDPP(8); break;
+        case 512: ORN_RDPP(16); break;
+        case 1024: ORN_RDPP(32); break;
+        case 2048: ORN_RDPP(64); break;
+        default: ORN_RDPP(128); break;
         }
+#undef ORN_RDPP
     } else if (T >= 1024) {
         hipLaunchKernelGGL(k_router_seq<4>, dim3((E + 63) / 64, (T + 15) / 16), dim3(256), 0, s,
                            xin, a->router, a->bias, T, D, E, a->logits, a->ctl);
