@@ -323,18 +323,16 @@ __global__ void __launch_bounds__(64)
 }
 
 // ---------------------------------------------------------------------------
-// Decode-sized batches: one wave per (token, 8 experts), the chain carried by
-// one lane per expert while the products come from its neighbours.
+// Decode-sized batches: one wave per (token, 8 experts); the lanes form the
+// products and exchange them through LDS so each expert's chain only adds.
 //
 // Lane l = 8*es + q (es: expert e0+es, q = 0..7) multiplies the k quad
 // 8*it + q of x and W(., e0+es), i.e. k = 32*it + 4q + j (j = 0..3), so a
 // wave load covers 8 experts x 32 k (W's [D/4][E][4] layout: 8 runs of 128
-// contiguous bytes).  The chain lane of expert es is lane 8*es: for q =
-// 0..7, j = 0..3 it adds the product held by lane 8*es + q, fetched by the
-// add itself (v_add_f32 with a DPP row_shl:q source; lanes 8es..8es+7 lie in
-// one 16-lane DPP row).  Each logit is therefore acc = acc + fl(x[k]*W[k])
-// for k ascending, one add per element, bit-identical to model.c:1017-1025
-// (addition commutes exactly, so DPP operand order does not matter).
+// contiguous bytes).  The lanes of expert es (every lane of the group keeps
+// the same chain) add the 32 products of the step in k order, read back
+// from LDS.  Each logit is therefore acc = acc + fl(x[k]*W[k]) for k
+// ascending, one add per element, bit-identical to model.c:1017-1025.
 //
 // ND = D/32 steps are fully unrolled, with W loads NR steps ahead in a
 // register ring.  The wave also stages x[t] in LDS and, when amax != NULL
@@ -343,20 +341,6 @@ __global__ void __launch_bounds__(64)
 // norm's sequential sum while its first weight loads are in flight; block
 // column 0 writes the normalised rows to xn_out).
 // ---------------------------------------------------------------------------
-template <int Q>
-__device__ __forceinline__ float dpp_shl(float v)
-{
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
-                                                                 0x100 + Q, 0xF, 0xF, true));
-}
-
-template <int Q>
-__device__ __forceinline__ void chain_add4(float &acc, const float (&p)[4])
-{
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc = (Q == 0 ? p[j] : dpp_shl<Q>(p[j])) + acc;
-}
-
 template <int ND>
 __global__ void __launch_bounds__(64)
     k_router_dpp(const float *__restrict__ x, const float *__restrict__ Wq,
@@ -425,35 +409,52 @@ __global__ void __launch_bounds__(64)
     }
     __syncthreads();
 
+    // Products of step it (k = 32it + 4q + j, lane 8es + q) go through LDS:
+    // pb[it % 3][lane] holds lane's four, so the chain lane of expert es
+    // reads its 32 products of a step in k order as 8 consecutive quads.
+    // Products are formed two steps ahead, read one step ahead, and added;
+    // the chain's adds then issue back to back (1.25 instructions per
+    // reduction value instead of 2 with a row-shift move per value).
+    __shared__ v4f pb[3][64];
+    auto prod = [&](int it, const v4f xv) {  // products of step it into pb[it % 3]
+        const v4f w = ring[it % NR];
+        if (it + NR < ND) ring[it % NR] = wp[(size_t)8 * (it + NR) * E];
+        pb[it % 3][lane] = xv * w;
+    };
+    auto rd = [&](v4f(&r)[8], int it) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) r[i] = pb[it % 3][8 * es + i];
+    };
     float acc = 0.0f;
-    // x of step it+1 is read from LDS during step it, so its latency is
-    // hidden behind a step of the chain.
-    v4f xnext = xs[q];
+    v4f ca[8], cb[8];
+    // x of step it+3 is read from LDS during step it, a step before use.
+    v4f xnext = ND > 2 ? xs[16 + q] : v4f{};
+    prod(0, xs[q]);
+    if (ND > 1) prod(1, xs[8 + q]);
+    wave_sync();
+    rd(ca, 0);
 #pragma unroll
     for (int it = 0; it < ND; ++it) {
-        const v4f xv = xnext;
-        if (it + 1 < ND) xnext = xs[8 * (it + 1) + q];
-        __builtin_amdgcn_sched_barrier(0);  // the read is issued before the chain
-        const v4f w = ring[it % NR];
-        const float p[4] = {xv.x * w.x, xv.y * w.y, xv.z * w.z, xv.w * w.w};
-        if (it + NR < ND) ring[it % NR] = wp[(size_t)8 * (it + NR) * E];
-        chain_add4<0>(acc, p);
-        chain_add4<1>(acc, p);
-        chain_add4<2>(acc, p);
-        chain_add4<3>(acc, p);
-        chain_add4<4>(acc, p);
-        chain_add4<5>(acc, p);
-        chain_add4<6>(acc, p);
-        chain_add4<7>(acc, p);
-        // The next step's weights pass through this point together with the
-        // chain, so its products cannot be computed ahead of this step's adds.
-        // There is no pin after the last step on purpose: the final adds then
-        // sink into the conditional store below, which keeps the compiler
-        // from folding the row shifts into v_add_f32_dpp anywhere.  A folded
-        // add needs two wait states after the previous add of the chain, so
-        // the chain (the critical path) is shorter with separate DPP moves,
-        // which issue off it.
-        if (it + 1 < ND) asm volatile("" : "+v"(acc), "+v"(ring[(it + 1) % NR]), "+v"(xnext));
+        v4f(&cur)[8] = (it & 1) ? cb : ca;
+        v4f(&nxt)[8] = (it & 1) ? ca : cb;
+        if (it + 2 < ND) {
+            const v4f xv = xnext;
+            if (it + 3 < ND) xnext = xs[8 * (it + 3) + q];
+            prod(it + 2, xv);
+        }
+        wave_sync();
+        if (it + 1 < ND) rd(nxt, it + 1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            acc = acc + cur[i].x;
+            acc = acc + cur[i].y;
+            acc = acc + cur[i].z;
+            acc = acc + cur[i].w;
+        }
+        // Keeps each step's adds in its step (they would otherwise sink into
+        // the conditional store below, holding every product in registers).
+        asm volatile("" : "+v"(acc));
     }
     if (q == 0 && e0 + es < E) logits[(size_t)t * E + e0 + es] = bias ? acc + bias[e0 + es] : acc;
 }
