@@ -24,6 +24,7 @@
 #include "common.h"
 #include "launch.h"
 
+#include <climits>
 #include <math.h>
 
 #define ORN_FUSED_SELECT_T 64
@@ -48,16 +49,32 @@ __device__ __forceinline__ float readlane_f(float v, int l)
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }
 
-// quad_perm [1,0,3,2], [2,3,0,1], then row_ror 4, 8: every lane of a 16-lane
-// row holds the row's value; the four rows are joined with readlane.
-__device__ __forceinline__ float wave_max(float v)
+// Wave max of the selection keys (every lane receives it): quad_perm
+// [1,0,3,2], [2,3,0,1], then row_ror 4, 8 give every lane of a 16-lane row
+// the row's value; the four rows are joined with readlane.
+__device__ __forceinline__ int wave_max_key(int v)
 {
-    v = fmaxf(v, dpp_f<0xB1>(v));
-    v = fmaxf(v, dpp_f<0x4E>(v));
-    v = fmaxf(v, dpp_f<0x124>(v));
-    v = fmaxf(v, dpp_f<0x128>(v));
-    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)),
-                 fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+    v = max(v, __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false));
+    v = max(v, __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false));
+    v = max(v, __builtin_amdgcn_mov_dpp(v, 0x124, 0xF, 0xF, false));
+    v = max(v, __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, false));
+    return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+               max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
+// Order-preserving integer key of a finite float (a < b <=> key(a) <
+// key(b)); -0 is folded into +0, so a -0/+0 pair compares equal, as the
+// two do under '>'.
+__device__ __forceinline__ int sel_key(float f)
+{
+    int b = __builtin_bit_cast(int, f);
+    b = b == INT_MIN ? 0 : b;
+    return b >= 0 ? b : b ^ 0x7FFFFFFF;
+}
+
+__device__ __forceinline__ float key_value(int k)
+{
+    return __builtin_bit_cast(float, k >= 0 ? k : k ^ 0x7FFFFFFF);
 }
 
 __device__ __forceinline__ float wave_sum(float v)
@@ -101,7 +118,8 @@ __device__ void select_token(const float *__restrict__ lg, int E, int k, int mod
                              float *lwo, float *val, int *ix, int *n_slow)
 {
     const int lane = threadIdx.x & 63;
-    float vo[4], v[4];
+    float vo[4];
+    int key[4];  // selection keys; INT_MIN: no expert, or already selected
     bool bad = false;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -109,25 +127,28 @@ __device__ void select_token(const float *__restrict__ lg, int E, int k, int mod
         const bool valid = e < E;
         vo[i] = valid ? lg[e] : -INFINITY;
         if (valid && !isfinite(vo[i])) bad = true;
-        v[i] = vo[i];
+        key[i] = valid ? sel_key(vo[i]) : INT_MIN;
     }
     bool slow = __ballot(bad) != 0ull;
 
-    // Lane r < k ends up holding the r-th selected (value, index).
+    // Lane r < k ends up holding the r-th selected (value, index).  The
+    // rounds compare integer keys of the finite logits (same order, one
+    // integer max per reduction step).
     float my_v = 0.0f, mx = 0.0f, prev = 0.0f;
     int my_e = 0;
     if (!slow) {
         const int rounds = k < E ? k + 1 : k;
         for (int r = 0; r < rounds; ++r) {
-            const float m = wave_max(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+            const int mk = wave_max_key(max(max(key[0], key[1]), max(key[2], key[3])));
+            const float m = key_value(mk);
             uint64_t b[4];
             int cnt = 0;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                b[i] = __ballot(v[i] == m);
+                b[i] = __ballot(key[i] == mk);
                 cnt += __popcll(b[i]);
             }
-            if (cnt != 1) {  // a tie (or -0 == +0): take the literal path
+            if (cnt != 1) {  // a tie (or a -0/+0 pair): take the literal path
                 slow = true;
                 break;
             }
@@ -135,9 +156,10 @@ __device__ void select_token(const float *__restrict__ lg, int E, int k, int mod
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 if (b[i]) e = 64 * i + __ffsll((unsigned long long)b[i]) - 1;
+            const bool hit = lane == (e & 63);  // the winner's lane; e >> 6 is uniform
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                if (lane + 64 * i == e) v[i] = -INFINITY;
+                if (hit && (e >> 6) == i) key[i] = INT_MIN;
             if (r == 0) {
                 mx = m;
             } else {
