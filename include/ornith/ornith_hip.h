@@ -38,6 +38,14 @@ void *gpu_device_ptr(gpu_context *ctx, gpu_buffer *buf);
 /* Name, compute-unit count and HBM size of the context's device. */
 int gpu_device_info(gpu_context *ctx, char *name, size_t name_len, int *n_cus, size_t *hbm_bytes);
 
+/* Measured read bandwidth of the context's device: a streaming-read kernel
+ * (16-byte loads, grid-stride) over a fresh buffer of `bytes` (allocated and
+ * freed by the call; use several times the 256 MB last-level cache), one
+ * untimed launch, then `iters` launches between HIP events on the context's
+ * stream.  Writes GB/s (1e9 B/s).  A measurement helper with no reference
+ * counterpart: it gives the achievable figure next to the spec-sheet peak. */
+int gpu_probe_read_bandwidth(gpu_context *ctx, size_t bytes, int iters, double *gb_per_s);
+
 /* ---------------------------------------------------------------------------
  * Dequantization on the device — the expert-slice / dequant API of
  * engine/src/gguf.h:111-137 with the same validation and bool results.

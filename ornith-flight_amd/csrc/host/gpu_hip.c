@@ -149,6 +149,45 @@ int gpu_device_info(gpu_context *ctx, char *name, size_t name_len, int *n_cus, s
     return ORN_OK;
 }
 
+int gpu_probe_read_bandwidth(gpu_context *ctx, size_t bytes, int iters, double *gb_per_s)
+{
+    if (!ctx || !gb_per_s || bytes < 16 || iters < 1) return ORN_EINVAL;
+    bytes &= ~(size_t)15;
+    void *buf = NULL;
+    uint32_t *out = NULL;
+    hipEvent_t e0 = NULL, e1 = NULL;
+    int rc = ORN_OK;
+    if (hipMalloc(&buf, bytes) != hipSuccess ||
+        hipMalloc((void **)&out, (size_t)ORNK_STREAM_GRID * 256 * sizeof(uint32_t)) != hipSuccess) {
+        rc = orn_set_err(ctx, ORN_ENOMEM, "probe buffer of %zu bytes", bytes);
+        goto done;
+    }
+    if ((rc = orn_hip_check(ctx, hipEventCreate(&e0), "hipEventCreate")) ||
+        (rc = orn_hip_check(ctx, hipEventCreate(&e1), "hipEventCreate")) ||
+        (rc = orn_hip_check(ctx, hipMemsetAsync(buf, 0x5a, bytes, ctx->stream), "hipMemsetAsync")) ||
+        (rc = orn_hip_check(ctx, (hipError_t)ornk_stream_read(buf, bytes, out, ctx->stream),
+                            "stream read")) ||
+        (rc = orn_hip_check(ctx, hipEventRecord(e0, ctx->stream), "hipEventRecord")))
+        goto done;
+    for (int i = 0; i < iters; ++i)
+        if ((rc = orn_hip_check(ctx, (hipError_t)ornk_stream_read(buf, bytes, out, ctx->stream),
+                                "stream read")))
+            goto done;
+    float ms = 0.0f;
+    if ((rc = orn_hip_check(ctx, hipEventRecord(e1, ctx->stream), "hipEventRecord")) ||
+        (rc = orn_hip_check(ctx, hipEventSynchronize(e1), "hipEventSynchronize")) ||
+        (rc = orn_hip_check(ctx, hipEventElapsedTime(&ms, e0, e1), "hipEventElapsedTime")))
+        goto done;
+    *gb_per_s = ms > 0.0f ? (double)bytes * iters / ((double)ms * 1e-3) / 1e9 : 0.0;
+done:
+    hipStreamSynchronize(ctx->stream);
+    if (e0) hipEventDestroy(e0);
+    if (e1) hipEventDestroy(e1);
+    if (out) hipFree(out);
+    if (buf) hipFree(buf);
+    return rc;
+}
+
 static void sync_ctx(gpu_context *ctx) { hipStreamSynchronize(ctx->stream); }
 
 void gpu_copy_to_device(gpu_context *ctx, gpu_buffer *dst, const void *src, size_t size)

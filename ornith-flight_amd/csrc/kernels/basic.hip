@@ -113,9 +113,39 @@ __global__ void k_add(float *out, const float *a, const float *b, int n)
     if (i < n) out[i] = a[i] + b[i];
 }
 
+// Streaming read of n16 16-byte words (grid-stride, 8 loads in flight per
+// thread), folded with xor into one word per thread so the loads are live.
+__global__ void __launch_bounds__(256) k_stream_read(const uint4 *__restrict__ p, size_t n16,
+                                                     uint32_t *__restrict__ out)
+{
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    uint32_t acc = 0;
+    for (; i + 7 * stride < n16; i += 8 * stride) {
+        uint4 v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = p[i + j * stride];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+    }
+    for (; i < n16; i += stride) {
+        const uint4 v = p[i];
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = acc;
+}
+
 inline int blocks_for(size_t n, int bs) { return (int)((n + (size_t)bs - 1) / (size_t)bs); }
 
 }  // namespace
+
+// out: ORNK_STREAM_GRID * 256 words.
+extern "C" int ornk_stream_read(const void *p, size_t bytes, uint32_t *out, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_stream_read, dim3(ORNK_STREAM_GRID), dim3(256), 0, s,
+                       reinterpret_cast<const uint4 *>(p), bytes / 16, out);
+    return hipGetLastError();
+}
 
 extern "C" int ornk_fill_f32(float *p, float v, size_t n, hipStream_t s)
 {

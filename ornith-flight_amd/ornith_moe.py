@@ -38,7 +38,7 @@ EXPORTED = [
     "gpu_moe_store_create", "gpu_moe_store_destroy", "gpu_moe_store_bytes",
     "gpu_moe_store_set_experts", "gpu_moe_store_set_router", "gpu_moe_store_set_norm",
     "gpu_moe_store_fill_synthetic", "gpu_moe_forward", "gpu_moe_forward_stack",
-    "gpu_moe_last_stats",
+    "gpu_moe_last_stats", "gpu_probe_read_bandwidth",
     "gpu_profile_enable", "gpu_profile_reset", "gpu_profile_count", "gpu_profile_name",
     "gpu_profile_total_ms", "gpu_profile_calls",
     "orn_synth_stream", "orn_synth_q4k", "orn_synth_q6k", "orn_synth_normal",
@@ -111,6 +111,7 @@ def lib():
         "gpu_moe_forward": (i, [vp, vp, i, vp, i, vp, vp, vp, vp, C.POINTER(MoEOpts)]),
         "gpu_moe_forward_stack": (i, [vp, vp, i, i, vp, vp, i, C.POINTER(MoEOpts)]),
         "gpu_moe_last_stats": (i, [vp, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+        "gpu_probe_read_bandwidth": (i, [vp, sz, i, C.POINTER(C.c_double)]),
         "gpu_profile_enable": (i, [vp, i]), "gpu_profile_reset": (None, [vp]),
         "gpu_profile_count": (i, [vp]), "gpu_profile_name": (C.c_char_p, [vp, i]),
         "gpu_profile_total_ms": (C.c_double, [vp, i]), "gpu_profile_calls": (C.c_long, [vp, i]),
@@ -240,6 +241,13 @@ class Context:
         hbm = C.c_size_t(0)
         self.check(lib().gpu_device_info(self.ptr, name, 256, C.byref(cus), C.byref(hbm)), "device_info")
         return name.value.decode(), cus.value, hbm.value
+
+    def read_bandwidth(self, nbytes, iters=5):
+        """Measured streaming-read GB/s of the device (gpu_probe_read_bandwidth)."""
+        gbs = C.c_double(0.0)
+        self.check(lib().gpu_probe_read_bandwidth(self.ptr, nbytes, iters, C.byref(gbs)),
+                   "probe_read_bandwidth")
+        return gbs.value
 
     def close(self):
         if self.ptr:

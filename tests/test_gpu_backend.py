@@ -261,3 +261,16 @@ def test_device_resident_dequant(om, ctx, golden_dir):
     assert np.array_equal(ctx.download(dst, np.float32, n).view(np.uint32), g["expected"].view(np.uint32))
     small = ctx.alloc(16)
     assert not om.lib().gpu_dequantize_tensor_buf(ctx.ptr, src.ptr, C.byref(info), small.ptr)
+
+
+# ------------------------------------------------- measurement helper
+def test_read_bandwidth_probe(om, ctx):
+    """gpu_probe_read_bandwidth: a positive, physically plausible figure, and
+    invalid arguments rejected without a launch."""
+    gbs = ctx.read_bandwidth(64 << 20, 2)
+    assert 10.0 < gbs < 100000.0
+    L = om.lib()
+    out = C.c_double(-1.0)
+    assert L.gpu_probe_read_bandwidth(ctx.ptr, 8, 1, C.byref(out)) != 0
+    assert L.gpu_probe_read_bandwidth(ctx.ptr, 1 << 20, 0, C.byref(out)) != 0
+    assert out.value == -1.0
