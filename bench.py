@@ -231,9 +231,9 @@ def main():
         src.free()
         dst.free()
         log(f"copy probe: {args.copy_probe} MiB device-to-device")
-    # Achievable streaming-read bandwidth of this device (4 GiB, 16 x the
+    # Achievable streaming-read bandwidth of this device (8 GiB, 32 x the
     # last-level cache), reported beside the spec-sheet peak.
-    read_gbs = ctx.read_bandwidth(4 << 30, 5)
+    read_gbs = ctx.read_bandwidth(8 << 30, 5)
     log(f"measured streaming read: {read_gbs:.0f} GB/s")
     store = om.Store(ctx, 2, D, H, E, K, True)
     t0 = time.perf_counter()

@@ -22,7 +22,7 @@ extern "C" {
 
 /* ---- generic fp32 ops behind gpu.h --------------------------------------- */
 int ornk_fill_f32(float *p, float v, size_t n, hipStream_t s);
-#define ORNK_STREAM_GRID 4096
+#define ORNK_STREAM_GRID 16384
 int ornk_stream_read(const void *p, size_t bytes, uint32_t *out, hipStream_t s);
 int ornk_matmul_f32(float *C, const float *A, const float *B, int M, int N, int K, hipStream_t s);
 int ornk_rmsnorm(float *out, const float *x, const float *w, int rows, int dim, hipStream_t s);
