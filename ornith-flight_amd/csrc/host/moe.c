@@ -786,7 +786,7 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
         a.dn_pf.dd = (const float *)((const uint8_t *)st->dd + slot0 * (DH / 64));
         a.dn_pf.dmax = st->dmax + slot0 * 3;
         a.x_amax = (float *)(ws + o_xamax);
-        a.router_amax = ornk_router_dpp_supported(T, D);
+        a.router_amax = ornk_router_pc_supported(T, D);
         a.mid_amax = (float *)(ws + o_midamax);
     }
 

@@ -484,7 +484,7 @@ __global__ void __launch_bounds__(256)
 extern "C" int ornk_moe_norm(const ornk_moe_args *a, hipStream_t s)
 {
     // the decode-sized router normalises its own input (ornk_moe_route)
-    if (!a->apply_norm || ornk_router_dpp_supported(a->T, a->D)) return hipSuccess;
+    if (!a->apply_norm || ornk_router_pc_supported(a->T, a->D)) return hipSuccess;
     return ornk_rmsnorm(a->xn, a->x, a->norm_w, a->T, a->D, s);
 }
 

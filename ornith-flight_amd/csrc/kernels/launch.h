@@ -108,8 +108,8 @@ int ornk_moe_norm(const ornk_moe_args *a, hipStream_t s);
 int ornk_moe_route(const ornk_moe_args *a, hipStream_t s);
 /* Batches the one-wave-per-(token, 8 experts) router takes (and that can
  * produce x_amax on the side). */
-#define ORN_ROUTER_DPP_MAX_T 64
-int ornk_router_dpp_supported(int T, int D);
+#define ORN_ROUTER_PC_MAX_T 64
+int ornk_router_pc_supported(int T, int D);
 int ornk_moe_dispatch(const ornk_moe_args *a, hipStream_t s);
 int ornk_moe_gateup(const ornk_moe_args *a, hipStream_t s);
 int ornk_moe_mid(const ornk_moe_args *a, hipStream_t s);

@@ -7,7 +7,7 @@
 // exchange selection with strict '>' (model.c:301-305 / 1040-1048).
 //
 // The MoE path computes every logit with exactly that arithmetic, one chain
-// per (token, expert), all chains in parallel (k_router_dpp for decode-sized
+// per (token, expert), all chains in parallel (k_router_pc for decode-sized
 // batches, k_router_dec / k_router_seq above), so the logits are
 // bit-identical to the reference's by construction.  Top-k selection and
 // the dispatch that follows it: dispatch.hip.
@@ -323,64 +323,87 @@ __global__ void __launch_bounds__(64)
 }
 
 // ---------------------------------------------------------------------------
-// Decode-sized batches: one wave per (token, 8 experts); the lanes form the
-// products and exchange them through LDS so each expert's chain only adds.
+// Decode-sized batches: one work group of two waves per (token, 8 experts).
+// Wave 1 (the producer) streams W and forms the products; wave 0 (the
+// consumer) only adds them, so its instruction stream is the chain itself.
 //
-// Lane l = 8*es + q (es: expert e0+es, q = 0..7) multiplies the k quad
-// 8*it + q of x and W(., e0+es), i.e. k = 32*it + 4q + j (j = 0..3), so a
-// wave load covers 8 experts x 32 k (W's [D/4][E][4] layout: 8 runs of 128
-// contiguous bytes).  The lanes of expert es (every lane of the group keeps
-// the same chain) add the 32 products of the step in k order, read back
-// from LDS.  Each logit is therefore acc = acc + fl(x[k]*W[k]) for k
-// ascending, one add per element, bit-identical to model.c:1017-1025.
+// Lane l = 8*es + q (es: expert e0+es, q = 0..7) of the producer multiplies
+// the k quad 8*it + q of x and W(., e0+es), i.e. k = 32*it + 4q + j (j =
+// 0..3), so a wave load covers 8 experts x 32 k (W's [D/4][E][4] layout: 8
+// runs of 128 contiguous bytes), and writes its four products to pb[it %
+// (3C)][l].  The consumer lanes of expert es (every lane of the group keeps
+// the same chain) read the 32 products of a step back in k order as 8
+// consecutive quads and add them.  Each logit is therefore acc = acc +
+// fl(x[k]*W[k]) for k ascending, one add per element, bit-identical to
+// model.c:1017-1025.
 //
-// ND = D/32 steps are fully unrolled, with W loads NR steps ahead in a
-// register ring.  The wave also stages x[t] in LDS and, when amax != NULL
-// (block column 0), writes max_k |x[t][k]| for the MFMA activation scaling.
-// With norm_w the input is first replaced by its rmsnorm (each wave runs the
-// norm's sequential sum while its first weight loads are in flight; block
-// column 0 writes the normalised rows to xn_out).
+// The ND = D/32 steps form chunks of C steps in a three-chunk LDS ring.  The
+// producer runs two chunks ahead: chunks 0 and 1 before barrier B_0, chunk
+// c+1 between B_{c-1} and B_c.  The consumer adds chunk c between B_c and
+// B_{c+1} and reads the next step a step ahead, across chunk edges too
+// (that chunk is complete since the previous barrier), so it never waits on
+// LDS.  Both waves pass the same ND/C barriers; the producer, ~4x shorter
+// per step, is the one that waits.
+//
+// Before that the group stages x[t] in LDS and, when amax != NULL (block
+// column 0), writes max_k |x[t][k]| for the MFMA activation scaling.  With
+// norm_w the input is first replaced by its rmsnorm (one thread runs the
+// norm's sequential sum while the producer's first weight loads are in
+// flight; block column 0 writes the normalised rows to xn_out).
 // ---------------------------------------------------------------------------
 template <int ND>
-__global__ void __launch_bounds__(64)
-    k_router_dpp(const float *__restrict__ x, const float *__restrict__ Wq,
-                 const float *__restrict__ bias, int T, int E, float *__restrict__ logits,
-                 int *ctl, float *__restrict__ amax, const float *__restrict__ norm_w,
-                 float *__restrict__ xn_out)
+__global__ void __launch_bounds__(128)
+    k_router_pc(const float *__restrict__ x, const float *__restrict__ Wq,
+                const float *__restrict__ bias, int T, int E, float *__restrict__ logits,
+                int *ctl, float *__restrict__ amax, const float *__restrict__ norm_w,
+                float *__restrict__ xn_out)
 {
     constexpr int D = 32 * ND, NR = ND < 16 ? ND : 16;
+    constexpr int C = ND < 8 ? ND : 8, NC = ND / C;
     __shared__ v4f xs[D / 4];
     __shared__ v4f ps[D / 4];  // x*x, with norm_w
-    __shared__ float inv_s;
-    const int lane = threadIdx.x;
+    __shared__ v4f pb[3 * C][64];
+    __shared__ float inv_s, mx_s[2];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the roles branch per wave
     const int es = lane >> 3, q = lane & 7;
     const int e0 = blockIdx.x * 8;
     const int t = blockIdx.y;
+    const bool producer = wave == 1;
     // The routing step is the first of every forward: clear its counters.
-    if (ctl && blockIdx.x == 0 && blockIdx.y == 0 && lane < 16) ctl[lane] = 0;
+    if (ctl && blockIdx.x == 0 && blockIdx.y == 0 && tid < 16) ctl[tid] = 0;
     const int e = min(e0 + es, E - 1);  // lanes past E compute a copy, never stored
     const v4f *wp = reinterpret_cast<const v4f *>(Wq) + (size_t)q * E + e;  // step it: + 8*it*E
     v4f ring[NR];
+    if (producer) {
 #pragma unroll
-    for (int i = 0; i < NR; ++i) ring[i] = wp[(size_t)8 * i * E];
+        for (int i = 0; i < NR; ++i) ring[i] = wp[(size_t)8 * i * E];
+    }
     {
         const v4f *xg = reinterpret_cast<const v4f *>(x + (size_t)t * D);
-        constexpr int NX = D / 256;  // v4f loads per lane
+        constexpr int NX = (D / 4 + 127) / 128;  // v4f per thread
         v4f tmp[NX], wn[NX];
 #pragma unroll
-        for (int i = 0; i < NX; ++i) tmp[i] = xg[lane + 64 * i];
+        for (int i = 0; i < NX; ++i) {
+            const int j = tid + 128 * i;
+            tmp[i] = j < D / 4 ? xg[j] : v4f{};
+        }
         if (norm_w) {
             // The layer's rmsnorm (gpu.c:144-156) on the fly: x*x into LDS,
-            // lane 0 sums the products in order (the reference's roundings),
-            // then x <- w * (x * inv_rms).  Block column 0 also writes the
-            // normalised row out for the expert steps.
+            // one thread sums the products in order (the reference's
+            // roundings), then x <- w * (x * inv_rms).  Block column 0 also
+            // writes the normalised row out for the expert steps.
             const v4f *wg = reinterpret_cast<const v4f *>(norm_w);
 #pragma unroll
-            for (int i = 0; i < NX; ++i) wn[i] = wg[lane + 64 * i];
-#pragma unroll
-            for (int i = 0; i < NX; ++i) ps[lane + 64 * i] = tmp[i] * tmp[i];
+            for (int i = 0; i < NX; ++i) {
+                const int j = tid + 128 * i;
+                if (j < D / 4) {
+                    wn[i] = wg[j];
+                    ps[j] = tmp[i] * tmp[i];
+                }
+            }
             __syncthreads();
-            if (lane == 0) {
+            if (tid == 0) {
                 const float ss = orn_lds_seq_sum32(ps, D / 32);
                 inv_s = 1.0f / sqrtf(ss / (float)D + 1e-6f);
             }
@@ -391,58 +414,69 @@ __global__ void __launch_bounds__(64)
             if (blockIdx.x == 0) {
                 v4f *xo = reinterpret_cast<v4f *>(xn_out + (size_t)t * D);
 #pragma unroll
-                for (int i = 0; i < NX; ++i) xo[lane + 64 * i] = tmp[i];
+                for (int i = 0; i < NX; ++i)
+                    if (tid + 128 * i < D / 4) xo[tid + 128 * i] = tmp[i];
             }
         }
         float mx = 0.0f;
 #pragma unroll
         for (int i = 0; i < NX; ++i) {
-            xs[lane + 64 * i] = tmp[i];
-            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(tmp[i].x), fabsf(tmp[i].y)),
-                                 fmaxf(fabsf(tmp[i].z), fabsf(tmp[i].w))));
+            const int j = tid + 128 * i;
+            if (j < D / 4) {
+                xs[j] = tmp[i];
+                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(tmp[i].x), fabsf(tmp[i].y)),
+                                     fmaxf(fabsf(tmp[i].z), fabsf(tmp[i].w))));
+            }
         }
         if (amax && blockIdx.x == 0) {
 #pragma unroll
             for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-            if (lane == 0) amax[t] = mx;
+            if (lane == 0) mx_s[wave] = mx;
         }
     }
     __syncthreads();
+    if (amax && blockIdx.x == 0 && tid == 0) amax[t] = fmaxf(mx_s[0], mx_s[1]);
 
-    // Products of step it (k = 32it + 4q + j, lane 8es + q) go through LDS:
-    // pb[it % 3][lane] holds lane's four, so the chain lane of expert es
-    // reads its 32 products of a step in k order as 8 consecutive quads.
-    // Products are formed two steps ahead, read one step ahead, and added;
-    // the chain's adds then issue back to back (1.25 instructions per
-    // reduction value instead of 2 with a row-shift move per value).
-    __shared__ v4f pb[3][64];
-    auto prod = [&](int it, const v4f xv) {  // products of step it into pb[it % 3]
-        const v4f w = ring[it % NR];
-        if (it + NR < ND) ring[it % NR] = wp[(size_t)8 * (it + NR) * E];
-        pb[it % 3][lane] = xv * w;
-    };
+    if (producer) {
+        auto prod = [&](int it, const v4f xv) {  // products of step it into pb[it % 3C]
+            const v4f w = ring[it % NR];
+            if (it + NR < ND) ring[it % NR] = wp[(size_t)8 * (it + NR) * E];
+            pb[it % (3 * C)][lane] = xv * w;
+        };
+        // x of step it+1 is read from LDS during step it.
+        v4f xnext = xs[q];
+        auto step = [&](int it) {
+            const v4f xv = xnext;
+            if (it + 1 < ND) xnext = xs[8 * (it + 1) + q];
+            prod(it, xv);
+        };
+#pragma unroll
+        for (int it = 0; it < (2 * C < ND ? 2 * C : ND); ++it) step(it);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            __syncthreads();  // B_c
+            if (c + 2 < NC) {
+#pragma unroll
+                for (int s = 0; s < C; ++s) step((c + 2) * C + s);
+            }
+        }
+        return;
+    }
+
     auto rd = [&](v4f(&r)[8], int it) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) r[i] = pb[it % 3][8 * es + i];
+        for (int i = 0; i < 8; ++i) r[i] = pb[it % (3 * C)][8 * es + i];
     };
     float acc = 0.0f;
     v4f ca[8], cb[8];
-    // x of step it+3 is read from LDS during step it, a step before use.
-    v4f xnext = ND > 2 ? xs[16 + q] : v4f{};
-    prod(0, xs[q]);
-    if (ND > 1) prod(1, xs[8 + q]);
-    wave_sync();
-    rd(ca, 0);
 #pragma unroll
     for (int it = 0; it < ND; ++it) {
+        if (it % C == 0) {
+            __syncthreads();  // B_{it/C}: chunk it/C + 1 is complete
+            if (it == 0) rd(ca, 0);
+        }
         v4f(&cur)[8] = (it & 1) ? cb : ca;
         v4f(&nxt)[8] = (it & 1) ? ca : cb;
-        if (it + 2 < ND) {
-            const v4f xv = xnext;
-            if (it + 3 < ND) xnext = xs[8 * (it + 3) + q];
-            prod(it + 2, xv);
-        }
-        wave_sync();
         if (it + 1 < ND) rd(nxt, it + 1);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -535,9 +569,9 @@ extern "C" int ornk_topk(const float *logits, int T, int E, int k, int mode, uin
 // ---------------------------------------------------------------------------
 // MoE routing step: exact logits into a->logits (selection: dispatch.hip).
 // ---------------------------------------------------------------------------
-extern "C" int ornk_router_dpp_supported(int T, int D)
+extern "C" int ornk_router_pc_supported(int T, int D)
 {
-    return T >= 1 && T <= ORN_ROUTER_DPP_MAX_T &&
+    return T >= 1 && T <= ORN_ROUTER_PC_MAX_T &&
            (D == 256 || D == 512 || D == 1024 || D == 2048 || D == 4096);
 }
 
@@ -551,23 +585,23 @@ extern "C" int ornk_moe_route(const ornk_moe_args *a, hipStream_t s)
     const float *xin = a->apply_norm ? a->xn : a->x;
     float *amax = a->router_amax ? a->x_amax : nullptr;
     const dim3 gd((E + 7) / 8, T);
-    if (a->router_amax && !ornk_router_dpp_supported(T, D)) return hipErrorInvalidValue;
-    if (ornk_router_dpp_supported(T, D)) {
+    if (a->router_amax && !ornk_router_pc_supported(T, D)) return hipErrorInvalidValue;
+    if (ornk_router_pc_supported(T, D)) {
         // the norm runs inside the router here (ornk_moe_norm launches nothing)
         const float *xr = a->apply_norm ? a->x : xin;
         const float *nw = a->apply_norm ? a->norm_w : nullptr;
         float *xo = a->apply_norm ? a->xn : nullptr;
-#define ORN_RDPP(N)                                                                              \
-    hipLaunchKernelGGL(k_router_dpp<N>, gd, dim3(64), 0, s, xr, a->router, a->bias, T, E,        \
+#define ORN_RPC(N)                                                                              \
+    hipLaunchKernelGGL(k_router_pc<N>, gd, dim3(128), 0, s, xr, a->router, a->bias, T, E,        \
                        a->logits, a->ctl, amax, nw, xo)
         switch (D) {
-        case 256: ORN_RDPP(8); break;
-        case 512: ORN_RDPP(16); break;
-        case 1024: ORN_RDPP(32); break;
-        case 2048: ORN_RDPP(64); break;
-        default: ORN_RDPP(128); break;
+        case 256: ORN_RPC(8); break;
+        case 512: ORN_RPC(16); break;
+        case 1024: ORN_RPC(32); break;
+        case 2048: ORN_RPC(64); break;
+        default: ORN_RPC(128); break;
         }
-#undef ORN_RDPP
+#undef ORN_RPC
     } else if (T >= 1024) {
         hipLaunchKernelGGL(k_router_seq<4>, dim3((E + 63) / 64, (T + 15) / 16), dim3(256), 0, s,
                            xin, a->router, a->bias, T, D, E, a->logits, a->ctl);
