@@ -32,6 +32,37 @@ __device__ __forceinline__ float orn_half_to_float(uint32_t h)
     return __uint_as_float(u & nz);
 }
 
+// The same sum over a compile-time count of NB batches, fully unrolled: the
+// reads of batch b+1 are issued before the adds of batch b and every add
+// issues back to back (no loop counter, no per-batch wait beyond the data).
+template <int NB>
+__device__ __forceinline__ float orn_lds_seq_sum32_n(const v4f *p4)
+{
+    float ss = 0.0f;
+    v4f A[8], B[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) A[i] = p4[i];
+#pragma unroll
+    for (int bt = 0; bt < NB; ++bt) {
+        v4f(&cur)[8] = (bt & 1) ? B : A;
+        v4f(&nxt)[8] = (bt & 1) ? A : B;
+        if (bt + 1 < NB) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) nxt[i] = p4[8 * (bt + 1) + i];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            ss += cur[i].x;
+            ss += cur[i].y;
+            ss += cur[i].z;
+            ss += cur[i].w;
+        }
+        asm volatile("" : "+v"(ss));  // each batch's adds stay in their batch
+    }
+    return ss;
+}
+
 // Sequential fp32 sum ((0 + p[0]) + p[1]) + ... of the 32 * nb floats at p4
 // (LDS), for one lane: batches of 32 in two register buffers, the reads of one
 // batch issued before the adds of the other, so only the chain of adds is

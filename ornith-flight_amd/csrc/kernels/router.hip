@@ -404,7 +404,7 @@ __global__ void __launch_bounds__(128)
             }
             __syncthreads();
             if (tid == 0) {
-                const float ss = orn_lds_seq_sum32(ps, D / 32);
+                const float ss = orn_lds_seq_sum32_n<ND>(ps);
                 inv_s = 1.0f / sqrtf(ss / (float)D + 1e-6f);
             }
             __syncthreads();
