@@ -18,8 +18,9 @@
 // row <-> (token, selection slot) maps.  Pairs with w < 1e-6 are skipped
 // (model.c:1066).  Scans are wave-level DPP scans joined through LDS.
 //
-// Up to ORN_FUSED_SELECT_T tokens, selection and dispatch run in one work
-// group of 16 waves (one launch); above, k_select (a wave per token) then
+// One token: a single wave selects and dispatches (k_select_dispatch1).  Up
+// to ORN_FUSED_SELECT_T tokens, selection and dispatch run in one work group
+// of 16 waves (one launch); above, k_select (a wave per token) then
 // k_dispatch.
 #include "common.h"
 #include "launch.h"
@@ -390,6 +391,55 @@ __global__ void __launch_bounds__(1024)
                    row_token, pair_row, items, items_max, tchunk);
 }
 
+// One token: selection and dispatch by a single wave, with no work-group
+// barrier.  Produces what dispatch_group does for T = 1: every active slot
+// holds one row (row index = slot index), the shared expert first, then the
+// selected experts with w >= 1e-6 in ascending id; one item per slot.
+__global__ void __launch_bounds__(64)
+    k_select_dispatch1(const float *__restrict__ logits, int E, int k, int mode,
+                       uint32_t *__restrict__ idx_out, float *__restrict__ w_out, int has_shared,
+                       int *ctl, int *slot_expert, int *slot_off, int *slot_cnt, int *row_token,
+                       int *pair_row, int4 *items, int items_max)
+{
+    __shared__ float sv[256];
+    __shared__ int si[256];
+    __shared__ int lidx[16];
+    __shared__ float lw[16];
+    select_token(logits, E, k, mode, idx_out, w_out, lidx, lw, sv, si, ctl + 3);
+    wave_sync();
+    const int lane = threadIdx.x;
+    auto kept = [&](int j) {  // pair j survives the skip rule (model.c:1066)
+        return !(lw[j] < 1e-6f) && (uint32_t)lidx[j] < (uint32_t)E;
+    };
+    const bool valid = lane < k && kept(lane);
+    const int e = lane < k ? lidx[lane] : 0;
+    int rank = 0;  // among the kept pairs, by expert id (the ids are distinct)
+    for (int j = 0; j < k; ++j) rank += (kept(j) && lidx[j] < e) ? 1 : 0;
+    const int hs = has_shared ? 1 : 0;
+    const int n_slots = hs + __popcll(__ballot(valid));
+    if (valid) {
+        const int sl = hs + rank;
+        slot_expert[sl] = e;
+        slot_off[sl] = sl;
+        slot_cnt[sl] = 1;
+        if (sl < items_max) items[sl] = make_int4(sl, sl, 1, e);
+        row_token[sl] = 0;
+    }
+    if (lane < k) pair_row[lane] = valid ? hs + rank : -1;
+    if (lane == 0) {
+        if (hs) {
+            slot_expert[0] = E;
+            slot_off[0] = 0;
+            slot_cnt[0] = 1;
+            if (items_max > 0) items[0] = make_int4(0, 0, 1, E);
+            row_token[0] = 0;
+        }
+        ctl[0] = n_slots;
+        ctl[1] = n_slots < items_max ? n_slots : items_max;
+        ctl[2] = n_slots;
+    }
+}
+
 }  // namespace
 
 // Selection + dispatch step of the MoE forward (after the router).
@@ -399,6 +449,12 @@ extern "C" int ornk_moe_dispatch(const ornk_moe_args *a, hipStream_t s)
     if (T <= 0) return hipSuccess;
     if (E < 1 || E > 256 || k < 1 || k > 16 || k > E) return hipErrorInvalidValue;
     int4 *items = reinterpret_cast<int4 *>(a->items);
+    if (T == 1) {
+        hipLaunchKernelGGL(k_select_dispatch1, dim3(1), dim3(64), 0, s, a->logits, E, k, a->mode,
+                           a->idx, a->w, a->has_shared, a->ctl, a->slot_expert, a->slot_off,
+                           a->slot_cnt, a->row_token, a->pair_row, items, a->items_max);
+        return hipGetLastError();
+    }
     if (T <= ORN_FUSED_SELECT_T) {
         hipLaunchKernelGGL(k_select_dispatch, dim3(1), dim3(1024), 0, s, a->logits, T, E, k,
                            a->mode, a->idx, a->w, a->has_shared, a->ctl, a->slot_expert,
