@@ -801,7 +801,9 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     } else {
         if ((rc = launch(ctx, "moe_gateup", ornk_moe_gateup, &a))) return rc;
     }
-    if ((rc = launch(ctx, "moe_mid", ornk_moe_mid, &a))) return rc;
+    /* One token: the decode down kernel forms mid from the gate/up partials. */
+    const int fused_mid = p.use_dec && ornk_down_dec_fuses_mid(T, H, p.ks_gu, p.ks_dn);
+    if (!fused_mid && (rc = launch(ctx, "moe_mid", ornk_moe_mid, &a))) return rc;
     if (p.use_dec) {
         if ((rc = launch(ctx, "moe_down_dec", ornk_moe_down_dec, &a))) return rc;
     } else if (use_mfma) {

@@ -254,22 +254,32 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
 // Down (Q6_K).  Logical tile = (item * ks + kslice) * (D/256) + b; output
 // dn[kslice][row][n].  Same structure (activation = mid row, hi/lo of
 // mid*s*d).
+//
+// KSG > 0 (one token: every item is one row): the work group forms its
+// slice of the mid row itself from the KSG gate/up split-K partials, with
+// the mid step's arithmetic (fixed-order sum from 0, clamped SiLU for
+// routed rows, model.c:1087-1088, plain for the shared expert's,
+// gpu.c:176-186), and scales the activation tile by the slice's own
+// max |mid|; the separate mid launch is skipped.
 // ---------------------------------------------------------------------------
 struct DnRing {
     uint4 q0, q1, sc[4];
 };
 
-template <int NR, int KT, int KC>
+template <int NR, int KT, int KC, int KSG>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
     k_down_dec(ornk_dn_prefill P, const float *__restrict__ mid,
                const float *__restrict__ mid_amax, const int *__restrict__ ctl,
                const int4 *__restrict__ items, float *__restrict__ dn, int D, int H, int ks,
-               int rows_max)
+               int rows_max, const float *__restrict__ gu, int shared_rows)
 {
     constexpr int NCHK = KT / KC, NBUF = NCHK > 1 ? 2 : 1;
     constexpr int LC = 2 * KC;
+    constexpr int KV = 32 * KT;  // reduction values of the slice
     __shared__ __align__(16) uint32_t As[NBUF][KC][2][16 * ORN_AST / 2];
     __shared__ float s_inv[16];
+    __shared__ __align__(16) float Ms[KSG ? KV : 4];  // the slice of the mid row (KSG > 0)
+    __shared__ float red[4];
 
     const int NBD = D >> 8;
     const int per_item = NBD * ks;
@@ -307,7 +317,44 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
     for (int i = 0; i < NR; ++i) load_b(st[i], i);
     __builtin_amdgcn_sched_barrier(0);
 
-    const float amax = mid_amax[itm.y + arow];
+    float amax;
+    if (KSG) {
+        const size_t sstr = (size_t)rows_max * 2 * H;  // between gate/up slices
+        const float *pg = gu + (size_t)itm.y * 2 * H + 32 * kt0;
+        float lmax = 0.0f;
+        for (int h = tid; h < KV; h += 256) {
+            float gv[KSG > 0 ? KSG : 1], uv[KSG > 0 ? KSG : 1];
+#pragma unroll
+            for (int sl = 0; sl < KSG; ++sl) {
+                gv[sl] = pg[sl * sstr + h];
+                uv[sl] = pg[sl * sstr + H + h];
+            }
+            float g = 0.0f, u = 0.0f;
+#pragma unroll
+            for (int sl = 0; sl < KSG; ++sl) {
+                g = g + gv[sl];
+                u = u + uv[sl];
+            }
+            float act;
+            if (itm.y < shared_rows) {
+                act = g / (1.0f + expf(-g));
+            } else {
+                if (g < -50.0f) act = 0.0f;
+                else if (g > 50.0f) act = g;
+                else act = g / (1.0f + expf(-g));
+            }
+            const float v = act * u;
+            Ms[h] = v;
+            lmax = fmaxf(lmax, fabsf(v));
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) lmax = fmaxf(lmax, __shfl_xor(lmax, off, 64));
+        if (lane == 0) red[wave] = lmax;
+        __syncthreads();
+        amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    } else {
+        amax = mid_amax[itm.y + arow];
+    }
     const float dmx = P.dmax[e * 3 + 2];
     const float *xr = mid + (size_t)(itm.y + arow) * H + 32 * kt0 + seg * LC;
     const float *dr = P.dd + (size_t)e * (DH / 256) + (size_t)b * H + 32 * kt0 + seg * LC;
@@ -319,7 +366,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
         if (!rows_live) return;
 #pragma unroll
         for (int i = 0; i < LC / 4; ++i) {
-            xv[i] = *reinterpret_cast<const v4f *>(xr + 32 * KC * ch + 4 * i);
+            xv[i] = KSG ? *reinterpret_cast<const v4f *>(&Ms[32 * KC * ch + seg * LC + 4 * i])
+                        : *reinterpret_cast<const v4f *>(xr + 32 * KC * ch + 4 * i);
             dv[i] = *reinterpret_cast<const v4f *>(dr + 32 * KC * ch + 4 * i);
         }
     };
@@ -444,6 +492,13 @@ extern "C" int ornk_moe_gateup_dec(const ornk_moe_args *a, hipStream_t s)
     return hipGetLastError();
 }
 
+// One token with 16 gate/up slices and 8-step down slices: the down kernel
+// forms mid itself (the instance compiled for that plan).
+extern "C" int ornk_down_dec_fuses_mid(int T, int H, int ks_gu, int ks_dn)
+{
+    return T == 1 && ks_gu == 16 && ks_dn >= 1 && H % (32 * ks_dn) == 0 && H / 32 / ks_dn == 8;
+}
+
 extern "C" int ornk_moe_down_dec(const ornk_moe_args *a, hipStream_t s)
 {
     const int ks = a->ks_dn;
@@ -452,10 +507,17 @@ extern "C" int ornk_moe_down_dec(const ornk_moe_args *a, hipStream_t s)
     const int KT = a->H / 32 / ks;
     if (!ornk_dec_supported(4, KT)) return hipErrorInvalidValue;
     const dim3 grid(a->items_max * (a->D / 256) * ks);
-#define ORN_DN_DEC(K)                                                                       \
-    hipLaunchKernelGGL((k_down_dec<ORN_DEC_NR, K, 4>), grid, dim3(256), 0, s, a->dn_pf, a->mid, \
-                       a->mid_amax, a->ctl, reinterpret_cast<const int4 *>(a->items),        \
-                       a->dn_part, a->D, a->H, ks, a->rows_max)
+    const int shared_rows = a->has_shared ? a->T : 0;
+    if (ornk_down_dec_fuses_mid(a->T, a->H, a->ks_gu, ks)) {
+        hipLaunchKernelGGL((k_down_dec<ORN_DEC_NR, 8, 4, 16>), grid, dim3(256), 0, s, a->dn_pf,
+                           a->mid, a->mid_amax, a->ctl, reinterpret_cast<const int4 *>(a->items),
+                           a->dn_part, a->D, a->H, ks, a->rows_max, a->gu_part, shared_rows);
+        return hipGetLastError();
+    }
+#define ORN_DN_DEC(K)                                                                          \
+    hipLaunchKernelGGL((k_down_dec<ORN_DEC_NR, K, 4, 0>), grid, dim3(256), 0, s, a->dn_pf, a->mid, \
+                       a->mid_amax, a->ctl, reinterpret_cast<const int4 *>(a->items),           \
+                       a->dn_part, a->D, a->H, ks, a->rows_max, a->gu_part, shared_rows)
     switch (KT) {
     case 4: ORN_DN_DEC(4); break;
     case 8: ORN_DN_DEC(8); break;

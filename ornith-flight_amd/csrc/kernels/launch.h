@@ -110,6 +110,9 @@ int ornk_moe_route(const ornk_moe_args *a, hipStream_t s);
  * produce x_amax on the side). */
 #define ORN_ROUTER_PC_MAX_T 64
 int ornk_router_pc_supported(int T, int D);
+/* Whether the decode down kernel forms mid itself (the mid step is then
+ * skipped): one token, 16 gate/up split-K slices, 8-step down slices. */
+int ornk_down_dec_fuses_mid(int T, int H, int ks_gu, int ks_dn);
 int ornk_moe_dispatch(const ornk_moe_args *a, hipStream_t s);
 int ornk_moe_gateup(const ornk_moe_args *a, hipStream_t s);
 int ornk_moe_mid(const ornk_moe_args *a, hipStream_t s);
