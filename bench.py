@@ -51,12 +51,12 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def measure(ctx, store, layer, T, steps, warmup, x_seed=1, stack_layers=0):
+def measure(ctx, store, layer, T, steps, warmup, x_seed=1, stack_layers=0, ep=(0, 0)):
     x = om.synth_normal(x_seed, om.synth_stream(0, om.SYN_ACT, 0), T * D, 1.0).reshape(T, D)
     xb = ctx.upload(x)
     ob = ctx.alloc(x.nbytes)
     L = om.lib()
-    opts = om.MoEOpts(om.ROUTE_RENORM, om.MOE_ASYNC)
+    opts = om.MoEOpts(om.ROUTE_RENORM, om.MOE_ASYNC, ep[0], ep[1])
 
     def step():
         if stack_layers:
@@ -281,6 +281,17 @@ def main():
                             "layer_hbm_gbs": round(st_x["n_slots"] * EXPERT_BYTES / (ms_x * 1e-3) / 1e9, 1),
                             "tflops": round(Tn * (K + 1) * FLOP_PER_PAIR / (ms_x * 1e-3) / 1e12, 2),
                             "dominant": roof_x,
+                            "kernels_us": {n: round(v["avg_us"], 2) for n, v in kern_x.items()}}
+            log(label, extra[label]["tokens_per_s"], "tok/s")
+        # One GPU's share of an 8-way expert-parallel layer (32 experts per
+        # rank, every rank routing all 16 tokens): rank 0 (also the shared
+        # expert) and rank 1.  The cross-rank reduction of the T x D partial
+        # outputs is not part of this one-GPU figure.
+        for label, ep in (("ep8_rank0_t16", (0, E // 8)), ("ep8_rank1_t16", (E // 8, E // 8))):
+            ms_x, kern_x, st_x = measure(ctx, store, 0, 16, args.steps, args.warmup, ep=ep)
+            extra[label] = {"tokens_per_s": round(16 / (ms_x * 1e-3), 1), "ms_per_step": round(ms_x, 4),
+                            "experts": list(ep), "active_experts": st_x["n_slots"],
+                            "layer_hbm_gbs": round(st_x["n_slots"] * EXPERT_BYTES / (ms_x * 1e-3) / 1e9, 1),
                             "kernels_us": {n: round(v["avg_us"], 2) for n, v in kern_x.items()}}
             log(label, extra[label]["tokens_per_s"], "tok/s")
         result["configs"] = extra

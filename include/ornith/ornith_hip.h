@@ -155,6 +155,14 @@ enum { ORN_ROUTE_RENORM = 0, ORN_ROUTE_LITERAL = 1 };
 typedef struct {
     int route_mode; /* ORN_ROUTE_RENORM (default, model_get_routing) or ORN_ROUTE_LITERAL */
     unsigned flags; /* ORN_MOE_* */
+    /* Expert-parallel share (no reference counterpart; 0, 0 = every expert):
+     * the forward routes every token over all experts, as each rank of an
+     * expert-parallel deployment does, but computes only the selected
+     * experts in [ep_first, ep_first + ep_count); the shared expert belongs
+     * to the share with ep_first == 0.  Summing the outputs of the shares
+     * that cover 0..E-1 (resid passed to one of them) gives the full
+     * layer's output; idx_out / w_out are the full selection in every share. */
+    int ep_first, ep_count;
 } ornith_moe_opts;
 
 /* One MoE block for n_tokens rows of x ([T][D] fp32):
@@ -168,7 +176,8 @@ int gpu_moe_forward(gpu_context *ctx, ornith_moe_store *store, int layer, const 
 
 /* Layer stack: for l in [first, first+n): x <- x + MoE_l(rmsnorm(x)) (the
  * per-layer MoE residual structure of model.c:992-1144).  tmp must hold
- * n_tokens*D floats. */
+ * n_tokens*D floats.  Every expert is computed (opts' expert share is not
+ * used: a share needs a reduction across ranks between layers). */
 int gpu_moe_forward_stack(gpu_context *ctx, ornith_moe_store *store, int first_layer,
                           int n_layers, gpu_buffer *x, gpu_buffer *tmp, int n_tokens,
                           const ornith_moe_opts *opts);

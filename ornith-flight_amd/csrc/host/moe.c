@@ -17,7 +17,7 @@
  * depend on is in the key (buffers by address, the workspace base). */
 #define ORN_GRAPH_SLOTS 32
 typedef struct {
-    int layer, n_layers, T, mode;
+    int layer, n_layers, T, mode, ep_first, ep_count;
     unsigned flags;
     const void *x, *resid, *out, *idx, *w;
     void *ws;
@@ -690,6 +690,11 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     const int mode = opts ? opts->route_mode : ORN_ROUTE_RENORM;
     if (mode != ORN_ROUTE_RENORM && mode != ORN_ROUTE_LITERAL)
         return orn_set_err(ctx, ORN_EINVAL, "bad route mode");
+    const int ep_first = opts ? opts->ep_first : 0, ep_count = opts ? opts->ep_count : 0;
+    if (ep_first < 0 || ep_count < 0 || (ep_count == 0 && ep_first != 0) ||
+        ep_first + ep_count > E)
+        return orn_set_err(ctx, ORN_EINVAL, "bad expert share [%d, %d)", ep_first,
+                           ep_first + ep_count);
     if ((flags & ORN_MOE_PATH_VALU) && (flags & ORN_MOE_PATH_MFMA))
         return orn_set_err(ctx, ORN_EINVAL, "both expert paths forced");
     /* The MFMA path needs the prefill layouts and Q6_K sub-scales with
@@ -737,7 +742,10 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     a.H = H;
     a.E = E;
     a.k = k;
-    a.has_shared = sh->has_shared;
+    /* an expert-parallel share computes the shared expert iff it starts at 0 */
+    a.has_shared = sh->has_shared && ep_first == 0;
+    a.ep_lo = ep_first;
+    a.ep_n = ep_count ? ep_count : E;
     a.mode = mode;
     a.apply_norm = (flags & ORN_MOE_NORM) ? 1 : 0;
     a.ks_gu = p.ks_gu;
@@ -922,13 +930,16 @@ int gpu_moe_forward(gpu_context *ctx, ornith_moe_store *st, int layer, const gpu
                  (float *)out->dev,
                  idx_out ? (uint32_t *)idx_out->dev : NULL,
                  w_out ? (float *)w_out->dev : NULL,
-                 {opts ? opts->route_mode : ORN_ROUTE_RENORM, flags | ORN_MOE_ASYNC}};
+                 {opts ? opts->route_mode : ORN_ROUTE_RENORM, flags | ORN_MOE_ASYNC,
+                  opts ? opts->ep_first : 0, opts ? opts->ep_count : 0}};
     orn_graph_key key;
     memset(&key, 0, sizeof key);
     key.layer = layer;
     key.n_layers = 1;
     key.T = n_tokens;
     key.mode = a.opts.route_mode;
+    key.ep_first = a.opts.ep_first;
+    key.ep_count = a.opts.ep_count;
     key.flags = flags & ~ORN_MOE_ASYNC;
     key.x = a.x;
     key.resid = a.resid;
@@ -974,13 +985,15 @@ int gpu_moe_forward_stack(gpu_context *ctx, ornith_moe_store *st, int first_laye
     const unsigned flags = opts ? opts->flags : 0u;
     stack_arg a = {first_layer, n_layers, n_tokens, (float *)x->dev, (float *)tmp->dev,
                    {opts ? opts->route_mode : ORN_ROUTE_RENORM,
-                    flags | ORN_MOE_NORM | ORN_MOE_ASYNC}};
+                    flags | ORN_MOE_NORM | ORN_MOE_ASYNC, 0, 0}};
     orn_graph_key key;
     memset(&key, 0, sizeof key);
     key.layer = first_layer;
     key.n_layers = n_layers;
     key.T = n_tokens;
     key.mode = a.opts.route_mode;
+    key.ep_first = a.opts.ep_first;
+    key.ep_count = a.opts.ep_count;
     key.flags = (flags & ~ORN_MOE_ASYNC) | 0x80000000u; /* stack calls never match a layer call */
     key.x = a.x;
     key.out = a.tmp;

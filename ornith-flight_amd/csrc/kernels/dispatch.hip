@@ -280,7 +280,8 @@ struct DispatchLds {
 
 template <typename IdxT>
 __device__ void dispatch_group(DispatchLds &L, const IdxT *sel_idx, const float *sel_w, int T,
-                               int k, int E, int has_shared, int *ctl, int *slot_expert,
+                               int k, int E, int ep_lo, int ep_n, int has_shared, int *ctl,
+                               int *slot_expert,
                                int *slot_off, int *slot_cnt, int *row_token, int *pair_row,
                                int4 *items, int items_max, int tchunk)
 {
@@ -292,7 +293,7 @@ __device__ void dispatch_group(DispatchLds &L, const IdxT *sel_idx, const float 
     __syncthreads();
     for (int p = tid; p < P; p += 1024) {
         const uint32_t e = (uint32_t)sel_idx[p];
-        if (!(sel_w[p] < 1e-6f) && e < (uint32_t)E) atomicAdd(&L.cnt[e + 1], 1);
+        if (!(sel_w[p] < 1e-6f) && e - (uint32_t)ep_lo < (uint32_t)ep_n) atomicAdd(&L.cnt[e + 1], 1);
     }
     if (tid == 0) L.cnt[0] = has_shared ? T : 0;
     __syncthreads();
@@ -344,8 +345,10 @@ __device__ void dispatch_group(DispatchLds &L, const IdxT *sel_idx, const float 
     for (int p = tid; p < P; p += 1024) {
         const uint32_t e = (uint32_t)sel_idx[p];
         // Skip rule of model.c:1066; an index outside [0, E) cannot come out
-        // of the router but is treated as skipped rather than trusted.
-        if (sel_w[p] < 1e-6f || e >= (uint32_t)E) {
+        // of the router but is treated as skipped rather than trusted.  Pairs
+        // of experts outside this forward's share [ep_lo, ep_lo + ep_n) are
+        // another rank's.
+        if (sel_w[p] < 1e-6f || e - (uint32_t)ep_lo >= (uint32_t)ep_n) {
             pair_row[p] = -1;
             continue;
         }
@@ -360,12 +363,12 @@ __device__ void dispatch_group(DispatchLds &L, const IdxT *sel_idx, const float 
 
 __global__ void __launch_bounds__(1024)
     k_dispatch(const uint32_t *__restrict__ idx, const float *__restrict__ w, int T, int k, int E,
-               int has_shared, int *ctl, int *slot_expert, int *slot_off, int *slot_cnt,
+               int ep_lo, int ep_n, int has_shared, int *ctl, int *slot_expert, int *slot_off, int *slot_cnt,
                int *row_token, int *pair_row, int4 *items, int items_max,
                int tchunk)
 {
     __shared__ DispatchLds L;
-    dispatch_group(L, idx, w, T, k, E, has_shared, ctl, slot_expert, slot_off, slot_cnt,
+    dispatch_group(L, idx, w, T, k, E, ep_lo, ep_n, has_shared, ctl, slot_expert, slot_off, slot_cnt,
                    row_token, pair_row, items, items_max, tchunk);
 }
 
@@ -373,9 +376,10 @@ __global__ void __launch_bounds__(1024)
 // followed by the dispatch, in one work group.
 __global__ void __launch_bounds__(1024)
     k_select_dispatch(const float *__restrict__ logits, int T, int E, int k, int mode,
-                      uint32_t *__restrict__ idx_out, float *__restrict__ w_out, int has_shared,
-                      int *ctl, int *slot_expert, int *slot_off, int *slot_cnt, int *row_token,
-                      int *pair_row, int4 *items, int items_max, int tchunk)
+                      uint32_t *__restrict__ idx_out, float *__restrict__ w_out, int ep_lo,
+                      int ep_n, int has_shared, int *ctl, int *slot_expert, int *slot_off,
+                      int *slot_cnt, int *row_token, int *pair_row, int4 *items, int items_max,
+                      int tchunk)
 {
     __shared__ DispatchLds L;
     __shared__ float sv[16][256];
@@ -387,7 +391,7 @@ __global__ void __launch_bounds__(1024)
         select_token(logits + (size_t)t * E, E, k, mode, idx_out + (size_t)t * k,
                      w_out + (size_t)t * k, lidx + t * k, lw + t * k, sv[wave], si[wave], ctl + 3);
     __syncthreads();
-    dispatch_group(L, lidx, lw, T, k, E, has_shared, ctl, slot_expert, slot_off, slot_cnt,
+    dispatch_group(L, lidx, lw, T, k, E, ep_lo, ep_n, has_shared, ctl, slot_expert, slot_off, slot_cnt,
                    row_token, pair_row, items, items_max, tchunk);
 }
 
@@ -397,9 +401,9 @@ __global__ void __launch_bounds__(1024)
 // selected experts with w >= 1e-6 in ascending id; one item per slot.
 __global__ void __launch_bounds__(64)
     k_select_dispatch1(const float *__restrict__ logits, int E, int k, int mode,
-                       uint32_t *__restrict__ idx_out, float *__restrict__ w_out, int has_shared,
-                       int *ctl, int *slot_expert, int *slot_off, int *slot_cnt, int *row_token,
-                       int *pair_row, int4 *items, int items_max)
+                       uint32_t *__restrict__ idx_out, float *__restrict__ w_out, int ep_lo,
+                       int ep_n, int has_shared, int *ctl, int *slot_expert, int *slot_off,
+                       int *slot_cnt, int *row_token, int *pair_row, int4 *items, int items_max)
 {
     __shared__ float sv[256];
     __shared__ int si[256];
@@ -408,8 +412,8 @@ __global__ void __launch_bounds__(64)
     select_token(logits, E, k, mode, idx_out, w_out, lidx, lw, sv, si, ctl + 3);
     wave_sync();
     const int lane = threadIdx.x;
-    auto kept = [&](int j) {  // pair j survives the skip rule (model.c:1066)
-        return !(lw[j] < 1e-6f) && (uint32_t)lidx[j] < (uint32_t)E;
+    auto kept = [&](int j) {  // pair j survives the skip rule (model.c:1066) and is this share's
+        return !(lw[j] < 1e-6f) && (uint32_t)(lidx[j] - ep_lo) < (uint32_t)ep_n;
     };
     const bool valid = lane < k && kept(lane);
     const int e = lane < k ? lidx[lane] : 0;
@@ -448,16 +452,17 @@ extern "C" int ornk_moe_dispatch(const ornk_moe_args *a, hipStream_t s)
     const int T = a->T, E = a->E, k = a->k;
     if (T <= 0) return hipSuccess;
     if (E < 1 || E > 256 || k < 1 || k > 16 || k > E) return hipErrorInvalidValue;
+    if (a->ep_lo < 0 || a->ep_n < 0 || a->ep_lo + a->ep_n > E) return hipErrorInvalidValue;
     int4 *items = reinterpret_cast<int4 *>(a->items);
     if (T == 1) {
         hipLaunchKernelGGL(k_select_dispatch1, dim3(1), dim3(64), 0, s, a->logits, E, k, a->mode,
-                           a->idx, a->w, a->has_shared, a->ctl, a->slot_expert, a->slot_off,
+                           a->idx, a->w, a->ep_lo, a->ep_n, a->has_shared, a->ctl, a->slot_expert, a->slot_off,
                            a->slot_cnt, a->row_token, a->pair_row, items, a->items_max);
         return hipGetLastError();
     }
     if (T <= ORN_FUSED_SELECT_T) {
         hipLaunchKernelGGL(k_select_dispatch, dim3(1), dim3(1024), 0, s, a->logits, T, E, k,
-                           a->mode, a->idx, a->w, a->has_shared, a->ctl, a->slot_expert,
+                           a->mode, a->idx, a->w, a->ep_lo, a->ep_n, a->has_shared, a->ctl, a->slot_expert,
                            a->slot_off, a->slot_cnt, a->row_token, a->pair_row, items,
                            a->items_max, a->tchunk);
         return hipGetLastError();
@@ -466,8 +471,8 @@ extern "C" int ornk_moe_dispatch(const ornk_moe_args *a, hipStream_t s)
                        a->idx, a->w, a->ctl + 3);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
-    hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), 0, s, a->idx, a->w, T, k, E,
-                       a->has_shared, a->ctl, a->slot_expert, a->slot_off, a->slot_cnt,
+    hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), 0, s, a->idx, a->w, T, k, E, a->ep_lo,
+                       a->ep_n, a->has_shared, a->ctl, a->slot_expert, a->slot_off, a->slot_cnt,
                        a->row_token, a->pair_row, items, a->items_max, a->tchunk);
     return hipGetLastError();
 }

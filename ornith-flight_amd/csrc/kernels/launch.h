@@ -73,6 +73,7 @@ typedef struct {
 
 typedef struct {
     int T, D, H, E, k, has_shared, mode, apply_norm;
+    int ep_lo, ep_n;  /* experts computed: [ep_lo, ep_lo + ep_n) (an expert-parallel share) */
     int ks_gu, ks_dn, rows_max, items_max, tchunk;
     const uint8_t *gate, *up, *down_body;
     const uint16_t *down_d;

@@ -59,7 +59,8 @@ class MoEShape(C.Structure):
 
 
 class MoEOpts(C.Structure):
-    _fields_ = [("route_mode", C.c_int), ("flags", C.c_uint)]
+    _fields_ = [("route_mode", C.c_int), ("flags", C.c_uint), ("ep_first", C.c_int),
+                ("ep_count", C.c_int)]
 
 
 _lib = None
@@ -295,15 +296,16 @@ class Store:
         self.set_router(layer, syn.router, syn.bias)
 
     def forward(self, layer, x: Buffer, T, out: Buffer, resid=None, idx=None, w=None,
-                mode=ROUTE_RENORM, flags=0):
-        o = MoEOpts(mode, flags)
+                mode=ROUTE_RENORM, flags=0, ep=(0, 0)):
+        """ep = (first, count): compute only that expert-parallel share (0, 0: all)."""
+        o = MoEOpts(mode, flags, ep[0], ep[1])
         rc = lib().gpu_moe_forward(self.ctx.ptr, self.ptr, layer, x.ptr, T,
                                    resid.ptr if resid else None, out.ptr,
                                    idx.ptr if idx else None, w.ptr if w else None, C.byref(o))
         self.ctx.check(rc, "gpu_moe_forward")
 
     def forward_stack(self, first, n, x: Buffer, tmp: Buffer, T, mode=ROUTE_RENORM, flags=0):
-        o = MoEOpts(mode, flags)
+        o = MoEOpts(mode, flags, 0, 0)
         self.ctx.check(lib().gpu_moe_forward_stack(self.ctx.ptr, self.ptr, first, n, x.ptr, tmp.ptr, T,
                                                    C.byref(o)), "gpu_moe_forward_stack")
 

@@ -393,3 +393,52 @@ def test_stack_teacher_forced(om, ctx):
     stacked = ctx.download(xb, np.float32, x.shape)
     assert np.array_equal(stacked.view(np.uint32), cur.view(np.uint32))
     L.store.close()
+
+
+# ------------------------------------------------------------ expert-parallel shares
+def run_share(ctx, layer, x, ep, resid=None):
+    T = x.shape[0]
+    xb = ctx.upload(x)
+    ob = ctx.alloc(x.nbytes)
+    ib = ctx.alloc(T * layer.k * 4)
+    wb = ctx.alloc(T * layer.k * 4)
+    rb = ctx.upload(resid) if resid is not None else None
+    layer.store.forward(0, xb, T, ob, resid=rb, idx=ib, w=wb, ep=ep)
+    out = ctx.download(ob, np.float32, x.shape)
+    idx = ctx.download(ib, np.uint32, (T, layer.k))
+    w = ctx.download(wb, np.float32, (T, layer.k))
+    for b in (xb, ob, ib, wb, rb):
+        if b is not None:
+            b.free()
+    return out, idx, w
+
+
+@pytest.mark.parametrize("T", [1, 16, 150])
+def test_expert_parallel_shares_sum_to_layer(om, ctx, small, T):
+    """Four shares of 4 experts (shared expert and residual on share 0):
+    every share returns the full selection, and the shares' outputs sum to
+    the whole layer's (each pair's expert output is the same computation;
+    only the order of the final sum differs)."""
+    x = act(om, 21, T, small.D)
+    resid = act(om, 22, T, small.D, stream=1)
+    full, fidx, fw = run_share(ctx, small, x, (0, 0), resid)
+    total = np.zeros(full.shape, np.float64)
+    n = 4
+    for r in range(n):
+        out, idx, w = run_share(ctx, small, x, (r * small.E // n, small.E // n),
+                                resid if r == 0 else None)
+        assert np.array_equal(idx, fidx) and np.array_equal(w, fw)
+        total += out
+    err = row_err(total.astype(np.float32), full.astype(np.float64))
+    say(f"  T={T} shares-sum vs layer: max row err {err.max():.2e}")
+    assert err.max() <= 1e-5
+
+
+def test_expert_parallel_share_rejects_bad_range(om, ctx, small):
+    x = act(om, 23, 2, small.D)
+    xb, ob = ctx.upload(x), ctx.alloc(x.nbytes)
+    for ep in ((-1, 4), (12, 8), (3, 0)):
+        with pytest.raises(RuntimeError):
+            small.store.forward(0, xb, 2, ob, ep=ep)
+    xb.free()
+    ob.free()
