@@ -62,6 +62,7 @@ int orn_hip_check(gpu_context *ctx, hipError_t e, const char *what);
 /* profiling hooks (moe.c) */
 int orn_prof_begin(gpu_context *ctx, const char *name);
 void orn_prof_end(gpu_context *ctx, int slot);
+int orn_prof_kernel(gpu_context *ctx, const char *name, hipEvent_t *start, hipEvent_t *stop);
 
 /* workspace (moe.c) */
 void *orn_ws_get(gpu_context *ctx, size_t bytes);

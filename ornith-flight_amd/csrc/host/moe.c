@@ -207,6 +207,30 @@ void orn_prof_end(gpu_context *ctx, int slot)
     hipEventRecord(ctx->prof_pending[slot].stop, ctx->stream);
 }
 
+/* A record whose events the caller hands to hipExtLaunchKernel (which stamps
+ * a kernel's own start and end into them) instead of recording them around
+ * the launch; *start = *stop = NULL when profiling is off. */
+int orn_prof_kernel(gpu_context *ctx, const char *name, hipEvent_t *start, hipEvent_t *stop)
+{
+    *start = *stop = NULL;
+    if (!ctx->prof_on) return -1;
+    if (ctx->prof_n_pending >= ORN_PROF_MAX_PENDING || ctx->prof_pool_used + 2 > ctx->prof_pool_n)
+        prof_collect(ctx);
+    int id = -1;
+    for (int i = 0; i < ctx->prof_n_names; ++i)
+        if (strcmp(ctx->prof_names[i], name) == 0) { id = i; break; }
+    if (id < 0) {
+        if (ctx->prof_n_names >= ORN_PROF_MAX_NAMES) return -1;
+        id = ctx->prof_n_names++;
+        snprintf(ctx->prof_names[id], sizeof ctx->prof_names[id], "%s", name);
+    }
+    orn_prof_rec *r = &ctx->prof_pending[ctx->prof_n_pending];
+    r->name_id = id;
+    r->start = *start = ctx->prof_pool[ctx->prof_pool_used++];
+    r->stop = *stop = ctx->prof_pool[ctx->prof_pool_used++];
+    return ctx->prof_n_pending++;
+}
+
 /* ---------------------------------------------------------------------------
  * Store
  * ------------------------------------------------------------------------- */
@@ -679,6 +703,20 @@ static int launch(gpu_context *ctx, const char *name, int (*fn)(const ornk_moe_a
     return ORN_OK;
 }
 
+/* An expert-product step: under profiling its main kernel carries the
+ * record's events (the kernel's own duration, as a kernel trace measures
+ * it, rather than the span between two event packets around the launch). */
+static int launch_expert(gpu_context *ctx, const char *name,
+                         int (*fn)(const ornk_moe_args *, hipStream_t), const ornk_moe_args *a)
+{
+    ornk_moe_args b = *a;
+    orn_prof_kernel(ctx, name, &b.ev_start, &b.ev_stop);
+    int e = fn(&b, ctx->stream);
+    if (e != hipSuccess)
+        return orn_set_err(ctx, ORN_EHIP, "%s: %s", name, hipGetErrorString((hipError_t)e));
+    return ORN_OK;
+}
+
 static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, const float *x,
                            int T, const float *resid, float *out, uint32_t *idx_out, float *w_out,
                            const ornith_moe_opts *opts)
@@ -803,9 +841,9 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     if ((rc = launch(ctx, "moe_route", ornk_moe_route, &a))) return rc;
     if ((rc = launch(ctx, "moe_dispatch", ornk_moe_dispatch, &a))) return rc;
     if (p.use_dec) {
-        if ((rc = launch(ctx, "moe_gateup_dec", ornk_moe_gateup_dec, &a))) return rc;
+        if ((rc = launch_expert(ctx, "moe_gateup_dec", ornk_moe_gateup_dec, &a))) return rc;
     } else if (use_mfma) {
-        if ((rc = launch(ctx, "moe_gateup_mfma", ornk_moe_gateup_mfma, &a))) return rc;
+        if ((rc = launch_expert(ctx, "moe_gateup_mfma", ornk_moe_gateup_mfma, &a))) return rc;
     } else {
         if ((rc = launch(ctx, "moe_gateup", ornk_moe_gateup, &a))) return rc;
     }
@@ -813,9 +851,9 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     const int fused_mid = p.use_dec && ornk_down_dec_fuses_mid(T, H, p.ks_gu, p.ks_dn);
     if (!fused_mid && (rc = launch(ctx, "moe_mid", ornk_moe_mid, &a))) return rc;
     if (p.use_dec) {
-        if ((rc = launch(ctx, "moe_down_dec", ornk_moe_down_dec, &a))) return rc;
+        if ((rc = launch_expert(ctx, "moe_down_dec", ornk_moe_down_dec, &a))) return rc;
     } else if (use_mfma) {
-        if ((rc = launch(ctx, "moe_down_mfma", ornk_moe_down_mfma, &a))) return rc;
+        if ((rc = launch_expert(ctx, "moe_down_mfma", ornk_moe_down_mfma, &a))) return rc;
     } else {
         if ((rc = launch(ctx, "moe_down", ornk_moe_down, &a))) return rc;
     }

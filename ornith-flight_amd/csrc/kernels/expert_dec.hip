@@ -22,6 +22,19 @@
 #include "launch.h"
 #include "mfma_ops.h"
 
+#include <hip/hip_ext.h>
+
+// The main kernel of an expert step: with the args' profiling events set,
+// hipExtLaunchKernel records the kernel's own start and end into them.
+#define ORN_LAUNCH_EV(a, K, grid, block, shmem, s, ...)                                       \
+    do {                                                                                       \
+        if ((a)->ev_start || (a)->ev_stop)                                                     \
+            hipExtLaunchKernelGGL(K, grid, block, shmem, s, (a)->ev_start, (a)->ev_stop, 0u,   \
+                                  __VA_ARGS__);                                                \
+        else                                                                                   \
+            hipLaunchKernelGGL(K, grid, block, shmem, s, __VA_ARGS__);                         \
+    } while (0)
+
 namespace {
 
 using namespace orn_mfma;
@@ -479,7 +492,7 @@ extern "C" int ornk_moe_gateup_dec(const ornk_moe_args *a, hipStream_t s)
     }
     const dim3 grid(a->items_max * 2 * (a->H / 256) * ks);
 #define ORN_GU_DEC(K)                                                                        \
-    hipLaunchKernelGGL((k_gateup_dec<ORN_DEC_NR, K, 4>), grid, dim3(256), 0, s, a->gu_pf, xin, \
+    ORN_LAUNCH_EV(a, (k_gateup_dec<ORN_DEC_NR, K, 4>), grid, dim3(256), 0, s, a->gu_pf, xin, \
                        a->x_amax, a->ctl, reinterpret_cast<const int4 *>(a->items),           \
                        a->row_token, a->gu_part, a->T, a->D, a->H, ks, a->rows_max)
     switch (KT) {
@@ -509,13 +522,13 @@ extern "C" int ornk_moe_down_dec(const ornk_moe_args *a, hipStream_t s)
     const dim3 grid(a->items_max * (a->D / 256) * ks);
     const int shared_rows = a->has_shared ? a->T : 0;
     if (ornk_down_dec_fuses_mid(a->T, a->H, a->ks_gu, ks)) {
-        hipLaunchKernelGGL((k_down_dec<ORN_DEC_NR, 8, 4, 16>), grid, dim3(256), 0, s, a->dn_pf,
+        ORN_LAUNCH_EV(a, (k_down_dec<ORN_DEC_NR, 8, 4, 16>), grid, dim3(256), 0, s, a->dn_pf,
                            a->mid, a->mid_amax, a->ctl, reinterpret_cast<const int4 *>(a->items),
                            a->dn_part, a->D, a->H, ks, a->rows_max, a->gu_part, shared_rows);
         return hipGetLastError();
     }
 #define ORN_DN_DEC(K)                                                                          \
-    hipLaunchKernelGGL((k_down_dec<ORN_DEC_NR, K, 4, 0>), grid, dim3(256), 0, s, a->dn_pf, a->mid, \
+    ORN_LAUNCH_EV(a, (k_down_dec<ORN_DEC_NR, K, 4, 0>), grid, dim3(256), 0, s, a->dn_pf, a->mid, \
                        a->mid_amax, a->ctl, reinterpret_cast<const int4 *>(a->items),           \
                        a->dn_part, a->D, a->H, ks, a->rows_max, a->gu_part, shared_rows)
     switch (KT) {

@@ -15,6 +15,19 @@
 #include "launch.h"
 #include "mfma_ops.h"
 
+#include <hip/hip_ext.h>
+
+// The main kernel of an expert step: with the args' profiling events set,
+// hipExtLaunchKernel records the kernel's own start and end into them.
+#define ORN_LAUNCH_EV(a, K, grid, block, shmem, s, ...)                                       \
+    do {                                                                                       \
+        if ((a)->ev_start || (a)->ev_stop)                                                     \
+            hipExtLaunchKernelGGL(K, grid, block, shmem, s, (a)->ev_start, (a)->ev_stop, 0u,   \
+                                  __VA_ARGS__);                                                \
+        else                                                                                   \
+            hipLaunchKernelGGL(K, grid, block, shmem, s, __VA_ARGS__);                         \
+    } while (0)
+
 namespace {
 
 using namespace orn_mfma;
@@ -544,11 +557,11 @@ extern "C" int ornk_moe_gateup_mfma(const ornk_moe_args *a, hipStream_t s)
     }
     const dim3 grid(a->items_max * 2 * (a->H / 256) * ks);
     if (a->tchunk <= 16)
-        hipLaunchKernelGGL(k_gateup_mfma<1>, grid, dim3(256), 0, s, a->gu_pf, xin, a->x_amax,
+        ORN_LAUNCH_EV(a, k_gateup_mfma<1>, grid, dim3(256), 0, s, a->gu_pf, xin, a->x_amax,
                            a->ctl, reinterpret_cast<const int4 *>(a->items), a->row_token,
                            a->gu_part, a->D, a->H, ks, a->rows_max);
     else
-        hipLaunchKernelGGL(k_gateup_mfma<4>, grid, dim3(256), 0, s, a->gu_pf, xin, a->x_amax,
+        ORN_LAUNCH_EV(a, k_gateup_mfma<4>, grid, dim3(256), 0, s, a->gu_pf, xin, a->x_amax,
                            a->ctl, reinterpret_cast<const int4 *>(a->items), a->row_token,
                            a->gu_part, a->D, a->H, ks, a->rows_max);
     return hipGetLastError();
@@ -561,11 +574,11 @@ extern "C" int ornk_moe_down_mfma(const ornk_moe_args *a, hipStream_t s)
         return hipErrorInvalidValue;
     const dim3 grid(a->items_max * (a->D / 256) * ks);
     if (a->tchunk <= 16)
-        hipLaunchKernelGGL(k_down_mfma<1>, grid, dim3(256), 0, s, a->dn_pf, a->mid, a->mid_amax,
+        ORN_LAUNCH_EV(a, k_down_mfma<1>, grid, dim3(256), 0, s, a->dn_pf, a->mid, a->mid_amax,
                            a->ctl, reinterpret_cast<const int4 *>(a->items), a->dn_part, a->D,
                            a->H, ks, a->rows_max);
     else
-        hipLaunchKernelGGL(k_down_mfma<4>, grid, dim3(256), 0, s, a->dn_pf, a->mid, a->mid_amax,
+        ORN_LAUNCH_EV(a, k_down_mfma<4>, grid, dim3(256), 0, s, a->dn_pf, a->mid, a->mid_amax,
                            a->ctl, reinterpret_cast<const int4 *>(a->items), a->dn_part, a->D,
                            a->H, ks, a->rows_max);
     return hipGetLastError();

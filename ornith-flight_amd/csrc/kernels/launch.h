@@ -103,6 +103,9 @@ typedef struct {
     float *x_amax;    /* [T] max |xin| per token */
     int router_amax;  /* 1: the routing step writes x_amax (else the MFMA launchers do) */
     float *mid_amax;  /* [rows_max] max |mid| per row (written by the mid step) */
+    /* Profiling: if set, the expert-product launchers launch their main kernel
+     * with hipExtLaunchKernel so that these events carry its start and end. */
+    hipEvent_t ev_start, ev_stop;
 } ornk_moe_args;
 
 int ornk_moe_norm(const ornk_moe_args *a, hipStream_t s);
