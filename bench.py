@@ -72,11 +72,11 @@ def measure(ctx, store, layer, T, steps, warmup, x_seed=1, stack_layers=0, ep=(0
         step()
     ctx.sync()
     stats = store.last_stats()
-    # Per-kernel region: HIP events on the library's stream.  The expert
-    # steps' main kernels are launched with hipExtLaunchKernel, which stamps
-    # the kernel's own start and end into the events (the duration a kernel
-    # trace reports); the other steps are bracketed by an event pair, which
-    # adds a few microseconds to them.
+    # Per-kernel region: HIP events on the library's stream.  Every step but
+    # the input norm is launched with hipExtLaunchKernel, which stamps the
+    # kernels' own start and end into the events (the duration a kernel
+    # trace reports); the norm is bracketed by an event pair, which adds a
+    # few microseconds to it.
     L.gpu_profile_enable(ctx.ptr, 1)
     L.gpu_profile_reset(ctx.ptr)
     ctx.sync()

@@ -703,10 +703,11 @@ static int launch(gpu_context *ctx, const char *name, int (*fn)(const ornk_moe_a
     return ORN_OK;
 }
 
-/* An expert-product step: under profiling its main kernel carries the
- * record's events (the kernel's own duration, as a kernel trace measures
- * it, rather than the span between two event packets around the launch). */
-static int launch_expert(gpu_context *ctx, const char *name,
+/* A step whose launcher takes its profiling events: under profiling its
+ * kernel carries the record's events (the kernel's own duration, as a
+ * kernel trace measures it, rather than the span between two event packets
+ * around the launch); a step of two kernels spans both. */
+static int launch_k(gpu_context *ctx, const char *name,
                          int (*fn)(const ornk_moe_args *, hipStream_t), const ornk_moe_args *a)
 {
     ornk_moe_args b = *a;
@@ -838,26 +839,26 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
 
     int rc;
     if ((rc = launch(ctx, "moe_norm", ornk_moe_norm, &a))) return rc;
-    if ((rc = launch(ctx, "moe_route", ornk_moe_route, &a))) return rc;
-    if ((rc = launch(ctx, "moe_dispatch", ornk_moe_dispatch, &a))) return rc;
+    if ((rc = launch_k(ctx, "moe_route", ornk_moe_route, &a))) return rc;
+    if ((rc = launch_k(ctx, "moe_dispatch", ornk_moe_dispatch, &a))) return rc;
     if (p.use_dec) {
-        if ((rc = launch_expert(ctx, "moe_gateup_dec", ornk_moe_gateup_dec, &a))) return rc;
+        if ((rc = launch_k(ctx, "moe_gateup_dec", ornk_moe_gateup_dec, &a))) return rc;
     } else if (use_mfma) {
-        if ((rc = launch_expert(ctx, "moe_gateup_mfma", ornk_moe_gateup_mfma, &a))) return rc;
+        if ((rc = launch_k(ctx, "moe_gateup_mfma", ornk_moe_gateup_mfma, &a))) return rc;
     } else {
-        if ((rc = launch(ctx, "moe_gateup", ornk_moe_gateup, &a))) return rc;
+        if ((rc = launch_k(ctx, "moe_gateup", ornk_moe_gateup, &a))) return rc;
     }
     /* One token: the decode down kernel forms mid from the gate/up partials. */
     const int fused_mid = p.use_dec && ornk_down_dec_fuses_mid(T, H, p.ks_gu, p.ks_dn);
-    if (!fused_mid && (rc = launch(ctx, "moe_mid", ornk_moe_mid, &a))) return rc;
+    if (!fused_mid && (rc = launch_k(ctx, "moe_mid", ornk_moe_mid, &a))) return rc;
     if (p.use_dec) {
-        if ((rc = launch_expert(ctx, "moe_down_dec", ornk_moe_down_dec, &a))) return rc;
+        if ((rc = launch_k(ctx, "moe_down_dec", ornk_moe_down_dec, &a))) return rc;
     } else if (use_mfma) {
-        if ((rc = launch_expert(ctx, "moe_down_mfma", ornk_moe_down_mfma, &a))) return rc;
+        if ((rc = launch_k(ctx, "moe_down_mfma", ornk_moe_down_mfma, &a))) return rc;
     } else {
-        if ((rc = launch(ctx, "moe_down", ornk_moe_down, &a))) return rc;
+        if ((rc = launch_k(ctx, "moe_down", ornk_moe_down, &a))) return rc;
     }
-    if ((rc = launch(ctx, "moe_combine", ornk_moe_combine, &a))) return rc;
+    if ((rc = launch_k(ctx, "moe_combine", ornk_moe_combine, &a))) return rc;
 
     ctx->last_ctl = a.ctl;
     if (!(flags & ORN_MOE_ASYNC))

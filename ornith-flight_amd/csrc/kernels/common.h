@@ -5,12 +5,28 @@
 // super-block geometry.  Only included from .hip translation units.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include "../../../include/ornith/kquant.h"
 
 #define ORN_WAVE 64
+
+// Kernel launch of a forward step: with the step's profiling events set
+// (ornk_moe_args ev_start/ev_stop), hipExtLaunchKernel stamps the kernel's
+// own start and end into them; otherwise a plain launch.  ORN_LAUNCH_EV2
+// takes the two events explicitly (a step of two kernels passes the start
+// event to its first and the stop event to its last).
+#define ORN_LAUNCH_EV2(st, sp, K, grid, block, shmem, s, ...)                                  \
+    do {                                                                                       \
+        if ((st) || (sp))                                                                      \
+            hipExtLaunchKernelGGL(K, grid, block, shmem, s, st, sp, 0u, __VA_ARGS__);          \
+        else                                                                                   \
+            hipLaunchKernelGGL(K, grid, block, shmem, s, __VA_ARGS__);                         \
+    } while (0)
+#define ORN_LAUNCH_EV(a, K, grid, block, shmem, s, ...) \
+    ORN_LAUNCH_EV2((a)->ev_start, (a)->ev_stop, K, grid, block, shmem, s, __VA_ARGS__)
 
 // Native 4-wide vector.  Loads through it are single vector loads; copying
 // HIP's float4 struct from global memory lowers to a memcpy, which keeps

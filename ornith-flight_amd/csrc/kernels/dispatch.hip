@@ -455,24 +455,24 @@ extern "C" int ornk_moe_dispatch(const ornk_moe_args *a, hipStream_t s)
     if (a->ep_lo < 0 || a->ep_n < 0 || a->ep_lo + a->ep_n > E) return hipErrorInvalidValue;
     int4 *items = reinterpret_cast<int4 *>(a->items);
     if (T == 1) {
-        hipLaunchKernelGGL(k_select_dispatch1, dim3(1), dim3(64), 0, s, a->logits, E, k, a->mode,
+        ORN_LAUNCH_EV(a, k_select_dispatch1, dim3(1), dim3(64), 0, s, a->logits, E, k, a->mode,
                            a->idx, a->w, a->ep_lo, a->ep_n, a->has_shared, a->ctl, a->slot_expert, a->slot_off,
                            a->slot_cnt, a->row_token, a->pair_row, items, a->items_max);
         return hipGetLastError();
     }
     if (T <= ORN_FUSED_SELECT_T) {
-        hipLaunchKernelGGL(k_select_dispatch, dim3(1), dim3(1024), 0, s, a->logits, T, E, k,
+        ORN_LAUNCH_EV(a, k_select_dispatch, dim3(1), dim3(1024), 0, s, a->logits, T, E, k,
                            a->mode, a->idx, a->w, a->ep_lo, a->ep_n, a->has_shared, a->ctl, a->slot_expert,
                            a->slot_off, a->slot_cnt, a->row_token, a->pair_row, items,
                            a->items_max, a->tchunk);
         return hipGetLastError();
     }
-    hipLaunchKernelGGL(k_select, dim3((T + 3) / 4), dim3(256), 0, s, a->logits, T, E, k, a->mode,
-                       a->idx, a->w, a->ctl + 3);
+    ORN_LAUNCH_EV2(a->ev_start, nullptr, k_select, dim3((T + 3) / 4), dim3(256), 0, s, a->logits,
+                   T, E, k, a->mode, a->idx, a->w, a->ctl + 3);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
-    hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), 0, s, a->idx, a->w, T, k, E, a->ep_lo,
-                       a->ep_n, a->has_shared, a->ctl, a->slot_expert, a->slot_off, a->slot_cnt,
-                       a->row_token, a->pair_row, items, a->items_max, a->tchunk);
+    ORN_LAUNCH_EV2(nullptr, a->ev_stop, k_dispatch, dim3(1), dim3(1024), 0, s, a->idx, a->w, T, k,
+                   E, a->ep_lo, a->ep_n, a->has_shared, a->ctl, a->slot_expert, a->slot_off,
+                   a->slot_cnt, a->row_token, a->pair_row, items, a->items_max, a->tchunk);
     return hipGetLastError();
 }

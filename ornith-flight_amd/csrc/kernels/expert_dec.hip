@@ -22,18 +22,6 @@
 #include "launch.h"
 #include "mfma_ops.h"
 
-#include <hip/hip_ext.h>
-
-// The main kernel of an expert step: with the args' profiling events set,
-// hipExtLaunchKernel records the kernel's own start and end into them.
-#define ORN_LAUNCH_EV(a, K, grid, block, shmem, s, ...)                                       \
-    do {                                                                                       \
-        if ((a)->ev_start || (a)->ev_stop)                                                     \
-            hipExtLaunchKernelGGL(K, grid, block, shmem, s, (a)->ev_start, (a)->ev_stop, 0u,   \
-                                  __VA_ARGS__);                                                \
-        else                                                                                   \
-            hipLaunchKernelGGL(K, grid, block, shmem, s, __VA_ARGS__);                         \
-    } while (0)
 
 namespace {
 
@@ -486,15 +474,17 @@ extern "C" int ornk_moe_gateup_dec(const ornk_moe_args *a, hipStream_t s)
     const int KT = a->D / 32 / ks;
     if (!ornk_dec_supported(KT, 4)) return hipErrorInvalidValue;
     const float *xin = a->apply_norm ? a->xn : a->x;
+    hipEvent_t st = a->ev_start;  // the step's first kernel carries the start event
     if (!a->router_amax) {
-        const int e = ornk_rowmax(xin, a->T, a->D, a->x_amax, s);
+        const int e = ornk_rowmax(xin, a->T, a->D, a->x_amax, st, s);
         if (e != hipSuccess) return e;
+        st = nullptr;
     }
     const dim3 grid(a->items_max * 2 * (a->H / 256) * ks);
-#define ORN_GU_DEC(K)                                                                        \
-    ORN_LAUNCH_EV(a, (k_gateup_dec<ORN_DEC_NR, K, 4>), grid, dim3(256), 0, s, a->gu_pf, xin, \
-                       a->x_amax, a->ctl, reinterpret_cast<const int4 *>(a->items),           \
-                       a->row_token, a->gu_part, a->T, a->D, a->H, ks, a->rows_max)
+#define ORN_GU_DEC(K)                                                                          \
+    ORN_LAUNCH_EV2(st, a->ev_stop, (k_gateup_dec<ORN_DEC_NR, K, 4>), grid, dim3(256), 0, s,    \
+                   a->gu_pf, xin, a->x_amax, a->ctl, reinterpret_cast<const int4 *>(a->items), \
+                   a->row_token, a->gu_part, a->T, a->D, a->H, ks, a->rows_max)
     switch (KT) {
     case 4: ORN_GU_DEC(4); break;
     case 8: ORN_GU_DEC(8); break;

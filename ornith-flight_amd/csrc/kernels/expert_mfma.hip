@@ -15,18 +15,6 @@
 #include "launch.h"
 #include "mfma_ops.h"
 
-#include <hip/hip_ext.h>
-
-// The main kernel of an expert step: with the args' profiling events set,
-// hipExtLaunchKernel records the kernel's own start and end into them.
-#define ORN_LAUNCH_EV(a, K, grid, block, shmem, s, ...)                                       \
-    do {                                                                                       \
-        if ((a)->ev_start || (a)->ev_stop)                                                     \
-            hipExtLaunchKernelGGL(K, grid, block, shmem, s, (a)->ev_start, (a)->ev_stop, 0u,   \
-                                  __VA_ARGS__);                                                \
-        else                                                                                   \
-            hipLaunchKernelGGL(K, grid, block, shmem, s, __VA_ARGS__);                         \
-    } while (0)
 
 namespace {
 
@@ -537,10 +525,12 @@ __global__ void __launch_bounds__(256)
 
 }  // namespace
 
-extern "C" int ornk_rowmax(const float *x, int rows, int D, float *out, hipStream_t s)
+extern "C" int ornk_rowmax(const float *x, int rows, int D, float *out, hipEvent_t start,
+                           hipStream_t s)
 {
     if (D % 4) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_rowmax, dim3((rows + 3) / 4), dim3(256), 0, s, x, rows, D, out);
+    ORN_LAUNCH_EV2(start, nullptr, k_rowmax, dim3((rows + 3) / 4), dim3(256), 0, s, x, rows, D,
+                   out);
     return hipGetLastError();
 }
 
@@ -551,19 +541,21 @@ extern "C" int ornk_moe_gateup_mfma(const ornk_moe_args *a, hipStream_t s)
         (a->D / 32 / ks) % 4 || a->D / 32 / ks > ORN_GU_KT_MAX)
         return hipErrorInvalidValue;
     const float *xin = a->apply_norm ? a->xn : a->x;
+    hipEvent_t st = a->ev_start;  // the step's first kernel carries the start event
     if (!a->router_amax) {
-        const int e = ornk_rowmax(xin, a->T, a->D, a->x_amax, s);
+        const int e = ornk_rowmax(xin, a->T, a->D, a->x_amax, st, s);
         if (e != hipSuccess) return e;
+        st = nullptr;
     }
     const dim3 grid(a->items_max * 2 * (a->H / 256) * ks);
     if (a->tchunk <= 16)
-        ORN_LAUNCH_EV(a, k_gateup_mfma<1>, grid, dim3(256), 0, s, a->gu_pf, xin, a->x_amax,
-                           a->ctl, reinterpret_cast<const int4 *>(a->items), a->row_token,
-                           a->gu_part, a->D, a->H, ks, a->rows_max);
+        ORN_LAUNCH_EV2(st, a->ev_stop, k_gateup_mfma<1>, grid, dim3(256), 0, s, a->gu_pf, xin,
+                       a->x_amax, a->ctl, reinterpret_cast<const int4 *>(a->items), a->row_token,
+                       a->gu_part, a->D, a->H, ks, a->rows_max);
     else
-        ORN_LAUNCH_EV(a, k_gateup_mfma<4>, grid, dim3(256), 0, s, a->gu_pf, xin, a->x_amax,
-                           a->ctl, reinterpret_cast<const int4 *>(a->items), a->row_token,
-                           a->gu_part, a->D, a->H, ks, a->rows_max);
+        ORN_LAUNCH_EV2(st, a->ev_stop, k_gateup_mfma<4>, grid, dim3(256), 0, s, a->gu_pf, xin,
+                       a->x_amax, a->ctl, reinterpret_cast<const int4 *>(a->items), a->row_token,
+                       a->gu_part, a->D, a->H, ks, a->rows_max);
     return hipGetLastError();
 }
 

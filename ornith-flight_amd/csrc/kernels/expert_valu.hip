@@ -499,7 +499,7 @@ extern "C" int ornk_moe_gateup(const ornk_moe_args *a, hipStream_t s)
     if (shmem > 64 * 1024) return hipErrorInvalidValue;
     const int n_it = RK / (4 * RW);
 #define ORN_GU(N, R)                                                                            \
-    hipLaunchKernelGGL((k_gateup<N, R>), dim3(a->items_max * a->ks_gu), dim3(256), shmem, s, a->gate, \
+    ORN_LAUNCH_EV(a, (k_gateup<N, R>), dim3(a->items_max * a->ks_gu), dim3(256), shmem, s, a->gate, \
                        a->up, a->xn, a->ctl, reinterpret_cast<const int4 *>(a->items),          \
                        a->slot_expert, a->row_token, a->gu_part, a->D, a->H, a->ks_gu,          \
                        a->rows_max)
@@ -516,7 +516,7 @@ extern "C" int ornk_moe_gateup(const ornk_moe_args *a, hipStream_t s)
 extern "C" int ornk_moe_mid(const ornk_moe_args *a, hipStream_t s)
 {
 #define ORN_MID(K)                                                                             \
-    hipLaunchKernelGGL(k_mid<K>, dim3(a->rows_max), dim3(256), 0, s, a->gu_part, a->ctl, a->mid, \
+    ORN_LAUNCH_EV(a, k_mid<K>, dim3(a->rows_max), dim3(256), 0, s, a->gu_part, a->ctl, a->mid,  \
                        a->H, a->ks_gu, a->rows_max, a->has_shared ? a->T : 0,                 \
                        a->use_mfma ? a->mid_amax : nullptr)
     switch (a->ks_gu) {
@@ -546,7 +546,7 @@ extern "C" int ornk_moe_down(const ornk_moe_args *a, hipStream_t s)
     if (shmem > 64 * 1024) return hipErrorInvalidValue;
     const int n_it = RH / (4 * RW);
 #define ORN_DN(N, R)                                                                             \
-    hipLaunchKernelGGL((k_down<N, R>), dim3(a->items_max * a->ks_dn * ncg), dim3(256), shmem, s,       \
+    ORN_LAUNCH_EV(a, (k_down<N, R>), dim3(a->items_max * a->ks_dn * ncg), dim3(256), shmem, s,        \
                        a->down_body, a->down_d, a->mid, a->ctl,                                  \
                        reinterpret_cast<const int4 *>(a->items), a->slot_expert, a->dn_part,     \
                        a->D, a->H, a->ks_dn, ncg, a->rows_max)
@@ -564,7 +564,7 @@ extern "C" int ornk_moe_combine(const ornk_moe_args *a, hipStream_t s)
 {
     const dim3 grid(a->T, (a->D + 255) / 256);
 #define ORN_CMB(KS, K)                                                                          \
-    hipLaunchKernelGGL((k_combine<KS, K>), grid, dim3(256), 0, s, a->dn_part, a->pair_row, a->w, \
+    ORN_LAUNCH_EV(a, (k_combine<KS, K>), grid, dim3(256), 0, s, a->dn_part, a->pair_row, a->w,  \
                        a->resid, a->out, a->T, a->D, a->k, a->rows_max, a->has_shared)
 #define ORN_CMB_K(KS)                  \
     if (a->k == 8) ORN_CMB(KS, 8);     \

@@ -130,7 +130,7 @@ int ornk_moe_gateup_dec(const ornk_moe_args *a, hipStream_t s);
 int ornk_dec_supported(int kt_gu, int kt_dn);
 int ornk_moe_down_dec(const ornk_moe_args *a, hipStream_t s);
 /* out[r] = max_k |x[r][k]| (D a multiple of 4). */
-int ornk_rowmax(const float *x, int rows, int D, float *out, hipStream_t s);
+int ornk_rowmax(const float *x, int rows, int D, float *out, hipEvent_t start, hipStream_t s);
 int ornk_moe_combine(const ornk_moe_args *a, hipStream_t s);
 
 #ifdef __cplusplus

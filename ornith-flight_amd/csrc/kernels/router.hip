@@ -592,7 +592,7 @@ extern "C" int ornk_moe_route(const ornk_moe_args *a, hipStream_t s)
         const float *nw = a->apply_norm ? a->norm_w : nullptr;
         float *xo = a->apply_norm ? a->xn : nullptr;
 #define ORN_RPC(N)                                                                              \
-    hipLaunchKernelGGL(k_router_pc<N>, gd, dim3(128), 0, s, xr, a->router, a->bias, T, E,        \
+    ORN_LAUNCH_EV(a, k_router_pc<N>, gd, dim3(128), 0, s, xr, a->router, a->bias, T, E,         \
                        a->logits, a->ctl, amax, nw, xo)
         switch (D) {
         case 256: ORN_RPC(8); break;
@@ -603,10 +603,10 @@ extern "C" int ornk_moe_route(const ornk_moe_args *a, hipStream_t s)
         }
 #undef ORN_RPC
     } else if (T >= 1024) {
-        hipLaunchKernelGGL(k_router_seq<4>, dim3((E + 63) / 64, (T + 15) / 16), dim3(256), 0, s,
+        ORN_LAUNCH_EV(a, k_router_seq<4>, dim3((E + 63) / 64, (T + 15) / 16), dim3(256), 0, s,
                            xin, a->router, a->bias, T, D, E, a->logits, a->ctl);
     } else {
-        hipLaunchKernelGGL(k_router_dec, dim3((E + 63) / 64, T), dim3(64), sizeof(float) * (size_t)D,
+        ORN_LAUNCH_EV(a, k_router_dec, dim3((E + 63) / 64, T), dim3(64), sizeof(float) * (size_t)D,
                            s, xin, a->router, a->bias, T, D, E, a->logits, a->ctl);
     }
     return hipGetLastError();
