@@ -204,12 +204,20 @@ def cpu_baseline(budget_s):
                 "sample": f"16-token decode batch through the oracle restatement, {dt:.2f} s"}
 
 
+# Extra configs reported beside the headline: (label, store layer, tokens).
+# Layer 1 carries a Zipf(1.1) router bias.
+EXTRA_CONFIGS = (("decode_t1", 0, 1), ("prefill_t2048", 0, 2048), ("zipf_t256", 1, 256))
+EXTRA_LABELS = [c[0] for c in EXTRA_CONFIGS]
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-extra", action="store_true", help="only the headline config")
+    ap.add_argument("--only", choices=EXTRA_LABELS, default=None,
+                    help="of the extra configs, time only this one (for a kernel trace of it)")
     ap.add_argument("--stack", action="store_true", help="also time the 40-layer stack (21 GB)")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -272,7 +280,9 @@ def main():
     }
     if not args.no_extra:
         extra = {}
-        for label, layer, Tn in (("decode_t1", 0, 1), ("prefill_t2048", 0, 2048), ("zipf_t256", 1, 256)):
+        for label, layer, Tn in EXTRA_CONFIGS:
+            if args.only and label != args.only:
+                continue
             steps = max(5, args.steps // (20 if Tn >= 256 else 1))
             ms_x, kern_x, st_x = measure(ctx, store, layer, Tn, steps, max(2, args.warmup // 4))
             _, roof_x = roofline_for(kern_x, st_x, Tn, label.split("_")[-1])
@@ -290,6 +300,8 @@ def main():
         # expert) and rank 1.  The cross-rank reduction of the T x D partial
         # outputs is not part of this one-GPU figure.
         for label, ep in (("ep8_rank0_t16", (0, E // 8)), ("ep8_rank1_t16", (E // 8, E // 8))):
+            if args.only:
+                break
             ms_x, kern_x, st_x = measure(ctx, store, 0, 16, args.steps, args.warmup, ep=ep)
             extra[label] = {"tokens_per_s": round(16 / (ms_x * 1e-3), 1), "ms_per_step": round(ms_x, 4),
                             "experts": list(ep), "active_experts": st_x["n_slots"],

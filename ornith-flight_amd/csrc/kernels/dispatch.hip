@@ -278,6 +278,39 @@ struct DispatchLds {
     int wtot[3][16];
 };
 
+#define ORN_DU 8  // pairs read per thread at a time in dispatch_group
+
+// Expert of a selected pair if it is dispatched here, else 0xFFFFFFFF: the
+// pair is skipped when w < 1e-6 (model.c:1066) or its expert lies outside
+// this forward's share [ep_lo, ep_lo + ep_n) (another rank's).
+template <typename IdxT>
+__device__ __forceinline__ uint32_t dispatch_key(IdxT idx, float w, int ep_lo, int ep_n)
+{
+    const uint32_t e = (uint32_t)idx;
+    return !(w < 1e-6f) && e - (uint32_t)ep_lo < (uint32_t)ep_n ? e : 0xFFFFFFFFu;
+}
+
+// Keys of pairs p0 + 1024 u, u < ORN_DU (0xFFFFFFFF past P).  The loads
+// are unconditional, at an index clamped to P - 1 (P >= 1 when called), so
+// that all of them are in flight before the first is used.
+template <typename IdxT>
+__device__ __forceinline__ void dispatch_keys(uint32_t (&ev)[ORN_DU], int p0, int P,
+                                              const IdxT *sel_idx, const float *sel_w, int ep_lo,
+                                              int ep_n)
+{
+    IdxT iv[ORN_DU];
+    float wv[ORN_DU];
+#pragma unroll
+    for (int u = 0; u < ORN_DU; ++u) {
+        const int p = min(p0 + u * 1024, P - 1);
+        iv[u] = sel_idx[p];
+        wv[u] = sel_w[p];
+    }
+#pragma unroll
+    for (int u = 0; u < ORN_DU; ++u)
+        ev[u] = p0 + u * 1024 < P ? dispatch_key(iv[u], wv[u], ep_lo, ep_n) : 0xFFFFFFFFu;
+}
+
 template <typename IdxT>
 __device__ void dispatch_group(DispatchLds &L, const IdxT *sel_idx, const float *sel_w, int T,
                                int k, int E, int ep_lo, int ep_n, int has_shared, int *ctl,
@@ -291,9 +324,16 @@ __device__ void dispatch_group(DispatchLds &L, const IdxT *sel_idx, const float 
     L.cnt[tid] = 0;
     L.cursor[tid] = 0;
     __syncthreads();
-    for (int p = tid; p < P; p += 1024) {
-        const uint32_t e = (uint32_t)sel_idx[p];
-        if (!(sel_w[p] < 1e-6f) && e - (uint32_t)ep_lo < (uint32_t)ep_n) atomicAdd(&L.cnt[e + 1], 1);
+    // Pairs are read ORN_DU at a time per thread, so that a thread has that
+    // many loads in flight rather than one per loop turn (16 turns at 2048
+    // tokens).  An index outside [0, E) cannot come out of the router; it
+    // lies outside every share, so it is skipped rather than trusted.
+    for (int p0 = tid; p0 < P; p0 += ORN_DU * 1024) {
+        uint32_t ev[ORN_DU];
+        dispatch_keys(ev, p0, P, sel_idx, sel_w, ep_lo, ep_n);
+#pragma unroll
+        for (int u = 0; u < ORN_DU; ++u)
+            if (ev[u] != 0xFFFFFFFFu) atomicAdd(&L.cnt[ev[u] + 1], 1);
     }
     if (tid == 0) L.cnt[0] = has_shared ? T : 0;
     __syncthreads();
@@ -342,20 +382,22 @@ __device__ void dispatch_group(DispatchLds &L, const IdxT *sel_idx, const float 
     }
     __syncthreads();
 
-    for (int p = tid; p < P; p += 1024) {
-        const uint32_t e = (uint32_t)sel_idx[p];
-        // Skip rule of model.c:1066; an index outside [0, E) cannot come out
-        // of the router but is treated as skipped rather than trusted.  Pairs
-        // of experts outside this forward's share [ep_lo, ep_lo + ep_n) are
-        // another rank's.
-        if (sel_w[p] < 1e-6f || e - (uint32_t)ep_lo >= (uint32_t)ep_n) {
-            pair_row[p] = -1;
-            continue;
+    for (int p0 = tid; p0 < P; p0 += ORN_DU * 1024) {
+        uint32_t ev[ORN_DU];
+        dispatch_keys(ev, p0, P, sel_idx, sel_w, ep_lo, ep_n);
+#pragma unroll
+        for (int u = 0; u < ORN_DU; ++u) {
+            const int p = p0 + u * 1024;
+            if (p >= P) break;
+            if (ev[u] == 0xFFFFFFFFu) {  // skipped, or another rank's expert
+                pair_row[p] = -1;
+                continue;
+            }
+            const int j = (int)ev[u] + 1;
+            const int r = L.rowoff[j] + atomicAdd(&L.cursor[j], 1);
+            row_token[r] = p / k;
+            pair_row[p] = r;
         }
-        const int j = (int)e + 1;
-        const int r = L.rowoff[j] + atomicAdd(&L.cursor[j], 1);
-        row_token[r] = p / k;
-        pair_row[p] = r;
     }
     if (has_shared)
         for (int t = tid; t < T; t += 1024) row_token[L.rowoff[0] + t] = t;
