@@ -100,6 +100,11 @@ typedef struct {
     int has_shared; /* 1: one always-on shared expert (model.c:1001-1007) */
     int prefill_layout; /* 1: also keep the MFMA (prefill) layouts of every expert,
                            about 1.2x the quantized bytes more; 0: decode layout only */
+    int file_layout;    /* 1: expert matrices and router in GGUF file orientation
+                           (input index fastest: ggml ne = [K, M]; see
+                           gpu_moe_store_set_experts); needs prefill_layout = 0.
+                           No reference counterpart: the reference reads every
+                           matrix as vec@mat (model.c:351-357). */
 } ornith_moe_shape;
 
 enum { ORN_MAT_GATE = 0, ORN_MAT_UP = 1, ORN_MAT_DOWN = 2 };
@@ -113,12 +118,18 @@ size_t gpu_moe_store_bytes(const ornith_moe_store *store);
  * vec@mat orientation (gate/up: K=D rows x M=H cols, Q4_K; down: K=H rows x
  * M=D cols, Q6_K), i.e. what gguf_dequantize_tensor_from_buf would read for
  * that expert.  expert_first == n_experts selects the shared expert.  The
- * store permutes whole blocks (never re-quantizes). */
+ * store permutes whole blocks (never re-quantizes).
+ * With shape.file_layout = 1 each expert's blocks are instead the GGUF file's
+ * bytes for that expert (blk.N.ffn_{gate,up,down}_exps.weight, experts
+ * slowest): gate/up H rows of D/256 Q4_K blocks along the input index, down
+ * D rows of H/256 Q6_K blocks; they are kept in file order. */
 int gpu_moe_store_set_experts(gpu_context *ctx, ornith_moe_store *store, int layer, int matrix,
                               int expert_first, int n, const void *blocks);
 
 /* Router weights W[d*E + e] (model.c:1022 layout) and an optional additive
- * per-expert logit bias (NULL = none).  */
+ * per-expert logit bias (NULL = none).  With shape.file_layout = 1, W is in
+ * file orientation instead (ffn_gate_inp.weight: W[e*D + d]); the logits
+ * are the same sequential sums over d either way.  */
 int gpu_moe_store_set_router(gpu_context *ctx, ornith_moe_store *store, int layer,
                              const float *W, const float *bias);
 

@@ -318,14 +318,38 @@ void orc_expert_ffn(const float *x, const float *Wg, const float *Wu, const floa
 
 static size_t tensor_bytes(int type, uint64_t n) { return orn_row_size(type, n); }
 
-/* Dequantize routed expert e's matrix (n_elems elements per expert). */
-static int fetch_expert(const orc_moe_cfg *c, const void *base, int type, uint64_t per,
-                        int e, float *out)
+/* Dequantize one K x M matrix stored in file orientation (element i*K + k
+ * = W(k, i)) into the vec@mat order out[k*M + i]. */
+static int fetch_file(const void *p, int type, int K, int M, float *out)
 {
+    const uint64_t n = (uint64_t)K * (uint64_t)M;
+    float *t = (float *)malloc(sizeof(float) * (size_t)n);
+    if (!t) return 0;
+    const int ok = orc_dequant_tensor(p, type, n, t);
+    if (ok)
+        for (int i = 0; i < M; ++i)
+            for (int k = 0; k < K; ++k) out[(size_t)k * M + i] = t[(size_t)i * K + k];
+    free(t);
+    return ok;
+}
+
+/* Dequantize routed expert e's K x M matrix (vec@mat: K input rows). */
+static int fetch_expert(const orc_moe_cfg *c, const void *base, int type, int K, int M, int e,
+                        float *out)
+{
+    const uint64_t per = (uint64_t)K * (uint64_t)M;
     if (c->layout == ORC_LAYOUT_INTERLEAVED)
         return orc_dequant_expert_slice(base, type, per * (uint64_t)c->E, (uint64_t)c->E, e, out);
     const uint8_t *p = (const uint8_t *)base + tensor_bytes(type, per) * (size_t)e;
+    if (c->layout == ORC_LAYOUT_FILE) return fetch_file(p, type, K, M, out);
     return orc_dequant_tensor(p, type, per, out);
+}
+
+/* The shared expert's K x M matrix (one tensor). */
+static int fetch_shared(const orc_moe_cfg *c, const void *p, int type, int K, int M, float *out)
+{
+    if (c->layout == ORC_LAYOUT_FILE) return fetch_file(p, type, K, M, out);
+    return orc_dequant_tensor(p, type, (uint64_t)K * (uint64_t)M, out);
 }
 
 /* model.c:992-1144, for T tokens.  Experts are visited expert-major (each
@@ -369,9 +393,9 @@ int orc_moe_layer(const orc_moe_cfg *c, int T, const float *x, const float *resi
     /* Shared expert (model.c:1003-1007): fp32 weights from a whole-tensor
      * dequant, unclamped silu, then x = x + down. */
     if (sh_gate && sh_up && sh_down) {
-        if (!orc_dequant_tensor(sh_gate, c->sh_gate_type, per, Wg) ||
-            !orc_dequant_tensor(sh_up, c->sh_up_type, per, Wu) ||
-            !orc_dequant_tensor(sh_down, c->sh_down_type, per, Wd)) { rc = -3; goto done; }
+        if (!fetch_shared(c, sh_gate, c->sh_gate_type, D, H, Wg) ||
+            !fetch_shared(c, sh_up, c->sh_up_type, D, H, Wu) ||
+            !fetch_shared(c, sh_down, c->sh_down_type, H, D, Wd)) { rc = -3; goto done; }
         for (int t = 0; t < T; ++t) {
             orc_expert_ffn(ffn_x + (size_t)t * D, Wg, Wu, Wd, D, H, 0, tmp);
             float *a = acc + (size_t)t * D;
@@ -394,9 +418,9 @@ int orc_moe_layer(const orc_moe_cfg *c, int T, const float *x, const float *resi
         for (int p = 0; p < T * K && !used; ++p)
             if ((int)idx[p] == e && !(wt[p] < 1e-6f)) used = 1;
         if (!used) continue;
-        if (!fetch_expert(c, gate, c->gate_type, per, e, Wg) ||
-            !fetch_expert(c, up, c->up_type, per, e, Wu) ||
-            !fetch_expert(c, down, c->down_type, per, e, Wd)) { rc = -5; goto done; }
+        if (!fetch_expert(c, gate, c->gate_type, D, H, e, Wg) ||
+            !fetch_expert(c, up, c->up_type, D, H, e, Wu) ||
+            !fetch_expert(c, down, c->down_type, H, D, e, Wd)) { rc = -5; goto done; }
         for (int p = 0; p < T * K; ++p) {
             if ((int)idx[p] != e || wt[p] < 1e-6f) continue;
             int t = p / K;

@@ -29,6 +29,11 @@
  *   orc_moe_layer (both layouts, both modes) golden layer outputs from the
  *                           compiled reference model_forward (interleaved
  *                           layout) + fp64 brute force (contiguous layout)
+ *   orc_moe_layer, file layout: equality with the contiguous layout on the
+ *                           transposed matrices, for weights whose every
+ *                           block shares one set of scales (the same matrix
+ *                           is then exactly representable in both
+ *                           orientations) + fp64 brute force
  */
 #ifndef ORNITH_ORACLE_H
 #define ORNITH_ORACLE_H
@@ -80,6 +85,12 @@ void orc_rmsnorm(float *out, const float *x, const float *w, int dim);
 /* Weight layouts for the routed experts. */
 #define ORC_LAYOUT_CONTIGUOUS 0  /* expert e's blocks at e * blocks_per_matrix */
 #define ORC_LAYOUT_INTERLEAVED 1 /* fused tensor, element i of e at i*E + e */
+/* GGUF file orientation (no reference counterpart: the reference reads every
+ * matrix as vec@mat, model.c:351-357): expert e's blocks at
+ * e * blocks_per_matrix, each matrix stored output-row-major with the input
+ * index fastest (ggml ne = [K, M]), so W(k, i) is element i*K + k.  Applies
+ * to the routed and the shared experts. */
+#define ORC_LAYOUT_FILE 2
 
 typedef struct {
     int D;       /* model dim (2048) */

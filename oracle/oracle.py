@@ -17,7 +17,7 @@ LIB_PATH = os.path.join(HERE, "liboracle.so")
 
 TYPE_F32, TYPE_F16, TYPE_Q4_K, TYPE_Q6_K = 0, 1, 12, 14
 MODE_RENORM, MODE_LITERAL = 0, 1
-LAYOUT_CONTIGUOUS, LAYOUT_INTERLEAVED = 0, 1
+LAYOUT_CONTIGUOUS, LAYOUT_INTERLEAVED, LAYOUT_FILE = 0, 1, 2
 
 _lib = None
 

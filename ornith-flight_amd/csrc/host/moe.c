@@ -240,7 +240,9 @@ static int shape_ok(const ornith_moe_shape *s)
            s->hidden % 256 == 0 && s->hidden <= 1024 && s->n_experts > 0 &&
            s->n_experts <= 256 && s->top_k > 0 && s->top_k <= 16 && s->top_k <= s->n_experts &&
            (s->has_shared == 0 || s->has_shared == 1) && s->d_model % 128 == 0 &&
-           (s->prefill_layout == 0 || s->prefill_layout == 1);
+           (s->prefill_layout == 0 || s->prefill_layout == 1) &&
+           (s->file_layout == 0 || (s->file_layout == 1 && !s->prefill_layout &&
+                                    ornk_file_supported(s->d_model, s->hidden)));
 }
 
 static void graphs_clear(ornith_moe_store *st)
@@ -487,9 +489,11 @@ int gpu_moe_store_set_experts(gpu_context *ctx, ornith_moe_store *st, int layer,
     if (matrix != ORN_MAT_DOWN) {
         uint8_t *tmp = (uint8_t *)malloc((size_t)n * nb * 144);
         if (!tmp) return orn_set_err(ctx, ORN_ENOMEM, "host staging");
-        for (int i = 0; i < n; ++i)
-            permute_q4k((const uint8_t *)blocks + (size_t)i * nb * ORN_Q4K_BYTES, tmp + i * nb * 144,
-                        D, H / 256);
+        for (int i = 0; i < n; ++i) {
+            const uint8_t *src = (const uint8_t *)blocks + (size_t)i * nb * ORN_Q4K_BYTES;
+            if (st->sh.file_layout) memcpy(tmp + i * nb * 144, src, nb * 144);  /* file order */
+            else permute_q4k(src, tmp + i * nb * 144, D, H / 256);
+        }
         uint8_t *dst = (matrix == ORN_MAT_GATE ? st->gate : st->up) + slot0 * nb * 144;
         rc = orn_hip_check(ctx, hipMemcpyAsync(dst, tmp, (size_t)n * nb * 144,
                                                hipMemcpyHostToDevice, s), "upload q4k");
@@ -505,9 +509,13 @@ int gpu_moe_store_set_experts(gpu_context *ctx, ornith_moe_store *st, int layer,
             free(dv);
             return orn_set_err(ctx, ORN_ENOMEM, "host staging");
         }
-        for (int i = 0; i < n; ++i)
-            permute_q6k((const uint8_t *)blocks + (size_t)i * nb * ORN_Q6K_BYTES, body + i * nb * 208,
-                        dv + i * nb, H, D / 256);
+        for (int i = 0; i < n; ++i) {
+            /* file order is D rows of H/256 blocks: the same split with the
+             * roles of the two block indices exchanged leaves it in place */
+            const uint8_t *src = (const uint8_t *)blocks + (size_t)i * nb * ORN_Q6K_BYTES;
+            if (st->sh.file_layout) permute_q6k(src, body + i * nb * 208, dv + i * nb, (int)nb, 1);
+            else permute_q6k(src, body + i * nb * 208, dv + i * nb, H, D / 256);
+        }
         rc = orn_hip_check(ctx, hipMemcpyAsync(st->down_body + slot0 * nb * 208, body,
                                                (size_t)n * nb * 208, hipMemcpyHostToDevice, s),
                            "upload q6k");
@@ -533,7 +541,8 @@ int gpu_moe_store_set_router(gpu_context *ctx, ornith_moe_store *st, int layer, 
     float *t = (float *)malloc(D * E * sizeof(float));
     if (!t) return orn_set_err(ctx, ORN_ENOMEM, "host staging");
     for (size_t d = 0; d < D; ++d)
-        for (size_t e = 0; e < E; ++e) t[((d >> 2) * E + e) * 4 + (d & 3)] = W[d * E + e];
+        for (size_t e = 0; e < E; ++e)
+            t[((d >> 2) * E + e) * 4 + (d & 3)] = st->sh.file_layout ? W[e * D + d] : W[d * E + e];
     hipStream_t s = ctx->stream;
     int rc = orn_hip_check(ctx, hipMemcpyAsync(st->router_q + (size_t)layer * E * D, t,
                                                D * E * sizeof(float), hipMemcpyHostToDevice, s),
@@ -690,6 +699,29 @@ static plan_t make_plan(const ornith_moe_shape *sh, int T, int use_mfma)
     return p;
 }
 
+/* File-orientation path: items of <= 16 rows (one MFMA row tile); the
+ * reduction is split so that each kernel has about 2048 work groups
+ * (gate/up 2H/64 per item and slice, down D/64), in whole super-blocks. */
+static plan_t make_plan_file(const ornith_moe_shape *sh, int T)
+{
+    plan_t p;
+    memset(&p, 0, sizeof p);
+    const int k = sh->top_k, E = sh->n_experts, D = sh->d_model, H = sh->hidden;
+    p.tchunk = 16;
+    p.rows_max = T * k + (sh->has_shared ? T : 0);
+    const int max_slots = (T * k < E ? T * k : E) + (sh->has_shared ? 1 : 0);
+    p.items_max = max_slots + (p.rows_max + p.tchunk - 1) / p.tchunk;
+    int est = max_slots + p.rows_max / p.tchunk;
+    if (est < 1) est = 1;
+    const int ng = 2048 / (est * (2 * H / 64)), nd = 2048 / (est * (D / 64));
+    int kg = pow2_floor(ng > 0 ? ng : 1), kd = pow2_floor(nd > 0 ? nd : 1);
+    while (kg > 1 && (D / 256) % kg) kg /= 2;
+    while (kd > 1 && (H / 256) % kd) kd /= 2;
+    p.ks_gu = kg;
+    p.ks_dn = kd;
+    return p;
+}
+
 static int check_buf(const gpu_buffer *b, size_t bytes) { return b && b->size >= bytes; }
 
 static int launch(gpu_context *ctx, const char *name, int (*fn)(const ornk_moe_args *, hipStream_t),
@@ -736,6 +768,10 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
                            ep_first + ep_count);
     if ((flags & ORN_MOE_PATH_VALU) && (flags & ORN_MOE_PATH_MFMA))
         return orn_set_err(ctx, ORN_EINVAL, "both expert paths forced");
+    const int file = sh->file_layout;
+    if (file && (flags & (ORN_MOE_PATH_VALU | ORN_MOE_PATH_MFMA)))
+        return orn_set_err(ctx, ORN_EUNSUPPORTED,
+                           "a file-layout store has one expert path; do not force one");
     /* The MFMA path needs the prefill layouts and Q6_K sub-scales with
      * |sc| <= 64 (so that sc * q is exact in fp16). */
     const int mfma_ok = sh->prefill_layout && st->q6_scmax[layer] <= 64;
@@ -747,7 +783,8 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
                                "MFMA path needs the prefill layout and |Q6_K scale| <= 64");
         use_mfma = 1;
     }
-    plan_t p = make_plan(sh, T, use_mfma);
+    if (file) use_mfma = 0;  /* the mid and combine steps run as on the VALU path */
+    plan_t p = file ? make_plan_file(sh, T) : make_plan(sh, T, use_mfma);
 
     size_t off = 0;
 #define CARVE(name, bytes)       \
@@ -769,6 +806,14 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     CARVE(o_dn, (size_t)p.ks_dn * p.rows_max * D * 4);
     CARVE(o_xamax, use_mfma ? (size_t)T * 4 : 0);
     CARVE(o_midamax, use_mfma ? (size_t)p.rows_max * 4 : 0);
+    CARVE(o_fxh, file ? (size_t)T * D * 2 : 0);
+    CARVE(o_fxl, file ? (size_t)T * D * 2 : 0);
+    CARVE(o_fsh, file ? (size_t)T * (D / 32) * 2 : 0);
+    CARVE(o_fsl, file ? (size_t)T * (D / 32) * 2 : 0);
+    CARVE(o_fxinv, file ? (size_t)T * 4 : 0);
+    CARVE(o_fmh, file ? (size_t)p.rows_max * H * 2 : 0);
+    CARVE(o_fml, file ? (size_t)p.rows_max * H * 2 : 0);
+    CARVE(o_fminv, file ? (size_t)p.rows_max * 4 : 0);
 #undef CARVE
     uint8_t *ws = (uint8_t *)orn_ws_get(ctx, off);
     if (!ws) return ORN_ENOMEM;
@@ -837,10 +882,33 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
         a.mid_amax = (float *)(ws + o_midamax);
     }
 
+    if (file) {
+        a.fw.xh = (uint32_t *)(ws + o_fxh);
+        a.fw.xl = (uint32_t *)(ws + o_fxl);
+        a.fw.xsh = (uint16_t *)(ws + o_fsh);
+        a.fw.xsl = (uint16_t *)(ws + o_fsl);
+        a.fw.xinv = (float *)(ws + o_fxinv);
+        a.fw.mh = (uint32_t *)(ws + o_fmh);
+        a.fw.ml = (uint32_t *)(ws + o_fml);
+        a.fw.minv = (float *)(ws + o_fminv);
+    }
+
     int rc;
     if ((rc = launch(ctx, "moe_norm", ornk_moe_norm, &a))) return rc;
     if ((rc = launch_k(ctx, "moe_route", ornk_moe_route, &a))) return rc;
     if ((rc = launch_k(ctx, "moe_dispatch", ornk_moe_dispatch, &a))) return rc;
+    if (file) {
+        if ((rc = launch_k(ctx, "moe_file_prep_x", ornk_file_prep_x, &a))) return rc;
+        if ((rc = launch_k(ctx, "moe_gateup_file", ornk_file_gateup, &a))) return rc;
+        if ((rc = launch_k(ctx, "moe_mid", ornk_moe_mid, &a))) return rc;
+        if ((rc = launch_k(ctx, "moe_file_prep_mid", ornk_file_prep_mid, &a))) return rc;
+        if ((rc = launch_k(ctx, "moe_down_file", ornk_file_down, &a))) return rc;
+        if ((rc = launch_k(ctx, "moe_combine", ornk_moe_combine, &a))) return rc;
+        ctx->last_ctl = a.ctl;
+        if (!(flags & ORN_MOE_ASYNC))
+            return orn_hip_check(ctx, hipStreamSynchronize(ctx->stream), "moe forward");
+        return ORN_OK;
+    }
     if (p.use_dec) {
         if ((rc = launch_k(ctx, "moe_gateup_dec", ornk_moe_gateup_dec, &a))) return rc;
     } else if (use_mfma) {

@@ -1,0 +1,358 @@
+// SPDX-License-Identifier: MIT
+//
+// Expert products for weights in GGUF file orientation (store built with
+// ornith_moe_shape.file_layout = 1).  In a GGUF file every matrix is stored
+// output-row-major with the input index fastest (ggml ne = [K, M]): row i of
+// gate/up (i < H) is D/256 Q4_K blocks along d, row n of down (n < D) is
+// H/256 Q6_K blocks along the hidden index.  The reference reads its
+// matrices as vec@mat (model.c:351-357) and has no path for this
+// orientation; the arithmetic per element is its block dequant (gguf.c:43-61
+// Q4_K, gguf.c:64-86 Q6_K) and the products accumulate in fp32.
+//
+// Here the block scales vary with the output column, so they cannot be
+// folded into the activation tile as in the vec@mat kernels.  MFMA roles:
+// rows = the item's token rows (16), columns = 16 output rows of the file
+// matrix, k = the input index.
+//   Q4_K (v_mfma_f32_16x16x32_f16): B = sc*q (sc the 6-bit sub-block scale
+//     of this column, exact in fp16), P = sum over one super-block (8 steps
+//     of 32), then acc += d(column) * P; the mins term is one more MFMA per
+//     super-block over the rows' sub-block sums: acc -= dmin(column) *
+//     sum_j m(column, j) * xsum(row, j).
+//   Q6_K (v_mfma_f32_16x16x16_f16): sub-block scales are int8 (|sc * q| up
+//     to 4096, not exact in fp16), so B = q - 32 and each 16-value
+//     sub-block is one step: acc += (d * sc)(column) * P.
+// Activations come from k_prep_rows, which splits each row (times a power
+// of two s, |x*s| < 2^14) into fp16 hi + lo once per forward; products of
+// hi and lo with the exact B accumulate in fp32, and outputs are scaled
+// back by 1/s.
+//
+// Any permutation of k applied to both A and B leaves a dot product
+// unchanged; the loads use two: within each group of 8 consecutive values
+// the prep stores the order [0,2,1,3,4,6,5,7], which is the order in which
+// one v_bfi of a word of nibbles (or one v_perm of a word of bytes) yields
+// fp16 pairs; and a Q4_K lane loads 16 consecutive bytes of nibbles (32
+// values of two sub-blocks) that feed four steps.
+#include "common.h"
+#include "launch.h"
+#include "mfma_ops.h"
+
+using namespace orn_mfma;
+
+namespace {
+
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+
+// Power of two s with amax * s in [2^13, 2^14); 1 for 0 or non-finite.
+__device__ __forceinline__ float prep_scale(float amax)
+{
+    if (!(amax > 0.0f) || !(amax <= 3.0e38f)) return 1.0f;
+    int e = 13 - ilogbf(amax);
+    e = e < -126 ? -126 : (e > 126 ? 126 : e);
+    return ldexpf(1.0f, e);
+}
+
+// ---------------------------------------------------------------------------
+// Row preparation: one work group per row of x ([n][K] fp32, K <= 2048,
+// K % 256 == 0).  Writes hi/lo fp16 of x*s in the pair order above, inv[r]
+// = 1/s, and with SUMS the sub-block sums sum_{32} x*s / 32 as fp16 hi/lo
+// ([n][K/32], natural order; /32 keeps them below 2^14).  Rows at or past
+// *live (when live is given) are skipped.
+// ---------------------------------------------------------------------------
+template <bool SUMS>
+__global__ void __launch_bounds__(256)
+    k_prep_rows(const float *__restrict__ x, int K, const int *__restrict__ live,
+                uint32_t *__restrict__ hi, uint32_t *__restrict__ lo, float *__restrict__ inv,
+                uint16_t *__restrict__ shi, uint16_t *__restrict__ slo)
+{
+    __shared__ float red[4];
+    const int r = blockIdx.x, tid = threadIdx.x;
+    if (live && r >= *live) return;
+    const int ng = K >> 3;  // groups of 8 values
+    const bool on = tid < ng;
+    const float *xr = x + (size_t)r * K + 8 * tid;
+    v4f a = {0.0f, 0.0f, 0.0f, 0.0f}, b = a;
+    if (on) {
+        a = *reinterpret_cast<const v4f *>(xr);
+        b = *reinterpret_cast<const v4f *>(xr + 4);
+    }
+    float m = fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                    fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float s = prep_scale(m);
+    a *= s;
+    b *= s;
+    if (on) {
+        uint32_t h[4], l[4];
+        split2(a.x, a.z, h[0], l[0]);
+        split2(a.y, a.w, h[1], l[1]);
+        split2(b.x, b.z, h[2], l[2]);
+        split2(b.y, b.w, h[3], l[3]);
+        const size_t o = (size_t)r * (K >> 1) + 4 * tid;  // u32 words
+        *reinterpret_cast<uint4 *>(hi + o) = make_uint4(h[0], h[1], h[2], h[3]);
+        *reinterpret_cast<uint4 *>(lo + o) = make_uint4(l[0], l[1], l[2], l[3]);
+    }
+    if (tid == 0) inv[r] = 1.0f / s;
+    if (SUMS) {
+        // 4 consecutive threads hold one 32-value sub-block
+        float t = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
+        t += __shfl_xor(t, 1, 64);
+        t += __shfl_xor(t, 2, 64);
+        if (on && (tid & 3) == 0) {
+            t *= 0.03125f;
+            const _Float16 th = (_Float16)t;
+            const _Float16 tl = (_Float16)(t - (float)th);
+            const size_t o = (size_t)r * (K >> 5) + (tid >> 2);
+            shi[o] = __builtin_bit_cast(uint16_t, th);
+            slo[o] = __builtin_bit_cast(uint16_t, tl);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Gate/up, Q4_K.  Logical tile = (item * ks + kslice) * (2H/64) + cb; wave w
+// of the work group covers output columns cb*64 + 16w .. +16 of the
+// concatenated [gate | up] outputs, over super-blocks kslice*nsb .. +nsb.
+// Output gu[kslice][row][2H].
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256)
+    k_gu_file(const uint8_t *__restrict__ gate, const uint8_t *__restrict__ up,
+              const uint32_t *__restrict__ xh, const uint32_t *__restrict__ xl,
+              const float *__restrict__ xinv, const uint16_t *__restrict__ sh,
+              const uint16_t *__restrict__ sl, const int *__restrict__ ctl,
+              const int4 *__restrict__ items, const int *__restrict__ row_token,
+              float *__restrict__ gu, int D, int H, int ks, int rows_max)
+{
+    const int NCB = (2 * H) >> 6;
+    const int per_item = NCB * ks;
+    const int n_live = ctl[1] * per_item;
+    if ((int)blockIdx.x >= n_live) return;
+    const int tile = xcd_remap(blockIdx.x, n_live);
+    const int cb = tile % NCB;
+    const int kslice = (tile / NCB) % ks;
+    const int4 itm = items[tile / per_item];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c = lane & 15;
+    const int col = cb * 64 + 16 * wave + c;  // in [0, 2H)
+    const int m = col >= H, h = col - m * H;
+    const int NSB = D >> 8, nsb = NSB / ks, s0 = kslice * nsb;
+    const uint8_t *rowp = (m ? up : gate) +
+                          ((size_t)itm.w * H + h) * (size_t)NSB * 144;  // row h of expert itm.w
+    const int nrows = itm.z;
+    const int tok = row_token[itm.y + (c < nrows ? c : nrows - 1)];  // A row = c
+    const uint32_t *ah = xh + (size_t)tok * (D >> 1);
+    const uint32_t *al = xl + (size_t)tok * (D >> 1);
+    const uint16_t *sah = sh + (size_t)tok * (D >> 5);
+    const uint16_t *sal = sl + (size_t)tok * (D >> 5);
+
+    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s = s0; s < s0 + nsb; ++s) {
+        const uint8_t *blk = rowp + (size_t)s * 144;
+        const uint4 hd = *reinterpret_cast<const uint4 *>(blk);  // d, dmin, scales[12]
+        uint4 w[2];
+        w[0] = *reinterpret_cast<const uint4 *>(blk + 16 + 16 * g);
+        w[1] = *reinterpret_cast<const uint4 *>(blk + 80 + 16 * g);
+        const float d = orn_half_to_float(hd.x & 0xFFFFu);
+        const float dmin = orn_half_to_float(hd.x >> 16);
+        v4f P = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int L = 0; L < 2; ++L) {
+            // this lane's 16 bytes: chunk p = 2L + g/2 (sub-blocks 2p low
+            // nibbles, 2p+1 high), positions 16*(g&1) .. +16
+            const int p = 2 * L + (g >> 1);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int j = 2 * p + (t >> 1);
+                uint32_t scj, mj;
+                orn_scale_min_k4(j, hd.y, hd.z, hd.w, scj, mj);
+                const _Float16 sf = (_Float16)(float)scj;
+                const v2h sv = {sf, sf};
+                const v2h ns = sv * (v2h){(_Float16)-1024.0f, (_Float16)-1024.0f};
+                const uint32_t wa = (t & 1) ? w[L].z : w[L].x;
+                const uint32_t wb = (t & 1) ? w[L].w : w[L].y;
+                const int sft = (t >> 1) ? 4 : 0;
+                const uint32_t pr[4] = {magic_pair(wa >> sft), magic_pair(wa >> (sft + 8)),
+                                        magic_pair(wb >> sft), magic_pair(wb >> (sft + 8))};
+                uint32_t o[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    o[i] = as_u32(__builtin_elementwise_fma(as_v2h(pr[i]), sv, ns));
+                const v8h bq = to_v8h(o[0], o[1], o[2], o[3]);
+                const int k = 256 * s + 32 * j + 16 * (g & 1) + 8 * (t & 1);
+                const uint4 xa = *reinterpret_cast<const uint4 *>(ah + (k >> 1));
+                const uint4 xb = *reinterpret_cast<const uint4 *>(al + (k >> 1));
+                P = mfma(__builtin_bit_cast(v8h, xa), bq, P);
+                P = mfma(__builtin_bit_cast(v8h, xb), bq, P);
+            }
+        }
+        // mins: k = sub-block e of this super-block on the g == 0 lanes
+        uint4 mh = make_uint4(0u, 0u, 0u, 0u), ml = mh, mb = mh;
+        if (g == 0) {
+            mh = *reinterpret_cast<const uint4 *>(sah + 8 * s);
+            ml = *reinterpret_cast<const uint4 *>(sal + 8 * s);
+            uint32_t mv[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                uint32_t scj;
+                orn_scale_min_k4(e, hd.y, hd.z, hd.w, scj, mv[e]);
+            }
+            // (1024 + m) as fp16 is 0x6400 | m; subtract 1024 (exact)
+            const v2h off = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+            uint32_t o[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                o[i] = as_u32(as_v2h(0x64006400u | mv[2 * i] | (mv[2 * i + 1] << 16)) + off);
+            mb = make_uint4(o[0], o[1], o[2], o[3]);
+        }
+        v4f Pm = {0.0f, 0.0f, 0.0f, 0.0f};
+        Pm = mfma(__builtin_bit_cast(v8h, mh), __builtin_bit_cast(v8h, mb), Pm);
+        Pm = mfma(__builtin_bit_cast(v8h, ml), __builtin_bit_cast(v8h, mb), Pm);
+        const float dm32 = -32.0f * dmin;  // the sums were stored divided by 32
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            acc[r] = fmaf(d, P[r], acc[r]);
+            acc[r] = fmaf(dm32, Pm[r], acc[r]);
+        }
+    }
+    float *out = gu + ((size_t)kslice * rows_max + itm.y) * (size_t)(2 * H) + col;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int row = 4 * g + r;
+        if (row < nrows) out[(size_t)row * (2 * H)] = acc[r] * xinv[row_token[itm.y + row]];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Down, Q6_K (gguf.c:64-86 value layout: within each 128-value half n, value
+// 32Q + l (Q = 0..3, l < 32) takes ql[64n + 32(Q&1) + l] (low nibble for Q <
+// 2, high for Q >= 2) and bits 2Q..2Q+1 of qh[32n + l], scale sc[8n + 2Q +
+// l/16]).  Logical tile = (item * ks + kslice) * (D/64) + cb; wave w covers
+// output columns cb*64 + 16w .. +16.  The store keeps each block's 208
+// leading bytes and its d apart (body / dv, block order as in the file).
+// Output dn[kslice][row][D].
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256)
+    k_dn_file(const uint8_t *__restrict__ body, const uint16_t *__restrict__ dv,
+              const uint32_t *__restrict__ mh, const uint32_t *__restrict__ ml,
+              const float *__restrict__ minv, const int *__restrict__ ctl,
+              const int4 *__restrict__ items, float *__restrict__ dn, int D, int H, int ks,
+              int rows_max)
+{
+    const int NCB = D >> 6;
+    const int per_item = NCB * ks;
+    const int n_live = ctl[1] * per_item;
+    if ((int)blockIdx.x >= n_live) return;
+    const int tile = xcd_remap(blockIdx.x, n_live);
+    const int cb = tile % NCB;
+    const int kslice = (tile / NCB) % ks;
+    const int4 itm = items[tile / per_item];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c = lane & 15;
+    const int n = cb * 64 + 16 * wave + c;  // output column = file row
+    const int NSB = H >> 8, nsb = NSB / ks, s0 = kslice * nsb;
+    const size_t b0 = ((size_t)itm.w * D + n) * NSB;  // first block of row n
+    const int nrows = itm.z;
+    const int arow = itm.y + (c < nrows ? c : nrows - 1);  // A row = c (mid rows)
+    const uint32_t *ah = mh + (size_t)arow * (H >> 1);
+    const uint32_t *al = ml + (size_t)arow * (H >> 1);
+
+    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s = s0; s < s0 + nsb; ++s) {
+        const uint8_t *blk = body + (b0 + s) * 208;
+        const float d = orn_half_to_float(dv[b0 + s]);
+        const uint4 scw = *reinterpret_cast<const uint4 *>(blk + 192);
+        const uint32_t scs[4] = {scw.x, scw.y, scw.z, scw.w};
+#pragma unroll
+        for (int hn = 0; hn < 2; ++hn) {
+#pragma unroll
+            for (int is = 0; is < 2; ++is) {
+                const int l0 = 16 * is + 4 * g;  // this lane's 4 positions l0 .. l0+3
+                const uint32_t q0 = *reinterpret_cast<const uint32_t *>(blk + 64 * hn + l0);
+                const uint32_t q1 = *reinterpret_cast<const uint32_t *>(blk + 64 * hn + 32 + l0);
+                const uint32_t qh = *reinterpret_cast<const uint32_t *>(blk + 128 + 32 * hn + l0);
+#pragma unroll
+                for (int Q = 0; Q < 4; ++Q) {
+                    const uint32_t ql = (Q & 1) ? q1 : q0;
+                    // bytes 0..63: low 4 bits from ql, high 2 from qh
+                    const uint32_t qv = ((ql >> (4 * (Q >> 1))) & 0x0F0F0F0Fu) |
+                                        (((qh >> (2 * Q)) & 0x03030303u) << 4);
+                    // fp16 pairs (1024 + byte) in the order (b0, b2), (b1, b3),
+                    // then - 1056: q - 32 exactly
+                    const v2h off = {(_Float16)-1056.0f, (_Float16)-1056.0f};
+                    const uint32_t p0 = as_u32(as_v2h(__builtin_amdgcn_perm(0x64646464u, qv, 0x04020400u)) + off);
+                    const uint32_t p1 = as_u32(as_v2h(__builtin_amdgcn_perm(0x64646464u, qv, 0x04030401u)) + off);
+                    const v4h bq = __builtin_bit_cast(v4h, make_uint2(p0, p1));
+                    const int sb = 8 * hn + 2 * Q + is;  // sub-block scale index
+                    const int scv = (int)(int8_t)((scs[sb >> 2] >> (8 * (sb & 3))) & 0xFFu);
+                    const int k = 256 * s + 128 * hn + 32 * Q + l0;
+                    const uint2 xa = *reinterpret_cast<const uint2 *>(ah + (k >> 1));
+                    const uint2 xb = *reinterpret_cast<const uint2 *>(al + (k >> 1));
+                    v4f P = {0.0f, 0.0f, 0.0f, 0.0f};
+                    P = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(v4h, xa), bq, P, 0, 0, 0);
+                    P = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(v4h, xb), bq, P, 0, 0, 0);
+                    const float dsc = d * (float)scv;  // exact: 11-bit d times 8-bit sc
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[r] = fmaf(dsc, P[r], acc[r]);
+                }
+            }
+        }
+    }
+    float *out = dn + ((size_t)kslice * rows_max + itm.y) * (size_t)D + n;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int row = 4 * g + r;
+        if (row < nrows) out[(size_t)row * D] = acc[r] * minv[itm.y + row];
+    }
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Launchers
+// ---------------------------------------------------------------------------
+extern "C" int ornk_file_supported(int D, int H)
+{
+    return D % 256 == 0 && H % 256 == 0 && D <= 2048 && H <= 2048;
+}
+
+// x (or its rmsnorm) -> hi/lo + sums, one work group per token.
+extern "C" int ornk_file_prep_x(const ornk_moe_args *a, hipStream_t s)
+{
+    if (!ornk_file_supported(a->D, a->H)) return hipErrorInvalidValue;
+    const ornk_file_ws &f = a->fw;
+    ORN_LAUNCH_EV(a, k_prep_rows<true>, dim3(a->T), dim3(256), 0, s, a->xn, a->D,
+                  (const int *)nullptr, f.xh, f.xl, f.xinv, f.xsh, f.xsl);
+    return hipGetLastError();
+}
+
+extern "C" int ornk_file_gateup(const ornk_moe_args *a, hipStream_t s)
+{
+    if (!ornk_file_supported(a->D, a->H) || (a->D / 256) % a->ks_gu) return hipErrorInvalidValue;
+    const ornk_file_ws &f = a->fw;
+    const dim3 grid(a->items_max * ((2 * a->H) / 64) * a->ks_gu);
+    ORN_LAUNCH_EV(a, k_gu_file, grid, dim3(256), 0, s, a->gate, a->up, f.xh, f.xl, f.xinv, f.xsh,
+                  f.xsl, a->ctl, reinterpret_cast<const int4 *>(a->items), a->row_token,
+                  a->gu_part, a->D, a->H, a->ks_gu, a->rows_max);
+    return hipGetLastError();
+}
+
+// mid rows -> hi/lo (rows past the live count ctl[2] are skipped).
+extern "C" int ornk_file_prep_mid(const ornk_moe_args *a, hipStream_t s)
+{
+    if (!ornk_file_supported(a->D, a->H)) return hipErrorInvalidValue;
+    const ornk_file_ws &f = a->fw;
+    ORN_LAUNCH_EV(a, k_prep_rows<false>, dim3(a->rows_max), dim3(256), 0, s, a->mid, a->H,
+                  a->ctl + 2, f.mh, f.ml, f.minv, (uint16_t *)nullptr, (uint16_t *)nullptr);
+    return hipGetLastError();
+}
+
+extern "C" int ornk_file_down(const ornk_moe_args *a, hipStream_t s)
+{
+    if (!ornk_file_supported(a->D, a->H) || (a->H / 256) % a->ks_dn) return hipErrorInvalidValue;
+    const ornk_file_ws &f = a->fw;
+    const dim3 grid(a->items_max * (a->D / 64) * a->ks_dn);
+    ORN_LAUNCH_EV(a, k_dn_file, grid, dim3(256), 0, s, a->down_body, a->down_d, f.mh, f.ml,
+                  f.minv, a->ctl, reinterpret_cast<const int4 *>(a->items), a->dn_part, a->D,
+                  a->H, a->ks_dn, a->rows_max);
+    return hipGetLastError();
+}

@@ -71,6 +71,17 @@ typedef struct {
     const float *dmax;   /* [E+1][3] */
 } ornk_dn_prefill;
 
+/* File-orientation path (expert_file.hip): activations split into fp16
+ * hi/lo (pairs in the order [0,2,1,3] within each group of 4 values), times
+ * a power of two per row; inv = its inverse. */
+typedef struct {
+    uint32_t *xh, *xl;   /* [T][D/2] */
+    uint16_t *xsh, *xsl; /* [T][D/32] sub-block sums / 32, hi and lo */
+    float *xinv;         /* [T] */
+    uint32_t *mh, *ml;   /* [rows_max][H/2] */
+    float *minv;         /* [rows_max] */
+} ornk_file_ws;
+
 typedef struct {
     int T, D, H, E, k, has_shared, mode, apply_norm;
     int ep_lo, ep_n;  /* experts computed: [ep_lo, ep_lo + ep_n) (an expert-parallel share) */
@@ -103,6 +114,9 @@ typedef struct {
     float *x_amax;    /* [T] max |xin| per token */
     int router_amax;  /* 1: the routing step writes x_amax (else the MFMA launchers do) */
     float *mid_amax;  /* [rows_max] max |mid| per row (written by the mid step) */
+    /* File-orientation path: gate/up [E+1][H][D/256] Q4_K blocks, down body
+     * and d [E+1][D][H/256] (the blocks in file order) */
+    ornk_file_ws fw;
     /* Profiling: if set, the expert-product launchers launch their main kernel
      * with hipExtLaunchKernel so that these events carry its start and end. */
     hipEvent_t ev_start, ev_stop;
@@ -130,6 +144,11 @@ int ornk_moe_gateup_dec(const ornk_moe_args *a, hipStream_t s);
 int ornk_dec_supported(int kt_gu, int kt_dn);
 int ornk_moe_down_dec(const ornk_moe_args *a, hipStream_t s);
 /* out[r] = max_k |x[r][k]| (D a multiple of 4). */
+int ornk_file_supported(int D, int H);
+int ornk_file_prep_x(const ornk_moe_args *a, hipStream_t s);
+int ornk_file_gateup(const ornk_moe_args *a, hipStream_t s);
+int ornk_file_prep_mid(const ornk_moe_args *a, hipStream_t s);
+int ornk_file_down(const ornk_moe_args *a, hipStream_t s);
 int ornk_rowmax(const float *x, int rows, int D, float *out, hipEvent_t start, hipStream_t s);
 int ornk_moe_combine(const ornk_moe_args *a, hipStream_t s);
 

@@ -55,7 +55,7 @@ class TensorInfo(C.Structure):
 
 class MoEShape(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("n_layers", "d_model", "hidden", "n_experts", "top_k",
-                                       "has_shared", "prefill_layout")]
+                                       "has_shared", "prefill_layout", "file_layout")]
 
 
 class MoEOpts(C.Structure):
@@ -259,10 +259,13 @@ class Context:
 
 
 class Store:
-    def __init__(self, ctx: Context, n_layers, D, H, E, k, has_shared=True, prefill_layout=True):
+    def __init__(self, ctx: Context, n_layers, D, H, E, k, has_shared=True, prefill_layout=True,
+                 file_layout=False):
+        """file_layout: experts and router in GGUF file orientation (input index
+        fastest); needs prefill_layout=False."""
         self.ctx = ctx
         self.shape = MoEShape(n_layers, D, H, E, k, 1 if has_shared else 0,
-                              1 if prefill_layout else 0)
+                              1 if prefill_layout else 0, 1 if file_layout else 0)
         self.ptr = lib().gpu_moe_store_create(ctx.ptr, C.byref(self.shape))
         if not self.ptr:
             raise RuntimeError("gpu_moe_store_create failed: " + ctx.last_error())

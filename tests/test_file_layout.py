@@ -1,0 +1,295 @@
+"""GGUF file-orientation experts (ornith_moe_shape.file_layout = 1).
+
+Real GGUF files store every matrix with the input index fastest (ggml ne =
+[K, M]); the reference reads matrices as vec@mat (model.c:351-357) and has no
+path for that orientation, so parity here is pinned by:
+  * CPU: the oracle's file layout equals its contiguous (vec@mat) layout
+    bit for bit on weights whose every block shares one set of scales (the
+    same dense matrix is then exactly representable in both orientations,
+    packed from one integer matrix), and matches an fp64 brute force built
+    from the pinned block dequant on random blocks;
+  * GPU: the file-layout kernels against the oracle (random blocks, Q6_K
+    sub-scales up to +-128), and against the already pinned vec@mat MFMA
+    path on the same matrices in the other orientation.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+TOL = 1e-3
+Q4K, Q6K = 144, 210
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+# ---------------------------------------------------------------- packers
+def fp16_bits(v):
+    return np.frombuffer(np.float16(v).tobytes(), np.uint16)[0]
+
+
+def pack_q4k(q, d, dmin, sc, m):
+    """q [nblk][256] ints 0..15; one (sc, m) < 16 for all 8 sub-blocks
+    (gguf.c:31-61 layout: d, dmin, scales[12], qs[128])."""
+    nb = q.shape[0]
+    out = np.zeros((nb, Q4K), np.uint8)
+    out[:, 0:2] = np.frombuffer(np.uint16(fp16_bits(d)).tobytes(), np.uint8)
+    out[:, 2:4] = np.frombuffer(np.uint16(fp16_bits(dmin)).tobytes(), np.uint8)
+    out[:, 4:8] = sc
+    out[:, 8:12] = m
+    out[:, 12:16] = sc | (m << 4)
+    for p in range(4):
+        lo = q[:, 64 * p: 64 * p + 32]
+        hi = q[:, 64 * p + 32: 64 * p + 64]
+        out[:, 16 + 32 * p: 48 + 32 * p] = (lo | (hi << 4)).astype(np.uint8)
+    return out
+
+
+def pack_q6k(q, d, sc):
+    """q [nblk][256] ints 0..63; one int8 sc for all 16 sub-blocks
+    (gguf.c:64-86 layout: ql[128], qh[64], scales[16], d)."""
+    nb = q.shape[0]
+    out = np.zeros((nb, Q6K), np.uint8)
+    for n in range(2):
+        b = q[:, 128 * n: 128 * n + 128]
+        y0, y1, y2, y3 = b[:, 0:32], b[:, 32:64], b[:, 64:96], b[:, 96:128]
+        out[:, 64 * n: 64 * n + 32] = ((y0 & 15) | ((y2 & 15) << 4)).astype(np.uint8)
+        out[:, 64 * n + 32: 64 * n + 64] = ((y1 & 15) | ((y3 & 15) << 4)).astype(np.uint8)
+        out[:, 128 + 32 * n: 160 + 32 * n] = ((y0 >> 4) | ((y1 >> 4) << 2) | ((y2 >> 4) << 4)
+                                              | ((y3 >> 4) << 6)).astype(np.uint8)
+    out[:, 192:208] = np.uint8(np.int8(sc).view(np.uint8))
+    out[:, 208:210] = np.frombuffer(np.uint16(fp16_bits(d)).tobytes(), np.uint8)
+    return out
+
+
+def both_orientations(qmat, packer, *args):
+    """qmat [K][M] integers -> (vec@mat blocks, file blocks) of one matrix."""
+    K, M = qmat.shape
+    ref = packer(qmat.reshape(K * M // 256, 256), *args)       # row k, blocks along i
+    fil = packer(qmat.T.reshape(M * K // 256, 256), *args)     # row i, blocks along k
+    return ref.reshape(-1), fil.reshape(-1)
+
+
+class TwoWay:
+    """One layer given in both orientations (E routed experts + shared)."""
+
+    def __init__(self, D, H, E, seed):
+        rng = np.random.default_rng(seed)
+        self.D, self.H, self.E = D, H, E
+        mats = {"gate": [], "up": [], "down": []}
+        for _ in range(E + 1):
+            for nm in ("gate", "up"):
+                mats[nm].append(both_orientations(rng.integers(0, 16, (D, H)), pack_q4k,
+                                                  0.0123, 0.0071, 5, 3))
+            mats["down"].append(both_orientations(rng.integers(0, 64, (H, D)), pack_q6k,
+                                                  0.0019, -7))
+        self.ref = {nm: np.concatenate([a for a, _ in v]) for nm, v in mats.items()}
+        self.fil = {nm: np.concatenate([b for _, b in v]) for nm, v in mats.items()}
+        self.router = (rng.standard_normal((D, E)) * 0.05).astype(np.float32)
+
+    def per(self, nm):
+        return self.D * self.H // 256 * (Q6K if nm == "down" else Q4K)
+
+    def oracle(self, x, file):
+        src = self.fil if file else self.ref
+        E, p = self.E, {nm: self.per(nm) for nm in src}
+        return O.moe_layer(D=self.D, H=self.H, E=E, k=8, x=x, router_W=self.router,
+                           gate=src["gate"][:E * p["gate"]], up=src["up"][:E * p["up"]],
+                           down=src["down"][:E * p["down"]],
+                           sh_gate=src["gate"][E * p["gate"]:], sh_up=src["up"][E * p["up"]:],
+                           sh_down=src["down"][E * p["down"]:],
+                           layout=O.LAYOUT_FILE if file else O.LAYOUT_CONTIGUOUS)
+
+
+# ---------------------------------------------------------------- CPU (oracle)
+def test_oracle_file_layout_equals_vecmat_on_shared_scales():
+    L = TwoWay(256, 256, 16, seed=5)
+    x = np.random.default_rng(1).standard_normal((3, 256)).astype(np.float32)
+    a = L.oracle(x, file=False)
+    b = L.oracle(x, file=True)
+    for u, v in zip(a, b):
+        assert np.array_equal(u, v)
+
+
+def test_oracle_file_layout_fp64_brute_force():
+    """Random synthetic blocks read in file orientation: the oracle against
+    float64 products of the dequantized (pinned) and transposed matrices."""
+    import ornith_moe as om
+    D = H = 256
+    E, k = 16, 8
+    syn = om.SyntheticLayer(23, 0, D, H, E, True, 0.0)
+    x = np.random.default_rng(2).standard_normal((2, D)).astype(np.float32)
+    out, idx, w = O.moe_layer(D=D, H=H, E=E, k=k, x=x, router_W=syn.router,
+                              gate=syn.routed("gate"), up=syn.routed("up"),
+                              down=syn.routed("down"), sh_gate=syn.shared("gate"),
+                              sh_up=syn.shared("up"), sh_down=syn.shared("down"),
+                              layout=O.LAYOUT_FILE)
+
+    def mat(which, e, K, M, typ):
+        data = syn.routed(which) if e < E else syn.shared(which)
+        per = D * H // 256 * (Q6K if typ == O.TYPE_Q6_K else Q4K)
+        blk = data[(e % E) * per:(e % E + 1) * per] if e < E else data
+        ok, v = O.dequant_tensor(blk, typ, K * M)
+        assert ok
+        return v.astype(np.float64).reshape(M, K)  # [out][in]
+
+    def ffn(xv, e, clamp):
+        g = mat("gate", e, D, H, O.TYPE_Q4_K) @ xv
+        u = mat("up", e, D, H, O.TYPE_Q4_K) @ xv
+        silu = g / (1.0 + np.exp(-np.clip(g, -80.0, 80.0)))
+        if clamp:  # model.c:1087-1088: 0 below -50, identity above 50
+            silu = np.where(g < -50.0, 0.0, np.where(g > 50.0, g, silu))
+        mid = silu * u
+        return mat("down", e, H, D, O.TYPE_Q6_K) @ mid
+
+    for t in range(x.shape[0]):
+        xv = x[t].astype(np.float64)
+        ref = ffn(xv, E, False)
+        for j in range(k):
+            ref = ref + float(w[t, j]) * ffn(xv, int(idx[t, j]), True)
+        err = np.abs(out[t] - ref).max() / np.abs(ref).max()
+        assert err < 1e-5, err
+
+
+# ---------------------------------------------------------------- GPU
+@pytest.fixture(scope="module")
+def om():
+    import ornith_moe
+    ornith_moe.lib()
+    return ornith_moe
+
+
+@pytest.fixture(scope="module")
+def ctx(om):
+    c = om.Context()
+    yield c
+    c.close()
+
+
+def row_err(out, ref):
+    scale = np.abs(ref).max(axis=1)
+    assert np.all(scale > 0) and np.all(np.isfinite(out)), "degenerate or non-finite output"
+    return np.abs(out.astype(np.float64) - ref).max(axis=1) / scale
+
+
+def forward(ctx, store, x, k):
+    T = x.shape[0]
+    xb, ob = ctx.upload(x), ctx.alloc(x.nbytes)
+    ib, wb = ctx.alloc(T * k * 4), ctx.alloc(T * k * 4)
+    store.forward(0, xb, T, ob, idx=ib, w=wb)
+    out = ctx.download(ob, np.float32, x.shape)
+    idx = ctx.download(ib, np.uint32, (T, k))
+    w = ctx.download(wb, np.float32, (T, k))
+    for b in (xb, ob, ib, wb):
+        b.free()
+    return out, idx, w
+
+
+def file_store(om, ctx, D, H, E, k, gate, up, down, router_de):
+    st = om.Store(ctx, 1, D, H, E, k, True, prefill_layout=False, file_layout=True)
+    st.set_experts(0, om.MAT_GATE, 0, gate, E + 1)
+    st.set_experts(0, om.MAT_UP, 0, up, E + 1)
+    st.set_experts(0, om.MAT_DOWN, 0, down, E + 1)
+    st.set_router(0, np.ascontiguousarray(router_de.T))  # file orientation: [E][D]
+    return st
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape,T", [((256, 256, 16), 1), ((256, 256, 16), 3),
+                                     ((256, 256, 16), 37), ((2048, 512, 256), 1),
+                                     ((2048, 512, 256), 16)])
+def test_file_layout_parity(om, ctx, shape, T):
+    D, H, E = shape
+    k = 8
+    say("file layout parity", shape, T)
+    syn = om.SyntheticLayer(31, 0, D, H, E, True, 0.0)
+    st = file_store(om, ctx, D, H, E, k, syn.gate, syn.up, syn.down, syn.router)
+    try:
+        x = np.random.default_rng(T).standard_normal((T, D)).astype(np.float32)
+        out, idx, w = forward(ctx, st, x, k)
+        ref, ridx, rw = O.moe_layer(D=D, H=H, E=E, k=k, x=x, router_W=syn.router,
+                                    gate=syn.routed("gate"), up=syn.routed("up"),
+                                    down=syn.routed("down"), sh_gate=syn.shared("gate"),
+                                    sh_up=syn.shared("up"), sh_down=syn.shared("down"),
+                                    layout=O.LAYOUT_FILE)
+        assert np.array_equal(idx, ridx)
+        # the device's expf may differ from the host's by an ulp
+        assert np.allclose(w, rw, rtol=1e-5, atol=1e-7)
+        e = row_err(out, ref)
+        say("  max row err", e.max())
+        assert e.max() <= TOL
+    finally:
+        st.close()
+
+
+@pytest.mark.gpu
+def test_file_layout_large_q6_scales(om, ctx):
+    """Q6_K sub-scales across the whole int8 range (real files reach +-128)."""
+    D, H, E, k, T = 256, 256, 16, 8, 9
+    syn = om.SyntheticLayer(37, 0, D, H, E, True, 0.0)
+    down = syn.down.copy().reshape(-1, Q6K)
+    rng = np.random.default_rng(3)
+    down[:, 192:208] = rng.integers(-128, 128, (down.shape[0], 16)).astype(np.int8).view(np.uint8)
+    down = down.reshape(-1)
+    st = file_store(om, ctx, D, H, E, k, syn.gate, syn.up, down, syn.router)
+    try:
+        x = rng.standard_normal((T, D)).astype(np.float32)
+        out, idx, w = forward(ctx, st, x, k)
+        per = D * H // 256 * Q6K
+        ref, ridx, _ = O.moe_layer(D=D, H=H, E=E, k=k, x=x, router_W=syn.router,
+                                   gate=syn.routed("gate"), up=syn.routed("up"),
+                                   down=down[:E * per], sh_gate=syn.shared("gate"),
+                                   sh_up=syn.shared("up"), sh_down=down[E * per:],
+                                   layout=O.LAYOUT_FILE)
+        assert np.array_equal(idx, ridx)
+        assert row_err(out, ref).max() <= TOL
+    finally:
+        st.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T", [1, 16, 100])
+def test_file_layout_matches_vecmat_path(om, ctx, T):
+    """The same matrices in both orientations: the file kernels against the
+    vec@mat MFMA kernels (and both against the oracle)."""
+    D, H, E, k = 256, 256, 16, 8
+    L = TwoWay(D, H, E, seed=9)
+    ref_st = om.Store(ctx, 1, D, H, E, k, True, prefill_layout=True)
+    ref_st.set_experts(0, om.MAT_GATE, 0, L.ref["gate"], E + 1)
+    ref_st.set_experts(0, om.MAT_UP, 0, L.ref["up"], E + 1)
+    ref_st.set_experts(0, om.MAT_DOWN, 0, L.ref["down"], E + 1)
+    ref_st.set_router(0, L.router)
+    fil_st = file_store(om, ctx, D, H, E, k, L.fil["gate"], L.fil["up"], L.fil["down"], L.router)
+    try:
+        x = np.random.default_rng(100 + T).standard_normal((T, D)).astype(np.float32)
+        a = forward(ctx, ref_st, x, k)
+        b = forward(ctx, fil_st, x, k)
+        assert np.array_equal(a[1], b[1]) and np.array_equal(a[2], b[2])
+        assert row_err(b[0], a[0].astype(np.float64)).max() <= 1e-4
+        ref = L.oracle(x, file=True)[0]
+        assert row_err(b[0], ref).max() <= TOL
+    finally:
+        ref_st.close()
+        fil_st.close()
+
+
+@pytest.mark.gpu
+def test_file_layout_refuses_forced_path_and_prefill_layout(om, ctx):
+    with pytest.raises(RuntimeError):
+        om.Store(ctx, 1, 256, 256, 16, 8, True, prefill_layout=True, file_layout=True)
+    syn = om.SyntheticLayer(31, 0, 256, 256, 16, True, 0.0)
+    st = file_store(om, ctx, 256, 256, 16, 8, syn.gate, syn.up, syn.down, syn.router)
+    try:
+        x = np.ones((1, 256), np.float32)
+        xb, ob = ctx.upload(x), ctx.alloc(x.nbytes)
+        with pytest.raises(RuntimeError):
+            st.forward(0, xb, 1, ob, flags=om.MOE_PATH_MFMA)
+        xb.free()
+        ob.free()
+    finally:
+        st.close()
