@@ -134,7 +134,8 @@ def roofline_for(kernels, stats, T, workload):
     rows = stats["n_rows"]    # token-expert pairs incl. the shared expert's
     work = {"moe_gateup": ("hbm", slots * GU_BYTES), "moe_down": ("hbm", slots * DN_BYTES),
             "moe_gateup_dec": ("hbm", slots * GU_BYTES), "moe_down_dec": ("hbm", slots * DN_BYTES),
-            "moe_gateup_mfma": ("mfma", rows * 2 * D * 2 * H), "moe_down_mfma": ("mfma", rows * 2 * H * D)}
+            "moe_gateup_mfma": ("mfma", rows * 2 * D * 2 * H), "moe_down_mfma": ("mfma", rows * 2 * H * D),
+            "moe_gateup_file": ("hbm", slots * GU_BYTES), "moe_down_file": ("hbm", slots * DN_BYTES)}
     present = [n for n in work if n in kernels]
     name = max(present, key=lambda n: kernels[n]["avg_us"] * kernels[n]["calls_per_step"])
     bound, amount = work[name]
@@ -207,7 +208,7 @@ def cpu_baseline(budget_s):
 # Extra configs reported beside the headline: (label, store layer, tokens).
 # Layer 1 carries a Zipf(1.1) router bias.
 EXTRA_CONFIGS = (("decode_t1", 0, 1), ("prefill_t2048", 0, 2048), ("zipf_t256", 1, 256))
-EXTRA_LABELS = [c[0] for c in EXTRA_CONFIGS]
+EXTRA_LABELS = [c[0] for c in EXTRA_CONFIGS] + ["file_t1", "file_t16"]
 
 
 def main():
@@ -308,6 +309,24 @@ def main():
                             "layer_hbm_gbs": round(st_x["n_slots"] * EXPERT_BYTES / (ms_x * 1e-3) / 1e9, 1),
                             "kernels_us": {n: round(v["avg_us"], 2) for n, v in kern_x.items()}}
             log(label, extra[label]["tokens_per_s"], "tok/s")
+        # Experts in GGUF file orientation (input index fastest, as real
+        # files store them): a store of its own, same synthetic bytes.
+        if not args.only or args.only.startswith("file_"):
+            fst = om.Store(ctx, 1, D, H, E, K, True, prefill_layout=False, file_layout=True)
+            fst.fill_synthetic(0, SEED)
+            for label, Tn in (("file_t1", 1), ("file_t16", 16)):
+                if args.only and label != args.only:
+                    continue
+                ms_x, kern_x, st_x = measure(ctx, fst, 0, Tn, args.steps, args.warmup)
+                _, roof_x = roofline_for(kern_x, st_x, Tn, label)
+                roof_x["frac_of_measured"] = round(roof_x["achieved"] / read_gbs, 4)
+                extra[label] = {"tokens_per_s": round(Tn / (ms_x * 1e-3), 1),
+                                "ms_per_step": round(ms_x, 4), "active_experts": st_x["n_slots"],
+                                "layer_hbm_gbs": round(st_x["n_slots"] * EXPERT_BYTES / (ms_x * 1e-3) / 1e9, 1),
+                                "dominant": roof_x,
+                                "kernels_us": {n: round(v["avg_us"], 2) for n, v in kern_x.items()}}
+                log(label, extra[label]["tokens_per_s"], "tok/s")
+            fst.close()
         result["configs"] = extra
     store.close()
     if args.stack:

@@ -701,7 +701,7 @@ static plan_t make_plan(const ornith_moe_shape *sh, int T, int use_mfma)
 
 /* File-orientation path: items of <= 16 rows (one MFMA row tile); the
  * reduction is split so that each kernel has about 2048 work groups
- * (gate/up 2H/64 per item and slice, down D/64), in whole super-blocks. */
+ * (gate/up 2H/256 per item and slice, down D/256), in whole super-blocks. */
 static plan_t make_plan_file(const ornith_moe_shape *sh, int T)
 {
     plan_t p;
@@ -713,7 +713,7 @@ static plan_t make_plan_file(const ornith_moe_shape *sh, int T)
     p.items_max = max_slots + (p.rows_max + p.tchunk - 1) / p.tchunk;
     int est = max_slots + p.rows_max / p.tchunk;
     if (est < 1) est = 1;
-    const int ng = 2048 / (est * (2 * H / 64)), nd = 2048 / (est * (D / 64));
+    const int ng = 2048 / (est * (2 * H / 256)), nd = 2048 / (est * (D / 256));
     int kg = pow2_floor(ng > 0 ? ng : 1), kd = pow2_floor(nd > 0 ? nd : 1);
     while (kg > 1 && (D / 256) % kg) kg /= 2;
     while (kd > 1 && (H / 256) % kd) kd /= 2;

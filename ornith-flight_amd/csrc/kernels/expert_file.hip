@@ -112,11 +112,14 @@ __global__ void __launch_bounds__(256)
 }
 
 // ---------------------------------------------------------------------------
-// Gate/up, Q4_K.  Logical tile = (item * ks + kslice) * (2H/64) + cb; wave w
-// of the work group covers output columns cb*64 + 16w .. +16 of the
-// concatenated [gate | up] outputs, over super-blocks kslice*nsb .. +nsb.
-// Output gu[kslice][row][2H].
+// Gate/up, Q4_K.  Logical tile = (item * ks + kslice) * (2H/256) + cb; wave
+// w of the work group covers output columns cb*256 + 64w + 16ct + c (ct <
+// ORN_FCT column tiles, c < 16) of the concatenated [gate | up] outputs,
+// over super-blocks kslice*nsb .. +nsb; each activation operand feeds the
+// ORN_FCT tiles.  Output gu[kslice][row][2H].
 // ---------------------------------------------------------------------------
+#define ORN_FCT 4
+
 __global__ void __launch_bounds__(256)
     k_gu_file(const uint8_t *__restrict__ gate, const uint8_t *__restrict__ up,
               const uint32_t *__restrict__ xh, const uint32_t *__restrict__ xl,
@@ -125,7 +128,7 @@ __global__ void __launch_bounds__(256)
               const int4 *__restrict__ items, const int *__restrict__ row_token,
               float *__restrict__ gu, int D, int H, int ks, int rows_max)
 {
-    const int NCB = (2 * H) >> 6;
+    const int NCB = (2 * H) >> 8;
     const int per_item = NCB * ks;
     const int n_live = ctl[1] * per_item;
     if ((int)blockIdx.x >= n_live) return;
@@ -134,11 +137,11 @@ __global__ void __launch_bounds__(256)
     const int kslice = (tile / NCB) % ks;
     const int4 itm = items[tile / per_item];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c = lane & 15;
-    const int col = cb * 64 + 16 * wave + c;  // in [0, 2H)
-    const int m = col >= H, h = col - m * H;
+    const int col0 = cb * 256 + 64 * wave;  // the wave's 64 columns lie in one matrix
+    const int m = col0 >= H, h0 = col0 - m * H + c;
     const int NSB = D >> 8, nsb = NSB / ks, s0 = kslice * nsb;
-    const uint8_t *rowp = (m ? up : gate) +
-                          ((size_t)itm.w * H + h) * (size_t)NSB * 144;  // row h of expert itm.w
+    const size_t rstride = (size_t)NSB * 144;  // bytes per file row
+    const uint8_t *rowp = (m ? up : gate) + ((size_t)itm.w * H + h0) * rstride;  // tile ct: + 16ct rows
     const int nrows = itm.z;
     const int tok = row_token[itm.y + (c < nrows ? c : nrows - 1)];  // A row = c
     const uint32_t *ah = xh + (size_t)tok * (D >> 1);
@@ -146,16 +149,21 @@ __global__ void __launch_bounds__(256)
     const uint16_t *sah = sh + (size_t)tok * (D >> 5);
     const uint16_t *sal = sl + (size_t)tok * (D >> 5);
 
-    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    v4f acc[ORN_FCT];
+#pragma unroll
+    for (int ct = 0; ct < ORN_FCT; ++ct) acc[ct] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
     for (int s = s0; s < s0 + nsb; ++s) {
-        const uint8_t *blk = rowp + (size_t)s * 144;
-        const uint4 hd = *reinterpret_cast<const uint4 *>(blk);  // d, dmin, scales[12]
-        uint4 w[2];
-        w[0] = *reinterpret_cast<const uint4 *>(blk + 16 + 16 * g);
-        w[1] = *reinterpret_cast<const uint4 *>(blk + 80 + 16 * g);
-        const float d = orn_half_to_float(hd.x & 0xFFFFu);
-        const float dmin = orn_half_to_float(hd.x >> 16);
-        v4f P = {0.0f, 0.0f, 0.0f, 0.0f};
+        uint4 hd[ORN_FCT], w[ORN_FCT][2];
+#pragma unroll
+        for (int ct = 0; ct < ORN_FCT; ++ct) {
+            const uint8_t *blk = rowp + (size_t)(16 * ct) * rstride + (size_t)s * 144;
+            hd[ct] = *reinterpret_cast<const uint4 *>(blk);  // d, dmin, scales[12]
+            w[ct][0] = *reinterpret_cast<const uint4 *>(blk + 16 + 16 * g);
+            w[ct][1] = *reinterpret_cast<const uint4 *>(blk + 80 + 16 * g);
+        }
+        v4f P[ORN_FCT];
+#pragma unroll
+        for (int ct = 0; ct < ORN_FCT; ++ct) P[ct] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int L = 0; L < 2; ++L) {
             // this lane's 16 bytes: chunk p = 2L + g/2 (sub-blocks 2p low
@@ -164,71 +172,90 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const int j = 2 * p + (t >> 1);
-                uint32_t scj, mj;
-                orn_scale_min_k4(j, hd.y, hd.z, hd.w, scj, mj);
-                const _Float16 sf = (_Float16)(float)scj;
-                const v2h sv = {sf, sf};
-                const v2h ns = sv * (v2h){(_Float16)-1024.0f, (_Float16)-1024.0f};
-                const uint32_t wa = (t & 1) ? w[L].z : w[L].x;
-                const uint32_t wb = (t & 1) ? w[L].w : w[L].y;
-                const int sft = (t >> 1) ? 4 : 0;
-                const uint32_t pr[4] = {magic_pair(wa >> sft), magic_pair(wa >> (sft + 8)),
-                                        magic_pair(wb >> sft), magic_pair(wb >> (sft + 8))};
-                uint32_t o[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    o[i] = as_u32(__builtin_elementwise_fma(as_v2h(pr[i]), sv, ns));
-                const v8h bq = to_v8h(o[0], o[1], o[2], o[3]);
                 const int k = 256 * s + 32 * j + 16 * (g & 1) + 8 * (t & 1);
-                const uint4 xa = *reinterpret_cast<const uint4 *>(ah + (k >> 1));
-                const uint4 xb = *reinterpret_cast<const uint4 *>(al + (k >> 1));
-                P = mfma(__builtin_bit_cast(v8h, xa), bq, P);
-                P = mfma(__builtin_bit_cast(v8h, xb), bq, P);
+                const v8h xa = __builtin_bit_cast(v8h, *reinterpret_cast<const uint4 *>(ah + (k >> 1)));
+                const v8h xb = __builtin_bit_cast(v8h, *reinterpret_cast<const uint4 *>(al + (k >> 1)));
+                const int sft = (t >> 1) ? 4 : 0;
+#pragma unroll
+                for (int ct = 0; ct < ORN_FCT; ++ct) {
+                    uint32_t scj, mj;
+                    orn_scale_min_k4(j, hd[ct].y, hd[ct].z, hd[ct].w, scj, mj);
+                    const _Float16 sf = (_Float16)(float)scj;
+                    const v2h sv = {sf, sf};
+                    const v2h ns = sv * (v2h){(_Float16)-1024.0f, (_Float16)-1024.0f};
+                    const uint32_t wa = (t & 1) ? w[ct][L].z : w[ct][L].x;
+                    const uint32_t wb = (t & 1) ? w[ct][L].w : w[ct][L].y;
+                    const uint32_t pr[4] = {magic_pair(wa >> sft), magic_pair(wa >> (sft + 8)),
+                                            magic_pair(wb >> sft), magic_pair(wb >> (sft + 8))};
+                    uint32_t o[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        o[i] = as_u32(__builtin_elementwise_fma(as_v2h(pr[i]), sv, ns));
+                    const v8h bq = to_v8h(o[0], o[1], o[2], o[3]);
+                    P[ct] = mfma(xa, bq, P[ct]);
+                    P[ct] = mfma(xb, bq, P[ct]);
+                }
             }
         }
         // mins: k = sub-block e of this super-block on the g == 0 lanes
-        uint4 mh = make_uint4(0u, 0u, 0u, 0u), ml = mh, mb = mh;
+        uint4 mh = make_uint4(0u, 0u, 0u, 0u), ml = mh;
         if (g == 0) {
             mh = *reinterpret_cast<const uint4 *>(sah + 8 * s);
             ml = *reinterpret_cast<const uint4 *>(sal + 8 * s);
-            uint32_t mv[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                uint32_t scj;
-                orn_scale_min_k4(e, hd.y, hd.z, hd.w, scj, mv[e]);
-            }
-            // (1024 + m) as fp16 is 0x6400 | m; subtract 1024 (exact)
-            const v2h off = {(_Float16)-1024.0f, (_Float16)-1024.0f};
-            uint32_t o[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                o[i] = as_u32(as_v2h(0x64006400u | mv[2 * i] | (mv[2 * i + 1] << 16)) + off);
-            mb = make_uint4(o[0], o[1], o[2], o[3]);
         }
-        v4f Pm = {0.0f, 0.0f, 0.0f, 0.0f};
-        Pm = mfma(__builtin_bit_cast(v8h, mh), __builtin_bit_cast(v8h, mb), Pm);
-        Pm = mfma(__builtin_bit_cast(v8h, ml), __builtin_bit_cast(v8h, mb), Pm);
-        const float dm32 = -32.0f * dmin;  // the sums were stored divided by 32
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            acc[r] = fmaf(d, P[r], acc[r]);
-            acc[r] = fmaf(dm32, Pm[r], acc[r]);
+        for (int ct = 0; ct < ORN_FCT; ++ct) {
+            uint4 mb = make_uint4(0u, 0u, 0u, 0u);
+            if (g == 0) {
+                uint32_t mv[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    uint32_t scj;
+                    orn_scale_min_k4(e, hd[ct].y, hd[ct].z, hd[ct].w, scj, mv[e]);
+                }
+                // (1024 + m) as fp16 is 0x6400 | m; subtract 1024 (exact)
+                const v2h off = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+                uint32_t o[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    o[i] = as_u32(as_v2h(0x64006400u | mv[2 * i] | (mv[2 * i + 1] << 16)) + off);
+                mb = make_uint4(o[0], o[1], o[2], o[3]);
+            }
+            v4f Pm = {0.0f, 0.0f, 0.0f, 0.0f};
+            Pm = mfma(__builtin_bit_cast(v8h, mh), __builtin_bit_cast(v8h, mb), Pm);
+            Pm = mfma(__builtin_bit_cast(v8h, ml), __builtin_bit_cast(v8h, mb), Pm);
+            const float d = orn_half_to_float(hd[ct].x & 0xFFFFu);
+            const float dm32 = -32.0f * orn_half_to_float(hd[ct].x >> 16);  // sums stored / 32
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                acc[ct][r] = fmaf(d, P[ct][r], acc[ct][r]);
+                acc[ct][r] = fmaf(dm32, Pm[r], acc[ct][r]);
+            }
         }
     }
-    float *out = gu + ((size_t)kslice * rows_max + itm.y) * (size_t)(2 * H) + col;
+    float inv[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int row = 4 * g + r;
-        if (row < nrows) out[(size_t)row * (2 * H)] = acc[r] * xinv[row_token[itm.y + row]];
+        inv[r] = row < nrows ? xinv[row_token[itm.y + row]] : 0.0f;
     }
+    float *out = gu + ((size_t)kslice * rows_max + itm.y) * (size_t)(2 * H) + col0 + c;
+#pragma unroll
+    for (int ct = 0; ct < ORN_FCT; ++ct)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = 4 * g + r;
+            if (row < nrows) out[(size_t)row * (2 * H) + 16 * ct] = acc[ct][r] * inv[r];
+        }
 }
 
 // ---------------------------------------------------------------------------
 // Down, Q6_K (gguf.c:64-86 value layout: within each 128-value half n, value
 // 32Q + l (Q = 0..3, l < 32) takes ql[64n + 32(Q&1) + l] (low nibble for Q <
 // 2, high for Q >= 2) and bits 2Q..2Q+1 of qh[32n + l], scale sc[8n + 2Q +
-// l/16]).  Logical tile = (item * ks + kslice) * (D/64) + cb; wave w covers
-// output columns cb*64 + 16w .. +16.  The store keeps each block's 208
+// l/16]).  Logical tile = (item * ks + kslice) * (D/256) + cb; wave w
+// covers output columns cb*256 + 64w + 16ct + c (ct < ORN_FCT), each
+// activation operand feeding the ORN_FCT tiles.  The store keeps each block's 208
 // leading bytes and its d apart (body / dv, block order as in the file).
 // Output dn[kslice][row][D].
 // ---------------------------------------------------------------------------
@@ -239,7 +266,7 @@ __global__ void __launch_bounds__(256)
               const int4 *__restrict__ items, float *__restrict__ dn, int D, int H, int ks,
               int rows_max)
 {
-    const int NCB = D >> 6;
+    const int NCB = D >> 8;
     const int per_item = NCB * ks;
     const int n_live = ctl[1] * per_item;
     if ((int)blockIdx.x >= n_live) return;
@@ -248,61 +275,82 @@ __global__ void __launch_bounds__(256)
     const int kslice = (tile / NCB) % ks;
     const int4 itm = items[tile / per_item];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c = lane & 15;
-    const int n = cb * 64 + 16 * wave + c;  // output column = file row
+    const int n0 = cb * 256 + 64 * wave + c;  // tile ct: output column n0 + 16ct = file row
     const int NSB = H >> 8, nsb = NSB / ks, s0 = kslice * nsb;
-    const size_t b0 = ((size_t)itm.w * D + n) * NSB;  // first block of row n
+    const size_t b0 = ((size_t)itm.w * D + n0) * NSB;  // first block of row n0
     const int nrows = itm.z;
     const int arow = itm.y + (c < nrows ? c : nrows - 1);  // A row = c (mid rows)
     const uint32_t *ah = mh + (size_t)arow * (H >> 1);
     const uint32_t *al = ml + (size_t)arow * (H >> 1);
 
-    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    v4f acc[ORN_FCT];
+#pragma unroll
+    for (int ct = 0; ct < ORN_FCT; ++ct) acc[ct] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
     for (int s = s0; s < s0 + nsb; ++s) {
-        const uint8_t *blk = body + (b0 + s) * 208;
-        const float d = orn_half_to_float(dv[b0 + s]);
-        const uint4 scw = *reinterpret_cast<const uint4 *>(blk + 192);
-        const uint32_t scs[4] = {scw.x, scw.y, scw.z, scw.w};
+        const uint8_t *blk[ORN_FCT];
+        float d[ORN_FCT];
+        uint32_t scs[ORN_FCT][4];
+#pragma unroll
+        for (int ct = 0; ct < ORN_FCT; ++ct) {
+            const size_t bi = b0 + (size_t)(16 * ct) * NSB + s;
+            blk[ct] = body + bi * 208;
+            d[ct] = orn_half_to_float(dv[bi]);
+            const uint4 scw = *reinterpret_cast<const uint4 *>(blk[ct] + 192);
+            scs[ct][0] = scw.x;
+            scs[ct][1] = scw.y;
+            scs[ct][2] = scw.z;
+            scs[ct][3] = scw.w;
+        }
 #pragma unroll
         for (int hn = 0; hn < 2; ++hn) {
 #pragma unroll
             for (int is = 0; is < 2; ++is) {
                 const int l0 = 16 * is + 4 * g;  // this lane's 4 positions l0 .. l0+3
-                const uint32_t q0 = *reinterpret_cast<const uint32_t *>(blk + 64 * hn + l0);
-                const uint32_t q1 = *reinterpret_cast<const uint32_t *>(blk + 64 * hn + 32 + l0);
-                const uint32_t qh = *reinterpret_cast<const uint32_t *>(blk + 128 + 32 * hn + l0);
+                uint32_t q0[ORN_FCT], q1[ORN_FCT], qh[ORN_FCT];
+#pragma unroll
+                for (int ct = 0; ct < ORN_FCT; ++ct) {
+                    q0[ct] = *reinterpret_cast<const uint32_t *>(blk[ct] + 64 * hn + l0);
+                    q1[ct] = *reinterpret_cast<const uint32_t *>(blk[ct] + 64 * hn + 32 + l0);
+                    qh[ct] = *reinterpret_cast<const uint32_t *>(blk[ct] + 128 + 32 * hn + l0);
+                }
 #pragma unroll
                 for (int Q = 0; Q < 4; ++Q) {
-                    const uint32_t ql = (Q & 1) ? q1 : q0;
-                    // bytes 0..63: low 4 bits from ql, high 2 from qh
-                    const uint32_t qv = ((ql >> (4 * (Q >> 1))) & 0x0F0F0F0Fu) |
-                                        (((qh >> (2 * Q)) & 0x03030303u) << 4);
-                    // fp16 pairs (1024 + byte) in the order (b0, b2), (b1, b3),
-                    // then - 1056: q - 32 exactly
-                    const v2h off = {(_Float16)-1056.0f, (_Float16)-1056.0f};
-                    const uint32_t p0 = as_u32(as_v2h(__builtin_amdgcn_perm(0x64646464u, qv, 0x04020400u)) + off);
-                    const uint32_t p1 = as_u32(as_v2h(__builtin_amdgcn_perm(0x64646464u, qv, 0x04030401u)) + off);
-                    const v4h bq = __builtin_bit_cast(v4h, make_uint2(p0, p1));
-                    const int sb = 8 * hn + 2 * Q + is;  // sub-block scale index
-                    const int scv = (int)(int8_t)((scs[sb >> 2] >> (8 * (sb & 3))) & 0xFFu);
                     const int k = 256 * s + 128 * hn + 32 * Q + l0;
-                    const uint2 xa = *reinterpret_cast<const uint2 *>(ah + (k >> 1));
-                    const uint2 xb = *reinterpret_cast<const uint2 *>(al + (k >> 1));
-                    v4f P = {0.0f, 0.0f, 0.0f, 0.0f};
-                    P = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(v4h, xa), bq, P, 0, 0, 0);
-                    P = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(v4h, xb), bq, P, 0, 0, 0);
-                    const float dsc = d * (float)scv;  // exact: 11-bit d times 8-bit sc
+                    const v4h xa = __builtin_bit_cast(v4h, *reinterpret_cast<const uint2 *>(ah + (k >> 1)));
+                    const v4h xb = __builtin_bit_cast(v4h, *reinterpret_cast<const uint2 *>(al + (k >> 1)));
+                    const int sb = 8 * hn + 2 * Q + is;  // sub-block scale index
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[r] = fmaf(dsc, P[r], acc[r]);
+                    for (int ct = 0; ct < ORN_FCT; ++ct) {
+                        const uint32_t ql = (Q & 1) ? q1[ct] : q0[ct];
+                        // bytes 0..63: low 4 bits from ql, high 2 from qh
+                        const uint32_t qv = ((ql >> (4 * (Q >> 1))) & 0x0F0F0F0Fu) |
+                                            (((qh[ct] >> (2 * Q)) & 0x03030303u) << 4);
+                        // fp16 pairs (1024 + byte) in the order (b0, b2), (b1, b3),
+                        // then - 1056: q - 32 exactly
+                        const v2h off = {(_Float16)-1056.0f, (_Float16)-1056.0f};
+                        const uint32_t p0 = as_u32(as_v2h(__builtin_amdgcn_perm(0x64646464u, qv, 0x04020400u)) + off);
+                        const uint32_t p1 = as_u32(as_v2h(__builtin_amdgcn_perm(0x64646464u, qv, 0x04030401u)) + off);
+                        const v4h bq = __builtin_bit_cast(v4h, make_uint2(p0, p1));
+                        const int scv = (int)(int8_t)((scs[ct][sb >> 2] >> (8 * (sb & 3))) & 0xFFu);
+                        v4f P = {0.0f, 0.0f, 0.0f, 0.0f};
+                        P = __builtin_amdgcn_mfma_f32_16x16x16f16(xa, bq, P, 0, 0, 0);
+                        P = __builtin_amdgcn_mfma_f32_16x16x16f16(xb, bq, P, 0, 0, 0);
+                        const float dsc = d[ct] * (float)scv;  // exact: 11-bit d times 8-bit sc
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) acc[ct][r] = fmaf(dsc, P[r], acc[ct][r]);
+                    }
                 }
             }
         }
     }
-    float *out = dn + ((size_t)kslice * rows_max + itm.y) * (size_t)D + n;
+    float *out = dn + ((size_t)kslice * rows_max + itm.y) * (size_t)D + n0;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int row = 4 * g + r;
-        if (row < nrows) out[(size_t)row * D] = acc[r] * minv[itm.y + row];
-    }
+    for (int ct = 0; ct < ORN_FCT; ++ct)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = 4 * g + r;
+            if (row < nrows) out[(size_t)row * D + 16 * ct] = acc[ct][r] * minv[itm.y + row];
+        }
 }
 
 }  // namespace
@@ -329,7 +377,7 @@ extern "C" int ornk_file_gateup(const ornk_moe_args *a, hipStream_t s)
 {
     if (!ornk_file_supported(a->D, a->H) || (a->D / 256) % a->ks_gu) return hipErrorInvalidValue;
     const ornk_file_ws &f = a->fw;
-    const dim3 grid(a->items_max * ((2 * a->H) / 64) * a->ks_gu);
+    const dim3 grid(a->items_max * ((2 * a->H) / 256) * a->ks_gu);
     ORN_LAUNCH_EV(a, k_gu_file, grid, dim3(256), 0, s, a->gate, a->up, f.xh, f.xl, f.xinv, f.xsh,
                   f.xsl, a->ctl, reinterpret_cast<const int4 *>(a->items), a->row_token,
                   a->gu_part, a->D, a->H, a->ks_gu, a->rows_max);
@@ -350,7 +398,7 @@ extern "C" int ornk_file_down(const ornk_moe_args *a, hipStream_t s)
 {
     if (!ornk_file_supported(a->D, a->H) || (a->H / 256) % a->ks_dn) return hipErrorInvalidValue;
     const ornk_file_ws &f = a->fw;
-    const dim3 grid(a->items_max * (a->D / 64) * a->ks_dn);
+    const dim3 grid(a->items_max * (a->D / 256) * a->ks_dn);
     ORN_LAUNCH_EV(a, k_dn_file, grid, dim3(256), 0, s, a->down_body, a->down_d, f.mh, f.ml,
                   f.minv, a->ctl, reinterpret_cast<const int4 *>(a->items), a->dn_part, a->D,
                   a->H, a->ks_dn, a->rows_max);
