@@ -22,7 +22,8 @@
 //     to 4096, not exact in fp16), so B = q - 32 and each 16-value
 //     sub-block is one step: acc += (d * sc)(column) * P.
 // Activations come from k_prep_rows, which splits each row (times a power
-// of two s, |x*s| < 2^14) into fp16 hi + lo once per forward; products of
+// of two s, |x*s| < 2^14) into fp16 hi + lo once per forward, and reach
+// the waves through one LDS tile per super-block and work group; products of
 // hi and lo with the exact B accumulate in fp32, and outputs are scaled
 // back by 1/s.
 //
@@ -49,6 +50,29 @@ __device__ __forceinline__ float prep_scale(float amax)
     int e = 13 - ilogbf(amax);
     e = e < -126 ? -126 : (e > 126 ? 126 : e);
     return ldexpf(1.0f, e);
+}
+
+// Activation tile of one super-block in LDS: [hi, lo][16 rows][256 values]
+// (row stride padded to 264 halves), staged once per work group from the
+// prepared rows src[r] (an LDS int[16]) and shared by its four waves.  Two
+// tiles alternate, so one barrier per super-block suffices: a wave writes
+// tile (s+1)&1 only after every wave has passed the barrier of super-block
+// s, which each reaches after its reads of that tile for super-block s-1.
+#define ORN_FAS 264
+typedef _Float16 FileTile[2][16][ORN_FAS];
+
+__device__ __forceinline__ void stage_tile(FileTile &As, const uint32_t *__restrict__ xh,
+                                           const uint32_t *__restrict__ xl, const int *src,
+                                           int K, int s)
+{
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {  // 2 planes x 16 rows x 32 chunks of 16 B
+        const int idx = threadIdx.x + 256 * i;
+        const int plane = idx >> 9, row = (idx >> 5) & 15, ch = idx & 31;
+        *reinterpret_cast<uint4 *>(&As[plane][row][8 * ch]) = *reinterpret_cast<const uint4 *>(
+            (plane ? xl : xh) + (size_t)src[row] * (K >> 1) + 128 * s + 4 * ch);
+    }
+    __syncthreads();
 }
 
 // ---------------------------------------------------------------------------
@@ -144,8 +168,11 @@ __global__ void __launch_bounds__(256)
     const uint8_t *rowp = (m ? up : gate) + ((size_t)itm.w * H + h0) * rstride;  // tile ct: + 16ct rows
     const int nrows = itm.z;
     const int tok = row_token[itm.y + (c < nrows ? c : nrows - 1)];  // A row = c
-    const uint32_t *ah = xh + (size_t)tok * (D >> 1);
-    const uint32_t *al = xl + (size_t)tok * (D >> 1);
+    __shared__ __align__(16) FileTile Ab[2];
+    __shared__ int src[16];
+    if (threadIdx.x < 16)
+        src[threadIdx.x] = row_token[itm.y + ((int)threadIdx.x < nrows ? (int)threadIdx.x : nrows - 1)];
+    __syncthreads();
     const uint16_t *sah = sh + (size_t)tok * (D >> 5);
     const uint16_t *sal = sl + (size_t)tok * (D >> 5);
 
@@ -161,6 +188,8 @@ __global__ void __launch_bounds__(256)
             w[ct][0] = *reinterpret_cast<const uint4 *>(blk + 16 + 16 * g);
             w[ct][1] = *reinterpret_cast<const uint4 *>(blk + 80 + 16 * g);
         }
+        FileTile &As = Ab[s & 1];
+        stage_tile(As, xh, xl, src, D, s);
         v4f P[ORN_FCT];
 #pragma unroll
         for (int ct = 0; ct < ORN_FCT; ++ct) P[ct] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
@@ -172,9 +201,9 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const int j = 2 * p + (t >> 1);
-                const int k = 256 * s + 32 * j + 16 * (g & 1) + 8 * (t & 1);
-                const v8h xa = __builtin_bit_cast(v8h, *reinterpret_cast<const uint4 *>(ah + (k >> 1)));
-                const v8h xb = __builtin_bit_cast(v8h, *reinterpret_cast<const uint4 *>(al + (k >> 1)));
+                const int kl = 32 * j + 16 * (g & 1) + 8 * (t & 1);  // k - 256 s
+                const v8h xa = *reinterpret_cast<const v8h *>(&As[0][c][kl]);
+                const v8h xb = *reinterpret_cast<const v8h *>(&As[1][c][kl]);
                 const int sft = (t >> 1) ? 4 : 0;
 #pragma unroll
                 for (int ct = 0; ct < ORN_FCT; ++ct) {
@@ -279,9 +308,11 @@ __global__ void __launch_bounds__(256)
     const int NSB = H >> 8, nsb = NSB / ks, s0 = kslice * nsb;
     const size_t b0 = ((size_t)itm.w * D + n0) * NSB;  // first block of row n0
     const int nrows = itm.z;
-    const int arow = itm.y + (c < nrows ? c : nrows - 1);  // A row = c (mid rows)
-    const uint32_t *ah = mh + (size_t)arow * (H >> 1);
-    const uint32_t *al = ml + (size_t)arow * (H >> 1);
+    __shared__ __align__(16) FileTile Ab[2];  // A row = c (mid rows)
+    __shared__ int src[16];
+    if (threadIdx.x < 16)
+        src[threadIdx.x] = itm.y + ((int)threadIdx.x < nrows ? (int)threadIdx.x : nrows - 1);
+    __syncthreads();
 
     v4f acc[ORN_FCT];
 #pragma unroll
@@ -301,6 +332,22 @@ __global__ void __launch_bounds__(256)
             scs[ct][2] = scw.z;
             scs[ct][3] = scw.w;
         }
+        // every q word of the super-block is requested before the first is
+        // used (one memory round trip per super-block)
+        uint32_t qa[2][2][ORN_FCT][3];
+#pragma unroll
+        for (int hn = 0; hn < 2; ++hn)
+#pragma unroll
+            for (int is = 0; is < 2; ++is)
+#pragma unroll
+                for (int ct = 0; ct < ORN_FCT; ++ct) {
+                    const int l0 = 16 * is + 4 * g;
+                    qa[hn][is][ct][0] = *reinterpret_cast<const uint32_t *>(blk[ct] + 64 * hn + l0);
+                    qa[hn][is][ct][1] = *reinterpret_cast<const uint32_t *>(blk[ct] + 64 * hn + 32 + l0);
+                    qa[hn][is][ct][2] = *reinterpret_cast<const uint32_t *>(blk[ct] + 128 + 32 * hn + l0);
+                }
+        FileTile &As = Ab[s & 1];
+        stage_tile(As, mh, ml, src, H, s);
 #pragma unroll
         for (int hn = 0; hn < 2; ++hn) {
 #pragma unroll
@@ -309,15 +356,15 @@ __global__ void __launch_bounds__(256)
                 uint32_t q0[ORN_FCT], q1[ORN_FCT], qh[ORN_FCT];
 #pragma unroll
                 for (int ct = 0; ct < ORN_FCT; ++ct) {
-                    q0[ct] = *reinterpret_cast<const uint32_t *>(blk[ct] + 64 * hn + l0);
-                    q1[ct] = *reinterpret_cast<const uint32_t *>(blk[ct] + 64 * hn + 32 + l0);
-                    qh[ct] = *reinterpret_cast<const uint32_t *>(blk[ct] + 128 + 32 * hn + l0);
+                    q0[ct] = qa[hn][is][ct][0];
+                    q1[ct] = qa[hn][is][ct][1];
+                    qh[ct] = qa[hn][is][ct][2];
                 }
 #pragma unroll
                 for (int Q = 0; Q < 4; ++Q) {
-                    const int k = 256 * s + 128 * hn + 32 * Q + l0;
-                    const v4h xa = __builtin_bit_cast(v4h, *reinterpret_cast<const uint2 *>(ah + (k >> 1)));
-                    const v4h xb = __builtin_bit_cast(v4h, *reinterpret_cast<const uint2 *>(al + (k >> 1)));
+                    const int kl = 128 * hn + 32 * Q + l0;  // k - 256 s
+                    const v4h xa = *reinterpret_cast<const v4h *>(&As[0][c][kl]);
+                    const v4h xb = *reinterpret_cast<const v4h *>(&As[1][c][kl]);
                     const int sb = 8 * hn + 2 * Q + is;  // sub-block scale index
 #pragma unroll
                     for (int ct = 0; ct < ORN_FCT; ++ct) {
