@@ -293,3 +293,30 @@ def test_file_layout_refuses_forced_path_and_prefill_layout(om, ctx):
         ob.free()
     finally:
         st.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T", [1, 16])
+def test_file_layout_graph_replay_matches_eager(om, ctx, T):
+    """ORN_MOE_GRAPH on a file-layout store: each replay sees new input
+    contents, with eager forwards and synchronisations in between, and must
+    equal an eager forward of the same input bit for bit."""
+    D, H, E, k = 256, 256, 16, 8
+    syn = om.SyntheticLayer(31, 0, D, H, E, True, 0.0)
+    st = file_store(om, ctx, D, H, E, k, syn.gate, syn.up, syn.down, syn.router)
+    xb, ob = ctx.alloc(T * D * 4), ctx.alloc(T * D * 4)
+    ib, wb = ctx.alloc(T * k * 4), ctx.alloc(T * k * 4)
+    try:
+        for i in range(4):
+            x = np.random.default_rng(700 + 10 * T + i).standard_normal((T, D)).astype(np.float32)
+            om.lib().gpu_copy_to_device(ctx.ptr, xb.ptr, x.ctypes.data, x.nbytes)
+            st.forward(0, xb, T, ob, idx=ib, w=wb, flags=om.MOE_GRAPH)
+            g = ctx.download(ob, np.float32, (T, D))
+            gi = ctx.download(ib, np.uint32, (T, k))
+            e, ei, _ = forward(ctx, st, x, k)
+            assert np.array_equal(gi, ei)
+            assert np.array_equal(g.view(np.uint32), e.view(np.uint32))
+    finally:
+        for b in (xb, ob, ib, wb):
+            b.free()
+        st.close()
