@@ -701,7 +701,7 @@ static plan_t make_plan(const ornith_moe_shape *sh, int T, int use_mfma)
 
 /* File-orientation path: items of <= 16 rows (one MFMA row tile); the
  * reduction is split, in whole super-blocks, so that gate/up has about
- * 8192 work groups (2H/256 per item and slice) and down about 4096 (D/256):
+ * 8192 work groups (2H/256 per item and slice) and down about 8192 (D/128):
  * at three waves per SIMD these kernels need several rounds of work groups
  * to hide their memory latency, and a wave that covers one super-block
  * uses every byte of its blocks while they are cached. */
@@ -716,7 +716,7 @@ static plan_t make_plan_file(const ornith_moe_shape *sh, int T)
     p.items_max = max_slots + (p.rows_max + p.tchunk - 1) / p.tchunk;
     int est = max_slots + p.rows_max / p.tchunk;
     if (est < 1) est = 1;
-    const int ng = 8192 / (est * (2 * H / 256)), nd = 4096 / (est * (D / 256));
+    const int ng = 8192 / (est * (2 * H / 256)), nd = 8192 / (est * (D / 128));
     int kg = pow2_floor(ng > 0 ? ng : 1), kd = pow2_floor(nd > 0 ? nd : 1);
     while (kg > 1 && (D / 256) % kg) kg /= 2;
     while (kd > 1 && (H / 256) % kd) kd /= 2;

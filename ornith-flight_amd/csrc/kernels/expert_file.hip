@@ -282,12 +282,14 @@ __global__ void __launch_bounds__(256)
 // Down, Q6_K (gguf.c:64-86 value layout: within each 128-value half n, value
 // 32Q + l (Q = 0..3, l < 32) takes ql[64n + 32(Q&1) + l] (low nibble for Q <
 // 2, high for Q >= 2) and bits 2Q..2Q+1 of qh[32n + l], scale sc[8n + 2Q +
-// l/16]).  Logical tile = (item * ks + kslice) * (D/256) + cb; wave w
-// covers output columns cb*256 + 64w + 16ct + c (ct < ORN_FCT), each
-// activation operand feeding the ORN_FCT tiles.  The store keeps each block's 208
+// l/16]).  Logical tile = (item * ks + kslice) * (D/(64*ORN_FDN)) + cb;
+// wave w covers output columns cb*64*ORN_FDN + 16*ORN_FDN*w + 16ct + c (ct <
+// ORN_FDN), each activation operand feeding the ORN_FDN tiles.  The store keeps each block's 208
 // leading bytes and its d apart (body / dv, block order as in the file).
 // Output dn[kslice][row][D].
 // ---------------------------------------------------------------------------
+#define ORN_FDN 2  // column tiles per wave in the down kernel
+
 __global__ void __launch_bounds__(256)
     k_dn_file(const uint8_t *__restrict__ body, const uint16_t *__restrict__ dv,
               const uint32_t *__restrict__ mh, const uint32_t *__restrict__ ml,
@@ -295,7 +297,7 @@ __global__ void __launch_bounds__(256)
               const int4 *__restrict__ items, float *__restrict__ dn, int D, int H, int ks,
               int rows_max)
 {
-    const int NCB = D >> 8;
+    const int NCB = D / (64 * ORN_FDN);
     const int per_item = NCB * ks;
     const int n_live = ctl[1] * per_item;
     if ((int)blockIdx.x >= n_live) return;
@@ -304,7 +306,7 @@ __global__ void __launch_bounds__(256)
     const int kslice = (tile / NCB) % ks;
     const int4 itm = items[tile / per_item];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c = lane & 15;
-    const int n0 = cb * 256 + 64 * wave + c;  // tile ct: output column n0 + 16ct = file row
+    const int n0 = cb * (64 * ORN_FDN) + 16 * ORN_FDN * wave + c;  // tile ct: column n0 + 16ct = file row
     const int NSB = H >> 8, nsb = NSB / ks, s0 = kslice * nsb;
     const size_t b0 = ((size_t)itm.w * D + n0) * NSB;  // first block of row n0
     const int nrows = itm.z;
@@ -314,15 +316,15 @@ __global__ void __launch_bounds__(256)
         src[threadIdx.x] = itm.y + ((int)threadIdx.x < nrows ? (int)threadIdx.x : nrows - 1);
     __syncthreads();
 
-    v4f acc[ORN_FCT];
+    v4f acc[ORN_FDN];
 #pragma unroll
-    for (int ct = 0; ct < ORN_FCT; ++ct) acc[ct] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+    for (int ct = 0; ct < ORN_FDN; ++ct) acc[ct] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
     for (int s = s0; s < s0 + nsb; ++s) {
-        const uint8_t *blk[ORN_FCT];
-        float d[ORN_FCT];
-        uint32_t scs[ORN_FCT][4];
+        const uint8_t *blk[ORN_FDN];
+        float d[ORN_FDN];
+        uint32_t scs[ORN_FDN][4];
 #pragma unroll
-        for (int ct = 0; ct < ORN_FCT; ++ct) {
+        for (int ct = 0; ct < ORN_FDN; ++ct) {
             const size_t bi = b0 + (size_t)(16 * ct) * NSB + s;
             blk[ct] = body + bi * 208;
             d[ct] = orn_half_to_float(dv[bi]);
@@ -334,13 +336,13 @@ __global__ void __launch_bounds__(256)
         }
         // every q word of the super-block is requested before the first is
         // used (one memory round trip per super-block)
-        uint32_t qa[2][2][ORN_FCT][3];
+        uint32_t qa[2][2][ORN_FDN][3];
 #pragma unroll
         for (int hn = 0; hn < 2; ++hn)
 #pragma unroll
             for (int is = 0; is < 2; ++is)
 #pragma unroll
-                for (int ct = 0; ct < ORN_FCT; ++ct) {
+                for (int ct = 0; ct < ORN_FDN; ++ct) {
                     const int l0 = 16 * is + 4 * g;
                     qa[hn][is][ct][0] = *reinterpret_cast<const uint32_t *>(blk[ct] + 64 * hn + l0);
                     qa[hn][is][ct][1] = *reinterpret_cast<const uint32_t *>(blk[ct] + 64 * hn + 32 + l0);
@@ -353,9 +355,9 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
             for (int is = 0; is < 2; ++is) {
                 const int l0 = 16 * is + 4 * g;  // this lane's 4 positions l0 .. l0+3
-                uint32_t q0[ORN_FCT], q1[ORN_FCT], qh[ORN_FCT];
+                uint32_t q0[ORN_FDN], q1[ORN_FDN], qh[ORN_FDN];
 #pragma unroll
-                for (int ct = 0; ct < ORN_FCT; ++ct) {
+                for (int ct = 0; ct < ORN_FDN; ++ct) {
                     q0[ct] = qa[hn][is][ct][0];
                     q1[ct] = qa[hn][is][ct][1];
                     qh[ct] = qa[hn][is][ct][2];
@@ -367,7 +369,7 @@ __global__ void __launch_bounds__(256)
                     const v4h xb = *reinterpret_cast<const v4h *>(&As[1][c][kl]);
                     const int sb = 8 * hn + 2 * Q + is;  // sub-block scale index
 #pragma unroll
-                    for (int ct = 0; ct < ORN_FCT; ++ct) {
+                    for (int ct = 0; ct < ORN_FDN; ++ct) {
                         const uint32_t ql = (Q & 1) ? q1[ct] : q0[ct];
                         // bytes 0..63: low 4 bits from ql, high 2 from qh
                         const uint32_t qv = ((ql >> (4 * (Q >> 1))) & 0x0F0F0F0Fu) |
@@ -392,7 +394,7 @@ __global__ void __launch_bounds__(256)
     }
     float *out = dn + ((size_t)kslice * rows_max + itm.y) * (size_t)D + n0;
 #pragma unroll
-    for (int ct = 0; ct < ORN_FCT; ++ct)
+    for (int ct = 0; ct < ORN_FDN; ++ct)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int row = 4 * g + r;
@@ -445,7 +447,8 @@ extern "C" int ornk_file_down(const ornk_moe_args *a, hipStream_t s)
 {
     if (!ornk_file_supported(a->D, a->H) || (a->H / 256) % a->ks_dn) return hipErrorInvalidValue;
     const ornk_file_ws &f = a->fw;
-    const dim3 grid(a->items_max * (a->D / 256) * a->ks_dn);
+    if (a->D % (64 * ORN_FDN)) return hipErrorInvalidValue;
+    const dim3 grid(a->items_max * (a->D / (64 * ORN_FDN)) * a->ks_dn);
     ORN_LAUNCH_EV(a, k_dn_file, grid, dim3(256), 0, s, a->down_body, a->down_d, f.mh, f.ml,
                   f.minv, a->ctl, reinterpret_cast<const int4 *>(a->items), a->dn_part, a->D,
                   a->H, a->ks_dn, a->rows_max);
