@@ -185,6 +185,24 @@ int gpu_moe_forward(gpu_context *ctx, ornith_moe_store *store, int layer, const 
                     int n_tokens, const gpu_buffer *resid, gpu_buffer *out, gpu_buffer *idx_out,
                     gpu_buffer *w_out, const ornith_moe_opts *opts);
 
+/* gpu_moe_forward that allocates nothing.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops or harnesses that forbid hipMalloc).  Same
+ * arguments and results as gpu_moe_forward; the forward's work buffers
+ * live in a fixed per-device scratch array of ORN_NOALLOC_SCRATCH_BYTES
+ * (32 MiB: decode batches up to 64 tokens at the Ornith shape D=2048,
+ * H=512, E=256, k=8), which each GPU the library runs on holds until the
+ * process ends.  A call whose work buffers would not fit returns ORN_EINVAL
+ * with the needed size in gpu_last_error(); ORN_MOE_GRAPH is refused
+ * (instantiating a graph allocates).  Every call on one GPU shares that
+ * GPU's scratch: calls that overlap on one GPU (two contexts, or
+ * ORN_MOE_ASYNC calls on different streams) race. */
+#define ORN_NOALLOC_SCRATCH_BYTES (32u << 20)
+int gpu_moe_forward_noalloc(gpu_context *ctx, ornith_moe_store *store, int layer,
+                            const gpu_buffer *x, int n_tokens, const gpu_buffer *resid,
+                            gpu_buffer *out, gpu_buffer *idx_out, gpu_buffer *w_out,
+                            const ornith_moe_opts *opts);
+
 /* Layer stack: for l in [first, first+n): x <- x + MoE_l(rmsnorm(x)) (the
  * per-layer MoE residual structure of model.c:992-1144).  tmp must hold
  * n_tokens*D floats.  Every expert is computed (opts' expert share is not

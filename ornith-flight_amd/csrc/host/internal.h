@@ -40,6 +40,9 @@ struct gpu_context {
     size_t used_memory;
     char err[256];
     orn_workspace ws;
+    /* this device's fixed scratch, resolved by the first
+     * gpu_moe_forward_noalloc call on the context (NULL until then) */
+    void *scratch;
     /* device counters read back after a forward */
     int *ctl_host; /* pinned mirror of the last forward's counters */
     int *last_ctl; /* device counters of the last forward (inside the workspace) */

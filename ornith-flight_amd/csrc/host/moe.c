@@ -753,9 +753,12 @@ static int launch_k(gpu_context *ctx, const char *name,
     return ORN_OK;
 }
 
+/* fixed_ws: NULL = the context's grow-only workspace; else the device's
+ * fixed scratch of ORNK_SCRATCH_BYTES (gpu_moe_forward_noalloc), and the
+ * call then allocates nothing. */
 static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, const float *x,
                            int T, const float *resid, float *out, uint32_t *idx_out, float *w_out,
-                           const ornith_moe_opts *opts)
+                           const ornith_moe_opts *opts, void *fixed_ws)
 {
     const ornith_moe_shape *sh = &st->sh;
     const int D = sh->d_model, H = sh->hidden, E = sh->n_experts, k = sh->top_k;
@@ -818,8 +821,18 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     CARVE(o_fml, file ? (size_t)p.rows_max * H * 2 : 0);
     CARVE(o_fminv, file ? (size_t)p.rows_max * 4 : 0);
 #undef CARVE
-    uint8_t *ws = (uint8_t *)orn_ws_get(ctx, off);
-    if (!ws) return ORN_ENOMEM;
+    uint8_t *ws;
+    if (fixed_ws) {
+        if (off > ORNK_SCRATCH_BYTES)
+            return orn_set_err(ctx, ORN_EINVAL,
+                               "gpu_moe_forward_noalloc: %d tokens need %zu bytes of work "
+                               "buffers; the fixed scratch holds %u",
+                               T, off, (unsigned)ORNK_SCRATCH_BYTES);
+        ws = (uint8_t *)fixed_ws;
+    } else {
+        ws = (uint8_t *)orn_ws_get(ctx, off);
+        if (!ws) return ORN_ENOMEM;
+    }
 
     const size_t E1nb = (size_t)E1 * st->blocks_per_matrix;
     ornk_moe_args a;
@@ -1012,7 +1025,29 @@ static int fwd_body(gpu_context *ctx, ornith_moe_store *st, const void *p)
 {
     const fwd_arg *a = (const fwd_arg *)p;
     return moe_forward_dev(ctx, st, a->layer, a->x, a->T, a->resid, a->out, a->idx, a->w,
-                           &a->opts);
+                           &a->opts, NULL);
+}
+
+/* Argument checks shared by the forward entry points (1: run, 0: nothing to
+ * do, negative: error). */
+static int forward_args_ok(gpu_context *ctx, const ornith_moe_store *st, int layer,
+                           const gpu_buffer *x, int n_tokens, const gpu_buffer *resid,
+                           const gpu_buffer *out, const gpu_buffer *idx_out,
+                           const gpu_buffer *w_out, const char *who)
+{
+    if (!st || !x || !out || n_tokens < 0)
+        return orn_set_err(ctx, ORN_EINVAL, "%s: NULL argument or negative T", who);
+    if (layer < 0 || layer >= st->sh.n_layers)
+        return orn_set_err(ctx, ORN_EINVAL, "%s: bad layer", who);
+    if (n_tokens == 0) return 0;
+    const size_t act = (size_t)n_tokens * st->sh.d_model * 4;
+    const size_t sel = (size_t)n_tokens * st->sh.top_k * 4;
+    if (!check_buf(x, act) || !check_buf(out, act) || (resid && !check_buf(resid, act)) ||
+        (idx_out && !check_buf(idx_out, sel)) || (w_out && !check_buf(w_out, sel)))
+        return orn_set_err(ctx, ORN_EINVAL, "%s: buffer too small", who);
+    if (out == x || out == resid)
+        return orn_set_err(ctx, ORN_EINVAL, "%s: out aliases an input", who);
+    return 1;
 }
 
 int gpu_moe_forward(gpu_context *ctx, ornith_moe_store *st, int layer, const gpu_buffer *x,
@@ -1020,18 +1055,9 @@ int gpu_moe_forward(gpu_context *ctx, ornith_moe_store *st, int layer, const gpu
                     gpu_buffer *w_out, const ornith_moe_opts *opts)
 {
     if (!ctx) return ORN_EINVAL;
-    if (!st || !x || !out || n_tokens < 0)
-        return orn_set_err(ctx, ORN_EINVAL, "gpu_moe_forward: NULL argument or negative T");
-    if (layer < 0 || layer >= st->sh.n_layers)
-        return orn_set_err(ctx, ORN_EINVAL, "gpu_moe_forward: bad layer");
-    if (n_tokens == 0) return ORN_OK;
-    const size_t act = (size_t)n_tokens * st->sh.d_model * 4;
-    const size_t sel = (size_t)n_tokens * st->sh.top_k * 4;
-    if (!check_buf(x, act) || !check_buf(out, act) || (resid && !check_buf(resid, act)) ||
-        (idx_out && !check_buf(idx_out, sel)) || (w_out && !check_buf(w_out, sel)))
-        return orn_set_err(ctx, ORN_EINVAL, "gpu_moe_forward: buffer too small");
-    if (out == x || out == resid)
-        return orn_set_err(ctx, ORN_EINVAL, "gpu_moe_forward: out aliases an input");
+    const int ok = forward_args_ok(ctx, st, layer, x, n_tokens, resid, out, idx_out, w_out,
+                                   "gpu_moe_forward");
+    if (ok <= 0) return ok;
     const unsigned flags = opts ? opts->flags : 0u;
     fwd_arg a = {layer,
                  n_tokens,
@@ -1059,6 +1085,40 @@ int gpu_moe_forward(gpu_context *ctx, ornith_moe_store *st, int layer, const gpu
     return run_body(ctx, st, &key, fwd_body, &a, !(flags & ORN_MOE_ASYNC));
 }
 
+/* gpu_moe_forward with the work buffers in the device's fixed scratch: no
+ * hipMalloc, hipFree, graph instantiation or other allocating call. */
+int gpu_moe_forward_noalloc(gpu_context *ctx, ornith_moe_store *st, int layer,
+                            const gpu_buffer *x, int n_tokens, const gpu_buffer *resid,
+                            gpu_buffer *out, gpu_buffer *idx_out, gpu_buffer *w_out,
+                            const ornith_moe_opts *opts)
+{
+    if (!ctx) return ORN_EINVAL;
+    const int ok = forward_args_ok(ctx, st, layer, x, n_tokens, resid, out, idx_out, w_out,
+                                   "gpu_moe_forward_noalloc");
+    if (ok <= 0) return ok;
+    if (!ctx->scratch) {
+        /* first call on this context: this device's address of the scratch
+         * array (looked up once per device, with the device current) */
+        hipError_t e = hipSetDevice(ctx->device);
+        if (e == hipSuccess) e = (hipError_t)ornk_scratch_resolve(ctx->device, &ctx->scratch);
+        if (e != hipSuccess) {
+            ctx->scratch = NULL;
+            return orn_set_err(ctx, ORN_EUNSUPPORTED,
+                               "gpu_moe_forward_noalloc: device scratch lookup failed: %s",
+                               hipGetErrorString(e));
+        }
+    }
+    const unsigned flags = opts ? opts->flags : 0u;
+    if (flags & ORN_MOE_GRAPH)
+        return orn_set_err(ctx, ORN_EINVAL,
+                           "gpu_moe_forward_noalloc: ORN_MOE_GRAPH (graph instantiation "
+                           "allocates)");
+    return moe_forward_dev(ctx, st, layer, (const float *)x->dev, n_tokens,
+                           resid ? (const float *)resid->dev : NULL, (float *)out->dev,
+                           idx_out ? (uint32_t *)idx_out->dev : NULL,
+                           w_out ? (float *)w_out->dev : NULL, opts, ctx->scratch);
+}
+
 typedef struct {
     int first, n, T;
     float *x, *tmp;
@@ -1074,7 +1134,8 @@ static int stack_body(gpu_context *ctx, ornith_moe_store *st, const void *p)
     float *cur = a->x;
     for (int l = 0; l < a->n; ++l) {
         float *dst = (l == a->n - 1) ? a->x : (cur == a->x ? a->tmp : a->x);
-        int rc = moe_forward_dev(ctx, st, a->first + l, cur, a->T, cur, dst, NULL, NULL, &a->opts);
+        int rc = moe_forward_dev(ctx, st, a->first + l, cur, a->T, cur, dst, NULL, NULL, &a->opts,
+                                 NULL);
         if (rc) return rc;
         cur = dst;
     }

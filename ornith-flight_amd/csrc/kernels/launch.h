@@ -30,6 +30,14 @@ int ornk_silu(float *out, const float *x, int n, hipStream_t s);
 int ornk_silu_mul(float *out, const float *g, const float *u, int n, hipStream_t s);
 int ornk_add(float *out, const float *a, const float *b, int n, hipStream_t s);
 
+/* ---- fixed scratch of the forward that allocates nothing (scratch.hip) ---- */
+/* Size of the per-device scratch array; equals ORN_NOALLOC_SCRATCH_BYTES of
+ * ornith_hip.h. */
+#define ORNK_SCRATCH_BYTES (32u << 20)
+/* Device address of the scratch array on `device`, which must be the current
+ * device; resolved once per device (hipGetSymbolAddress) and cached. */
+int ornk_scratch_resolve(int device, void **addr);
+
 /* ---- GGUF dequant (gguf.c:605-711 semantics) ----------------------------- */
 int ornk_dequant(const void *src, int type, uint64_t n_elems, float *dst, hipStream_t s);
 int ornk_dequant_slice(const void *src, int type, uint64_t n_elems, uint64_t n_experts,

@@ -37,7 +37,8 @@ EXPORTED = [
     "gpu_dequantize_tensor_buf", "gpu_dequantize_expert_slice_buf",
     "gpu_moe_store_create", "gpu_moe_store_destroy", "gpu_moe_store_bytes",
     "gpu_moe_store_set_experts", "gpu_moe_store_set_router", "gpu_moe_store_set_norm",
-    "gpu_moe_store_fill_synthetic", "gpu_moe_forward", "gpu_moe_forward_stack",
+    "gpu_moe_store_fill_synthetic", "gpu_moe_forward", "gpu_moe_forward_noalloc",
+    "gpu_moe_forward_stack",
     "gpu_moe_last_stats", "gpu_probe_read_bandwidth",
     "gpu_profile_enable", "gpu_profile_reset", "gpu_profile_count", "gpu_profile_name",
     "gpu_profile_total_ms", "gpu_profile_calls",
@@ -110,6 +111,7 @@ def lib():
         "gpu_moe_store_set_norm": (i, [vp, vp, i, vp]),
         "gpu_moe_store_fill_synthetic": (i, [vp, vp, i, u64, f]),
         "gpu_moe_forward": (i, [vp, vp, i, vp, i, vp, vp, vp, vp, C.POINTER(MoEOpts)]),
+        "gpu_moe_forward_noalloc": (i, [vp, vp, i, vp, i, vp, vp, vp, vp, C.POINTER(MoEOpts)]),
         "gpu_moe_forward_stack": (i, [vp, vp, i, i, vp, vp, i, C.POINTER(MoEOpts)]),
         "gpu_moe_last_stats": (i, [vp, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int)]),
         "gpu_probe_read_bandwidth": (i, [vp, sz, i, C.POINTER(C.c_double)]),
@@ -299,13 +301,15 @@ class Store:
         self.set_router(layer, syn.router, syn.bias)
 
     def forward(self, layer, x: Buffer, T, out: Buffer, resid=None, idx=None, w=None,
-                mode=ROUTE_RENORM, flags=0, ep=(0, 0)):
-        """ep = (first, count): compute only that expert-parallel share (0, 0: all)."""
+                mode=ROUTE_RENORM, flags=0, ep=(0, 0), noalloc=False):
+        """ep = (first, count): compute only that expert-parallel share (0, 0: all).
+        noalloc: call gpu_moe_forward_noalloc (work buffers in the device's
+        fixed scratch) instead of gpu_moe_forward."""
         o = MoEOpts(mode, flags, ep[0], ep[1])
-        rc = lib().gpu_moe_forward(self.ctx.ptr, self.ptr, layer, x.ptr, T,
-                                   resid.ptr if resid else None, out.ptr,
-                                   idx.ptr if idx else None, w.ptr if w else None, C.byref(o))
-        self.ctx.check(rc, "gpu_moe_forward")
+        fn = lib().gpu_moe_forward_noalloc if noalloc else lib().gpu_moe_forward
+        rc = fn(self.ctx.ptr, self.ptr, layer, x.ptr, T, resid.ptr if resid else None, out.ptr,
+                idx.ptr if idx else None, w.ptr if w else None, C.byref(o))
+        self.ctx.check(rc, "gpu_moe_forward_noalloc" if noalloc else "gpu_moe_forward")
 
     def forward_stack(self, first, n, x: Buffer, tmp: Buffer, T, mode=ROUTE_RENORM, flags=0):
         o = MoEOpts(mode, flags, 0, 0)
