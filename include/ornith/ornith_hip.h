@@ -211,6 +211,14 @@ int gpu_moe_forward_stack(gpu_context *ctx, ornith_moe_store *store, int first_l
                           int n_layers, gpu_buffer *x, gpu_buffer *tmp, int n_tokens,
                           const ornith_moe_opts *opts);
 
+/* Router logits of the last forward on this context (of the last layer,
+ * after a stack call): T x E fp32, row-major, the values the top-k selection
+ * ran on (the sums of model.c:1017-1025 plus the bias).  Copies
+ * min(max_floats, T*E) floats to the host array `out` and stores T*E in
+ * *n_floats (0 before any forward).  No reference counterpart: a test and
+ * measurement helper like gpu_moe_last_stats. */
+int gpu_moe_last_logits(gpu_context *ctx, float *out, size_t max_floats, size_t *n_floats);
+
 /* Counters of the last forward: number of active expert slots (incl. the
  * shared expert), token rows, and tokens whose top-k ran the literal
  * exchange selection (tied or non-finite logits among the top k+1). */

@@ -54,6 +54,8 @@ def lib():
         L.orc_q6k_one.argtypes = [C.c_void_p, C.c_int]
         L.orc_router_logits.restype = None
         L.orc_router_logits.argtypes = [f32p, f32p, C.c_int, C.c_int, C.c_void_p, f32p]
+        L.orc_rmsnorm.restype = None
+        L.orc_rmsnorm.argtypes = [f32p, f32p, f32p, C.c_int]
         for fn in (L.orc_topk_renorm, L.orc_topk_literal):
             fn.restype = C.c_int
             fn.argtypes = [f32p, C.c_int, C.c_int, u32p, f32p]
@@ -98,6 +100,24 @@ def router_logits(x, W, bias=None):
     out = np.zeros(E, np.float32)
     b = None if bias is None else np.ascontiguousarray(bias, np.float32)
     lib().orc_router_logits(x, W.reshape(-1), D, E, _ptr(b), out)
+    return out
+
+
+def router_logits_rows(x, W, bias=None):
+    """orc_router_logits for every row of x [T][D] -> [T][E]."""
+    x = np.ascontiguousarray(x, np.float32)
+    return np.stack([router_logits(x[t], W, bias) for t in range(x.shape[0])])
+
+
+def rmsnorm(x, w):
+    """orc_rmsnorm (gpu.c:144-156) of every row of x [T][D]."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.empty_like(x)
+    for t in range(x.shape[0]):
+        row = np.empty(x.shape[1], np.float32)
+        lib().orc_rmsnorm(row, x[t], w, x.shape[1])
+        out[t] = row
     return out
 
 

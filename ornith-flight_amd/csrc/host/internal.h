@@ -46,6 +46,8 @@ struct gpu_context {
     /* device counters read back after a forward */
     int *ctl_host; /* pinned mirror of the last forward's counters */
     int *last_ctl; /* device counters of the last forward (inside the workspace) */
+    float *last_logits; /* [last_T][last_E] router logits of the last forward */
+    int last_T, last_E;
     /* profiling */
     int prof_on;
     int prof_n_names;

@@ -28,6 +28,8 @@ typedef struct {
     orn_graph_key key;
     hipGraphExec_t exec;
     int *ctl; /* the call's device counters (for gpu_moe_last_stats) */
+    float *logits; /* and its last layer's router logits (gpu_moe_last_logits) */
+    int lT, lE;
     unsigned long long tick;
 } orn_graph;
 
@@ -84,6 +86,7 @@ void *orn_ws_get(gpu_context *ctx, size_t bytes)
     ctx->ws.base = NULL;
     ctx->ws.bytes = 0;
     ctx->last_ctl = NULL;
+    ctx->last_logits = NULL;
     size_t want = bytes + (bytes >> 3);
     if (hipMalloc(&ctx->ws.base, want) != hipSuccess) {
         orn_set_err(ctx, ORN_ENOMEM, "workspace allocation of %zu bytes failed", want);
@@ -701,10 +704,11 @@ static plan_t make_plan(const ornith_moe_shape *sh, int T, int use_mfma)
 
 /* File-orientation path: items of <= 16 rows (one MFMA row tile); the
  * reduction is split, in whole super-blocks, so that gate/up has about
- * 8192 work groups (2H/256 per item and slice) and down about 8192 (D/128):
- * at three waves per SIMD these kernels need several rounds of work groups
- * to hide their memory latency, and a wave that covers one super-block
- * uses every byte of its blocks while they are cached. */
+ * 8192 work groups (2H/256 per item and slice) and down about 8192
+ * (D / ornk_file_down_cols() per item and slice): these kernels need
+ * several rounds of work groups to hide their memory latency, and a wave
+ * that covers one super-block uses every byte of its blocks while they are
+ * cached. */
 static plan_t make_plan_file(const ornith_moe_shape *sh, int T)
 {
     plan_t p;
@@ -716,7 +720,7 @@ static plan_t make_plan_file(const ornith_moe_shape *sh, int T)
     p.items_max = max_slots + (p.rows_max + p.tchunk - 1) / p.tchunk;
     int est = max_slots + p.rows_max / p.tchunk;
     if (est < 1) est = 1;
-    const int ng = 8192 / (est * (2 * H / 256)), nd = 8192 / (est * (D / 128));
+    const int ng = 8192 / (est * (2 * H / 256)), nd = 8192 / (est * (D / ornk_file_down_cols()));
     int kg = pow2_floor(ng > 0 ? ng : 1), kd = pow2_floor(nd > 0 ? nd : 1);
     while (kg > 1 && (D / 256) % kg) kg /= 2;
     while (kd > 1 && (H / 256) % kd) kd /= 2;
@@ -921,6 +925,9 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
         if ((rc = launch_k(ctx, "moe_down_file", ornk_file_down, &a))) return rc;
         if ((rc = launch_k(ctx, "moe_combine", ornk_moe_combine, &a))) return rc;
         ctx->last_ctl = a.ctl;
+        ctx->last_logits = a.logits;
+        ctx->last_T = T;
+        ctx->last_E = E;
         if (!(flags & ORN_MOE_ASYNC))
             return orn_hip_check(ctx, hipStreamSynchronize(ctx->stream), "moe forward");
         return ORN_OK;
@@ -945,6 +952,9 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     if ((rc = launch_k(ctx, "moe_combine", ornk_moe_combine, &a))) return rc;
 
     ctx->last_ctl = a.ctl;
+    ctx->last_logits = a.logits;
+    ctx->last_T = T;
+    ctx->last_E = E;
     if (!(flags & ORN_MOE_ASYNC))
         return orn_hip_check(ctx, hipStreamSynchronize(ctx->stream), "moe forward");
     return ORN_OK;
@@ -978,6 +988,9 @@ static int run_body(gpu_context *ctx, ornith_moe_store *st, orn_graph_key *key, 
             rc = orn_hip_check(ctx, hipGraphLaunch(g->exec, ctx->stream), "graph launch");
             if (rc) return rc;
             ctx->last_ctl = g->ctl;
+            ctx->last_logits = g->logits;
+            ctx->last_T = g->lT;
+            ctx->last_E = g->lE;
         } else {
             if ((rc = body(ctx, st, arg))) return rc;
             key->ws = ctx->ws.base;
@@ -1000,6 +1013,9 @@ static int run_body(gpu_context *ctx, ornith_moe_store *st, orn_graph_key *key, 
                 slot->key = *key;
                 slot->exec = exec;
                 slot->ctl = ctx->last_ctl;
+                slot->logits = ctx->last_logits;
+                slot->lT = ctx->last_T;
+                slot->lE = ctx->last_E;
                 slot->tick = ++st->graph_tick;
             }
             if (graph) hipGraphDestroy(graph);
@@ -1169,6 +1185,22 @@ int gpu_moe_forward_stack(gpu_context *ctx, ornith_moe_store *st, int first_laye
     key.x = a.x;
     key.out = a.tmp;
     return run_body(ctx, st, &key, stack_body, &a, !(flags & ORN_MOE_ASYNC));
+}
+
+int gpu_moe_last_logits(gpu_context *ctx, float *out, size_t max_floats, size_t *n_floats)
+{
+    if (!ctx) return ORN_EINVAL;
+    const size_t n = ctx->last_logits ? (size_t)ctx->last_T * (size_t)ctx->last_E : 0;
+    if (n_floats) *n_floats = n;
+    const size_t m = n < max_floats ? n : max_floats;
+    if (m && !out) return orn_set_err(ctx, ORN_EINVAL, "gpu_moe_last_logits: NULL output");
+    if (m) {
+        int rc = orn_hip_check(ctx, hipMemcpyAsync(out, ctx->last_logits, m * sizeof(float),
+                                                   hipMemcpyDeviceToHost, ctx->stream),
+                               "logits copy");
+        if (rc) return rc;
+    }
+    return orn_hip_check(ctx, hipStreamSynchronize(ctx->stream), "logits copy");
 }
 
 int gpu_moe_last_stats(gpu_context *ctx, int *n_slots, int *n_rows, int *n_literal)

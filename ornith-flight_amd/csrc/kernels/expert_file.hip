@@ -407,6 +407,8 @@ __global__ void __launch_bounds__(256)
 // ---------------------------------------------------------------------------
 // Launchers
 // ---------------------------------------------------------------------------
+extern "C" int ornk_file_down_cols(void) { return 64 * ORN_FDN; }
+
 extern "C" int ornk_file_supported(int D, int H)
 {
     return D % 256 == 0 && H % 256 == 0 && D <= 2048 && H <= 2048;

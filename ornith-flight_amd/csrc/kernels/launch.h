@@ -153,6 +153,8 @@ int ornk_dec_supported(int kt_gu, int kt_dn);
 int ornk_moe_down_dec(const ornk_moe_args *a, hipStream_t s);
 /* out[r] = max_k |x[r][k]| (D a multiple of 4). */
 int ornk_file_supported(int D, int H);
+/* Output columns of one work group of the file-orientation down kernel. */
+int ornk_file_down_cols(void);
 int ornk_file_prep_x(const ornk_moe_args *a, hipStream_t s);
 int ornk_file_gateup(const ornk_moe_args *a, hipStream_t s);
 int ornk_file_prep_mid(const ornk_moe_args *a, hipStream_t s);

@@ -39,7 +39,7 @@ EXPORTED = [
     "gpu_moe_store_set_experts", "gpu_moe_store_set_router", "gpu_moe_store_set_norm",
     "gpu_moe_store_fill_synthetic", "gpu_moe_forward", "gpu_moe_forward_noalloc",
     "gpu_moe_forward_stack",
-    "gpu_moe_last_stats", "gpu_probe_read_bandwidth",
+    "gpu_moe_last_stats", "gpu_moe_last_logits", "gpu_probe_read_bandwidth",
     "gpu_profile_enable", "gpu_profile_reset", "gpu_profile_count", "gpu_profile_name",
     "gpu_profile_total_ms", "gpu_profile_calls",
     "orn_synth_stream", "orn_synth_q4k", "orn_synth_q6k", "orn_synth_normal",
@@ -114,6 +114,7 @@ def lib():
         "gpu_moe_forward_noalloc": (i, [vp, vp, i, vp, i, vp, vp, vp, vp, C.POINTER(MoEOpts)]),
         "gpu_moe_forward_stack": (i, [vp, vp, i, i, vp, vp, i, C.POINTER(MoEOpts)]),
         "gpu_moe_last_stats": (i, [vp, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+        "gpu_moe_last_logits": (i, [vp, vp, sz, C.POINTER(C.c_size_t)]),
         "gpu_probe_read_bandwidth": (i, [vp, sz, i, C.POINTER(C.c_double)]),
         "gpu_profile_enable": (i, [vp, i]), "gpu_profile_reset": (None, [vp]),
         "gpu_profile_count": (i, [vp]), "gpu_profile_name": (C.c_char_p, [vp, i]),
@@ -320,6 +321,15 @@ class Store:
         a, b, c = C.c_int(), C.c_int(), C.c_int()
         self.ctx.check(lib().gpu_moe_last_stats(self.ctx.ptr, C.byref(a), C.byref(b), C.byref(c)), "stats")
         return {"n_slots": a.value, "n_rows": b.value, "n_literal": c.value}
+
+    def last_logits(self, T):
+        """Router logits [T][E] of the context's last forward (gpu_moe_last_logits)."""
+        out = np.empty((T, self.E), np.float32)
+        n = C.c_size_t(0)
+        self.ctx.check(lib().gpu_moe_last_logits(self.ctx.ptr, _p(out), out.size, C.byref(n)),
+                       "last_logits")
+        assert n.value == out.size, (n.value, out.size)
+        return out
 
     def bytes(self):
         return lib().gpu_moe_store_bytes(self.ptr)

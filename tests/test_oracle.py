@@ -316,13 +316,17 @@ def np_moe_fp64(D, H, E, k, x, W, gate, up, down, sh, bias=None):
 def test_contiguous_layout_vs_fp64():
     import ornith_moe as om
     D, H, E, k, T = 256, 256, 16, 8, 6
-    syn = om.SyntheticLayer(99, 0, D, H, E)
+    # with a Zipf(1.1) router bias, so the bias term of the logits is pinned too
+    syn = om.SyntheticLayer(99, 0, D, H, E, True, 1.1)
+    assert syn.bias is not None and np.ptp(syn.bias) > 1.0
     x = om.synth_normal(99, om.synth_stream(0, om.SYN_ACT, 0), T * D, 1.0).reshape(T, D)
-    out, idx, w = O.moe_layer(D=D, H=H, E=E, k=k, x=x, router_W=syn.router, gate=syn.routed("gate"),
-                              up=syn.routed("up"), down=syn.routed("down"), sh_gate=syn.shared("gate"),
+    out, idx, w = O.moe_layer(D=D, H=H, E=E, k=k, x=x, router_W=syn.router, bias=syn.bias,
+                              gate=syn.routed("gate"), up=syn.routed("up"),
+                              down=syn.routed("down"), sh_gate=syn.shared("gate"),
                               sh_up=syn.shared("up"), sh_down=syn.shared("down"))
     ref, ridx = np_moe_fp64(D, H, E, k, x, syn.router, syn.routed("gate"), syn.routed("up"),
-                            syn.routed("down"), [syn.shared(m) for m in ("gate", "up", "down")])
+                            syn.routed("down"), [syn.shared(m) for m in ("gate", "up", "down")],
+                            bias=syn.bias.astype(np.float64))
     assert np.array_equal(idx.astype(np.int64), ridx)
     assert np.allclose(w.sum(axis=1), 1.0, atol=1e-6)
     err = np.abs(out - ref).max(axis=1) / np.abs(ref).max(axis=1)
