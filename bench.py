@@ -9,7 +9,8 @@ experts, combine); inputs are already in HBM when the timed region starts.
 
 Prints ONE JSON line (rank 0).  Also reported in "configs": the other
 BASELINE configs measured the same way (1-token decode, 2048-token prefill,
-Zipf-skewed 256 tokens; the 40-layer stack with --stack).
+Zipf-skewed 256 tokens, and the 40-layer resident stack at 1 and 16 tokens;
+--no-stack skips the stack).
 
 `roofline` is for the dominant kernel of the step: algorithmic bytes of the
 expert weights that kernel streams (active experts x bytes per expert) over
@@ -149,10 +150,16 @@ def roofline_for(kernels, stats, T, workload):
                "avg_us": round(kernels[name]["avg_us"], 2)}
     else:
         ach = amount / avg_s / 1e12
+        # the same kernel's weight bytes against HBM (both bounds are reported
+        # for matrix-core kernels: mixed batches sit between them)
+        wbytes = slots * (GU_BYTES if "gateup" in name else DN_BYTES)
+        hbm = wbytes / avg_s / 1e9
         out = {"bound": "mfma", "achieved": round(ach, 1), "peak": MFMA_F16_PEAK_TFLOPS,
                "unit": "TFLOP/s", "frac": round(ach / MFMA_F16_PEAK_TFLOPS, 4), "traffic": traffic,
                "kernel": name, "flops_per_launch": amount,
-               "avg_us": round(kernels[name]["avg_us"], 2)}
+               "avg_us": round(kernels[name]["avg_us"], 2),
+               "hbm": {"achieved": round(hbm, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                       "frac": round(hbm / HBM_PEAK_GBS, 4), "bytes_per_launch": wbytes}}
     if src:
         out["traffic_source"] = src
     return name, out
@@ -205,6 +212,54 @@ def cpu_baseline(budget_s):
                 "sample": f"16-token decode batch through the oracle restatement, {dt:.2f} s"}
 
 
+def stack_active_experts(ctx, st, n_layers, T):
+    """Active experts (incl. the shared one) of every layer of one stack
+    step, from the same layers run one call at a time (x <- x +
+    MoE_l(rmsnorm(x)), the stack's arithmetic) outside the timed region."""
+    x = om.synth_normal(1, om.synth_stream(0, om.SYN_ACT, 0), T * D, 1.0).reshape(T, D)
+    xb, ob = ctx.upload(x), ctx.alloc(x.nbytes)
+    total = 0
+    for l in range(n_layers):
+        st.forward(l, xb, T, ob, resid=xb, flags=om.MOE_NORM)
+        total += st.last_stats()["n_slots"]
+        om.lib().gpu_copy_buffer(ctx.ptr, xb.ptr, ob.ptr, x.nbytes)
+    xb.free()
+    ob.free()
+    return total
+
+
+def measure_stack(ctx, steps):
+    """40 Ornith-shape layers x 257 experts resident in
+    HBM (47 GB with the MFMA layouts, generated on the device), a step = one
+    gpu_moe_forward_stack over all 40 layers (rmsnorm, MoE, residual per
+    layer).  40 x 257 experts cannot stay in the 256 MB last-level cache
+    between steps, unlike one layer's active experts."""
+    n_layers = 40
+    st = om.Store(ctx, n_layers, D, H, E, K, True)
+    t0 = time.perf_counter()
+    for l in range(n_layers):
+        st.fill_synthetic(l, SEED + l)
+    log(f"40-layer store ({st.bytes() / 1e9:.1f} GB) filled on the device in "
+        f"{time.perf_counter() - t0:.1f} s")
+    out = {}
+    for Ts in (1, 16):
+        active = stack_active_experts(ctx, st, n_layers, Ts)
+        ms_s, kern_s, _ = measure(ctx, st, 0, Ts, max(10, steps // 10), 3, stack_layers=n_layers)
+        gbs = active * EXPERT_BYTES / (ms_s * 1e-3) / 1e9
+        out[f"stack40_t{Ts}"] = {
+            "tokens_per_s": round(Ts / (ms_s * 1e-3), 1), "ms_per_step": round(ms_s, 4),
+            "us_per_layer": round(ms_s * 1e3 / n_layers, 2),
+            "active_experts_per_step": active,
+            "expert_bytes_per_step": active * EXPERT_BYTES,
+            "hbm": {"achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(gbs / HBM_PEAK_GBS, 4)},
+            "kernels_us": {n: round(v["avg_us"], 2) for n, v in kern_s.items()},
+            "kernel_calls_per_step": {n: round(v["calls_per_step"], 1) for n, v in kern_s.items()}}
+        log(f"stack40_t{Ts}", out[f"stack40_t{Ts}"]["tokens_per_s"], "tok/s")
+    st.close()
+    return out
+
+
 # Extra configs reported beside the headline: (label, store layer, tokens).
 # Layer 1 carries a Zipf(1.1) router bias.
 EXTRA_CONFIGS = (("decode_t1", 0, 1), ("prefill_t2048", 0, 2048), ("zipf_t256", 1, 256))
@@ -219,7 +274,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="only the headline config")
     ap.add_argument("--only", choices=EXTRA_LABELS, default=None,
                     help="of the extra configs, time only this one (for a kernel trace of it)")
-    ap.add_argument("--stack", action="store_true", help="also time the 40-layer stack (21 GB)")
+    ap.add_argument("--no-stack", action="store_true",
+                    help="skip the 40-layer resident stack (BASELINE configs[2])")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -329,21 +385,8 @@ def main():
             fst.close()
         result["configs"] = extra
     store.close()
-    if args.stack:
-        st = om.Store(ctx, 40, D, H, E, K, True)
-        t0 = time.perf_counter()
-        for l in range(40):
-            st.fill_synthetic(l, SEED + l)
-        log(f"40-layer store filled in {time.perf_counter() - t0:.1f} s")
-        # 40 x 257 experts (~21 GB) cannot stay in the 256 MB last-level
-        # cache between forwards, unlike one layer's active experts.
-        for Ts in (1, 16):
-            ms_s, kern_s, st_s = measure(ctx, st, 0, Ts, 20, 3, stack_layers=40)
-            result.setdefault("configs", {})[f"stack40_t{Ts}"] = {
-                "tokens_per_s": round(Ts / (ms_s * 1e-3), 1), "ms_per_step": round(ms_s, 4),
-                "us_per_layer": round(ms_s * 1e3 / 40, 2),
-                "kernels_us": {n: round(v["avg_us"], 2) for n, v in kern_s.items()}}
-        st.close()
+    if not args.no_stack and not args.only:
+        result.setdefault("configs", {}).update(measure_stack(ctx, args.steps))
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_budget)
     ctx.close()

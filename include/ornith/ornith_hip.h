@@ -139,9 +139,17 @@ int gpu_moe_store_set_norm(gpu_context *ctx, ornith_moe_store *store, int layer,
                            const float *w);
 
 /* Fill one layer from the deterministic synthetic generator (orn_synth_*),
- * with an optional Zipf(s) router bias when zipf_s > 0. */
+ * with an optional Zipf(s) router bias when zipf_s > 0.  The blocks and the
+ * router are generated on the device (the same bytes as the host
+ * generator), so a 40-layer store fills in seconds. */
 int gpu_moe_store_fill_synthetic(gpu_context *ctx, ornith_moe_store *store, int layer,
                                  uint64_t seed, float zipf_s);
+
+/* Read back n experts of one matrix of one layer: the inverse of
+ * gpu_moe_store_set_experts (same orientation and block streams).  No
+ * reference counterpart: for checks and for saving a store. */
+int gpu_moe_store_get_experts(gpu_context *ctx, ornith_moe_store *store, int layer, int matrix,
+                              int expert_first, int n, void *blocks);
 
 enum { ORN_ROUTE_RENORM = 0, ORN_ROUTE_LITERAL = 1 };
 #define ORN_MOE_ASYNC 1u /* return without synchronising the stream */

@@ -62,6 +62,7 @@ struct ornith_moe_store {
     float *dmax;
     float *dmax_host;         /* host mirror of dmax, [L][E+1][3] */
     int *q6_scmax;            /* host [L]: largest |Q6_K sub-scale| uploaded */
+    int *dev_scmax;           /* device [1]: the same, computed by the device packer */
     size_t bytes;
     /* HIP graphs of earlier calls made with ORN_MOE_GRAPH (least recently
      * used replaced first); any upload to the store drops them all. */
@@ -278,6 +279,7 @@ static void store_free(ornith_moe_store *st)
     hipFree(st->dsc);
     hipFree(st->dd);
     hipFree(st->dmax);
+    hipFree(st->dev_scmax);
     free(st->dmax_host);
     free(st->q6_scmax);
     free(st->has_bias);
@@ -333,7 +335,8 @@ ornith_moe_store *gpu_moe_store_create(gpu_context *ctx, const ornith_moe_shape 
         }
         st->dmax_host = (float *)calloc(LE * 3, sizeof(float));
         st->q6_scmax = (int *)calloc(L, sizeof(int));
-        if (!st->dmax_host || !st->q6_scmax) {
+        if (hipMalloc((void **)&st->dev_scmax, sizeof(int)) != hipSuccess) st->dev_scmax = NULL;
+        if (!st->dmax_host || !st->q6_scmax || !st->dev_scmax) {
             store_free(st);
             return NULL;
         }
@@ -574,43 +577,156 @@ int gpu_moe_store_set_norm(gpu_context *ctx, ornith_moe_store *st, int layer, co
     return rc;
 }
 
+/* The layer's synthetic experts and router are generated on the device
+ * (synth.hip: the same bytes as the host generator orn_synth_*, written
+ * into the store's order), and with prefill_layout the MFMA layouts are
+ * built there too; only the Zipf bias (E floats) comes from the host. */
 int gpu_moe_store_fill_synthetic(gpu_context *ctx, ornith_moe_store *st, int layer, uint64_t seed,
                                  float zipf_s)
 {
     if (!ctx || !st) return ORN_EINVAL;
     if (layer < 0 || layer >= st->sh.n_layers) return orn_set_err(ctx, ORN_EINVAL, "bad layer");
+    graphs_clear(st);
     const int E = st->sh.n_experts, E1 = E + st->sh.has_shared;
+    const size_t S = (size_t)E + 1; /* slots per layer in the store */
     const size_t nb = st->blocks_per_matrix;
-    const size_t D = (size_t)st->sh.d_model;
-    uint8_t *buf = (uint8_t *)malloc(nb * ORN_Q6K_BYTES);
-    float *W = (float *)malloc(D * (size_t)E * sizeof(float));
-    float *b = (float *)malloc((size_t)E * sizeof(float));
-    if (!buf || !W || !b) {
-        free(buf);
-        free(W);
+    const size_t D = (size_t)st->sh.d_model, H = (size_t)st->sh.hidden;
+    const size_t slot0 = (size_t)layer * S;
+    hipStream_t s = ctx->stream;
+    ornk_synth_args g;
+    memset(&g, 0, sizeof g);
+    g.seed = seed;
+    g.layer = layer;
+    g.D = (int)D;
+    g.H = (int)H;
+    g.n_experts = E;
+    g.has_shared = st->sh.has_shared;
+    g.file = st->sh.file_layout;
+    g.gate = st->gate + slot0 * nb * 144;
+    g.up = st->up + slot0 * nb * 144;
+    g.down_body = st->down_body + slot0 * nb * 208;
+    g.down_d = st->down_d + slot0 * nb;
+    g.router = st->router_q + (size_t)layer * E * D;
+    int rc = orn_hip_check(ctx, (hipError_t)ornk_synth_layer(&g, s), "synthetic layer");
+    if (rc) return rc;
+    if (zipf_s > 0.0f) {
+        float *b = (float *)malloc((size_t)E * sizeof(float));
+        if (!b) return orn_set_err(ctx, ORN_ENOMEM, "host staging");
+        orn_synth_zipf_bias(seed, orn_synth_stream(layer, ORN_SYN_ZIPF, 0), E, zipf_s, b);
+        rc = orn_hip_check(ctx, hipMemcpyAsync(st->bias + (size_t)layer * E, b,
+                                               (size_t)E * sizeof(float), hipMemcpyHostToDevice, s),
+                           "upload bias");
+        hipStreamSynchronize(s);
         free(b);
+        if (rc) return rc;
+    }
+    st->has_bias[layer] = zipf_s > 0.0f ? 1 : 0;
+    if (st->sh.prefill_layout) {
+        const size_t DH = D * H;
+        ornk_pack_args pa;
+        memset(&pa, 0, sizeof pa);
+        pa.D = (int)D;
+        pa.H = (int)H;
+        pa.n_e = E1;
+        pa.gu[0] = g.gate;
+        pa.gu[1] = g.up;
+        pa.down_body = g.down_body;
+        pa.down_d = g.down_d;
+        for (int m = 0; m < 2; ++m) {
+            pa.pq[m] = (uint32_t *)((uint8_t *)st->pq[m] + slot0 * (DH / 2));
+            pa.psc[m] = (uint16_t *)((uint8_t *)st->psc[m] + slot0 * (DH / 16));
+            pa.pmn[m] = (uint16_t *)((uint8_t *)st->pmn[m] + slot0 * (DH / 16));
+            pa.pd[m] = (float *)((uint8_t *)st->pd[m] + slot0 * (DH / 64));
+            pa.pdm[m] = (float *)((uint8_t *)st->pdm[m] + slot0 * (DH / 64));
+        }
+        pa.dq = st->dq + slot0 * DH;
+        pa.dsc = (uint16_t *)((uint8_t *)st->dsc + slot0 * (DH / 8));
+        pa.dd = (float *)((uint8_t *)st->dd + slot0 * (DH / 64));
+        pa.dmax = st->dmax + slot0 * 3;
+        pa.scmax = st->dev_scmax;
+        rc = orn_hip_check(ctx, (hipError_t)ornk_pack_prefill(&pa, s), "prefill layouts");
+        if (rc) return rc;
+        /* host mirrors: the per-slot maxima (re-uploaded by later partial
+         * uploads of the layer) and the layer's largest Q6_K sub-scale */
+        int scmax = 0;
+        rc = orn_hip_check(ctx, hipMemcpyAsync(st->dmax_host + slot0 * 3, pa.dmax,
+                                               (size_t)E1 * 3 * sizeof(float),
+                                               hipMemcpyDeviceToHost, s), "dmax copy");
+        if (!rc)
+            rc = orn_hip_check(ctx, hipMemcpyAsync(&scmax, st->dev_scmax, sizeof(int),
+                                                   hipMemcpyDeviceToHost, s), "scmax copy");
+        if (!rc) rc = orn_hip_check(ctx, hipStreamSynchronize(s), "prefill layouts");
+        if (rc) return rc;
+        st->q6_scmax[layer] = scmax;
+    }
+    return orn_hip_check(ctx, hipStreamSynchronize(s), "synthetic layer");
+}
+
+/* Inverse of gpu_moe_store_set_experts: the GGUF block stream of n experts
+ * of one matrix, in the orientation set_experts takes. */
+int gpu_moe_store_get_experts(gpu_context *ctx, ornith_moe_store *st, int layer, int matrix,
+                              int expert_first, int n, void *blocks)
+{
+    if (!ctx || !st || !blocks) return ORN_EINVAL;
+    const int E1 = st->sh.n_experts + 1;
+    if (layer < 0 || layer >= st->sh.n_layers || expert_first < 0 || n < 0 ||
+        expert_first + n > E1 || matrix < 0 || matrix > 2)
+        return orn_set_err(ctx, ORN_EINVAL, "get_experts: bad layer/expert range/matrix");
+    if (n == 0) return ORN_OK;
+    const int D = st->sh.d_model, H = st->sh.hidden, file = st->sh.file_layout;
+    const size_t nb = st->blocks_per_matrix;
+    const size_t slot0 = (size_t)layer * E1 + (size_t)expert_first;
+    hipStream_t s = ctx->stream;
+    uint8_t *out = (uint8_t *)blocks;
+    int rc;
+    if (matrix != ORN_MAT_DOWN) {
+        const uint8_t *src = (matrix == ORN_MAT_GATE ? st->gate : st->up) + slot0 * nb * 144;
+        uint8_t *tmp = (uint8_t *)malloc((size_t)n * nb * 144);
+        if (!tmp) return orn_set_err(ctx, ORN_ENOMEM, "host staging");
+        rc = orn_hip_check(ctx, hipMemcpyAsync(tmp, src, (size_t)n * nb * 144,
+                                               hipMemcpyDeviceToHost, s), "download q4k");
+        if (!rc) rc = orn_hip_check(ctx, hipStreamSynchronize(s), "download q4k");
+        const int K = D, NBc = H / 256;
+        for (int i = 0; i < n && !rc; ++i) {
+            const uint8_t *t = tmp + (size_t)i * nb * 144;
+            uint8_t *o = out + (size_t)i * nb * ORN_Q4K_BYTES;
+            if (file) {
+                memcpy(o, t, nb * 144);
+                continue;
+            }
+            for (int k = 0; k < K; ++k)
+                for (int c = 0; c < NBc; ++c)
+                    memcpy(o + ((size_t)k * NBc + c) * 144, t + ((size_t)c * K + k) * 144, 144);
+        }
+        free(tmp);
+        return rc;
+    }
+    uint8_t *body = (uint8_t *)malloc((size_t)n * nb * 208);
+    uint16_t *dv = (uint16_t *)malloc((size_t)n * nb * 2);
+    if (!body || !dv) {
+        free(body);
+        free(dv);
         return orn_set_err(ctx, ORN_ENOMEM, "host staging");
     }
-    int rc = ORN_OK;
-    for (int e = 0; e < E1 && !rc; ++e) {
-        orn_synth_q4k(seed, orn_synth_stream(layer, ORN_SYN_GATE, e), 0, nb, buf);
-        rc = gpu_moe_store_set_experts(ctx, st, layer, ORN_MAT_GATE, e, 1, buf);
-        if (rc) break;
-        orn_synth_q4k(seed, orn_synth_stream(layer, ORN_SYN_UP, e), 0, nb, buf);
-        rc = gpu_moe_store_set_experts(ctx, st, layer, ORN_MAT_UP, e, 1, buf);
-        if (rc) break;
-        orn_synth_q6k(seed, orn_synth_stream(layer, ORN_SYN_DOWN, e), 0, nb, buf);
-        rc = gpu_moe_store_set_experts(ctx, st, layer, ORN_MAT_DOWN, e, 1, buf);
-    }
-    if (!rc) {
-        orn_synth_normal(seed, orn_synth_stream(layer, ORN_SYN_ROUTER, 0), D * (size_t)E, 0.02f, W);
-        if (zipf_s > 0.0f)
-            orn_synth_zipf_bias(seed, orn_synth_stream(layer, ORN_SYN_ZIPF, 0), E, zipf_s, b);
-        rc = gpu_moe_store_set_router(ctx, st, layer, W, zipf_s > 0.0f ? b : NULL);
-    }
-    free(buf);
-    free(W);
-    free(b);
+    rc = orn_hip_check(ctx, hipMemcpyAsync(body, st->down_body + slot0 * nb * 208,
+                                           (size_t)n * nb * 208, hipMemcpyDeviceToHost, s),
+                       "download q6k");
+    if (!rc)
+        rc = orn_hip_check(ctx, hipMemcpyAsync(dv, st->down_d + slot0 * nb, (size_t)n * nb * 2,
+                                               hipMemcpyDeviceToHost, s), "download q6k d");
+    if (!rc) rc = orn_hip_check(ctx, hipStreamSynchronize(s), "download q6k");
+    const int K = file ? (int)nb : H, NBc = file ? 1 : D / 256;
+    for (int i = 0; i < n && !rc; ++i)
+        for (int k = 0; k < K; ++k)
+            for (int c = 0; c < NBc; ++c) {
+                const size_t q = (size_t)i * nb + (size_t)c * K + k;
+                uint8_t *o = out + ((size_t)i * nb + (size_t)k * NBc + c) * ORN_Q6K_BYTES;
+                memcpy(o, body + q * 208, 208);
+                o[ORN_Q6K_OFF_D] = (uint8_t)dv[q];
+                o[ORN_Q6K_OFF_D + 1] = (uint8_t)(dv[q] >> 8);
+            }
+    free(body);
+    free(dv);
     return rc;
 }
 
@@ -914,7 +1030,11 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     }
 
     int rc;
-    if ((rc = launch(ctx, "moe_norm", ornk_moe_norm, &a))) return rc;
+    /* A separate norm kernel runs only where the router does not fuse the
+     * norm (profiled only then, so that every recorded step is a kernel). */
+    if (a.apply_norm && !ornk_router_pc_supported(T, D) &&
+        (rc = launch(ctx, "moe_norm", ornk_moe_norm, &a)))
+        return rc;
     if ((rc = launch_k(ctx, "moe_route", ornk_moe_route, &a))) return rc;
     if ((rc = launch_k(ctx, "moe_dispatch", ornk_moe_dispatch, &a))) return rc;
     if (file) {

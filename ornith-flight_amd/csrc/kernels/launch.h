@@ -38,6 +38,38 @@ int ornk_add(float *out, const float *a, const float *b, int n, hipStream_t s);
  * device; resolved once per device (hipGetSymbolAddress) and cached. */
 int ornk_scratch_resolve(int device, void **addr);
 
+/* ---- synthetic layers generated on the device (synth.hip) ------------------
+ * The same bytes as the host generator (synth.c), written into one layer's
+ * resident arrays: gate/up Q4_K blocks, down Q6_K bodies + d (store order:
+ * vec@mat block-column-major, or file order when file = 1) and the router in
+ * the [D/4][E][4] layout. */
+typedef struct {
+    uint64_t seed;
+    int layer, D, H, n_experts, has_shared, file;
+    uint8_t *gate, *up, *down_body;
+    uint16_t *down_d;
+    float *router;
+} ornk_synth_args;
+int ornk_synth_layer(const ornk_synth_args *a, hipStream_t s);
+
+/* MFMA (prefill) layouts of n_e expert slots built from their resident
+ * vec@mat blocks (prefill_pack.c arithmetic); dmax [n_e][3] and *scmax
+ * (largest |Q6_K sub-scale|) are recomputed. */
+typedef struct {
+    int D, H, n_e;
+    const uint8_t *gu[2], *down_body;
+    const uint16_t *down_d;
+    uint32_t *pq[2];
+    uint16_t *psc[2], *pmn[2];
+    float *pd[2], *pdm[2];
+    uint8_t *dq;
+    uint16_t *dsc;
+    float *dd;
+    float *dmax;
+    int *scmax;
+} ornk_pack_args;
+int ornk_pack_prefill(const ornk_pack_args *a, hipStream_t s);
+
 /* ---- GGUF dequant (gguf.c:605-711 semantics) ----------------------------- */
 int ornk_dequant(const void *src, int type, uint64_t n_elems, float *dst, hipStream_t s);
 int ornk_dequant_slice(const void *src, int type, uint64_t n_elems, uint64_t n_experts,

@@ -36,7 +36,8 @@ EXPORTED = [
     "gpu_dequantize_tensor_from_buf", "gpu_dequantize_expert_slice_from_buf",
     "gpu_dequantize_tensor_buf", "gpu_dequantize_expert_slice_buf",
     "gpu_moe_store_create", "gpu_moe_store_destroy", "gpu_moe_store_bytes",
-    "gpu_moe_store_set_experts", "gpu_moe_store_set_router", "gpu_moe_store_set_norm",
+    "gpu_moe_store_set_experts", "gpu_moe_store_get_experts", "gpu_moe_store_set_router",
+    "gpu_moe_store_set_norm",
     "gpu_moe_store_fill_synthetic", "gpu_moe_forward", "gpu_moe_forward_noalloc",
     "gpu_moe_forward_stack",
     "gpu_moe_last_stats", "gpu_moe_last_logits", "gpu_probe_read_bandwidth",
@@ -107,6 +108,7 @@ def lib():
         "gpu_moe_store_create": (vp, [vp, C.POINTER(MoEShape)]),
         "gpu_moe_store_destroy": (None, [vp, vp]), "gpu_moe_store_bytes": (sz, [vp]),
         "gpu_moe_store_set_experts": (i, [vp, vp, i, i, i, i, vp]),
+        "gpu_moe_store_get_experts": (i, [vp, vp, i, i, i, i, vp]),
         "gpu_moe_store_set_router": (i, [vp, vp, i, vp, vp]),
         "gpu_moe_store_set_norm": (i, [vp, vp, i, vp]),
         "gpu_moe_store_fill_synthetic": (i, [vp, vp, i, u64, f]),
@@ -278,6 +280,14 @@ class Store:
         b = np.ascontiguousarray(blocks, np.uint8)
         self.ctx.check(lib().gpu_moe_store_set_experts(self.ctx.ptr, self.ptr, layer, matrix, first, n, _p(b)),
                        "set_experts")
+
+    def get_experts(self, layer, matrix, first, n):
+        """The block streams of n experts (inverse of set_experts)."""
+        nb = self.D * self.H // 256
+        out = np.empty(n * nb * (Q6K_BYTES if matrix == MAT_DOWN else Q4K_BYTES), np.uint8)
+        self.ctx.check(lib().gpu_moe_store_get_experts(self.ctx.ptr, self.ptr, layer, matrix, first,
+                                                       n, _p(out)), "get_experts")
+        return out
 
     def set_router(self, layer, W, bias=None):
         W = np.ascontiguousarray(W, np.float32)
