@@ -256,12 +256,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
 // dn[kslice][row][n].  Same structure (activation = mid row, hi/lo of
 // mid*s*d).
 //
-// KSG > 0 (one token: every item is one row): the work group forms its
-// slice of the mid row itself from the KSG gate/up split-K partials, with
-// the mid step's arithmetic (fixed-order sum from 0, clamped SiLU for
-// routed rows, model.c:1087-1088, plain for the shared expert's,
-// gpu.c:176-186), and scales the activation tile by the slice's own
-// max |mid|; the separate mid launch is skipped.
+// KSG > 0: the work group forms its rows' slice of mid itself from the KSG
+// gate/up split-K partials, with the mid step's arithmetic (fixed-order sum
+// from 0, clamped SiLU for routed rows, model.c:1087-1088, plain for the
+// shared expert's, gpu.c:176-186), and scales each row's activation tile by
+// that row's max |mid| over the slice (a power of two either way: only the
+// hi/lo split point moves); the separate mid launch is skipped.
 // ---------------------------------------------------------------------------
 struct DnRing {
     uint4 q0, q1, sc[4];
@@ -279,8 +279,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
     constexpr int KV = 32 * KT;  // reduction values of the slice
     __shared__ __align__(16) uint32_t As[NBUF][KC][2][16 * ORN_AST / 2];
     __shared__ float s_inv[16];
-    __shared__ __align__(16) float Ms[KSG ? KV : 4];  // the slice of the mid row (KSG > 0)
-    __shared__ float red[4];
+    __shared__ __align__(16) float Ms[KSG ? 16 : 1][KSG ? KV : 4];  // the rows' mid slices
+    __shared__ unsigned int s_amax[16];
 
     const int NBD = D >> 8;
     const int per_item = NBD * ks;
@@ -321,38 +321,43 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
     float amax;
     if (KSG) {
         const size_t sstr = (size_t)rows_max * 2 * H;  // between gate/up slices
-        const float *pg = gu + (size_t)itm.y * 2 * H + 32 * kt0;
-        float lmax = 0.0f;
-        for (int h = tid; h < KV; h += 256) {
-            float gv[KSG > 0 ? KSG : 1], uv[KSG > 0 ? KSG : 1];
-#pragma unroll
-            for (int sl = 0; sl < KSG; ++sl) {
-                gv[sl] = pg[sl * sstr + h];
-                uv[sl] = pg[sl * sstr + H + h];
-            }
-            float g = 0.0f, u = 0.0f;
-#pragma unroll
-            for (int sl = 0; sl < KSG; ++sl) {
-                g = g + gv[sl];
-                u = u + uv[sl];
-            }
-            float act;
-            if (itm.y < shared_rows) {
-                act = g / (1.0f + expf(-g));
-            } else {
-                if (g < -50.0f) act = 0.0f;
-                else if (g > 50.0f) act = g;
-                else act = g / (1.0f + expf(-g));
-            }
-            const float v = act * u;
-            Ms[h] = v;
-            lmax = fmaxf(lmax, fabsf(v));
-        }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) lmax = fmaxf(lmax, __shfl_xor(lmax, off, 64));
-        if (lane == 0) red[wave] = lmax;
+        if (tid < 16) s_amax[tid] = 0u;
         __syncthreads();
-        amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        for (int r = 0; r < nrows; ++r) {  // uniform
+            const float *pg = gu + (size_t)(itm.y + r) * 2 * H + 32 * kt0;
+            float lmax = 0.0f;
+            for (int h = tid; h < KV; h += 256) {
+                float gv[KSG > 0 ? KSG : 1], uv[KSG > 0 ? KSG : 1];
+#pragma unroll
+                for (int sl = 0; sl < KSG; ++sl) {
+                    gv[sl] = pg[sl * sstr + h];
+                    uv[sl] = pg[sl * sstr + H + h];
+                }
+                float g = 0.0f, u = 0.0f;
+#pragma unroll
+                for (int sl = 0; sl < KSG; ++sl) {
+                    g = g + gv[sl];
+                    u = u + uv[sl];
+                }
+                float act;
+                if (itm.y + r < shared_rows) {
+                    act = g / (1.0f + expf(-g));
+                } else {
+                    if (g < -50.0f) act = 0.0f;
+                    else if (g > 50.0f) act = g;
+                    else act = g / (1.0f + expf(-g));
+                }
+                const float v = act * u;
+                Ms[r][h] = v;
+                lmax = fmaxf(lmax, fabsf(v));
+            }
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) lmax = fmaxf(lmax, __shfl_xor(lmax, off, 64));
+            // non-negative floats order like their bit patterns
+            if (lane == 0) atomicMax(&s_amax[r], __float_as_uint(lmax));
+        }
+        __syncthreads();
+        amax = __uint_as_float(s_amax[arow]);
     } else {
         amax = mid_amax[itm.y + arow];
     }
@@ -367,7 +372,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
         if (!rows_live) return;
 #pragma unroll
         for (int i = 0; i < LC / 4; ++i) {
-            xv[i] = KSG ? *reinterpret_cast<const v4f *>(&Ms[32 * KC * ch + seg * LC + 4 * i])
+            xv[i] = KSG ? *reinterpret_cast<const v4f *>(&Ms[KSG ? arow : 0][32 * KC * ch + seg * LC + 4 * i])
                         : *reinterpret_cast<const v4f *>(xr + 32 * KC * ch + 4 * i);
             dv[i] = *reinterpret_cast<const v4f *>(dr + 32 * KC * ch + 4 * i);
         }
@@ -495,11 +500,12 @@ extern "C" int ornk_moe_gateup_dec(const ornk_moe_args *a, hipStream_t s)
     return hipGetLastError();
 }
 
-// One token with 16 gate/up slices and 8-step down slices: the down kernel
-// forms mid itself (the instance compiled for that plan).
+// Decode plans with 4, 8 or 16 gate/up slices and 8-step down slices: the
+// down kernel forms mid itself (the instances compiled for those plans).
 extern "C" int ornk_down_dec_fuses_mid(int T, int H, int ks_gu, int ks_dn)
 {
-    return T == 1 && ks_gu == 16 && ks_dn >= 1 && H % (32 * ks_dn) == 0 && H / 32 / ks_dn == 8;
+    return T >= 1 && (ks_gu == 4 || ks_gu == 8 || ks_gu == 16) && ks_dn >= 1 &&
+           H % (32 * ks_dn) == 0 && H / 32 / ks_dn == 8;
 }
 
 extern "C" int ornk_moe_down_dec(const ornk_moe_args *a, hipStream_t s)
@@ -512,9 +518,16 @@ extern "C" int ornk_moe_down_dec(const ornk_moe_args *a, hipStream_t s)
     const dim3 grid(a->items_max * (a->D / 256) * ks);
     const int shared_rows = a->has_shared ? a->T : 0;
     if (ornk_down_dec_fuses_mid(a->T, a->H, a->ks_gu, ks)) {
-        ORN_LAUNCH_EV(a, (k_down_dec<ORN_DEC_NR, 8, 4, 16>), grid, dim3(256), 0, s, a->dn_pf,
-                           a->mid, a->mid_amax, a->ctl, reinterpret_cast<const int4 *>(a->items),
-                           a->dn_part, a->D, a->H, ks, a->rows_max, a->gu_part, shared_rows);
+#define ORN_DN_MID(KSG)                                                                         \
+    ORN_LAUNCH_EV(a, (k_down_dec<ORN_DEC_NR, 8, 4, KSG>), grid, dim3(256), 0, s, a->dn_pf,      \
+                  a->mid, a->mid_amax, a->ctl, reinterpret_cast<const int4 *>(a->items),         \
+                  a->dn_part, a->D, a->H, ks, a->rows_max, a->gu_part, shared_rows)
+        switch (a->ks_gu) {
+        case 4: ORN_DN_MID(4); break;
+        case 8: ORN_DN_MID(8); break;
+        default: ORN_DN_MID(16); break;
+        }
+#undef ORN_DN_MID
         return hipGetLastError();
     }
 #define ORN_DN_DEC(K)                                                                          \
