@@ -83,6 +83,87 @@ bool gpu_dequantize_expert_slice_buf(gpu_context *ctx, const gpu_buffer *data,
                                      gpu_buffer *output);
 
 /* ---------------------------------------------------------------------------
+ * GGUF container reader — the API of engine/src/gguf.h:67-108 (parse
+ * gguf.c:289-404, open/close/accessors 408-487, tensor data 489-506, pread
+ * reads 575-601) under orn_gguf_* names, so a model file goes to the device
+ * without the engine's parser.  Same arguments, results and NULL/0/false
+ * failures; gguf_open's err_buf gets the reason.  On files the reference
+ * misparses (n_dims > 4, an alignment that is not a power of two, nested
+ * arrays with elements, lengths past the end of the file) this reader
+ * fails cleanly or, for nested arrays, skips them whole.
+ * ------------------------------------------------------------------------- */
+typedef struct orn_gguf orn_gguf;
+
+/* Layout-compatible with gguf_metadata_value (gguf.h:44-66); `type` and
+ * `elem_type` are gguf_value_type (0 uint8 .. 12 float64; 8 string, 9 array).
+ * string.data is not NUL-terminated; array.data points at the raw elements
+ * (for string arrays, at the first (u64 length, bytes) record).  Both stay
+ * valid until orn_gguf_close. */
+typedef struct {
+    int type;
+    union {
+        uint8_t uint8;
+        int8_t int8;
+        uint16_t uint16;
+        int16_t int16;
+        uint32_t uint32;
+        int32_t int32;
+        uint64_t uint64;
+        int64_t int64;
+        float float32;
+        double float64;
+        bool boolean;
+        struct {
+            const char *data;
+            size_t len;
+        } string;
+        struct {
+            int elem_type;
+            size_t count;
+            const void *data;
+        } array;
+    } value;
+} orn_gguf_value;
+
+orn_gguf *orn_gguf_open(const char *path, char *err_buf, size_t err_buf_size); /* gguf.h:70 */
+void orn_gguf_close(orn_gguf *g);                                                /* gguf.h:71 */
+uint32_t orn_gguf_version(const orn_gguf *g);                                    /* gguf.h:73 */
+uint64_t orn_gguf_tensor_count(const orn_gguf *g);                               /* gguf.h:74 */
+uint64_t orn_gguf_metadata_count(const orn_gguf *g);                             /* gguf.h:75 */
+const char *orn_gguf_architecture(const orn_gguf *g);                            /* gguf.h:77 */
+size_t orn_gguf_alignment(const orn_gguf *g);                                    /* gguf.h:78 */
+/* File offset of the data section (no reference accessor; gguf.c:375). */
+size_t orn_gguf_data_offset(const orn_gguf *g);
+bool orn_gguf_find_metadata(const orn_gguf *g, const char *key,
+                            orn_gguf_value *out); /* gguf.h:80-81 */
+const orn_tensor_info *orn_gguf_find_tensor(const orn_gguf *g, const char *name); /* gguf.h:83 */
+uint64_t orn_gguf_list_tensors(const orn_gguf *g, const orn_tensor_info **tensors,
+                               uint64_t max_count); /* gguf.h:84-86, sorted by name */
+/* Address of a tensor's bytes in a read-only mapping of the file
+ * (gguf.h:87-89); NULL if the mapping failed or the tensor runs past the
+ * end of the file. */
+const void *orn_gguf_tensor_data(const orn_gguf *g, const char *name);
+const void *orn_gguf_tensor_data_from_info(const orn_gguf *g, const orn_tensor_info *info);
+/* pread of a whole tensor (buffer_size >= size_bytes) or of the byte range
+ * [byte_offset, byte_offset + n) of one; bytes read, 0 on failure
+ * (gguf.h:96-108). */
+size_t orn_gguf_read_tensor_data(const orn_gguf *g, const orn_tensor_info *tensor, void *buffer,
+                                 size_t buffer_size);
+size_t orn_gguf_read_tensor_bytes(const orn_gguf *g, const orn_tensor_info *tensor,
+                                  size_t byte_offset, void *buffer, size_t n);
+/* "<general.architecture>.<param>" as uint32 (gguf.h:137). */
+bool orn_gguf_get_param_u32(const orn_gguf *g, const char *param, uint32_t *out);
+
+/* gguf_dequantize_tensor / gguf_dequantize_expert_slice (gguf.h:129-135,
+ * gguf.c:641-648, 714-722): the tensor's bytes are read from the file, the
+ * dequantization runs on the GPU as in the _from_buf calls above. */
+bool gpu_dequantize_tensor_gguf(gpu_context *ctx, const orn_gguf *g,
+                                const orn_tensor_info *tensor, float *output);
+bool gpu_dequantize_expert_slice_gguf(gpu_context *ctx, const orn_gguf *g,
+                                      const orn_tensor_info *tensor, int expert_idx,
+                                      float *output);
+
+/* ---------------------------------------------------------------------------
  * Resident routed-MoE layers.  Replaces the per-token expert loop of
  * model.c:1009-1143 (router model.c:1017-1025, selection model.c:1027-1049 /
  * model_get_routing model.c:264-321, slice cache model.c:692-753, expert FFN
@@ -150,6 +231,20 @@ int gpu_moe_store_fill_synthetic(gpu_context *ctx, ornith_moe_store *store, int 
  * reference counterpart: for checks and for saving a store. */
 int gpu_moe_store_get_experts(gpu_context *ctx, ornith_moe_store *store, int layer, int matrix,
                               int expert_first, int n, void *blocks);
+
+/* Upload n_layers MoE layers of a model file (file layers from
+ * file_first_layer, store layers from store_first_layer) into a store
+ * created with file_layout = 1: blk.N.ffn_{gate,up,down}_exps.weight
+ * (Q4_K, Q4_K, Q6_K; ne = [D, H, E], [D, H, E], [H, D, E]), with a shared
+ * expert blk.N.ffn_{gate,up,down}_shexp.weight (ne = [D, H], [D, H],
+ * [H, D]), blk.N.ffn_gate_inp.weight (f32 or f16, ne = [D, E], W[e*D + d])
+ * and blk.N.post_attention_norm.weight (f32 [D], when present).  Names as
+ * model.c:707-711, 807, 847-852, 861; the bytes are read by range (32
+ * experts at a time) and uploaded as they are, never re-quantized.
+ * ORN_EUNSUPPORTED for a vec@mat store or a tensor of another type or
+ * shape; ORN_EINVAL for a missing tensor or a failed read. */
+int gpu_moe_store_load_gguf(gpu_context *ctx, ornith_moe_store *store, const orn_gguf *g,
+                            int file_first_layer, int store_first_layer, int n_layers);
 
 enum { ORN_ROUTE_RENORM = 0, ORN_ROUTE_LITERAL = 1 };
 #define ORN_MOE_ASYNC 1u /* return without synchronising the stream */

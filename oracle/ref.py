@@ -3,8 +3,9 @@ infrastructure only.
 
 The library is compiled from the reference's own C sources by `make -C oracle
 ref` (only in the container that holds /root/reference); the built .so is
-what travels.  It is used to (a) write the golden vectors under tests/golden/
-and (b) time the reference CPU path for bench.py's cpu_baseline leg.
+what travels.  It is used to (a) write the golden vectors under tests/golden/,
+(b) time the reference CPU path for bench.py's cpu_baseline leg and (c) check
+the library's GGUF reader against the reference parser on the same files.
 
 Reference entry points used (engine/src/...):
   gguf_dequantize_tensor_from_buf        gguf.c:605-638
@@ -12,6 +13,8 @@ Reference entry points used (engine/src/...):
   model_load / model_unload              model.c:160-243
   model_get_routing                      model.c:264-321
   model_forward                          model.c:878-1234 (MoE block 992-1144)
+  gguf_open .. gguf_get_param_u32        gguf.c:289-506, 575-601 (parser, lookups,
+                                         pread reads; declared in gguf.h:67-137)
 """
 from __future__ import annotations
 
@@ -69,6 +72,22 @@ def lib():
         L.model_forward.restype = None
         L.model_forward.argtypes = [C.c_void_p, C.c_uint32, C.c_void_p, C.POINTER(ModelBuffers),
                                     C.c_int, C.c_int]
+        vp, sz = C.c_void_p, C.c_size_t
+        for name, res, args in (
+                ("gguf_open", vp, [C.c_char_p, C.c_char_p, sz]), ("gguf_close", None, [vp]),
+                ("gguf_version", C.c_uint32, [vp]), ("gguf_tensor_count", C.c_uint64, [vp]),
+                ("gguf_metadata_count", C.c_uint64, [vp]),
+                ("gguf_architecture", C.c_char_p, [vp]), ("gguf_alignment", sz, [vp]),
+                ("gguf_find_metadata", C.c_bool, [vp, C.c_char_p, vp]),
+                ("gguf_find_tensor", C.POINTER(TensorInfo), [vp, C.c_char_p]),
+                ("gguf_list_tensors", C.c_uint64, [vp, C.POINTER(C.POINTER(TensorInfo)), C.c_uint64]),
+                ("gguf_tensor_data", vp, [vp, C.c_char_p]),
+                ("gguf_tensor_data_from_info", vp, [vp, C.POINTER(TensorInfo)]),
+                ("gguf_read_tensor_data", sz, [vp, C.POINTER(TensorInfo), vp, sz]),
+                ("gguf_read_tensor_bytes", sz, [vp, C.POINTER(TensorInfo), sz, vp, sz]),
+                ("gguf_get_param_u32", C.c_bool, [vp, C.c_char_p, C.POINTER(C.c_uint32)])):
+            fn = getattr(L, name)
+            fn.restype, fn.argtypes = res, args
         _lib = L
     return _lib
 

@@ -69,6 +69,12 @@ int orn_prof_begin(gpu_context *ctx, const char *name);
 void orn_prof_end(gpu_context *ctx, int slot);
 int orn_prof_kernel(gpu_context *ctx, const char *name, hipEvent_t *start, hipEvent_t *stop);
 
+/* the shape a store was created with (moe.c) */
+const ornith_moe_shape *orn_store_shape(const ornith_moe_store *st);
+
+/* fp16 bits -> float with the reference's rule, gguf.c:16-26 (prefill_pack.c) */
+float orn_quirk_half(uint16_t h);
+
 /* workspace (moe.c) */
 void *orn_ws_get(gpu_context *ctx, size_t bytes);
 void orn_ws_release(gpu_context *ctx);

@@ -365,6 +365,8 @@ void gpu_moe_store_destroy(gpu_context *ctx, ornith_moe_store *store)
 
 size_t gpu_moe_store_bytes(const ornith_moe_store *store) { return store ? store->bytes : 0; }
 
+const ornith_moe_shape *orn_store_shape(const ornith_moe_store *st) { return &st->sh; }
+
 /* Permute one expert's GGUF block stream (row-major: block (k, c) at
  * k*NBc + c) into the device's block-column-major order (c*K + k). */
 static void permute_q4k(const uint8_t *src, uint8_t *dst, int K, int NBc)

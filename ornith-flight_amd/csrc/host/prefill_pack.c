@@ -31,7 +31,7 @@
 #include <string.h>
 
 /* gguf.c:16-26: 0 -> 0, otherwise exponent bias 112 for every pattern. */
-static float quirk_half(uint16_t h)
+float orn_quirk_half(uint16_t h)
 {
     if (h == 0) return 0.0f;
     uint32_t u = ((uint32_t)(h & 0x8000u) << 16) | ((((h & 0x7C00u) >> 10) + 112u) << 23) |
@@ -96,8 +96,8 @@ void orn_pack_q4k_prefill(const uint8_t *blocks, int K, int M, uint32_t *qn, uin
         const int shift = 4 * (e / 2) + 16 * (e % 2);
         for (int b = 0; b < NB; ++b) {
             const uint8_t *blk = blocks + ((size_t)k * NB + b) * ORN_Q4K_BYTES;
-            const float dv = quirk_half((uint16_t)(blk[0] | (blk[1] << 8)));
-            const float dmv = quirk_half((uint16_t)(blk[2] | (blk[3] << 8)));
+            const float dv = orn_quirk_half((uint16_t)(blk[0] | (blk[1] << 8)));
+            const float dmv = orn_quirk_half((uint16_t)(blk[2] | (blk[3] << 8)));
             d[(size_t)b * K + k] = dv;
             dm[(size_t)b * K + k] = dmv;
             if (dv == dv && dv > mx) mx = dv;
@@ -136,7 +136,7 @@ int orn_pack_q6k_prefill(const uint8_t *blocks, int K, int M, uint8_t *qb, uint1
             const uint8_t *ql = blk + ORN_Q6K_OFF_QL, *qh = blk + ORN_Q6K_OFF_QH;
             const int8_t *scs = (const int8_t *)(blk + ORN_Q6K_OFF_SCALES);
             const float dv =
-                quirk_half((uint16_t)(blk[ORN_Q6K_OFF_D] | (blk[ORN_Q6K_OFF_D + 1] << 8)));
+                orn_quirk_half((uint16_t)(blk[ORN_Q6K_OFF_D] | (blk[ORN_Q6K_OFF_D + 1] << 8)));
             d[(size_t)b * K + k] = dv;
             if (dv == dv && dv > mx) mx = dv;
             if (dv == dv && -dv > mx) mx = -dv;

@@ -45,6 +45,12 @@ EXPORTED = [
     "gpu_profile_total_ms", "gpu_profile_calls",
     "orn_synth_stream", "orn_synth_q4k", "orn_synth_q6k", "orn_synth_normal",
     "orn_synth_zipf_bias",
+    "orn_gguf_open", "orn_gguf_close", "orn_gguf_version", "orn_gguf_tensor_count",
+    "orn_gguf_metadata_count", "orn_gguf_architecture", "orn_gguf_alignment",
+    "orn_gguf_data_offset", "orn_gguf_find_metadata", "orn_gguf_find_tensor",
+    "orn_gguf_list_tensors", "orn_gguf_tensor_data", "orn_gguf_tensor_data_from_info",
+    "orn_gguf_read_tensor_data", "orn_gguf_read_tensor_bytes", "orn_gguf_get_param_u32",
+    "gpu_dequantize_tensor_gguf", "gpu_dequantize_expert_slice_gguf", "gpu_moe_store_load_gguf",
 ]
 
 
@@ -53,6 +59,26 @@ class TensorInfo(C.Structure):
     _fields_ = [("name", C.c_char_p), ("type", C.c_int), ("n_dims", C.c_uint32),
                 ("dims", C.c_uint64 * 4), ("offset", C.c_size_t), ("size_bytes", C.c_size_t),
                 ("n_elems", C.c_size_t)]
+
+
+class _Str(C.Structure):
+    _fields_ = [("data", C.c_void_p), ("len", C.c_size_t)]
+
+
+class _Arr(C.Structure):
+    _fields_ = [("elem_type", C.c_int), ("count", C.c_size_t), ("data", C.c_void_p)]
+
+
+class _Val(C.Union):
+    _fields_ = [("uint8", C.c_uint8), ("int8", C.c_int8), ("uint16", C.c_uint16),
+                ("int16", C.c_int16), ("uint32", C.c_uint32), ("int32", C.c_int32),
+                ("uint64", C.c_uint64), ("int64", C.c_int64), ("float32", C.c_float),
+                ("float64", C.c_double), ("boolean", C.c_bool), ("string", _Str), ("array", _Arr)]
+
+
+class GGUFValue(C.Structure):
+    """orn_gguf_value (layout of the reference's gguf_metadata_value, gguf.h:44-66)."""
+    _fields_ = [("type", C.c_int), ("value", _Val)]
 
 
 class MoEShape(C.Structure):
@@ -126,6 +152,21 @@ def lib():
         "orn_synth_q6k": (None, [u64, u64, u64, u64, vp]),
         "orn_synth_normal": (None, [u64, u64, u64, f, vp]),
         "orn_synth_zipf_bias": (None, [u64, u64, i, f, vp]),
+        "orn_gguf_open": (vp, [C.c_char_p, C.c_char_p, sz]), "orn_gguf_close": (None, [vp]),
+        "orn_gguf_version": (C.c_uint32, [vp]), "orn_gguf_tensor_count": (u64, [vp]),
+        "orn_gguf_metadata_count": (u64, [vp]), "orn_gguf_architecture": (C.c_char_p, [vp]),
+        "orn_gguf_alignment": (sz, [vp]), "orn_gguf_data_offset": (sz, [vp]),
+        "orn_gguf_find_metadata": (C.c_bool, [vp, C.c_char_p, C.POINTER(GGUFValue)]),
+        "orn_gguf_find_tensor": (C.POINTER(TensorInfo), [vp, C.c_char_p]),
+        "orn_gguf_list_tensors": (u64, [vp, C.POINTER(C.POINTER(TensorInfo)), u64]),
+        "orn_gguf_tensor_data": (vp, [vp, C.c_char_p]),
+        "orn_gguf_tensor_data_from_info": (vp, [vp, C.POINTER(TensorInfo)]),
+        "orn_gguf_read_tensor_data": (sz, [vp, C.POINTER(TensorInfo), vp, sz]),
+        "orn_gguf_read_tensor_bytes": (sz, [vp, C.POINTER(TensorInfo), sz, vp, sz]),
+        "orn_gguf_get_param_u32": (C.c_bool, [vp, C.c_char_p, C.POINTER(C.c_uint32)]),
+        "gpu_dequantize_tensor_gguf": (C.c_bool, [vp, vp, C.POINTER(TensorInfo), vp]),
+        "gpu_dequantize_expert_slice_gguf": (C.c_bool, [vp, vp, C.POINTER(TensorInfo), i, vp]),
+        "gpu_moe_store_load_gguf": (i, [vp, vp, vp, i, i, i]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -341,6 +382,12 @@ class Store:
         assert n.value == out.size, (n.value, out.size)
         return out
 
+    def load_gguf(self, gguf: "GGUF", file_first_layer=0, store_first_layer=0, n_layers=1):
+        """Upload MoE layers of a model file (gpu_moe_store_load_gguf)."""
+        self.ctx.check(lib().gpu_moe_store_load_gguf(self.ctx.ptr, self.ptr, gguf.ptr,
+                                                     file_first_layer, store_first_layer, n_layers),
+                       "load_gguf")
+
     def bytes(self):
         return lib().gpu_moe_store_bytes(self.ptr)
 
@@ -364,3 +411,104 @@ def tensor_info(typ, dims, size_bytes=None):
                       TYPE_Q6_K: n // 256 * Q6K_BYTES}.get(typ, 0)
     arr = (C.c_uint64 * 4)(*(list(dims) + [1] * (4 - len(dims))))
     return TensorInfo(b"t", typ, len(dims), arr, 0, size_bytes, n)
+
+
+# ---------------------------------------------------------------- GGUF reader
+class GGUF:
+    """orn_gguf_* (the reference's gguf_* API, gguf.h:67-137).  open() raises
+    with the reader's reason when orn_gguf_open returns NULL."""
+
+    def __init__(self, path):
+        err = C.create_string_buffer(256)
+        self.ptr = lib().orn_gguf_open(os.fsencode(path), err, 256)
+        if not self.ptr:
+            raise ValueError(err.value.decode())
+
+    def close(self):
+        if self.ptr:
+            lib().orn_gguf_close(self.ptr)
+            self.ptr = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    version = property(lambda s: lib().orn_gguf_version(s.ptr))
+    tensor_count = property(lambda s: lib().orn_gguf_tensor_count(s.ptr))
+    metadata_count = property(lambda s: lib().orn_gguf_metadata_count(s.ptr))
+    alignment = property(lambda s: lib().orn_gguf_alignment(s.ptr))
+    data_offset = property(lambda s: lib().orn_gguf_data_offset(s.ptr))
+
+    @property
+    def architecture(self):
+        a = lib().orn_gguf_architecture(self.ptr)
+        return None if a is None else a.decode(errors="replace")
+
+    def metadata(self, key):
+        """The raw GGUFValue of `key`, or None."""
+        v = GGUFValue()
+        return v if lib().orn_gguf_find_metadata(self.ptr, key.encode(), C.byref(v)) else None
+
+    def value(self, key):
+        """`key`'s value as Python: scalars, str, or a list for arrays of
+        scalars or strings; None when absent."""
+        v = self.metadata(key)
+        if v is None:
+            return None
+        scal = {0: "uint8", 1: "int8", 2: "uint16", 3: "int16", 4: "uint32", 5: "int32",
+                6: "float32", 7: "boolean", 10: "uint64", 11: "int64", 12: "float64"}
+        if v.type in scal:
+            return getattr(v.value, scal[v.type])
+        if v.type == 8:
+            return C.string_at(v.value.string.data, v.value.string.len).decode()
+        a = v.value.array
+        dt = {0: np.uint8, 1: np.int8, 2: np.uint16, 3: np.int16, 4: np.uint32, 5: np.int32,
+              6: np.float32, 7: np.bool_, 10: np.uint64, 11: np.int64, 12: np.float64}
+        if a.elem_type in dt:
+            n = a.count * np.dtype(dt[a.elem_type]).itemsize
+            return np.frombuffer(C.string_at(a.data, n), dt[a.elem_type]).tolist() if n else []
+        if a.elem_type == 8:
+            out, p = [], a.data
+            for _ in range(a.count):
+                ln = C.c_uint64.from_address(p).value
+                out.append(C.string_at(p + 8, ln).decode())
+                p += 8 + ln
+            return out
+        raise ValueError(f"array of type {a.elem_type}")
+
+    def param_u32(self, param):
+        v = C.c_uint32(0)
+        return v.value if lib().orn_gguf_get_param_u32(self.ptr, param.encode(), C.byref(v)) else None
+
+    def find_tensor(self, name):
+        """The TensorInfo of `name` (owned by the handle), or None."""
+        p = lib().orn_gguf_find_tensor(self.ptr, name.encode())
+        return p.contents if p else None
+
+    def list_tensors(self, max_count=None):
+        n = lib().orn_gguf_list_tensors(self.ptr, None, 0)
+        if max_count is not None:
+            n = min(n, max_count)
+        arr = (C.POINTER(TensorInfo) * max(n, 1))()
+        got = lib().orn_gguf_list_tensors(self.ptr, arr, n)
+        return [arr[i].contents for i in range(got)]
+
+    def read_tensor_data(self, info, buffer_size=None):
+        """Bytes of a whole tensor (None when the read fails)."""
+        size = info.size_bytes if buffer_size is None else buffer_size
+        buf = np.empty(max(size, 1), np.uint8)
+        n = lib().orn_gguf_read_tensor_data(self.ptr, C.byref(info), _p(buf), size)
+        return buf[:n] if n else None
+
+    def read_tensor_bytes(self, info, offset, n):
+        buf = np.empty(max(n, 1), np.uint8)
+        got = lib().orn_gguf_read_tensor_bytes(self.ptr, C.byref(info), offset, _p(buf), n)
+        return buf[:got] if got else None
+
+    def tensor_data(self, name):
+        """The tensor's bytes through the file mapping (orn_gguf_tensor_data)."""
+        info = self.find_tensor(name)
+        p = lib().orn_gguf_tensor_data(self.ptr, name.encode())
+        return None if not p else np.frombuffer(C.string_at(p, info.size_bytes), np.uint8)
