@@ -16,9 +16,14 @@
  *   gpu_matmul_int4                   gpu.h:51-53   (gpu.c:131-140, zero-fills C)
  *   gpu_rmsnorm                       gpu.h:55-57   (gpu.c:144-156, eps 1e-6)
  *   gpu_silu / gpu_silu_mul           gpu.h:59-63   (gpu.c:158-186, no clamp)
- *   gpu_rope/gpu_attention/
- *     gpu_deltanet_step               gpu.h:65-75   (gpu.c:188-206: no-ops in the
- *                                                    CPU backend; same here)
+ *   gpu_rope                          gpu.h:65-67   (gpu_metal.m:495-548,
+ *                                                    ops.metal:113-139 semantics)
+ *   gpu_attention                     gpu.h:69-71   (gpu_metal.m:550-583,
+ *                                                    attention.metal:17-68; head_dim
+ *                                                    <= 256)
+ *   gpu_deltanet_step                 gpu.h:73-75   (a no-op in both reference
+ *                                                    backends, gpu.c:202-206,
+ *                                                    gpu_metal.m:587-591; same here)
  *   gpu_expert_mlp                    gpu.h:77-80   (mlp.metal:49-87 semantics)
  *   gpu_router                        gpu.h:82-84   (mlp.metal:94-109 semantics)
  *   gpu_topk_softmax                  gpu.h:86-87   (gpu_metal.m:663-685 semantics)

@@ -32,6 +32,18 @@ extern "C" {
  * the reference reports errors through err_buf strings (gguf.c:408-429). */
 const char *gpu_last_error(gpu_context *ctx);
 
+/* The Metal shader steps that gpu.h has no declaration for
+ * (attention.metal:80-125): the gated DeltaNet step, state[j][i] =
+ * gate*state[j][i] + (1-gate)*K[i]*V[j] over the dim x dim state, then
+ * out[i] = sum_j Q[j]*state[j][i]; and the KV-cache append, K_cache[pos] =
+ * K_new, V_cache[pos] = V_new (rows of head_dim floats).  Synchronous; 0 or
+ * a negative status. */
+int gpu_deltanet_step_gated(gpu_context *ctx, gpu_buffer *state, const gpu_buffer *Q,
+                            const gpu_buffer *K, const gpu_buffer *V, gpu_buffer *out, int dim,
+                            float gate);
+int gpu_kv_cache_append(gpu_context *ctx, gpu_buffer *K_cache, gpu_buffer *V_cache,
+                        const gpu_buffer *K_new, const gpu_buffer *V_new, int pos, int head_dim);
+
 /* Device address of a buffer (for interop and tests). */
 void *gpu_device_ptr(gpu_context *ctx, gpu_buffer *buf);
 

@@ -451,3 +451,65 @@ done:
     free(Wg); free(Wu); free(Wd); free(tmp);
     return rc;
 }
+
+/* ops.metal:113-139 for every (head, pair); the CPU attention layer does the
+ * same per head (model.c:599-622).  The frequency is rounded once from
+ * double (the reference takes it from powf, within an ulp of this). */
+void orc_rope(float *x, int n_heads, int head_dim, int pos, float theta)
+{
+    const int rot = head_dim < 64 ? head_dim : 64;
+    for (int h = 0; h < n_heads; ++h) {
+        float *v = x + (size_t)h * head_dim;
+        for (int i = 0; i + 1 < rot; i += 2) {
+            const float inv_freq = (float)(1.0 / pow((double)theta, (double)i / (double)rot));
+            const float ang = (float)pos * inv_freq;
+            const float c = cosf(ang), s = sinf(ang);
+            const float a = v[i], b = v[i + 1];
+            v[i] = a * c - b * s;
+            v[i + 1] = a * s + b * c;
+        }
+    }
+}
+
+/* attention.metal:17-68.  The shader's thread (row, col) recomputes every
+ * score; a score does not depend on col, so it is computed once per (row, t)
+ * here with the same d order, and each col's sums run over t ascending as
+ * the shader's: the same roundings, without the factor hd of work. */
+void orc_attention(float *out, const float *Q, const float *K, const float *V, int seq, int hd,
+                   float scale)
+{
+    float *w = (float *)malloc((size_t)seq * sizeof(float));
+    if (!w) return;
+    for (int r = 0; r < seq; ++r) {
+        float sw = 0.0f;
+        for (int t = 0; t < seq; ++t) {
+            float score = 0.0f;
+            for (int d = 0; d < hd; ++d) score += Q[(size_t)r * hd + d] * K[(size_t)t * hd + d];
+            score *= scale;
+            w[t] = expf(score);
+            sw += w[t];
+        }
+        for (int c = 0; c < hd; ++c) {
+            float ov = 0.0f;
+            for (int t = 0; t < seq; ++t) ov += w[t] * V[(size_t)t * hd + c];
+            if (sw > 1e-10f) ov /= sw;
+            out[(size_t)r * hd + c] = ov;
+        }
+    }
+    free(w);
+}
+
+/* attention.metal:80-108: thread i's two loops, for every i. */
+void orc_deltanet_step(float *state, const float *Q, const float *K, const float *V, float *out,
+                       int dim, float gate)
+{
+    for (int i = 0; i < dim; ++i) {
+        for (int j = 0; j < dim; ++j) {
+            const size_t idx = (size_t)j * dim + i;
+            state[idx] = gate * state[idx] + (1.0f - gate) * K[i] * V[j];
+        }
+        float sum = 0.0f;
+        for (int j = 0; j < dim; ++j) sum += Q[j] * state[(size_t)j * dim + i];
+        out[i] = sum;
+    }
+}

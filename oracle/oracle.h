@@ -34,6 +34,12 @@
  *                           block shares one set of scales (the same matrix
  *                           is then exactly representable in both
  *                           orientations) + fp64 brute force
+ *   orc_rope                fp64 complex rotation (same frequency formula),
+ *                           pos 0 = identity, pair norms preserved
+ *   orc_attention           fp64 softmax(QK^T/sqrt(d))V; seq 1 -> V; equal
+ *                           keys -> mean of V
+ *   orc_deltanet_step       fp64 recurrence; gate 1 -> state kept,
+ *                           gate 0 -> state = outer(v, k)
  */
 #ifndef ORNITH_ORACLE_H
 #define ORNITH_ORACLE_H
@@ -116,6 +122,23 @@ int orc_moe_layer(const orc_moe_cfg *cfg, int T, const float *x, const float *re
                   const void *gate, const void *up, const void *down,
                   const void *sh_gate, const void *sh_up, const void *sh_down,
                   float *out, uint32_t *idx_out, float *w_out);
+
+/* ops.metal:113-139 (= model.c:599-622 for one head): the pairs (i, i+1),
+ * i < rot = min(head_dim, 64), of n_heads heads of x [n_heads][head_dim]
+ * rotated by pos * inv_freq, inv_freq = 1/theta^(i/rot) rounded once from
+ * double. */
+void orc_rope(float *x, int n_heads, int head_dim, int pos, float theta);
+
+/* attention.metal:17-68: out[r][c] = sum_t e^(s_rt) V[t][c] / sum_t e^(s_rt),
+ * s_rt = (sum_d Q[r][d]*K[t][d]) * scale, t and d ascending, exp not
+ * shifted, division only if the sum > 1e-10 (as the shader). */
+void orc_attention(float *out, const float *Q, const float *K, const float *V, int seq, int hd,
+                   float scale);
+
+/* attention.metal:80-108 (the whole grid): state[j][i] = gate*state[j][i] +
+ * (1-gate)*K[i]*V[j]; out[i] = sum_j Q[j]*state[j][i]. */
+void orc_deltanet_step(float *state, const float *Q, const float *K, const float *V, float *out,
+                       int dim, float gate);
 
 /* Single (token, expert) FFN with the routed-expert SiLU clamp
  * (model.c:1085-1088) on already dequantized fp32 weights. */

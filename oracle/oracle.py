@@ -65,6 +65,12 @@ def lib():
                                     C.c_void_p, C.c_void_p, C.c_void_p,
                                     C.c_void_p, C.c_void_p, C.c_void_p,
                                     C.c_void_p, C.c_void_p, C.c_void_p]
+        L.orc_rope.restype = None
+        L.orc_rope.argtypes = [f32p, C.c_int, C.c_int, C.c_int, C.c_float]
+        L.orc_attention.restype = None
+        L.orc_attention.argtypes = [f32p, f32p, f32p, f32p, C.c_int, C.c_int, C.c_float]
+        L.orc_deltanet_step.restype = None
+        L.orc_deltanet_step.argtypes = [f32p, f32p, f32p, f32p, f32p, C.c_int, C.c_float]
         _lib = L
     return _lib
 
@@ -119,6 +125,33 @@ def rmsnorm(x, w):
         lib().orc_rmsnorm(row, x[t], w, x.shape[1])
         out[t] = row
     return out
+
+
+def rope(x, pos, theta):
+    """orc_rope (ops.metal:113-139) of x [n_heads][head_dim]; returns a copy."""
+    y = np.array(x, np.float32, order="C", copy=True)
+    lib().orc_rope(y, y.shape[0], y.shape[1], pos, theta)
+    return y
+
+
+def attention(Q, K, V, scale=None):
+    """orc_attention (attention.metal:17-68) of one head, [seq][hd] each."""
+    Q, K, V = (np.ascontiguousarray(a, np.float32) for a in (Q, K, V))
+    seq, hd = Q.shape
+    if scale is None:
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    out = np.empty_like(Q)
+    lib().orc_attention(out, Q, K, V, seq, hd, scale)
+    return out
+
+
+def deltanet_step(state, q, k, v, gate):
+    """orc_deltanet_step (attention.metal:80-108); returns (state', out)."""
+    st = np.array(state, np.float32, order="C", copy=True)
+    out = np.empty(len(q), np.float32)
+    lib().orc_deltanet_step(st, *(np.ascontiguousarray(a, np.float32) for a in (q, k, v)), out,
+                            len(q), gate)
+    return st, out
 
 
 def topk(logits, k, mode=MODE_RENORM):

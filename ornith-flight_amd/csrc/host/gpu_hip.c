@@ -16,6 +16,7 @@
  */
 #include "internal.h"
 
+#include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -289,23 +290,91 @@ void gpu_silu_mul(gpu_context *ctx, gpu_buffer *out, const gpu_buffer *gate, con
 
 /* RoPE, attention and the DeltaNet step are no-ops in the CPU backend
  * (gpu.c:188-206); the MoE hot path does not use them. */
+/* gpu_metal.m:495-548 + ops.metal:113-139: rotate the first min(head_dim, 64)
+ * dims of each of the n_heads Q heads and n_kv_heads K heads (one position,
+ * pos_start; seq_len is unused, as there). */
 void gpu_rope(gpu_context *ctx, gpu_buffer *Q, gpu_buffer *K, int seq_len, int head_dim,
               int n_heads, int n_kv_heads, float base, int pos_start)
 {
-    (void)ctx; (void)Q; (void)K; (void)seq_len; (void)head_dim;
-    (void)n_heads; (void)n_kv_heads; (void)base; (void)pos_start;
+    (void)seq_len;
+    if (!ctx || !Q || !K || head_dim <= 0 || n_heads < 0 || n_kv_heads < 0) return;
+    if (!fits(Q, (size_t)n_heads * head_dim) || !fits(K, (size_t)n_kv_heads * head_dim)) return;
+    orn_hip_check(ctx, (hipError_t)ornk_rope((float *)Q->dev, (float *)K->dev, head_dim, n_heads,
+                                             n_kv_heads, pos_start, base, ctx->stream),
+                  "gpu_rope");
+    sync_ctx(ctx);
 }
 
+/* gpu_metal.m:550-583 + attention.metal:17-68: one head, Q/K/V/out
+ * [seq_len][head_dim], scale 1/sqrt(head_dim), every key for every query.
+ * head_dim up to 256 (the kernel's register tile); larger is refused with an
+ * error message. */
 void gpu_attention(gpu_context *ctx, gpu_buffer *out, const gpu_buffer *Q,
                    const gpu_buffer *K_cache, const gpu_buffer *V_cache, int seq_len, int head_dim)
 {
-    (void)ctx; (void)out; (void)Q; (void)K_cache; (void)V_cache; (void)seq_len; (void)head_dim;
+    if (!ctx || !out || !Q || !K_cache || !V_cache || seq_len <= 0 || head_dim <= 0) return;
+    const size_t n = (size_t)seq_len * head_dim;
+    if (!fits(out, n) || !fits(Q, n) || !fits(K_cache, n) || !fits(V_cache, n)) return;
+    if (head_dim > 256) {
+        orn_set_err(ctx, ORN_EUNSUPPORTED, "gpu_attention: head_dim %d > 256", head_dim);
+        return;
+    }
+    const float scale = 1.0f / sqrtf((float)head_dim);
+    orn_hip_check(ctx, (hipError_t)ornk_attention((float *)out->dev, (const float *)Q->dev,
+                                                  (const float *)K_cache->dev,
+                                                  (const float *)V_cache->dev, seq_len, head_dim,
+                                                  scale, ctx->stream),
+                  "gpu_attention");
+    sync_ctx(ctx);
 }
 
+/* A no-op, as in both reference backends (gpu.c:202-206, gpu_metal.m:587-591):
+ * the declaration has no output and no gate.  The Metal shader's step
+ * (attention.metal:80-108) is gpu_deltanet_step_gated. */
 void gpu_deltanet_step(gpu_context *ctx, gpu_buffer *state, const gpu_buffer *Q,
                        const gpu_buffer *K, const gpu_buffer *V, int dim)
 {
     (void)ctx; (void)state; (void)Q; (void)K; (void)V; (void)dim;
+}
+
+int gpu_deltanet_step_gated(gpu_context *ctx, gpu_buffer *state, const gpu_buffer *Q,
+                            const gpu_buffer *K, const gpu_buffer *V, gpu_buffer *out, int dim,
+                            float gate)
+{
+    if (!ctx) return ORN_EINVAL;
+    if (!state || !Q || !K || !V || !out || dim <= 0)
+        return orn_set_err(ctx, ORN_EINVAL, "gpu_deltanet_step_gated: bad arguments");
+    if (!fits(state, (size_t)dim * dim) || !fits(Q, (size_t)dim) || !fits(K, (size_t)dim) ||
+        !fits(V, (size_t)dim) || !fits(out, (size_t)dim))
+        return orn_set_err(ctx, ORN_EINVAL, "gpu_deltanet_step_gated: buffer too small");
+    int rc = orn_hip_check(ctx, (hipError_t)ornk_deltanet_step(
+                                    (float *)state->dev, (const float *)Q->dev,
+                                    (const float *)K->dev, (const float *)V->dev,
+                                    (float *)out->dev, dim, gate, ctx->stream),
+                           "gpu_deltanet_step_gated");
+    sync_ctx(ctx);
+    return rc;
+}
+
+int gpu_kv_cache_append(gpu_context *ctx, gpu_buffer *K_cache, gpu_buffer *V_cache,
+                        const gpu_buffer *K_new, const gpu_buffer *V_new, int pos, int head_dim)
+{
+    if (!ctx) return ORN_EINVAL;
+    if (!K_cache || !V_cache || !K_new || !V_new || pos < 0 || head_dim <= 0)
+        return orn_set_err(ctx, ORN_EINVAL, "gpu_kv_cache_append: bad arguments");
+    const size_t end = ((size_t)pos + 1) * (size_t)head_dim;
+    if (!fits(K_cache, end) || !fits(V_cache, end) || !fits(K_new, (size_t)head_dim) ||
+        !fits(V_new, (size_t)head_dim))
+        return orn_set_err(ctx, ORN_EINVAL, "gpu_kv_cache_append: position %d past the cache",
+                           pos);
+    int rc = orn_hip_check(ctx, (hipError_t)ornk_kv_append((float *)K_cache->dev,
+                                                           (float *)V_cache->dev,
+                                                           (const float *)K_new->dev,
+                                                           (const float *)V_new->dev, pos,
+                                                           head_dim, ctx->stream),
+                           "gpu_kv_cache_append");
+    sync_ctx(ctx);
+    return rc;
 }
 
 /* mlp.metal:49-87: out = (silu(x@gate) * (x@up)) @ down in fp32, no clamp. */

@@ -30,6 +30,19 @@ int ornk_silu(float *out, const float *x, int n, hipStream_t s);
 int ornk_silu_mul(float *out, const float *g, const float *u, int n, hipStream_t s);
 int ornk_add(float *out, const float *a, const float *b, int n, hipStream_t s);
 
+/* ---- attention-side ops behind gpu.h (attn.hip) --------------------------- */
+/* RoPE on n_q heads of Q and n_k heads of K (first min(head_dim, 64) dims). */
+int ornk_rope(float *Q, float *K, int head_dim, int n_q, int n_k, int pos, float theta,
+              hipStream_t s);
+/* Single-head attention, Q/K/V/out [seq][hd], hd <= 256. */
+int ornk_attention(float *out, const float *Q, const float *K, const float *V, int seq, int hd,
+                   float scale, hipStream_t s);
+size_t ornk_attention_lds(int hd);
+int ornk_deltanet_step(float *state, const float *Q, const float *K, const float *V, float *out,
+                       int dim, float gate, hipStream_t s);
+int ornk_kv_append(float *Kc, float *Vc, const float *Kn, const float *Vn, int pos, int hd,
+                   hipStream_t s);
+
 /* ---- fixed scratch of the forward that allocates nothing (scratch.hip) ---- */
 /* Size of the per-device scratch array; equals ORN_NOALLOC_SCRATCH_BYTES of
  * ornith_hip.h. */

@@ -51,6 +51,7 @@ EXPORTED = [
     "orn_gguf_list_tensors", "orn_gguf_tensor_data", "orn_gguf_tensor_data_from_info",
     "orn_gguf_read_tensor_data", "orn_gguf_read_tensor_bytes", "orn_gguf_get_param_u32",
     "gpu_dequantize_tensor_gguf", "gpu_dequantize_expert_slice_gguf", "gpu_moe_store_load_gguf",
+    "gpu_deltanet_step_gated", "gpu_kv_cache_append",
 ]
 
 
@@ -167,6 +168,8 @@ def lib():
         "gpu_dequantize_tensor_gguf": (C.c_bool, [vp, vp, C.POINTER(TensorInfo), vp]),
         "gpu_dequantize_expert_slice_gguf": (C.c_bool, [vp, vp, C.POINTER(TensorInfo), i, vp]),
         "gpu_moe_store_load_gguf": (i, [vp, vp, vp, i, i, i]),
+        "gpu_deltanet_step_gated": (i, [vp, vp, vp, vp, vp, vp, i, f]),
+        "gpu_kv_cache_append": (i, [vp, vp, vp, vp, vp, i, i]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
