@@ -10,7 +10,8 @@ experts, combine); inputs are already in HBM when the timed region starts.
 Prints ONE JSON line (rank 0).  Also reported in "configs": the other
 BASELINE configs measured the same way (1-token decode, 2048-token prefill,
 Zipf-skewed 256 tokens, and the 40-layer resident stack at 1 and 16 tokens;
---no-stack skips the stack).
+--no-stack skips the stack), the file-orientation store, streamed experts
+(host tier + device slots) and the attention-side gpu.h ops.
 
 `roofline` is for the dominant kernel of the step: algorithmic bytes of the
 expert weights that kernel streams (active experts x bytes per expert) over
@@ -260,6 +261,93 @@ def measure_stack(ctx, steps):
     return out
 
 
+def measure_streamed(ctx, steps):
+    """Streamed experts (shape.cache_slots): 8 Ornith-shape layers in the
+    pinned host tier, streamed through a pool of device slots.  A step is one
+    forward of every layer in turn for a batch drawn from a pool of 16
+    seeded batches (so routing, and with it the misses, varies).  Reported:
+    layer forwards per second, the slot hit rate, and the host->device
+    expert bytes per second against the PCIe Gen5 x16 peak (64 GB/s)."""
+    n_layers = 8
+    out = {}
+    for Ts, slots in ((1, 64), (16, 192)):
+        st = om.Store(ctx, n_layers, D, H, E, K, True, cache_slots=slots)
+        for l in range(n_layers):
+            st.fill_synthetic(l, SEED + l)
+        pool = [ctx.upload(om.synth_normal(100 + i, om.synth_stream(0, om.SYN_ACT, 0), Ts * D,
+                                           1.0)) for i in range(16)]
+        ob = ctx.alloc(Ts * D * 4)
+        L = om.lib()
+        opts = om.MoEOpts(om.ROUTE_RENORM, 0, 0, 0)
+
+        def sweep(i):
+            for l in range(n_layers):
+                rc = L.gpu_moe_forward(ctx.ptr, st.ptr, l, pool[i % 16].ptr, Ts, None, ob.ptr,
+                                       None, None, om.C.byref(opts))
+                if rc:
+                    raise RuntimeError(ctx.last_error())
+
+        for i in range(16):
+            sweep(i)
+        st.cache_stats(reset=True)
+        n = max(8, steps // 10)
+        t0 = time.perf_counter()
+        for i in range(n):
+            sweep(i)
+        ctx.sync()
+        dt = time.perf_counter() - t0
+        cs = st.cache_stats()
+        fwd = n * n_layers
+        h2d = cs["bytes_uploaded"] / dt / 1e9
+        out[f"streamed_t{Ts}_slots{slots}"] = {
+            "layer_forwards_per_s": round(fwd / dt, 1),
+            "tokens_per_s_per_layer": round(Ts * fwd / dt, 1),
+            "us_per_layer": round(dt / fwd * 1e6, 1), "layers": n_layers, "slots": slots,
+            "hit_rate": round(cs["hits"] / max(1, cs["hits"] + cs["misses"]), 4),
+            "misses_per_layer": round(cs["misses"] / fwd, 2),
+            "h2d": {"achieved": round(h2d, 2), "peak": 64.0, "unit": "GB/s",
+                    "frac": round(h2d / 64.0, 4)},
+            "host_tier_gb": round(cs["host_bytes"] / 1e9, 2),
+            "slot_pool_gb": round(cs["device_bytes"] / 1e9, 3)}
+        log(f"streamed_t{Ts}", out[f"streamed_t{Ts}_slots{slots}"])
+        for b in pool + [ob]:
+            b.free()
+        st.close()
+    return out
+
+
+def measure_attention(ctx):
+    """gpu_rope / gpu_attention (the Metal backend's semantics) at Ornith's
+    head size: one head, 4096 positions, head_dim 256, fp32 VALU; 4*S^2*d
+    flops per call against the MI355X fp32 vector peak (157.3 TFLOP/s)."""
+    S, hd = 4096, 256
+    rng = np.random.default_rng(0)
+    bufs = [ctx.upload(rng.standard_normal((S, hd)).astype(np.float32)) for _ in range(3)]
+    ob = ctx.alloc(S * hd * 4)
+    L = om.lib()
+    L.gpu_attention(ctx.ptr, ob.ptr, bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, S, hd)
+    n = 5
+    t0 = time.perf_counter()
+    for _ in range(n):
+        L.gpu_attention(ctx.ptr, ob.ptr, bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, S, hd)
+    dt = (time.perf_counter() - t0) / n
+    tf = 4.0 * S * S * hd / dt / 1e12
+    q, k = ctx.upload(np.ones((16, 256), np.float32)), ctx.upload(np.ones((2, 256), np.float32))
+    m = 200
+    t0 = time.perf_counter()
+    for i in range(m):
+        L.gpu_rope(ctx.ptr, q.ptr, k.ptr, 1, 256, 16, 2, om.C.c_float(1e7), i)
+    rope_us = (time.perf_counter() - t0) / m * 1e6
+    for b in bufs + [ob, q, k]:
+        b.free()
+    res = {"attention_s4096_d256": {"ms": round(dt * 1e3, 3), "tflops": round(tf, 2),
+                                    "peak_fp32_valu_tflops": 157.3,
+                                    "frac": round(tf / 157.3, 4)},
+           "rope_16q2k_d256_us_per_call": round(rope_us, 2)}
+    log("attention", res)
+    return res
+
+
 # Extra configs reported beside the headline: (label, store layer, tokens).
 # Layer 1 carries a Zipf(1.1) router bias.
 EXTRA_CONFIGS = (("decode_t1", 0, 1), ("prefill_t2048", 0, 2048), ("zipf_t256", 1, 256))
@@ -326,7 +414,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16 hi+lo MFMA, f32 accumulate (Q4_K/Q6_K weights exact as f16 sc*q)",
-        "data": "synthetic (seeded Q4_K/Q6_K experts, N(0,1)-like activations)",
+        "data": "synthetic (seeded Q4_K/Q6_K experts; activations and router weights are "
+                "Irwin-Hall(12) sums: mean 0, sd 1 (router 0.02), bounded at 6 sd)",
         "config": {"workload": "BASELINE configs[1]: single Ornith-shape MoE layer, 16-token decode",
                    "tokens": T, "d_model": D, "expert_ffn": H, "experts": E, "top_k": K,
                    "shared_experts": 1, "active_experts_incl_shared": U,
@@ -387,6 +476,9 @@ def main():
     store.close()
     if not args.no_stack and not args.only:
         result.setdefault("configs", {}).update(measure_stack(ctx, args.steps))
+    if not args.no_extra and not args.only:
+        result.setdefault("configs", {}).update(measure_streamed(ctx, args.steps))
+        result["configs"].update(measure_attention(ctx))
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_budget)
     ctx.close()

@@ -198,6 +198,11 @@ typedef struct {
                            gpu_moe_store_set_experts); needs prefill_layout = 0.
                            No reference counterpart: the reference reads every
                            matrix as vec@mat (model.c:351-357). */
+    int cache_slots;    /* 0: every expert resident in HBM.  N > 0: the experts
+                           live in a host tier (pinned host memory) and stream
+                           through N device slots, least recently used first
+                           (the tiering of memory.c:79-421 over quantized
+                           blocks); see gpu_moe_store_prefetch. */
 } ornith_moe_shape;
 
 enum { ORN_MAT_GATE = 0, ORN_MAT_UP = 1, ORN_MAT_DOWN = 2 };
@@ -257,6 +262,43 @@ int gpu_moe_store_get_experts(gpu_context *ctx, ornith_moe_store *store, int lay
  * shape; ORN_EINVAL for a missing tensor or a failed read. */
 int gpu_moe_store_load_gguf(gpu_context *ctx, ornith_moe_store *store, const orn_gguf *g,
                             int file_first_layer, int store_first_layer, int n_layers);
+
+/* ---- streamed experts (shape.cache_slots > 0) ------------------------------
+ * set_experts / fill_synthetic / load_gguf write the host tier; a forward
+ * reads back the experts its dispatch chose (one device->host copy and a
+ * stream synchronisation per layer), copies the missing ones into free or
+ * least recently used slots (never a pinned one, never one it needs) and
+ * runs on the slots.  A forward that needs more experts than there are
+ * unpinned slots returns ORN_EINVAL.  ORN_MOE_GRAPH is refused.  Results are
+ * those of a resident store, bit for bit. */
+
+/* cache_stats (memory.h:40-55) for the device slots. */
+typedef struct {
+    uint64_t hits, misses, evictions; /* per (forward or pin, expert) */
+    uint64_t prefetches;              /* experts loaded by gpu_moe_store_prefetch */
+    uint64_t prefetch_hits;           /* of those, later used by a forward */
+    uint64_t bytes_uploaded;          /* host -> device expert bytes */
+    int slots, resident, pinned;
+    size_t device_bytes, host_bytes;  /* slot pool and host tier */
+} ornith_moe_cache_stats;
+
+/* memory_prefetch_submit (memory.c:216-240) for experts: start loading
+ * these experts of `layer` on the store's copy stream, into free or least
+ * recently used slots that neither a pinned expert nor the last forward
+ * holds; returns at once.  A hint: experts with no slot to go to are
+ * skipped.  The next forward waits for the copies only if it reads or
+ * replaces their slots. */
+int gpu_moe_store_prefetch(gpu_context *ctx, ornith_moe_store *store, int layer,
+                           const int *experts, int n);
+/* memory_hot_promote (memory.c:196-212): load these experts (synchronously)
+ * and exempt them from eviction (pin = 1), or make them evictable again
+ * (pin = 0). */
+int gpu_moe_store_pin(gpu_context *ctx, ornith_moe_store *store, int layer, const int *experts,
+                      int n, int pin);
+/* memory_get_stats / memory_reset_stats (memory.c:386-405); ORN_EINVAL for a
+ * resident store. */
+int gpu_moe_store_cache_stats(gpu_context *ctx, ornith_moe_store *store,
+                              ornith_moe_cache_stats *out, int reset);
 
 enum { ORN_ROUTE_RENORM = 0, ORN_ROUTE_LITERAL = 1 };
 #define ORN_MOE_ASYNC 1u /* return without synchronising the stream */

@@ -75,6 +75,23 @@ const ornith_moe_shape *orn_store_shape(const ornith_moe_store *st);
 /* fp16 bits -> float with the reference's rule, gguf.c:16-26 (prefill_pack.c) */
 float orn_quirk_half(uint16_t h);
 
+/* streamed experts (cache.c): a host tier and a pool of device slots */
+typedef struct orn_cache orn_cache;
+orn_cache *orn_cache_create(gpu_context *ctx, const ornith_moe_shape *sh);
+void orn_cache_destroy(orn_cache *c);
+size_t orn_cache_device_bytes(const orn_cache *c);
+size_t orn_cache_host_bytes(const orn_cache *c);
+/* base pointers of the host tier ([L][E+1] experts, the device layout) */
+void orn_cache_host_tier(orn_cache *c, uint8_t **gate, uint8_t **up, uint8_t **body,
+                         uint16_t **dv);
+int orn_cache_quiesce(gpu_context *ctx, orn_cache *c);
+void orn_cache_invalidate(orn_cache *c, int layer, int first, int n);
+void orn_cache_slot_arrays(orn_cache *c, ornk_moe_args *a);
+int orn_cache_prepare(gpu_context *ctx, orn_cache *c, int layer, ornk_moe_args *a);
+int orn_cache_prefetch(gpu_context *ctx, orn_cache *c, int layer, const int *experts, int n);
+int orn_cache_pin(gpu_context *ctx, orn_cache *c, int layer, const int *experts, int n, int pin);
+void orn_cache_stats(orn_cache *c, ornith_moe_cache_stats *out, int reset);
+
 /* workspace (moe.c) */
 void *orn_ws_get(gpu_context *ctx, size_t bytes);
 void orn_ws_release(gpu_context *ctx);

@@ -64,6 +64,10 @@ struct ornith_moe_store {
     int *q6_scmax;            /* host [L]: largest |Q6_K sub-scale| uploaded */
     int *dev_scmax;           /* device [1]: the same, computed by the device packer */
     size_t bytes;
+    /* shape.cache_slots > 0: the experts live in this cache's host tier and
+     * device slots; gate/up/down_body/down_d and the prefill arrays above
+     * are then unused (NULL) */
+    orn_cache *cache;
     /* HIP graphs of earlier calls made with ORN_MOE_GRAPH (least recently
      * used replaced first); any upload to the store drops them all. */
     orn_graph graphs[ORN_GRAPH_SLOTS];
@@ -246,7 +250,8 @@ static int shape_ok(const ornith_moe_shape *s)
            (s->has_shared == 0 || s->has_shared == 1) && s->d_model % 128 == 0 &&
            (s->prefill_layout == 0 || s->prefill_layout == 1) &&
            (s->file_layout == 0 || (s->file_layout == 1 && !s->prefill_layout &&
-                                    ornk_file_supported(s->d_model, s->hidden)));
+                                    ornk_file_supported(s->d_model, s->hidden))) &&
+           s->cache_slots >= 0;
 }
 
 static void graphs_clear(ornith_moe_store *st)
@@ -280,6 +285,7 @@ static void store_free(ornith_moe_store *st)
     hipFree(st->dd);
     hipFree(st->dmax);
     hipFree(st->dev_scmax);
+    orn_cache_destroy(st->cache);
     free(st->dmax_host);
     free(st->q6_scmax);
     free(st->has_bias);
@@ -305,7 +311,8 @@ ornith_moe_store *gpu_moe_store_create(gpu_context *ctx, const ornith_moe_shape 
     void **ptrs[7] = {(void **)&st->gate, (void **)&st->up, (void **)&st->down_body,
                       (void **)&st->down_d, (void **)&st->router_q, (void **)&st->bias,
                       (void **)&st->norm};
-    for (int i = 0; i < 7; ++i) {
+    const int cached = shape->cache_slots > 0;
+    for (int i = cached ? 4 : 0; i < 7; ++i) {
         if (hipMalloc(ptrs[i], sizes[i]) != hipSuccess ||
             hipMemsetAsync(*ptrs[i], 0, sizes[i], ctx->stream) != hipSuccess) {
             orn_set_err(ctx, ORN_ENOMEM, "store allocation of %zu bytes failed", sizes[i]);
@@ -314,7 +321,16 @@ ornith_moe_store *gpu_moe_store_create(gpu_context *ctx, const ornith_moe_shape 
         }
         st->bytes += sizes[i];
     }
-    if (shape->prefill_layout) {
+    if (cached) {
+        st->cache = orn_cache_create(ctx, shape);
+        st->q6_scmax = (int *)calloc(L, sizeof(int));
+        if (!st->cache || !st->q6_scmax) {
+            if (st->cache) orn_set_err(ctx, ORN_ENOMEM, "store allocation failed");
+            store_free(st);
+            return NULL;
+        }
+        st->bytes += orn_cache_device_bytes(st->cache);
+    } else if (shape->prefill_layout) {
         const size_t LE = L * E1, DH = D * H;
         size_t psz[14] = {LE * DH / 2, LE * DH / 2, LE * DH / 16, LE * DH / 16, LE * DH / 16,
                           LE * DH / 16, LE * DH / 64, LE * DH / 64, LE * DH / 64, LE * DH / 64,
@@ -366,6 +382,36 @@ void gpu_moe_store_destroy(gpu_context *ctx, ornith_moe_store *store)
 size_t gpu_moe_store_bytes(const ornith_moe_store *store) { return store ? store->bytes : 0; }
 
 const ornith_moe_shape *orn_store_shape(const ornith_moe_store *st) { return &st->sh; }
+
+/* Where the experts' decode-layout blocks live: the device arrays of a
+ * resident store, or the host tier of a streamed one (same [L][E+1]
+ * layout; copies to and from either use hipMemcpyDefault). */
+static void expert_arrays(ornith_moe_store *st, uint8_t **g, uint8_t **u, uint8_t **b,
+                          uint16_t **d)
+{
+    if (st->cache) {
+        orn_cache_host_tier(st->cache, g, u, b, d);
+        return;
+    }
+    *g = st->gate;
+    *u = st->up;
+    *b = st->down_body;
+    *d = st->down_d;
+}
+
+/* Largest |Q6_K sub-scale| of n experts' down bodies (208-byte bodies, the
+ * 16 int8 scales at offset 192). */
+static int q6_scmax_of(const uint8_t *body, size_t n_bodies)
+{
+    int mx = 0;
+    for (size_t i = 0; i < n_bodies; ++i)
+        for (int j = 0; j < 16; ++j) {
+            const int v = (int8_t)body[i * 208 + 192 + j];
+            if (v > mx) mx = v;
+            if (-v > mx) mx = -v;
+        }
+    return mx;
+}
 
 /* Permute one expert's GGUF block stream (row-major: block (k, c) at
  * k*NBc + c) into the device's block-column-major order (c*K + k). */
@@ -494,6 +540,14 @@ int gpu_moe_store_set_experts(gpu_context *ctx, ornith_moe_store *st, int layer,
     const size_t slot0 = (size_t)layer * E1 + (size_t)expert_first;
     hipStream_t s = ctx->stream;
     int rc = ORN_OK;
+    uint8_t *a_gate, *a_up, *a_body;
+    uint16_t *a_d;
+    expert_arrays(st, &a_gate, &a_up, &a_body, &a_d);
+    if (st->cache) {  /* the host tier is rewritten: no copy may read it now */
+        if ((rc = orn_cache_quiesce(ctx, st->cache))) return rc;
+        if ((rc = orn_hip_check(ctx, hipStreamSynchronize(s), "set_experts"))) return rc;
+        orn_cache_invalidate(st->cache, layer, expert_first, n);
+    }
     if (matrix != ORN_MAT_DOWN) {
         uint8_t *tmp = (uint8_t *)malloc((size_t)n * nb * 144);
         if (!tmp) return orn_set_err(ctx, ORN_ENOMEM, "host staging");
@@ -502,13 +556,13 @@ int gpu_moe_store_set_experts(gpu_context *ctx, ornith_moe_store *st, int layer,
             if (st->sh.file_layout) memcpy(tmp + i * nb * 144, src, nb * 144);  /* file order */
             else permute_q4k(src, tmp + i * nb * 144, D, H / 256);
         }
-        uint8_t *dst = (matrix == ORN_MAT_GATE ? st->gate : st->up) + slot0 * nb * 144;
-        rc = orn_hip_check(ctx, hipMemcpyAsync(dst, tmp, (size_t)n * nb * 144,
-                                               hipMemcpyHostToDevice, s), "upload q4k");
+        uint8_t *dst = (matrix == ORN_MAT_GATE ? a_gate : a_up) + slot0 * nb * 144;
+        rc = orn_hip_check(ctx, hipMemcpyAsync(dst, tmp, (size_t)n * nb * 144, hipMemcpyDefault,
+                                               s), "upload q4k");
         hipStreamSynchronize(s);
         free(tmp);
-        if (!rc && st->sh.prefill_layout) rc = upload_q4k_prefill(ctx, st, layer, matrix,
-                                                                  expert_first, n, blocks);
+        if (!rc && st->sh.prefill_layout && !st->cache)
+            rc = upload_q4k_prefill(ctx, st, layer, matrix, expert_first, n, blocks);
     } else {
         uint8_t *body = (uint8_t *)malloc((size_t)n * nb * 208);
         uint16_t *dv = (uint16_t *)malloc((size_t)n * nb * 2);
@@ -524,16 +578,22 @@ int gpu_moe_store_set_experts(gpu_context *ctx, ornith_moe_store *st, int layer,
             if (st->sh.file_layout) permute_q6k(src, body + i * nb * 208, dv + i * nb, (int)nb, 1);
             else permute_q6k(src, body + i * nb * 208, dv + i * nb, H, D / 256);
         }
-        rc = orn_hip_check(ctx, hipMemcpyAsync(st->down_body + slot0 * nb * 208, body,
-                                               (size_t)n * nb * 208, hipMemcpyHostToDevice, s),
+        rc = orn_hip_check(ctx, hipMemcpyAsync(a_body + slot0 * nb * 208, body,
+                                               (size_t)n * nb * 208, hipMemcpyDefault, s),
                            "upload q6k");
         if (!rc)
-            rc = orn_hip_check(ctx, hipMemcpyAsync(st->down_d + slot0 * nb, dv, (size_t)n * nb * 2,
-                                                   hipMemcpyHostToDevice, s), "upload q6k d");
+            rc = orn_hip_check(ctx, hipMemcpyAsync(a_d + slot0 * nb, dv, (size_t)n * nb * 2,
+                                                   hipMemcpyDefault, s), "upload q6k d");
         hipStreamSynchronize(s);
+        if (!rc && st->cache) {
+            /* the MFMA layouts are packed on the device when an expert is
+             * loaded into a slot; the path choice needs the scale range now */
+            const int scmax = q6_scmax_of(body, (size_t)n * nb);
+            if (scmax > st->q6_scmax[layer]) st->q6_scmax[layer] = scmax;
+        }
         free(body);
         free(dv);
-        if (!rc && st->sh.prefill_layout)
+        if (!rc && st->sh.prefill_layout && !st->cache)
             rc = upload_q6k_prefill(ctx, st, layer, expert_first, n, blocks);
     }
     return rc;
@@ -604,13 +664,49 @@ int gpu_moe_store_fill_synthetic(gpu_context *ctx, ornith_moe_store *st, int lay
     g.n_experts = E;
     g.has_shared = st->sh.has_shared;
     g.file = st->sh.file_layout;
-    g.gate = st->gate + slot0 * nb * 144;
-    g.up = st->up + slot0 * nb * 144;
-    g.down_body = st->down_body + slot0 * nb * 208;
-    g.down_d = st->down_d + slot0 * nb;
     g.router = st->router_q + (size_t)layer * E * D;
-    int rc = orn_hip_check(ctx, (hipError_t)ornk_synth_layer(&g, s), "synthetic layer");
-    if (rc) return rc;
+    int rc;
+    if (st->cache) {
+        /* generated on the device into a one-layer staging area, then
+         * copied to the host tier */
+        if ((rc = orn_cache_quiesce(ctx, st->cache))) return rc;
+        orn_cache_invalidate(st->cache, layer, 0, E + 1);
+        uint8_t *tmp = NULL;
+        const size_t bytes = S * nb * 500;
+        if (hipMalloc((void **)&tmp, bytes) != hipSuccess)
+            return orn_set_err(ctx, ORN_ENOMEM, "fill_synthetic: %zu bytes of staging", bytes);
+        g.gate = tmp;
+        g.up = tmp + S * nb * 144;
+        g.down_body = tmp + S * nb * 288;
+        g.down_d = (uint16_t *)(tmp + S * nb * 496);
+        rc = orn_hip_check(ctx, (hipError_t)ornk_synth_layer(&g, s), "synthetic layer");
+        uint8_t *a_gate, *a_up, *a_body;
+        uint16_t *a_d;
+        expert_arrays(st, &a_gate, &a_up, &a_body, &a_d);
+        if (!rc)
+            rc = orn_hip_check(ctx, hipMemcpyAsync(a_gate + slot0 * nb * 144, g.gate,
+                                                   S * nb * 144, hipMemcpyDefault, s), "tier");
+        if (!rc)
+            rc = orn_hip_check(ctx, hipMemcpyAsync(a_up + slot0 * nb * 144, g.up, S * nb * 144,
+                                                   hipMemcpyDefault, s), "tier");
+        if (!rc)
+            rc = orn_hip_check(ctx, hipMemcpyAsync(a_body + slot0 * nb * 208, g.down_body,
+                                                   S * nb * 208, hipMemcpyDefault, s), "tier");
+        if (!rc)
+            rc = orn_hip_check(ctx, hipMemcpyAsync(a_d + slot0 * nb, g.down_d, S * nb * 2,
+                                                   hipMemcpyDefault, s), "tier");
+        if (!rc) rc = orn_hip_check(ctx, hipStreamSynchronize(s), "synthetic layer");
+        hipFree(tmp);
+        if (rc) return rc;
+        st->q6_scmax[layer] = q6_scmax_of(a_body + slot0 * nb * 208, (size_t)E1 * nb);
+    } else {
+        g.gate = st->gate + slot0 * nb * 144;
+        g.up = st->up + slot0 * nb * 144;
+        g.down_body = st->down_body + slot0 * nb * 208;
+        g.down_d = st->down_d + slot0 * nb;
+        rc = orn_hip_check(ctx, (hipError_t)ornk_synth_layer(&g, s), "synthetic layer");
+        if (rc) return rc;
+    }
     if (zipf_s > 0.0f) {
         float *b = (float *)malloc((size_t)E * sizeof(float));
         if (!b) return orn_set_err(ctx, ORN_ENOMEM, "host staging");
@@ -623,7 +719,7 @@ int gpu_moe_store_fill_synthetic(gpu_context *ctx, ornith_moe_store *st, int lay
         if (rc) return rc;
     }
     st->has_bias[layer] = zipf_s > 0.0f ? 1 : 0;
-    if (st->sh.prefill_layout) {
+    if (st->sh.prefill_layout && !st->cache) {
         const size_t DH = D * H;
         ornk_pack_args pa;
         memset(&pa, 0, sizeof pa);
@@ -681,12 +777,15 @@ int gpu_moe_store_get_experts(gpu_context *ctx, ornith_moe_store *st, int layer,
     hipStream_t s = ctx->stream;
     uint8_t *out = (uint8_t *)blocks;
     int rc;
+    uint8_t *a_gate, *a_up, *a_body;
+    uint16_t *a_d;
+    expert_arrays(st, &a_gate, &a_up, &a_body, &a_d);
     if (matrix != ORN_MAT_DOWN) {
-        const uint8_t *src = (matrix == ORN_MAT_GATE ? st->gate : st->up) + slot0 * nb * 144;
+        const uint8_t *src = (matrix == ORN_MAT_GATE ? a_gate : a_up) + slot0 * nb * 144;
         uint8_t *tmp = (uint8_t *)malloc((size_t)n * nb * 144);
         if (!tmp) return orn_set_err(ctx, ORN_ENOMEM, "host staging");
-        rc = orn_hip_check(ctx, hipMemcpyAsync(tmp, src, (size_t)n * nb * 144,
-                                               hipMemcpyDeviceToHost, s), "download q4k");
+        rc = orn_hip_check(ctx, hipMemcpyAsync(tmp, src, (size_t)n * nb * 144, hipMemcpyDefault,
+                                               s), "download q4k");
         if (!rc) rc = orn_hip_check(ctx, hipStreamSynchronize(s), "download q4k");
         const int K = D, NBc = H / 256;
         for (int i = 0; i < n && !rc; ++i) {
@@ -710,12 +809,11 @@ int gpu_moe_store_get_experts(gpu_context *ctx, ornith_moe_store *st, int layer,
         free(dv);
         return orn_set_err(ctx, ORN_ENOMEM, "host staging");
     }
-    rc = orn_hip_check(ctx, hipMemcpyAsync(body, st->down_body + slot0 * nb * 208,
-                                           (size_t)n * nb * 208, hipMemcpyDeviceToHost, s),
-                       "download q6k");
+    rc = orn_hip_check(ctx, hipMemcpyAsync(body, a_body + slot0 * nb * 208, (size_t)n * nb * 208,
+                                           hipMemcpyDefault, s), "download q6k");
     if (!rc)
-        rc = orn_hip_check(ctx, hipMemcpyAsync(dv, st->down_d + slot0 * nb, (size_t)n * nb * 2,
-                                               hipMemcpyDeviceToHost, s), "download q6k d");
+        rc = orn_hip_check(ctx, hipMemcpyAsync(dv, a_d + slot0 * nb, (size_t)n * nb * 2,
+                                               hipMemcpyDefault, s), "download q6k d");
     if (!rc) rc = orn_hip_check(ctx, hipStreamSynchronize(s), "download q6k");
     const int K = file ? (int)nb : H, NBc = file ? 1 : D / 256;
     for (int i = 0; i < n && !rc; ++i)
@@ -975,10 +1073,12 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     a.rows_max = p.rows_max;
     a.items_max = p.items_max;
     a.tchunk = p.tchunk;
-    a.gate = st->gate + (size_t)layer * E1nb * 144;
-    a.up = st->up + (size_t)layer * E1nb * 144;
-    a.down_body = st->down_body + (size_t)layer * E1nb * 208;
-    a.down_d = st->down_d + (size_t)layer * E1nb;
+    if (!st->cache) {  /* a streamed store's slots are set after the dispatch */
+        a.gate = st->gate + (size_t)layer * E1nb * 144;
+        a.up = st->up + (size_t)layer * E1nb * 144;
+        a.down_body = st->down_body + (size_t)layer * E1nb * 208;
+        a.down_d = st->down_d + (size_t)layer * E1nb;
+    }
     a.router = st->router_q + (size_t)layer * E * D;
     a.bias = st->has_bias[layer] ? st->bias + (size_t)layer * E : NULL;
     a.norm_w = st->norm + (size_t)layer * D;
@@ -1001,7 +1101,7 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     a.mid = (float *)(ws + o_mid);
     a.dn_part = (float *)(ws + o_dn);
     a.use_mfma = use_mfma;
-    if (use_mfma) {
+    if (use_mfma && !st->cache) {  /* a streamed store's slot arrays come from the cache */
         const size_t slot0 = (size_t)layer * E1, DH = (size_t)D * H;
         for (int m = 0; m < 2; ++m) {
             a.gu_pf.pq[m] = (const uint32_t *)((const uint8_t *)st->pq[m] + slot0 * (DH / 2));
@@ -1015,6 +1115,8 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
         a.dn_pf.dsc = (const uint16_t *)((const uint8_t *)st->dsc + slot0 * (DH / 8));
         a.dn_pf.dd = (const float *)((const uint8_t *)st->dd + slot0 * (DH / 64));
         a.dn_pf.dmax = st->dmax + slot0 * 3;
+    }
+    if (use_mfma) {
         a.x_amax = (float *)(ws + o_xamax);
         a.router_amax = ornk_router_pc_supported(T, D);
         a.mid_amax = (float *)(ws + o_midamax);
@@ -1039,6 +1141,9 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
         return rc;
     if ((rc = launch_k(ctx, "moe_route", ornk_moe_route, &a))) return rc;
     if ((rc = launch_k(ctx, "moe_dispatch", ornk_moe_dispatch, &a))) return rc;
+    /* streamed experts: read the dispatch's experts back, load the missing
+     * ones into slots and renumber the work items (host round trip) */
+    if (st->cache && (rc = orn_cache_prepare(ctx, st->cache, layer, &a))) return rc;
     if (file) {
         if ((rc = launch_k(ctx, "moe_file_prep_x", ornk_file_prep_x, &a))) return rc;
         if ((rc = launch_k(ctx, "moe_gateup_file", ornk_file_gateup, &a))) return rc;
@@ -1197,6 +1302,10 @@ int gpu_moe_forward(gpu_context *ctx, ornith_moe_store *st, int layer, const gpu
                                    "gpu_moe_forward");
     if (ok <= 0) return ok;
     const unsigned flags = opts ? opts->flags : 0u;
+    if (st->cache && (flags & ORN_MOE_GRAPH))
+        return orn_set_err(ctx, ORN_EUNSUPPORTED,
+                           "gpu_moe_forward: a streamed store reads its routing back on the "
+                           "host; ORN_MOE_GRAPH cannot capture that");
     fwd_arg a = {layer,
                  n_tokens,
                  (const float *)x->dev,
@@ -1292,6 +1401,10 @@ int gpu_moe_forward_stack(gpu_context *ctx, ornith_moe_store *st, int first_laye
         return orn_set_err(ctx, ORN_EINVAL, "gpu_moe_forward_stack: buffer too small");
     if (n_tokens == 0 || n_layers == 0) return ORN_OK;
     const unsigned flags = opts ? opts->flags : 0u;
+    if (st->cache && (flags & ORN_MOE_GRAPH))
+        return orn_set_err(ctx, ORN_EUNSUPPORTED,
+                           "gpu_moe_forward_stack: a streamed store reads its routing back on "
+                           "the host; ORN_MOE_GRAPH cannot capture that");
     stack_arg a = {first_layer, n_layers, n_tokens, (float *)x->dev, (float *)tmp->dev,
                    {opts ? opts->route_mode : ORN_ROUTE_RENORM,
                     flags | ORN_MOE_NORM | ORN_MOE_ASYNC, 0, 0}};
@@ -1339,5 +1452,36 @@ int gpu_moe_last_stats(gpu_context *ctx, int *n_slots, int *n_rows, int *n_liter
     if (n_slots) *n_slots = ctx->ctl_host[0];
     if (n_rows) *n_rows = ctx->ctl_host[2];
     if (n_literal) *n_literal = ctx->ctl_host[3];
+    return ORN_OK;
+}
+
+/* ---------------------------------------------------------------------------
+ * Streamed experts (cache.c): prefetch, pinning, statistics
+ * ------------------------------------------------------------------------- */
+int gpu_moe_store_prefetch(gpu_context *ctx, ornith_moe_store *st, int layer, const int *experts,
+                           int n)
+{
+    if (!ctx) return ORN_EINVAL;
+    if (!st || !st->cache)
+        return orn_set_err(ctx, ORN_EINVAL, "gpu_moe_store_prefetch: not a streamed store");
+    return orn_cache_prefetch(ctx, st->cache, layer, experts, n);
+}
+
+int gpu_moe_store_pin(gpu_context *ctx, ornith_moe_store *st, int layer, const int *experts, int n,
+                      int pin)
+{
+    if (!ctx) return ORN_EINVAL;
+    if (!st || !st->cache)
+        return orn_set_err(ctx, ORN_EINVAL, "gpu_moe_store_pin: not a streamed store");
+    return orn_cache_pin(ctx, st->cache, layer, experts, n, pin);
+}
+
+int gpu_moe_store_cache_stats(gpu_context *ctx, ornith_moe_store *st, ornith_moe_cache_stats *out,
+                              int reset)
+{
+    if (!ctx) return ORN_EINVAL;
+    if (!st || !st->cache)
+        return orn_set_err(ctx, ORN_EINVAL, "gpu_moe_store_cache_stats: not a streamed store");
+    orn_cache_stats(st->cache, out, reset);
     return ORN_OK;
 }

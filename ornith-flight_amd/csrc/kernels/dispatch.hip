@@ -236,7 +236,27 @@ __global__ void __launch_bounds__(64)
                  row_token, pair_row, items, items_max, nullptr);
 }
 
+// Expert ids -> cache slots, in place, for a store that streams its experts
+// through a fixed set of device slots: items[i].w for the forward's items and
+// slot_expert[s] for its slots.  Every id the dispatch wrote has an entry
+// (the host filled remap from slot_expert itself).
+__global__ void k_remap_items(int4 *items, int *slot_expert, const int *ctl,
+                              const int *__restrict__ remap, int items_max, int slots_max)
+{
+    const int n_items = min(ctl[1], items_max), n_slots = min(ctl[0], slots_max);
+    for (int i = threadIdx.x; i < n_items; i += blockDim.x) items[i].w = remap[items[i].w];
+    for (int i = threadIdx.x; i < n_slots; i += blockDim.x) slot_expert[i] = remap[slot_expert[i]];
+}
+
 }  // namespace
+
+extern "C" int ornk_remap_items(int *items, int *slot_expert, const int *ctl, const int *remap,
+                                int items_max, int slots_max, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_remap_items, dim3(1), dim3(1024), 0, s, reinterpret_cast<int4 *>(items),
+                       slot_expert, ctl, remap, items_max, slots_max);
+    return hipGetLastError();
+}
 
 // Selection + dispatch step of the MoE forward (after the router).
 extern "C" int ornk_moe_dispatch(const ornk_moe_args *a, hipStream_t s)

@@ -80,8 +80,28 @@ typedef struct {
     float *dd;
     float *dmax;
     int *scmax;
+    /* NULL: slots [0, n_e) of the arrays above.  Else the n_e slot numbers
+     * to pack (device-readable); the caller zeroes their dmax entries. */
+    const int *slots;
 } ornk_pack_args;
 int ornk_pack_prefill(const ornk_pack_args *a, hipStream_t s);
+
+/* Expert loads of a streamed store (cache.hip): for i < n, expert loads[2i]
+ * of the host tier (device addresses of pinned host memory, [L*(E+1)]
+ * experts) is copied into device slot loads[2i+1]; slots_out[i] receives
+ * the slot and, with dmax, the slot's three dmax entries are zeroed. */
+typedef struct {
+    const int *loads;
+    int n;
+    const uint8_t *h_gate, *h_up, *h_body;
+    const uint16_t *h_d;
+    uint8_t *gate, *up, *body;
+    uint16_t *d;
+    int *slots_out;
+    float *dmax;
+    size_t nb;
+} ornk_gather_args;
+int ornk_cache_gather(const ornk_gather_args *a, hipStream_t s);
 
 /* ---- GGUF dequant (gguf.c:605-711 semantics) ----------------------------- */
 int ornk_dequant(const void *src, int type, uint64_t n_elems, float *dst, hipStream_t s);
@@ -185,6 +205,10 @@ int ornk_router_pc_supported(int T, int D);
  * skipped): one token, 16 gate/up split-K slices, 8-step down slices. */
 int ornk_down_dec_fuses_mid(int T, int H, int ks_gu, int ks_dn);
 int ornk_moe_dispatch(const ornk_moe_args *a, hipStream_t s);
+/* items[i].w (i < min(ctl[1], items_max)) and slot_expert[s] (s < min(ctl[0],
+ * slots_max)) replaced by remap[] of themselves: expert ids -> cache slots. */
+int ornk_remap_items(int *items, int *slot_expert, const int *ctl, const int *remap,
+                     int items_max, int slots_max, hipStream_t s);
 int ornk_moe_gateup(const ornk_moe_args *a, hipStream_t s);
 int ornk_moe_mid(const ornk_moe_args *a, hipStream_t s);
 int ornk_moe_down(const ornk_moe_args *a, hipStream_t s);

@@ -196,20 +196,32 @@ __device__ __forceinline__ int q6_at(const uint8_t *ql, const uint8_t *qh, int p
 }
 
 // Non-negative floats order like their bit patterns: max by integer atomics.
+// One atomic per wave: every wave of the packers below lies inside one expert
+// (its K * NB threads are a multiple of 64), so lane 0 adds the wave's max.
 __device__ __forceinline__ void atomic_max_abs(float *p, float v)
 {
-    atomicMax(reinterpret_cast<unsigned int *>(p), __float_as_uint(fabsf(v)));
+    unsigned u = __float_as_uint(fabsf(v));
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) u = max(u, (unsigned)__shfl_xor((int)u, o, 64));
+    if ((threadIdx.x & 63) == 0) atomicMax(reinterpret_cast<unsigned int *>(p), u);
+}
+
+__device__ __forceinline__ void atomic_max_wave(int *p, int v)
+{
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
+    if ((threadIdx.x & 63) == 0) atomicMax(p, v);
 }
 
 // Q4_K nibble words: thread = one 32-bit word (8 values of one column).
 // Blocks: [n_e][NB][K] in vec@mat store order (block (k, b) at b*K + k).
 __global__ void k_pack_q4k_words(const uint8_t *__restrict__ blocks, uint32_t *__restrict__ qn,
-                                 int n_e, int K, int NB)
+                                 int n_e, int K, int NB, const int *__restrict__ slots)
 {
     const size_t per_e = (size_t)K * NB * 32;  // words per expert: K/32 * NB * 4 * 64 * 4
     const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= per_e * (size_t)n_e) return;
-    const int e = (int)(t / per_e);
+    const int e = slots ? slots[t / per_e] : (int)(t / per_e);
     size_t w = t % per_e;
     const int ntl = (int)(w % 4);
     w /= 4;
@@ -235,12 +247,12 @@ __global__ void k_pack_q4k_words(const uint8_t *__restrict__ blocks, uint32_t *_
 __global__ void k_pack_q4k_scales(const uint8_t *__restrict__ blocks, uint16_t *__restrict__ sc,
                                   uint16_t *__restrict__ mn, float *__restrict__ d,
                                   float *__restrict__ dm, float *__restrict__ dmax, int dmax_col,
-                                  int n_e, int K, int NB)
+                                  int n_e, int K, int NB, const int *__restrict__ slots)
 {
     const size_t per_e = (size_t)K * NB;
     const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= per_e * (size_t)n_e) return;
-    const int e = (int)(t / per_e);
+    const int e = slots ? slots[t / per_e] : (int)(t / per_e);
     const int q = (int)(t % per_e);
     const int b = q / K, k = q % K;
     const uint8_t *blk = blocks + ((size_t)e * per_e + q) * ORN_Q4K_BYTES;
@@ -270,12 +282,12 @@ __global__ void k_pack_q4k_scales(const uint8_t *__restrict__ blocks, uint16_t *
 // Q6_K q + 32 bytes: thread = one 8-byte group (8 values of one column).
 // Bodies: [n_e][NB][K] x 208 B in store order, d separately.
 __global__ void k_pack_q6k_bytes(const uint8_t *__restrict__ body, uint8_t *__restrict__ qb,
-                                 int n_e, int K, int NB)
+                                 int n_e, int K, int NB, const int *__restrict__ slots)
 {
     const size_t per_e = (size_t)K * NB * 32;  // 8-byte groups per expert
     const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= per_e * (size_t)n_e) return;
-    const int e = (int)(t / per_e);
+    const int e = slots ? slots[t / per_e] : (int)(t / per_e);
     size_t w = t % per_e;
     const int ntl = (int)(w % 4);
     w /= 4;
@@ -302,12 +314,12 @@ __global__ void k_pack_q6k_bytes(const uint8_t *__restrict__ body, uint8_t *__re
 __global__ void k_pack_q6k_scales(const uint8_t *__restrict__ body, const uint16_t *__restrict__ dd,
                                   uint16_t *__restrict__ sc, float *__restrict__ d,
                                   float *__restrict__ dmax, int *__restrict__ scmax, int n_e,
-                                  int K, int NB)
+                                  int K, int NB, const int *__restrict__ slots)
 {
     const size_t per_e = (size_t)K * NB;
     const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= per_e * (size_t)n_e) return;
-    const int e = (int)(t / per_e);
+    const int e = slots ? slots[t / per_e] : (int)(t / per_e);
     const int q = (int)(t % per_e);
     const int b = q / K, k = q % K;
     const uint8_t *blk = body + ((size_t)e * per_e + q) * 208;
@@ -322,7 +334,7 @@ __global__ void k_pack_q6k_scales(const uint8_t *__restrict__ body, const uint16
         mx = max(mx, v < 0 ? -v : v);
         sc[(size_t)e * (per_e * 16) + (((size_t)kt * NB + b) * 16 + nt) * 32 + kk] = int_half(v);
     }
-    atomicMax(scmax, mx);
+    atomic_max_wave(scmax, mx);
 }
 
 inline dim3 grid_for(size_t n) { return dim3((unsigned)((n + 255) / 256)); }
@@ -352,18 +364,20 @@ extern "C" int ornk_pack_prefill(const ornk_pack_args *a, hipStream_t s)
     const int D = a->D, H = a->H, n = a->n_e;
     const size_t DH = (size_t)D * H;
     if (D % 256 || H % 256 || n < 1) return hipErrorInvalidValue;
-    hipMemsetAsync(a->dmax, 0, (size_t)n * 3 * sizeof(float), s);
+    // with a slot list the caller has zeroed the slots' dmax entries
+    if (!a->slots) hipMemsetAsync(a->dmax, 0, (size_t)n * 3 * sizeof(float), s);
     hipMemsetAsync(a->scmax, 0, sizeof(int), s);
     for (int m = 0; m < 2; ++m) {
         hipLaunchKernelGGL(k_pack_q4k_words, grid_for((size_t)n * DH / 8), dim3(256), 0, s,
-                           a->gu[m], a->pq[m], n, D, H / 256);
+                           a->gu[m], a->pq[m], n, D, H / 256, a->slots);
         hipLaunchKernelGGL(k_pack_q4k_scales, grid_for((size_t)n * DH / 256), dim3(256), 0, s,
                            a->gu[m], a->psc[m], a->pmn[m], a->pd[m], a->pdm[m], a->dmax, m, n, D,
-                           H / 256);
+                           H / 256, a->slots);
     }
     hipLaunchKernelGGL(k_pack_q6k_bytes, grid_for((size_t)n * DH / 8), dim3(256), 0, s,
-                       a->down_body, a->dq, n, H, D / 256);
+                       a->down_body, a->dq, n, H, D / 256, a->slots);
     hipLaunchKernelGGL(k_pack_q6k_scales, grid_for((size_t)n * DH / 256), dim3(256), 0, s,
-                       a->down_body, a->down_d, a->dsc, a->dd, a->dmax, a->scmax, n, H, D / 256);
+                       a->down_body, a->down_d, a->dsc, a->dd, a->dmax, a->scmax, n, H, D / 256,
+                       a->slots);
     return hipGetLastError();
 }

@@ -52,6 +52,7 @@ EXPORTED = [
     "orn_gguf_read_tensor_data", "orn_gguf_read_tensor_bytes", "orn_gguf_get_param_u32",
     "gpu_dequantize_tensor_gguf", "gpu_dequantize_expert_slice_gguf", "gpu_moe_store_load_gguf",
     "gpu_deltanet_step_gated", "gpu_kv_cache_append",
+    "gpu_moe_store_prefetch", "gpu_moe_store_pin", "gpu_moe_store_cache_stats",
 ]
 
 
@@ -84,7 +85,19 @@ class GGUFValue(C.Structure):
 
 class MoEShape(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("n_layers", "d_model", "hidden", "n_experts", "top_k",
-                                       "has_shared", "prefill_layout", "file_layout")]
+                                       "has_shared", "prefill_layout", "file_layout",
+                                       "cache_slots")]
+
+
+class CacheStats(C.Structure):
+    """ornith_moe_cache_stats (the reference's cache_stats, memory.h:40-55)."""
+    _fields_ = [("hits", C.c_uint64), ("misses", C.c_uint64), ("evictions", C.c_uint64),
+                ("prefetches", C.c_uint64), ("prefetch_hits", C.c_uint64),
+                ("bytes_uploaded", C.c_uint64), ("slots", C.c_int), ("resident", C.c_int),
+                ("pinned", C.c_int), ("device_bytes", C.c_size_t), ("host_bytes", C.c_size_t)]
+
+    def as_dict(self):
+        return {n: getattr(self, n) for n, _ in self._fields_}
 
 
 class MoEOpts(C.Structure):
@@ -170,6 +183,9 @@ def lib():
         "gpu_moe_store_load_gguf": (i, [vp, vp, vp, i, i, i]),
         "gpu_deltanet_step_gated": (i, [vp, vp, vp, vp, vp, vp, i, f]),
         "gpu_kv_cache_append": (i, [vp, vp, vp, vp, vp, i, i]),
+        "gpu_moe_store_prefetch": (i, [vp, vp, i, vp, i]),
+        "gpu_moe_store_pin": (i, [vp, vp, i, vp, i, i]),
+        "gpu_moe_store_cache_stats": (i, [vp, vp, C.POINTER(CacheStats), i]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -309,12 +325,13 @@ class Context:
 
 class Store:
     def __init__(self, ctx: Context, n_layers, D, H, E, k, has_shared=True, prefill_layout=True,
-                 file_layout=False):
+                 file_layout=False, cache_slots=0):
         """file_layout: experts and router in GGUF file orientation (input index
-        fastest); needs prefill_layout=False."""
+        fastest); needs prefill_layout=False.  cache_slots > 0: experts in a
+        host tier, streamed through that many device slots."""
         self.ctx = ctx
         self.shape = MoEShape(n_layers, D, H, E, k, 1 if has_shared else 0,
-                              1 if prefill_layout else 0, 1 if file_layout else 0)
+                              1 if prefill_layout else 0, 1 if file_layout else 0, cache_slots)
         self.ptr = lib().gpu_moe_store_create(ctx.ptr, C.byref(self.shape))
         if not self.ptr:
             raise RuntimeError("gpu_moe_store_create failed: " + ctx.last_error())
@@ -393,6 +410,22 @@ class Store:
 
     def bytes(self):
         return lib().gpu_moe_store_bytes(self.ptr)
+
+    def prefetch(self, layer, experts):
+        e = np.ascontiguousarray(experts, np.int32)
+        self.ctx.check(lib().gpu_moe_store_prefetch(self.ctx.ptr, self.ptr, layer, _p(e), e.size),
+                       "prefetch")
+
+    def pin(self, layer, experts, pin=True):
+        e = np.ascontiguousarray(experts, np.int32)
+        self.ctx.check(lib().gpu_moe_store_pin(self.ctx.ptr, self.ptr, layer, _p(e), e.size,
+                                               1 if pin else 0), "pin")
+
+    def cache_stats(self, reset=False):
+        st = CacheStats()
+        self.ctx.check(lib().gpu_moe_store_cache_stats(self.ctx.ptr, self.ptr, C.byref(st),
+                                                       1 if reset else 0), "cache_stats")
+        return st.as_dict()
 
     def close(self):
         if self.ptr:
