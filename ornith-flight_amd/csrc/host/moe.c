@@ -930,7 +930,10 @@ static plan_t make_plan_file(const ornith_moe_shape *sh, int T)
     plan_t p;
     memset(&p, 0, sizeof p);
     const int k = sh->top_k, E = sh->n_experts, D = sh->d_model, H = sh->hidden;
-    p.tchunk = 16;
+    /* items of up to 64 rows (four row tiles per work group, each expert's
+     * weights streamed once per 64 rows) once routed experts average 16
+     * rows or more; 16 below, where most items hold a row or two */
+    p.tchunk = T * k >= 16 * E ? 64 : 16;
     p.rows_max = T * k + (sh->has_shared ? T : 0);
     const int max_slots = (T * k < E ? T * k : E) + (sh->has_shared ? 1 : 0);
     p.items_max = max_slots + (p.rows_max + p.tchunk - 1) / p.tchunk;

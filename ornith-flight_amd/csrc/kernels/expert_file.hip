@@ -58,18 +58,31 @@ __device__ __forceinline__ float prep_scale(float amax)
 // tiles alternate, so one barrier per super-block suffices: a wave writes
 // tile (s+1)&1 only after every wave has passed the barrier of super-block
 // s, which each reaches after its reads of that tile for super-block s-1.
+//
+// Prefill-sized work items (up to 64 rows, RT = 4 row tiles of 16) stage one
+// tile of 64 rows (68 KB) per work group instead of two alternating ones of
+// 16: the tile is then rewritten only after a barrier that every wave
+// reaches once done with the previous super-block, so that two work groups
+// still fit in a CU's LDS.  Each converted weight operand then feeds RT row
+// tiles, and each expert's weights stream once per 64 rows.
 #define ORN_FAS 264
-typedef _Float16 FileTile[2][16][ORN_FAS];
+template <int RT>
+struct FileTileT {
+    _Float16 v[2][16 * RT][ORN_FAS];
+};
+typedef FileTileT<1> FileTile;
 
-__device__ __forceinline__ void stage_tile(FileTile &As, const uint32_t *__restrict__ xh,
+template <int RT>
+__device__ __forceinline__ void stage_tile(FileTileT<RT> &As, const uint32_t *__restrict__ xh,
                                            const uint32_t *__restrict__ xl, const int *src,
                                            int K, int s)
 {
+    if (RT > 1) __syncthreads();  // one tile: every wave is done with the last one
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {  // 2 planes x 16 rows x 32 chunks of 16 B
+    for (int i = 0; i < 4 * RT; ++i) {  // 2 planes x 16RT rows x 32 chunks of 16 B
         const int idx = threadIdx.x + 256 * i;
-        const int plane = idx >> 9, row = (idx >> 5) & 15, ch = idx & 31;
-        *reinterpret_cast<uint4 *>(&As[plane][row][8 * ch]) = *reinterpret_cast<const uint4 *>(
+        const int plane = idx / (512 * RT), row = (idx >> 5) % (16 * RT), ch = idx & 31;
+        *reinterpret_cast<uint4 *>(&As.v[plane][row][8 * ch]) = *reinterpret_cast<const uint4 *>(
             (plane ? xl : xh) + (size_t)src[row] * (K >> 1) + 128 * s + 4 * ch);
     }
     __syncthreads();
@@ -136,15 +149,22 @@ __global__ void __launch_bounds__(256)
 }
 
 // ---------------------------------------------------------------------------
-// Gate/up, Q4_K.  Logical tile = (item * ks + kslice) * (2H/256) + cb; wave
-// w of the work group covers output columns cb*256 + 64w + 16ct + c (ct <
+// Gate/up, Q4_K.  Logical tile = (item * ks + kslice) * NCB + cb; wave w of
+// the work group covers output columns cb*64F + 16Fw + 16ct + c (ct < F =
 // ORN_FCT column tiles, c < 16) of the concatenated [gate | up] outputs,
 // over super-blocks kslice*nsb .. +nsb; each activation operand feeds the
 // ORN_FCT tiles.  Output gu[kslice][row][2H].
 // ---------------------------------------------------------------------------
-#define ORN_FCT 4
+// Column tiles per wave: 4 for 16-row items; 2 for 64-row items, whose
+// accumulators (4 row tiles) would otherwise leave one wave per SIMD.
+template <int RT>
+constexpr int gu_fct()
+{
+    return RT == 1 ? 4 : 2;
+}
 
-__global__ void __launch_bounds__(256)
+template <int RT>
+__global__ void __launch_bounds__(256, 2)
     k_gu_file(const uint8_t *__restrict__ gate, const uint8_t *__restrict__ up,
               const uint32_t *__restrict__ xh, const uint32_t *__restrict__ xl,
               const float *__restrict__ xinv, const uint16_t *__restrict__ sh,
@@ -152,7 +172,8 @@ __global__ void __launch_bounds__(256)
               const int4 *__restrict__ items, const int *__restrict__ row_token,
               float *__restrict__ gu, int D, int H, int ks, int rows_max)
 {
-    const int NCB = (2 * H) >> 8;
+    constexpr int ORN_FCT = gu_fct<RT>();
+    const int NCB = (2 * H) / (64 * ORN_FCT);
     const int per_item = NCB * ks;
     const int n_live = ctl[1] * per_item;
     if ((int)blockIdx.x >= n_live) return;
@@ -161,24 +182,33 @@ __global__ void __launch_bounds__(256)
     const int kslice = (tile / NCB) % ks;
     const int4 itm = items[tile / per_item];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, c = lane & 15;
-    const int col0 = cb * 256 + 64 * wave;  // the wave's 64 columns lie in one matrix
+    // the wave's 16 * ORN_FCT columns lie in one matrix
+    const int col0 = cb * (64 * ORN_FCT) + 16 * ORN_FCT * wave;
     const int m = col0 >= H, h0 = col0 - m * H + c;
     const int NSB = D >> 8, nsb = NSB / ks, s0 = kslice * nsb;
     const size_t rstride = (size_t)NSB * 144;  // bytes per file row
     const uint8_t *rowp = (m ? up : gate) + ((size_t)itm.w * H + h0) * rstride;  // tile ct: + 16ct rows
     const int nrows = itm.z;
-    const int tok = row_token[itm.y + (c < nrows ? c : nrows - 1)];  // A row = c
-    __shared__ __align__(16) FileTile Ab[2];
-    __shared__ int src[16];
-    if (threadIdx.x < 16)
+    const int nrt = RT == 1 ? 1 : (nrows + 15) >> 4;  // live row tiles
+    constexpr int NB = RT == 1 ? 2 : 1;                // activation tiles in LDS
+    __shared__ __align__(16) FileTileT<RT> Ab[NB];
+    __shared__ int src[16 * RT];
+    if (threadIdx.x < 16 * RT)
         src[threadIdx.x] = row_token[itm.y + ((int)threadIdx.x < nrows ? (int)threadIdx.x : nrows - 1)];
     __syncthreads();
-    const uint16_t *sah = sh + (size_t)tok * (D >> 5);
-    const uint16_t *sal = sl + (size_t)tok * (D >> 5);
-
-    v4f acc[ORN_FCT];
+    const uint16_t *sah[RT], *sal[RT];  // A row 16rt + c of the mins operand
 #pragma unroll
-    for (int ct = 0; ct < ORN_FCT; ++ct) acc[ct] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+    for (int rt = 0; rt < RT; ++rt) {
+        const int tok = src[16 * rt + c];
+        sah[rt] = sh + (size_t)tok * (D >> 5);
+        sal[rt] = sl + (size_t)tok * (D >> 5);
+    }
+
+    v4f acc[RT][ORN_FCT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < ORN_FCT; ++ct) acc[rt][ct] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
     for (int s = s0; s < s0 + nsb; ++s) {
         uint4 hd[ORN_FCT], w[ORN_FCT][2];
 #pragma unroll
@@ -188,11 +218,13 @@ __global__ void __launch_bounds__(256)
             w[ct][0] = *reinterpret_cast<const uint4 *>(blk + 16 + 16 * g);
             w[ct][1] = *reinterpret_cast<const uint4 *>(blk + 80 + 16 * g);
         }
-        FileTile &As = Ab[s & 1];
-        stage_tile(As, xh, xl, src, D, s);
-        v4f P[ORN_FCT];
+        FileTileT<RT> &As = Ab[NB == 2 ? (s & 1) : 0];
+        stage_tile<RT>(As, xh, xl, src, D, s);
+        v4f P[RT][ORN_FCT];
 #pragma unroll
-        for (int ct = 0; ct < ORN_FCT; ++ct) P[ct] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < ORN_FCT; ++ct) P[rt][ct] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int L = 0; L < 2; ++L) {
             // this lane's 16 bytes: chunk p = 2L + g/2 (sub-blocks 2p low
@@ -202,8 +234,14 @@ __global__ void __launch_bounds__(256)
             for (int t = 0; t < 4; ++t) {
                 const int j = 2 * p + (t >> 1);
                 const int kl = 32 * j + 16 * (g & 1) + 8 * (t & 1);  // k - 256 s
-                const v8h xa = *reinterpret_cast<const v8h *>(&As[0][c][kl]);
-                const v8h xb = *reinterpret_cast<const v8h *>(&As[1][c][kl]);
+                v8h xa[RT], xb[RT];
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+                    if (rt < nrt) {
+                        xa[rt] = *reinterpret_cast<const v8h *>(&As.v[0][16 * rt + c][kl]);
+                        xb[rt] = *reinterpret_cast<const v8h *>(&As.v[1][16 * rt + c][kl]);
+                    }
+                }
                 const int sft = (t >> 1) ? 4 : 0;
 #pragma unroll
                 for (int ct = 0; ct < ORN_FCT; ++ct) {
@@ -221,16 +259,26 @@ __global__ void __launch_bounds__(256)
                     for (int i = 0; i < 4; ++i)
                         o[i] = as_u32(__builtin_elementwise_fma(as_v2h(pr[i]), sv, ns));
                     const v8h bq = to_v8h(o[0], o[1], o[2], o[3]);
-                    P[ct] = mfma(xa, bq, P[ct]);
-                    P[ct] = mfma(xb, bq, P[ct]);
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt) {
+                        if (rt < nrt) {
+                            P[rt][ct] = mfma(xa[rt], bq, P[rt][ct]);
+                            P[rt][ct] = mfma(xb[rt], bq, P[rt][ct]);
+                        }
+                    }
                 }
             }
         }
         // mins: k = sub-block e of this super-block on the g == 0 lanes
-        uint4 mh = make_uint4(0u, 0u, 0u, 0u), ml = mh;
-        if (g == 0) {
-            mh = *reinterpret_cast<const uint4 *>(sah + 8 * s);
-            ml = *reinterpret_cast<const uint4 *>(sal + 8 * s);
+        uint4 mh[RT], ml[RT];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            mh[rt] = make_uint4(0u, 0u, 0u, 0u);
+            ml[rt] = mh[rt];
+            if (g == 0 && rt < nrt) {
+                mh[rt] = *reinterpret_cast<const uint4 *>(sah[rt] + 8 * s);
+                ml[rt] = *reinterpret_cast<const uint4 *>(sal[rt] + 8 * s);
+            }
         }
 #pragma unroll
         for (int ct = 0; ct < ORN_FCT; ++ct) {
@@ -250,32 +298,40 @@ __global__ void __launch_bounds__(256)
                     o[i] = as_u32(as_v2h(0x64006400u | mv[2 * i] | (mv[2 * i + 1] << 16)) + off);
                 mb = make_uint4(o[0], o[1], o[2], o[3]);
             }
-            v4f Pm = {0.0f, 0.0f, 0.0f, 0.0f};
-            Pm = mfma(__builtin_bit_cast(v8h, mh), __builtin_bit_cast(v8h, mb), Pm);
-            Pm = mfma(__builtin_bit_cast(v8h, ml), __builtin_bit_cast(v8h, mb), Pm);
             const float d = orn_half_to_float(hd[ct].x & 0xFFFFu);
             const float dm32 = -32.0f * orn_half_to_float(hd[ct].x >> 16);  // sums stored / 32
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                acc[ct][r] = fmaf(d, P[ct][r], acc[ct][r]);
-                acc[ct][r] = fmaf(dm32, Pm[r], acc[ct][r]);
+            for (int rt = 0; rt < RT; ++rt) {
+                if (rt < nrt) {
+                    v4f Pm = {0.0f, 0.0f, 0.0f, 0.0f};
+                    Pm = mfma(__builtin_bit_cast(v8h, mh[rt]), __builtin_bit_cast(v8h, mb), Pm);
+                    Pm = mfma(__builtin_bit_cast(v8h, ml[rt]), __builtin_bit_cast(v8h, mb), Pm);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        acc[rt][ct][r] = fmaf(d, P[rt][ct][r], acc[rt][ct][r]);
+                        acc[rt][ct][r] = fmaf(dm32, Pm[r], acc[rt][ct][r]);
+                    }
+                }
             }
         }
     }
-    float inv[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int row = 4 * g + r;
-        inv[r] = row < nrows ? xinv[row_token[itm.y + row]] : 0.0f;
-    }
-    float *out = gu + ((size_t)kslice * rows_max + itm.y) * (size_t)(2 * H) + col0 + c;
-#pragma unroll
-    for (int ct = 0; ct < ORN_FCT; ++ct)
+    for (int rt = 0; rt < RT; ++rt) {
+        float inv[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int row = 4 * g + r;
-            if (row < nrows) out[(size_t)row * (2 * H) + 16 * ct] = acc[ct][r] * inv[r];
+            const int row = 16 * rt + 4 * g + r;
+            inv[r] = row < nrows ? xinv[src[row]] : 0.0f;
         }
+        float *out = gu + ((size_t)kslice * rows_max + itm.y + 16 * rt) * (size_t)(2 * H) + col0 + c;
+#pragma unroll
+        for (int ct = 0; ct < ORN_FCT; ++ct)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = 16 * rt + 4 * g + r;
+                if (row < nrows) out[(size_t)(4 * g + r) * (2 * H) + 16 * ct] = acc[rt][ct][r] * inv[r];
+            }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -290,6 +346,7 @@ __global__ void __launch_bounds__(256)
 // ---------------------------------------------------------------------------
 #define ORN_FDN 2  // column tiles per wave in the down kernel
 
+template <int RT>
 __global__ void __launch_bounds__(256)
     k_dn_file(const uint8_t *__restrict__ body, const uint16_t *__restrict__ dv,
               const uint32_t *__restrict__ mh, const uint32_t *__restrict__ ml,
@@ -310,15 +367,19 @@ __global__ void __launch_bounds__(256)
     const int NSB = H >> 8, nsb = NSB / ks, s0 = kslice * nsb;
     const size_t b0 = ((size_t)itm.w * D + n0) * NSB;  // first block of row n0
     const int nrows = itm.z;
-    __shared__ __align__(16) FileTile Ab[2];  // A row = c (mid rows)
-    __shared__ int src[16];
-    if (threadIdx.x < 16)
+    const int nrt = RT == 1 ? 1 : (nrows + 15) >> 4;
+    constexpr int NB = RT == 1 ? 2 : 1;
+    __shared__ __align__(16) FileTileT<RT> Ab[NB];  // A row = 16rt + c (mid rows)
+    __shared__ int src[16 * RT];
+    if (threadIdx.x < 16 * RT)
         src[threadIdx.x] = itm.y + ((int)threadIdx.x < nrows ? (int)threadIdx.x : nrows - 1);
     __syncthreads();
 
-    v4f acc[ORN_FDN];
+    v4f acc[RT][ORN_FDN];
 #pragma unroll
-    for (int ct = 0; ct < ORN_FDN; ++ct) acc[ct] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < ORN_FDN; ++ct) acc[rt][ct] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
     for (int s = s0; s < s0 + nsb; ++s) {
         const uint8_t *blk[ORN_FDN];
         float d[ORN_FDN];
@@ -348,32 +409,31 @@ __global__ void __launch_bounds__(256)
                     qa[hn][is][ct][1] = *reinterpret_cast<const uint32_t *>(blk[ct] + 64 * hn + 32 + l0);
                     qa[hn][is][ct][2] = *reinterpret_cast<const uint32_t *>(blk[ct] + 128 + 32 * hn + l0);
                 }
-        FileTile &As = Ab[s & 1];
-        stage_tile(As, mh, ml, src, H, s);
+        FileTileT<RT> &As = Ab[NB == 2 ? (s & 1) : 0];
+        stage_tile<RT>(As, mh, ml, src, H, s);
 #pragma unroll
         for (int hn = 0; hn < 2; ++hn) {
 #pragma unroll
             for (int is = 0; is < 2; ++is) {
                 const int l0 = 16 * is + 4 * g;  // this lane's 4 positions l0 .. l0+3
-                uint32_t q0[ORN_FDN], q1[ORN_FDN], qh[ORN_FDN];
-#pragma unroll
-                for (int ct = 0; ct < ORN_FDN; ++ct) {
-                    q0[ct] = qa[hn][is][ct][0];
-                    q1[ct] = qa[hn][is][ct][1];
-                    qh[ct] = qa[hn][is][ct][2];
-                }
 #pragma unroll
                 for (int Q = 0; Q < 4; ++Q) {
                     const int kl = 128 * hn + 32 * Q + l0;  // k - 256 s
-                    const v4h xa = *reinterpret_cast<const v4h *>(&As[0][c][kl]);
-                    const v4h xb = *reinterpret_cast<const v4h *>(&As[1][c][kl]);
+                    v4h xa[RT], xb[RT];
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt) {
+                        if (rt < nrt) {
+                            xa[rt] = *reinterpret_cast<const v4h *>(&As.v[0][16 * rt + c][kl]);
+                            xb[rt] = *reinterpret_cast<const v4h *>(&As.v[1][16 * rt + c][kl]);
+                        }
+                    }
                     const int sb = 8 * hn + 2 * Q + is;  // sub-block scale index
 #pragma unroll
                     for (int ct = 0; ct < ORN_FDN; ++ct) {
-                        const uint32_t ql = (Q & 1) ? q1[ct] : q0[ct];
+                        const uint32_t ql = (Q & 1) ? qa[hn][is][ct][1] : qa[hn][is][ct][0];
                         // bytes 0..63: low 4 bits from ql, high 2 from qh
                         const uint32_t qv = ((ql >> (4 * (Q >> 1))) & 0x0F0F0F0Fu) |
-                                            (((qh[ct] >> (2 * Q)) & 0x03030303u) << 4);
+                                            (((qa[hn][is][ct][2] >> (2 * Q)) & 0x03030303u) << 4);
                         // fp16 pairs (1024 + byte) in the order (b0, b2), (b1, b3),
                         // then - 1056: q - 32 exactly
                         const v2h off = {(_Float16)-1056.0f, (_Float16)-1056.0f};
@@ -381,25 +441,34 @@ __global__ void __launch_bounds__(256)
                         const uint32_t p1 = as_u32(as_v2h(__builtin_amdgcn_perm(0x64646464u, qv, 0x04030401u)) + off);
                         const v4h bq = __builtin_bit_cast(v4h, make_uint2(p0, p1));
                         const int scv = (int)(int8_t)((scs[ct][sb >> 2] >> (8 * (sb & 3))) & 0xFFu);
-                        v4f P = {0.0f, 0.0f, 0.0f, 0.0f};
-                        P = __builtin_amdgcn_mfma_f32_16x16x16f16(xa, bq, P, 0, 0, 0);
-                        P = __builtin_amdgcn_mfma_f32_16x16x16f16(xb, bq, P, 0, 0, 0);
                         const float dsc = d[ct] * (float)scv;  // exact: 11-bit d times 8-bit sc
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) acc[ct][r] = fmaf(dsc, P[r], acc[ct][r]);
+                        for (int rt = 0; rt < RT; ++rt) {
+                            if (rt < nrt) {
+                                v4f P = {0.0f, 0.0f, 0.0f, 0.0f};
+                                P = __builtin_amdgcn_mfma_f32_16x16x16f16(xa[rt], bq, P, 0, 0, 0);
+                                P = __builtin_amdgcn_mfma_f32_16x16x16f16(xb[rt], bq, P, 0, 0, 0);
+#pragma unroll
+                                for (int r = 0; r < 4; ++r) acc[rt][ct][r] = fmaf(dsc, P[r], acc[rt][ct][r]);
+                            }
+                        }
                     }
                 }
             }
         }
     }
-    float *out = dn + ((size_t)kslice * rows_max + itm.y) * (size_t)D + n0;
 #pragma unroll
-    for (int ct = 0; ct < ORN_FDN; ++ct)
+    for (int rt = 0; rt < RT; ++rt) {
+        float *out = dn + ((size_t)kslice * rows_max + itm.y + 16 * rt) * (size_t)D + n0;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int row = 4 * g + r;
-            if (row < nrows) out[(size_t)row * D + 16 * ct] = acc[ct][r] * minv[itm.y + row];
-        }
+        for (int ct = 0; ct < ORN_FDN; ++ct)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = 16 * rt + 4 * g + r;
+                if (row < nrows)
+                    out[(size_t)(4 * g + r) * D + 16 * ct] = acc[rt][ct][r] * minv[itm.y + row];
+            }
+    }
 }
 
 }  // namespace
@@ -428,10 +497,18 @@ extern "C" int ornk_file_gateup(const ornk_moe_args *a, hipStream_t s)
 {
     if (!ornk_file_supported(a->D, a->H) || (a->D / 256) % a->ks_gu) return hipErrorInvalidValue;
     const ornk_file_ws &f = a->fw;
-    const dim3 grid(a->items_max * ((2 * a->H) / 256) * a->ks_gu);
-    ORN_LAUNCH_EV(a, k_gu_file, grid, dim3(256), 0, s, a->gate, a->up, f.xh, f.xl, f.xinv, f.xsh,
-                  f.xsl, a->ctl, reinterpret_cast<const int4 *>(a->items), a->row_token,
-                  a->gu_part, a->D, a->H, a->ks_gu, a->rows_max);
+    if (a->tchunk > 64) return hipErrorInvalidValue;
+    const int RT = a->tchunk > 16 ? 4 : 1;
+    const dim3 grid(a->items_max * ((2 * a->H) / (64 * (RT == 4 ? gu_fct<4>() : gu_fct<1>()))) *
+                    a->ks_gu);
+    if (RT == 4)
+        ORN_LAUNCH_EV(a, k_gu_file<4>, grid, dim3(256), 0, s, a->gate, a->up, f.xh, f.xl, f.xinv,
+                      f.xsh, f.xsl, a->ctl, reinterpret_cast<const int4 *>(a->items),
+                      a->row_token, a->gu_part, a->D, a->H, a->ks_gu, a->rows_max);
+    else
+        ORN_LAUNCH_EV(a, k_gu_file<1>, grid, dim3(256), 0, s, a->gate, a->up, f.xh, f.xl, f.xinv,
+                      f.xsh, f.xsl, a->ctl, reinterpret_cast<const int4 *>(a->items),
+                      a->row_token, a->gu_part, a->D, a->H, a->ks_gu, a->rows_max);
     return hipGetLastError();
 }
 
@@ -451,8 +528,14 @@ extern "C" int ornk_file_down(const ornk_moe_args *a, hipStream_t s)
     const ornk_file_ws &f = a->fw;
     if (a->D % (64 * ORN_FDN)) return hipErrorInvalidValue;
     const dim3 grid(a->items_max * (a->D / (64 * ORN_FDN)) * a->ks_dn);
-    ORN_LAUNCH_EV(a, k_dn_file, grid, dim3(256), 0, s, a->down_body, a->down_d, f.mh, f.ml,
-                  f.minv, a->ctl, reinterpret_cast<const int4 *>(a->items), a->dn_part, a->D,
-                  a->H, a->ks_dn, a->rows_max);
+    if (a->tchunk > 64) return hipErrorInvalidValue;
+    if (a->tchunk > 16)
+        ORN_LAUNCH_EV(a, k_dn_file<4>, grid, dim3(256), 0, s, a->down_body, a->down_d, f.mh, f.ml,
+                      f.minv, a->ctl, reinterpret_cast<const int4 *>(a->items), a->dn_part, a->D,
+                      a->H, a->ks_dn, a->rows_max);
+    else
+        ORN_LAUNCH_EV(a, k_dn_file<1>, grid, dim3(256), 0, s, a->down_body, a->down_d, f.mh, f.ml,
+                      f.minv, a->ctl, reinterpret_cast<const int4 *>(a->items), a->dn_part, a->D,
+                      a->H, a->ks_dn, a->rows_max);
     return hipGetLastError();
 }
