@@ -72,18 +72,27 @@ struct FileTileT {
 };
 typedef FileTileT<1> FileTile;
 
-template <int RT>
+// With LIVE_ONLY (the down kernel's 16-row items) only the item's nr live
+// rows are staged: an MFMA output row depends on its own A row alone, and
+// rows at or past nr are never stored, so whatever the tile holds there (an
+// earlier super-block's rows, or uninitialised LDS) cannot reach an output.
+// Decode items hold a row or two.  Elsewhere every row is staged (clamped
+// to the last live one): measured, predicated copies cost more there than
+// the rows they skip.
+template <int RT, bool LIVE_ONLY>
 __device__ __forceinline__ void stage_tile(FileTileT<RT> &As, const uint32_t *__restrict__ xh,
                                            const uint32_t *__restrict__ xl, const int *src,
-                                           int K, int s)
+                                           int K, int s, int nr)
 {
     if (RT > 1) __syncthreads();  // one tile: every wave is done with the last one
 #pragma unroll
     for (int i = 0; i < 4 * RT; ++i) {  // 2 planes x 16RT rows x 32 chunks of 16 B
         const int idx = threadIdx.x + 256 * i;
         const int plane = idx / (512 * RT), row = (idx >> 5) % (16 * RT), ch = idx & 31;
-        *reinterpret_cast<uint4 *>(&As.v[plane][row][8 * ch]) = *reinterpret_cast<const uint4 *>(
-            (plane ? xl : xh) + (size_t)src[row] * (K >> 1) + 128 * s + 4 * ch);
+        if (!LIVE_ONLY || RT > 1 || row < nr)
+            *reinterpret_cast<uint4 *>(&As.v[plane][row][8 * ch]) =
+                *reinterpret_cast<const uint4 *>((plane ? xl : xh) + (size_t)src[row] * (K >> 1) +
+                                                 128 * s + 4 * ch);
     }
     __syncthreads();
 }
@@ -219,7 +228,7 @@ __global__ void __launch_bounds__(256, 2)
             w[ct][1] = *reinterpret_cast<const uint4 *>(blk + 80 + 16 * g);
         }
         FileTileT<RT> &As = Ab[NB == 2 ? (s & 1) : 0];
-        stage_tile<RT>(As, xh, xl, src, D, s);
+        stage_tile<RT, false>(As, xh, xl, src, D, s, nrows);
         v4f P[RT][ORN_FCT];
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
@@ -410,7 +419,7 @@ __global__ void __launch_bounds__(256)
                     qa[hn][is][ct][2] = *reinterpret_cast<const uint32_t *>(blk[ct] + 128 + 32 * hn + l0);
                 }
         FileTileT<RT> &As = Ab[NB == 2 ? (s & 1) : 0];
-        stage_tile<RT>(As, mh, ml, src, H, s);
+        stage_tile<RT, true>(As, mh, ml, src, H, s, nrows);
 #pragma unroll
         for (int hn = 0; hn < 2; ++hn) {
 #pragma unroll
