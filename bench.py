@@ -354,7 +354,41 @@ def measure_attention(ctx):
 # Extra configs reported beside the headline: (label, store layer, tokens).
 # Layer 1 carries a Zipf(1.1) router bias.
 EXTRA_CONFIGS = (("decode_t1", 0, 1), ("prefill_t2048", 0, 2048), ("zipf_t256", 1, 256))
-EXTRA_LABELS = [c[0] for c in EXTRA_CONFIGS] + ["file_t1", "file_t16", "file_t2048"]
+EXTRA_LABELS = [c[0] for c in EXTRA_CONFIGS] + ["file_t1", "file_t16", "file_t2048", "stack40",
+                                                 "streamed", "attention"]
+
+
+def headline(ctx, store, args, read_gbs):
+    """the 16-token decode step of one Ornith-shape layer."""
+    T = 16
+    ms, kernels, stats = measure(ctx, store, 0, T, args.steps, args.warmup)
+    dom, roof = roofline_for(kernels, stats, T, "t16")
+    roof["measured_read_peak"] = round(read_gbs, 1)
+    roof["frac_of_measured"] = round(roof["achieved"] / read_gbs, 4)
+    U = stats["n_slots"]
+    result = {
+        "metric": "MoE-layer tokens/s at batch 1/16/2048; achieved HBM GB/s & MFMA % vs peak",
+        "value": round(T / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 hi+lo MFMA, f32 accumulate (Q4_K/Q6_K weights exact as f16 sc*q)",
+        "data": "synthetic (seeded Q4_K/Q6_K experts; activations and router weights are "
+                "Irwin-Hall(12) sums: mean 0, sd 1 (router 0.02), bounded at 6 sd)",
+        "config": {"workload": "BASELINE configs[1]: single Ornith-shape MoE layer, 16-token decode",
+                   "tokens": T, "d_model": D, "expert_ffn": H, "experts": E, "top_k": K,
+                   "shared_experts": 1, "active_experts_incl_shared": U,
+                   "expert_bytes_streamed": U * EXPERT_BYTES},
+        "roofline": roof,
+        "kernels_us": {n: round(v["avg_us"], 2) for n, v in kernels.items()},
+        "layer_hbm_gbs": round(U * EXPERT_BYTES / (ms * 1e-3) / 1e9, 1),
+    }
+    return result
 
 
 def main():
@@ -400,33 +434,12 @@ def main():
     log(f"store filled in {time.perf_counter() - t0:.1f} s ({store.bytes() / 1e9:.2f} GB)")
 
     T = 16
-    ms, kernels, stats = measure(ctx, store, 0, T, args.steps, args.warmup)
-    dom, roof = roofline_for(kernels, stats, T, "t16")
-    roof["measured_read_peak"] = round(read_gbs, 1)
-    roof["frac_of_measured"] = round(roof["achieved"] / read_gbs, 4)
-    U = stats["n_slots"]
-    result = {
-        "metric": "MoE-layer tokens/s at batch 1/16/2048; achieved HBM GB/s & MFMA % vs peak",
-        "value": round(T / (ms * 1e-3), 1),
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f16 hi+lo MFMA, f32 accumulate (Q4_K/Q6_K weights exact as f16 sc*q)",
-        "data": "synthetic (seeded Q4_K/Q6_K experts; activations and router weights are "
-                "Irwin-Hall(12) sums: mean 0, sd 1 (router 0.02), bounded at 6 sd)",
-        "config": {"workload": "BASELINE configs[1]: single Ornith-shape MoE layer, 16-token decode",
-                   "tokens": T, "d_model": D, "expert_ffn": H, "experts": E, "top_k": K,
-                   "shared_experts": 1, "active_experts_incl_shared": U,
-                   "expert_bytes_streamed": U * EXPERT_BYTES},
-        "roofline": roof,
-        "kernels_us": {n: round(v["avg_us"], 2) for n, v in kernels.items()},
-        "layer_hbm_gbs": round(U * EXPERT_BYTES / (ms * 1e-3) / 1e9, 1),
-    }
+    if args.only:
+        # one extra config alone (a kernel trace of it): the headline's
+        # kernels are not timed, and the line carries only that config
+        result = {"only": args.only, "steps": args.steps, "warmup": args.warmup}
+    else:
+        result = headline(ctx, store, args, read_gbs)
     if not args.no_extra:
         extra = {}
         for label, layer, Tn in EXTRA_CONFIGS:
@@ -467,8 +480,9 @@ def main():
                     continue
                 steps = max(5, args.steps // (20 if Tn >= 256 else 1))
                 ms_x, kern_x, st_x = measure(ctx, fst, 0, Tn, steps, max(2, args.warmup // 4))
-                _, roof_x = roofline_for(kern_x, st_x, Tn, label)
-                roof_x["frac_of_measured"] = round(roof_x["achieved"] / read_gbs, 4)
+                _, roof_x = roofline_for(kern_x, st_x, Tn, label.split("_")[-1])
+                if roof_x["bound"] == "hbm":
+                    roof_x["frac_of_measured"] = round(roof_x["achieved"] / read_gbs, 4)
                 extra[label] = {"tokens_per_s": round(Tn / (ms_x * 1e-3), 1),
                                 "ms_per_step": round(ms_x, 4), "active_experts": st_x["n_slots"],
                                 "layer_hbm_gbs": round(st_x["n_slots"] * EXPERT_BYTES / (ms_x * 1e-3) / 1e9, 1),
@@ -478,11 +492,13 @@ def main():
             fst.close()
         result["configs"] = extra
     store.close()
-    if not args.no_stack and not args.only:
+    want = lambda label: not args.only or args.only == label  # noqa: E731
+    if not args.no_stack and want("stack40"):
         result.setdefault("configs", {}).update(measure_stack(ctx, args.steps))
-    if not args.no_extra and not args.only:
+    if not args.no_extra and want("streamed"):
         result.setdefault("configs", {}).update(measure_streamed(ctx, args.steps))
-        result["configs"].update(measure_attention(ctx))
+    if not args.no_extra and want("attention"):
+        result.setdefault("configs", {}).update(measure_attention(ctx))
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_budget)
     ctx.close()
