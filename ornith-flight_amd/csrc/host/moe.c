@@ -858,9 +858,14 @@ static plan_t make_plan(const ornith_moe_shape *sh, int T, int use_mfma)
     p.use_dec = 0;
     const int k = sh->top_k, E = sh->n_experts;
     const int D = sh->d_model, H = sh->hidden;
-    /* MFMA work items hold at most one 16-row tile at decode sizes (the
-     * kernel instance with a single row tile), four at prefill sizes. */
-    p.tchunk = use_mfma ? (T <= 64 ? 16 : 64) : (T <= 64 ? 2 : 8);
+    /* MFMA work items hold at most one 16-row tile (the decode kernels) at
+     * decode sizes and wherever the batch averages at most 16 rows per
+     * expert, four (the prefill grouped GEMMs) above.  Skewed batches of the
+     * first kind (a few hot experts, many cold ones) then split each hot
+     * expert into items of 16 rows instead of running every cold expert
+     * through a 64-row tile: an MFMA item costs its weight conversion
+     * whatever its rows. */
+    p.tchunk = use_mfma ? (T <= 64 || T * k <= 16 * E ? 16 : 64) : (T <= 64 ? 2 : 8);
     p.rows_max = T * k + (sh->has_shared ? T : 0);
     const int max_slots = (T * k < E ? T * k : E) + (sh->has_shared ? 1 : 0);
     p.items_max = max_slots + (p.rows_max + p.tchunk - 1) / p.tchunk;
@@ -1169,7 +1174,9 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     } else {
         if ((rc = launch_k(ctx, "moe_gateup", ornk_moe_gateup, &a))) return rc;
     }
-    /* One token: the decode down kernel forms mid from the gate/up partials. */
+    /* Up to 64 tokens the decode down kernel forms mid from the gate/up
+     * partials (each of its work groups for its item's rows); above, where
+     * a hot expert's rows span many items, mid is a step of its own. */
     const int fused_mid = p.use_dec && ornk_down_dec_fuses_mid(T, H, p.ks_gu, p.ks_dn);
     if (!fused_mid && (rc = launch_k(ctx, "moe_mid", ornk_moe_mid, &a))) return rc;
     if (p.use_dec) {

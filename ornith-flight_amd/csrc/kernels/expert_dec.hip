@@ -500,11 +500,13 @@ extern "C" int ornk_moe_gateup_dec(const ornk_moe_args *a, hipStream_t s)
     return hipGetLastError();
 }
 
-// Decode plans with 4, 8 or 16 gate/up slices and 8-step down slices: the
-// down kernel forms mid itself (the instances compiled for those plans).
+// Decode plans of up to 64 tokens with 4, 8 or 16 gate/up slices and 8-step
+// down slices: the down kernel forms mid itself (the instances compiled for
+// those plans).  Larger batches, whose mid rows every column block of an
+// item would form again, run the mid step.
 extern "C" int ornk_down_dec_fuses_mid(int T, int H, int ks_gu, int ks_dn)
 {
-    return T >= 1 && (ks_gu == 4 || ks_gu == 8 || ks_gu == 16) && ks_dn >= 1 &&
+    return T >= 1 && T <= 64 && (ks_gu == 4 || ks_gu == 8 || ks_gu == 16) && ks_dn >= 1 &&
            H % (32 * ks_dn) == 0 && H / 32 / ks_dn == 8;
 }
 

@@ -138,6 +138,43 @@ def test_small_layer_mfma_parity(om, ctx, small, T, mode):
     assert err.max() <= TOL
 
 
+def test_skewed_batch_on_decode_items(om, ctx):
+    """A batch of more than 64 tokens averaging at most 16 rows per expert,
+    Zipf-skewed: the hot experts are split into 16-row items of the decode
+    kernels (several items per expert, mid as a step of its own) instead of
+    64-row MFMA tiles; every token against the oracle, eager and as a
+    replayed graph."""
+    L = Layer(om, ctx, 256, 256, 64, 8, seed=21, zipf_s=1.1)
+    try:
+        T = 120
+        x = act(om, 777, T, 256)
+        lib = om.lib()
+        lib.gpu_profile_enable(ctx.ptr, 1)
+        lib.gpu_profile_reset(ctx.ptr)
+        try:
+            out, idx, w = run(ctx, L, x, flags=om.MOE_PATH_MFMA)
+            prof = om.profile(ctx)
+        finally:
+            lib.gpu_profile_enable(ctx.ptr, 0)
+        counts = np.bincount(idx.reshape(-1).astype(np.int64), minlength=64)
+        say(f"  rows per expert: max {counts.max()}, experts over 16 rows: "
+            f"{int((counts > 16).sum())}; steps {sorted(prof)}")
+        assert counts.max() > 32  # a hot expert spans three items or more
+        assert {"moe_gateup_dec", "moe_mid", "moe_down_dec"} <= set(prof)
+        assert "moe_gateup_mfma" not in prof
+        ref, ridx, rw = L.oracle(x)
+        assert np.array_equal(idx, ridx)
+        err = row_err(out, ref)
+        say("  max row err", err.max())
+        assert err.max() <= TOL
+        for i in range(3):
+            g, gi, _ = run(ctx, L, x, flags=om.MOE_PATH_MFMA | om.MOE_GRAPH)
+            assert np.array_equal(gi, idx)
+            assert np.array_equal(g.view(np.uint32), out.view(np.uint32)), i
+    finally:
+        L.store.close()
+
+
 def test_mfma_residual_norm_and_row_independence(om, ctx, small):
     T = 70
     x = act(om, 17, T, small.D)
