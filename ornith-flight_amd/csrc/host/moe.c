@@ -859,13 +859,13 @@ static plan_t make_plan(const ornith_moe_shape *sh, int T, int use_mfma)
     const int k = sh->top_k, E = sh->n_experts;
     const int D = sh->d_model, H = sh->hidden;
     /* MFMA work items hold at most one 16-row tile (the decode kernels) at
-     * decode sizes and wherever the batch averages at most 16 rows per
-     * expert, four (the prefill grouped GEMMs) above.  Skewed batches of the
-     * first kind (a few hot experts, many cold ones) then split each hot
-     * expert into items of 16 rows instead of running every cold expert
-     * through a 64-row tile: an MFMA item costs its weight conversion
-     * whatever its rows. */
-    p.tchunk = use_mfma ? (T <= 64 || T * k <= 16 * E ? 16 : 64) : (T <= 64 ? 2 : 8);
+     * decode sizes, two (the decode kernels' two-tile instances) above 64
+     * tokens wherever the batch averages at most 16 rows per expert, four
+     * (the prefill grouped GEMMs) beyond.  Skewed batches of the middle
+     * kind (a few hot experts, many cold ones) then split each hot expert
+     * into items of 32 rows instead of running every cold expert through a
+     * 64-row tile: an item costs its weight conversion whatever its rows. */
+    p.tchunk = use_mfma ? (T <= 64 ? 16 : T * k <= 16 * E ? 32 : 64) : (T <= 64 ? 2 : 8);
     p.rows_max = T * k + (sh->has_shared ? T : 0);
     const int max_slots = (T * k < E ? T * k : E) + (sh->has_shared ? 1 : 0);
     p.items_max = max_slots + (p.rows_max + p.tchunk - 1) / p.tchunk;
@@ -900,7 +900,7 @@ static plan_t make_plan(const ornith_moe_shape *sh, int T, int use_mfma)
         if (kdn > H / 32) kdn = H / 32;
         p.ks_gu = kg;
         p.ks_dn = kdn;
-        if (p.tchunk <= 16) {
+        if (p.tchunk <= 32) {
             /* Decode kernels (slices of 4..32 reduction steps compiled).
              * Gate/up: about 2048 work groups over the estimated items, slices
              * of 4..16 steps (measured best: 16 at 16 tokens, 4 at 1 token);

@@ -65,14 +65,24 @@ __device__ __forceinline__ v2f bload8f(rsrc_t r, uint32_t voff, uint32_t soff)
 // (hi/lo of x*s*d and of x*s*dmin); after one barrier every wave streams its
 // own weights with no further synchronisation.
 // ---------------------------------------------------------------------------
+// N = 4: one 16-byte LDS store of w[0..3]; N = 2: one 8-byte store of w[0..1]
+template <int N>
+__device__ __forceinline__ void st_words(uint32_t *p, const uint32_t *w)
+{
+    if constexpr (N == 4)
+        *reinterpret_cast<uint4 *>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+    else
+        *reinterpret_cast<uint2 *>(p) = make_uint2(w[0], w[1]);
+}
+
 struct GuRing {
     uint4 q;       // nibble words of column tiles 4w..4w+3
     uint4 s0, s1;  // scales of sub-blocks 2w, 2w+1 at k = 8g..8g+7
     uint4 mn;      // mins of sub-block 2w + (c & 1) at k = 8g..8g+7
 };
 
-template <int NR, int KT, int KC>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
+template <int NR, int KT, int KC, int RT>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT > 1 ? 2 : 3)))
     k_gateup_dec(ornk_gu_prefill P, const float *__restrict__ xn,
                  const float *__restrict__ x_amax, const int *__restrict__ ctl,
                  const int4 *__restrict__ items, const int *__restrict__ row_token,
@@ -80,8 +90,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
 {
     constexpr int NCHK = KT / KC, NBUF = NCHK > 1 ? 2 : 1;
     constexpr int LC = 2 * KC;  // activation values a thread prepares per chunk
-    __shared__ __align__(16) uint32_t As[NBUF][KC][4][16 * ORN_AST / 2];
-    __shared__ float s_inv[16];
+    constexpr int GV = LC < 8 ? LC : 8;  // values per LDS store (8: 16 bytes, 4: 8 bytes)
+    static_assert(LC % GV == 0 && (GV == 4 || GV == 8), "chunks of 2 or 4k steps");
+    __shared__ __align__(16) uint32_t As[NBUF][KC][RT][4][16 * ORN_AST / 2];
+    __shared__ float s_inv[16 * RT];
 
     // The item and the live item count are read together; work groups past
     // the dispatched items then leave.
@@ -118,9 +130,15 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
         st.mn = bload16(rm, m_off, kt * sstep);
     };
 
+    // Row tile rt holds the item's rows 16*rt .. 16*rt+15; thread (ar, seg)
+    // prepares row ar of every tile.
     const int ar = tid >> 4, seg = tid & 15;
-    const int arow = ar < nrows ? ar : 0;  // rows past the item read a valid row, scaled by 0
-    const int tok = row_token[itm.y + arow];
+    int tok[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        const int row = 16 * rt + ar;
+        tok[rt] = row_token[itm.y + (row < nrows ? row : 0)];  // rows past the item: a valid row, scaled by 0
+    }
     GuRing st[NR];
 #pragma unroll
     for (int i = 0; i < NR; ++i) load_b(st[i], i);
@@ -129,73 +147,104 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
     // Activation tiles: A = x*s*d and Am = x*s*dmin, hi/lo, one chunk of KC
     // steps at a time (chunk ch in LDS buffer ch % 2).  Thread (ar, seg)
     // owns the LC values seg*LC.. of row ar in every chunk.
-    const float amax = x_amax[tok];
     const float dmx = P.dmax[e * 3 + m];
-    const float *xr = xn + (size_t)tok * D + 32 * kt0 + seg * LC;
+    const float *xr[RT];
+    float amax[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        amax[rt] = x_amax[tok[rt]];
+        xr[rt] = xn + (size_t)tok[rt] * D + 32 * kt0 + seg * LC;
+    }
     const float *dr = P.pd[m] + (size_t)e * (DH / 256) + (size_t)b * D + 32 * kt0 + seg * LC;
     const float *dmr = P.pdm[m] + (size_t)e * (DH / 256) + (size_t)b * D + 32 * kt0 + seg * LC;
-    // Wave w prepares rows 4w..4w+3.  A wave whose rows all lie past the
-    // item (most waves at decode sizes, where items hold one or a few rows)
-    // zeroes its rows of both buffers once and then skips the loads and the
-    // arithmetic (uniform per wave).
-    const bool rows_live = __builtin_amdgcn_readfirstlane(4 * (tid >> 6)) < nrows;
-    v4f xv[LC / 4], dv[LC / 4], mv[LC / 4];
+    // Wave w prepares rows 4w..4w+3 of each row tile.  A wave whose rows of
+    // a tile all lie past the item (most waves at decode sizes, where items
+    // hold one or a few rows) zeroes them in both buffers once and then
+    // skips their loads and arithmetic (uniform per wave).  The d / dmin
+    // values are the column block's, the same for every row.
+    bool rows_live[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+        rows_live[rt] = __builtin_amdgcn_readfirstlane(16 * rt + 4 * (tid >> 6)) < nrows;
+    v4f xv[RT][LC / 4], dv[LC / 4], mv[LC / 4];
     auto a_load = [&](int ch) {
-        if (!rows_live) return;
+        if (!rows_live[0]) return;
 #pragma unroll
         for (int i = 0; i < LC / 4; ++i) {
-            xv[i] = *reinterpret_cast<const v4f *>(xr + 32 * KC * ch + 4 * i);
             dv[i] = *reinterpret_cast<const v4f *>(dr + 32 * KC * ch + 4 * i);
             mv[i] = *reinterpret_cast<const v4f *>(dmr + 32 * KC * ch + 4 * i);
         }
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+            if (rows_live[rt])
+#pragma unroll
+                for (int i = 0; i < LC / 4; ++i)
+                    xv[rt][i] = *reinterpret_cast<const v4f *>(xr[rt] + 32 * KC * ch + 4 * i);
     };
-    float ascale = 0.0f;
-    if (!rows_live) {
+    float ascale[RT];
 #pragma unroll
-        for (int buf = 0; buf < NBUF; ++buf)
+    for (int rt = 0; rt < RT; ++rt) {
+        ascale[rt] = 0.0f;
+        if (!rows_live[rt]) {
+            const uint32_t z[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-            for (int o = 0; o < LC / 8; ++o) {
-                const int kk = seg * LC + 8 * o, kl = kk >> 5, ko = kk & 31;
-                const int w0 = (ar * ORN_AST + ko) >> 1;
+            for (int buf = 0; buf < NBUF; ++buf)
 #pragma unroll
-                for (int a = 0; a < 4; ++a)
-                    *reinterpret_cast<uint4 *>(&As[buf][kl][a][w0]) = make_uint4(0u, 0u, 0u, 0u);
-            }
+                for (int o = 0; o < LC / GV; ++o) {
+                    const int kk = seg * LC + GV * o, kl = kk >> 5, ko = kk & 31;
+                    const int w0 = (ar * ORN_AST + ko) >> 1;
+#pragma unroll
+                    for (int a = 0; a < 4; ++a) st_words<GV / 2>(&As[buf][kl][rt][a][w0], z);
+                }
+        }
     }
     auto a_store = [&](int ch) {
-        if (!rows_live) return;
         const int buf = ch % NBUF;
 #pragma unroll
-        for (int o = 0; o < LC / 8; ++o) {  // groups of 8 values: one 16-byte LDS store per array
-            const int kk = seg * LC + 8 * o;  // within the chunk
-            const int kl = kk >> 5, ko = kk & 31;
-            uint32_t hi[4], lo[4], mh[4], ml[4];
+        for (int rt = 0; rt < RT; ++rt) {
+            if (!rows_live[rt]) continue;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const v4f x4 = xv[2 * o + (j >> 1)], d4 = dv[2 * o + (j >> 1)], m4 = mv[2 * o + (j >> 1)];
-                const int u = 2 * (j & 1);
-                const float x0 = x4[u] * ascale, x1 = x4[u + 1] * ascale;
-                split2(x0 * d4[u], x1 * d4[u + 1], hi[j], lo[j]);
-                split2(x0 * m4[u], x1 * m4[u + 1], mh[j], ml[j]);
+            for (int o = 0; o < LC / GV; ++o) {  // groups of GV values: one LDS store per array
+                const int kk = seg * LC + GV * o;  // within the chunk
+                const int kl = kk >> 5, ko = kk & 31;
+                uint32_t hi[GV / 2], lo[GV / 2], mh[GV / 2], ml[GV / 2];
+#pragma unroll
+                for (int j = 0; j < GV / 2; ++j) {
+                    const int v = GV * o + 2 * j;  // the pair's first value in the thread's run
+                    const v4f x4 = xv[rt][v >> 2], d4 = dv[v >> 2], m4 = mv[v >> 2];
+                    const int u = v & 3;
+                    const float x0 = x4[u] * ascale[rt], x1 = x4[u + 1] * ascale[rt];
+                    split2(x0 * d4[u], x1 * d4[u + 1], hi[j], lo[j]);
+                    split2(x0 * m4[u], x1 * m4[u + 1], mh[j], ml[j]);
+                }
+                const int w0 = (ar * ORN_AST + ko) >> 1;
+                st_words<GV / 2>(&As[buf][kl][rt][0][w0], hi);
+                st_words<GV / 2>(&As[buf][kl][rt][1][w0], lo);
+                st_words<GV / 2>(&As[buf][kl][rt][2][w0], mh);
+                st_words<GV / 2>(&As[buf][kl][rt][3][w0], ml);
             }
-            const int w0 = (ar * ORN_AST + ko) >> 1;
-            *reinterpret_cast<uint4 *>(&As[buf][kl][0][w0]) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-            *reinterpret_cast<uint4 *>(&As[buf][kl][1][w0]) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-            *reinterpret_cast<uint4 *>(&As[buf][kl][2][w0]) = make_uint4(mh[0], mh[1], mh[2], mh[3]);
-            *reinterpret_cast<uint4 *>(&As[buf][kl][3][w0]) = make_uint4(ml[0], ml[1], ml[2], ml[3]);
         }
     };
     a_load(0);
-    ascale = ar < nrows ? row_scale(amax, dmx) : 0.0f;
-    if (seg == 0) s_inv[ar] = ascale != 0.0f ? 1.0f / ascale : 0.0f;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        ascale[rt] = 16 * rt + ar < nrows ? row_scale(amax[rt], dmx) : 0.0f;
+        if (seg == 0) s_inv[16 * rt + ar] = ascale[rt] != 0.0f ? 1.0f / ascale[rt] : 0.0f;
+    }
     a_store(0);
     if (NCHK > 1) a_load(1);
     __syncthreads();
 
-    v4f acc[4];
+    // the second row tile's products only where the item reaches it
+    // (uniform over the work group)
+    const int rt_live = RT > 1 && nrows > 16 ? RT : 1;
+    v4f acc[RT][4], accm[RT];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[j] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
-    v4f accm = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int rt = 0; rt < RT; ++rt) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[rt][j] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+        accm[rt] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+    }
     const int ro = c * ORN_AST + 8 * g;
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
@@ -211,18 +260,22 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
         __builtin_amdgcn_sched_barrier(0);
         if (kt + NR < KT) load_b(r, kt + NR);
         __builtin_amdgcn_sched_barrier(0);
-        const _Float16 *A = reinterpret_cast<const _Float16 *>(As[ch % NBUF][kl][0]);
-        const v8h ahi = *reinterpret_cast<const v8h *>(A + ro);
-        const v8h alo = *reinterpret_cast<const v8h *>(A + 16 * ORN_AST + ro);
-        const v8h mhi = *reinterpret_cast<const v8h *>(A + 32 * ORN_AST + ro);
-        const v8h mlo = *reinterpret_cast<const v8h *>(A + 48 * ORN_AST + ro);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            acc[j] = mfma(ahi, bq[j], acc[j]);
-            acc[j] = mfma(alo, bq[j], acc[j]);
+        for (int rt = 0; rt < RT; ++rt) {
+            if (rt >= rt_live) break;
+            const _Float16 *A = reinterpret_cast<const _Float16 *>(As[ch % NBUF][kl][rt][0]);
+            const v8h ahi = *reinterpret_cast<const v8h *>(A + ro);
+            const v8h alo = *reinterpret_cast<const v8h *>(A + 16 * ORN_AST + ro);
+            const v8h mhi = *reinterpret_cast<const v8h *>(A + 32 * ORN_AST + ro);
+            const v8h mlo = *reinterpret_cast<const v8h *>(A + 48 * ORN_AST + ro);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc[rt][j] = mfma(ahi, bq[j], acc[rt][j]);
+                acc[rt][j] = mfma(alo, bq[j], acc[rt][j]);
+            }
+            accm[rt] = mfma(mhi, bm, accm[rt]);
+            accm[rt] = mfma(mlo, bm, accm[rt]);
         }
-        accm = mfma(mhi, bm, accm);
-        accm = mfma(mlo, bm, accm);
         if (kl == 0 && ch + 1 < NCHK) {
             // Next chunk's tiles into the other buffer (last read in chunk
             // ch-1, which every wave finished before the barrier below it),
@@ -236,19 +289,21 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
     float *row0 = gu + ((size_t)kslice * rows_max + itm.y) * (2 * H);
     const int colb = m * H + 256 * b + 64 * wave + c;
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-        const int row = 4 * g + rr;
-        const float si = s_inv[row];
-        const float m0 = __shfl(accm[rr], 16 * g, 64);
-        const float m1 = __shfl(accm[rr], 16 * g + 1, 64);
-        if (row < nrows) {
-            float *o = row0 + (size_t)row * (2 * H) + colb;
-            o[0] = (acc[0][rr] - m0) * si;
-            o[16] = (acc[1][rr] - m0) * si;
-            o[32] = (acc[2][rr] - m1) * si;
-            o[48] = (acc[3][rr] - m1) * si;
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const int row = 16 * rt + 4 * g + rr;
+            const float si = s_inv[row];
+            const float m0 = __shfl(accm[rt][rr], 16 * g, 64);
+            const float m1 = __shfl(accm[rt][rr], 16 * g + 1, 64);
+            if (row < nrows) {
+                float *o = row0 + (size_t)row * (2 * H) + colb;
+                o[0] = (acc[rt][0][rr] - m0) * si;
+                o[16] = (acc[rt][1][rr] - m0) * si;
+                o[32] = (acc[rt][2][rr] - m1) * si;
+                o[48] = (acc[rt][3][rr] - m1) * si;
+            }
         }
-    }
 }
 
 // ---------------------------------------------------------------------------
@@ -267,8 +322,8 @@ struct DnRing {
     uint4 q0, q1, sc[4];
 };
 
-template <int NR, int KT, int KC, int KSG>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
+template <int NR, int KT, int KC, int KSG, int RT>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT > 1 ? 2 : 3)))
     k_down_dec(ornk_dn_prefill P, const float *__restrict__ mid,
                const float *__restrict__ mid_amax, const int *__restrict__ ctl,
                const int4 *__restrict__ items, float *__restrict__ dn, int D, int H, int ks,
@@ -277,8 +332,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
     constexpr int NCHK = KT / KC, NBUF = NCHK > 1 ? 2 : 1;
     constexpr int LC = 2 * KC;
     constexpr int KV = 32 * KT;  // reduction values of the slice
-    __shared__ __align__(16) uint32_t As[NBUF][KC][2][16 * ORN_AST / 2];
-    __shared__ float s_inv[16];
+    static_assert(KSG == 0 || RT == 1, "mid is formed in the kernel for one row tile only");
+    __shared__ __align__(16) uint32_t As[NBUF][KC][RT][2][16 * ORN_AST / 2];
+    __shared__ float s_inv[16 * RT];
     __shared__ __align__(16) float Ms[KSG ? 16 : 1][KSG ? KV : 4];  // the rows' mid slices
     __shared__ unsigned int s_amax[16];
 
@@ -311,14 +367,16 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
         for (int j = 0; j < 4; ++j) st.sc[j] = bload16(rs, s_off + 64 * j, kt * sstep);
     };
 
-    const int ar = tid >> 4, seg = tid & 15;
-    const int arow = ar < nrows ? ar : 0;
+    const int ar = tid >> 4, seg = tid & 15;  // row ar of each row tile, as in k_gateup_dec
+    int arow[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) arow[rt] = 16 * rt + ar < nrows ? 16 * rt + ar : 0;
     DnRing st[NR];
 #pragma unroll
     for (int i = 0; i < NR; ++i) load_b(st[i], i);
     __builtin_amdgcn_sched_barrier(0);
 
-    float amax;
+    float amax[RT];
     if (KSG) {
         const size_t sstr = (size_t)rows_max * 2 * H;  // between gate/up slices
         if (tid < 16) s_amax[tid] = 0u;
@@ -357,67 +415,90 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
             if (lane == 0) atomicMax(&s_amax[r], __float_as_uint(lmax));
         }
         __syncthreads();
-        amax = __uint_as_float(s_amax[arow]);
+        amax[0] = __uint_as_float(s_amax[arow[0]]);
     } else {
-        amax = mid_amax[itm.y + arow];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) amax[rt] = mid_amax[itm.y + arow[rt]];
     }
     const float dmx = P.dmax[e * 3 + 2];
-    const float *xr = mid + (size_t)(itm.y + arow) * H + 32 * kt0 + seg * LC;
+    const float *xr[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) xr[rt] = mid + (size_t)(itm.y + arow[rt]) * H + 32 * kt0 + seg * LC;
     const float *dr = P.dd + (size_t)e * (DH / 256) + (size_t)b * H + 32 * kt0 + seg * LC;
-    // Waves whose rows all lie past the item zero them once and skip the
-    // loads and the arithmetic, as in the gate/up kernel.
-    const bool rows_live = __builtin_amdgcn_readfirstlane(4 * (tid >> 6)) < nrows;
-    v4f xv[LC / 4], dv[LC / 4];
+    // Waves whose rows of a tile all lie past the item zero them once and
+    // skip their loads and arithmetic, as in the gate/up kernel.
+    bool rows_live[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+        rows_live[rt] = __builtin_amdgcn_readfirstlane(16 * rt + 4 * (tid >> 6)) < nrows;
+    v4f xv[RT][LC / 4], dv[LC / 4];
     auto a_load = [&](int ch) {
-        if (!rows_live) return;
+        if (!rows_live[0]) return;
 #pragma unroll
-        for (int i = 0; i < LC / 4; ++i) {
-            xv[i] = KSG ? *reinterpret_cast<const v4f *>(&Ms[KSG ? arow : 0][32 * KC * ch + seg * LC + 4 * i])
-                        : *reinterpret_cast<const v4f *>(xr + 32 * KC * ch + 4 * i);
-            dv[i] = *reinterpret_cast<const v4f *>(dr + 32 * KC * ch + 4 * i);
-        }
+        for (int i = 0; i < LC / 4; ++i) dv[i] = *reinterpret_cast<const v4f *>(dr + 32 * KC * ch + 4 * i);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+            if (rows_live[rt])
+#pragma unroll
+                for (int i = 0; i < LC / 4; ++i)
+                    xv[rt][i] = KSG ? *reinterpret_cast<const v4f *>(
+                                          &Ms[KSG ? arow[0] : 0][32 * KC * ch + seg * LC + 4 * i])
+                                    : *reinterpret_cast<const v4f *>(xr[rt] + 32 * KC * ch + 4 * i);
     };
-    float ascale = 0.0f;
-    if (!rows_live) {
+    float ascale[RT];
 #pragma unroll
-        for (int buf = 0; buf < NBUF; ++buf)
+    for (int rt = 0; rt < RT; ++rt) {
+        ascale[rt] = 0.0f;
+        if (!rows_live[rt]) {
 #pragma unroll
-            for (int o = 0; o < LC / 8; ++o) {
-                const int kk = seg * LC + 8 * o, kl = kk >> 5, ko = kk & 31;
-                const int w0 = (ar * ORN_AST + ko) >> 1;
-                *reinterpret_cast<uint4 *>(&As[buf][kl][0][w0]) = make_uint4(0u, 0u, 0u, 0u);
-                *reinterpret_cast<uint4 *>(&As[buf][kl][1][w0]) = make_uint4(0u, 0u, 0u, 0u);
-            }
+            for (int buf = 0; buf < NBUF; ++buf)
+#pragma unroll
+                for (int o = 0; o < LC / 8; ++o) {
+                    const int kk = seg * LC + 8 * o, kl = kk >> 5, ko = kk & 31;
+                    const int w0 = (ar * ORN_AST + ko) >> 1;
+                    *reinterpret_cast<uint4 *>(&As[buf][kl][rt][0][w0]) = make_uint4(0u, 0u, 0u, 0u);
+                    *reinterpret_cast<uint4 *>(&As[buf][kl][rt][1][w0]) = make_uint4(0u, 0u, 0u, 0u);
+                }
+        }
     }
     auto a_store = [&](int ch) {
-        if (!rows_live) return;
         const int buf = ch % NBUF;
 #pragma unroll
-        for (int o = 0; o < LC / 8; ++o) {
-            const int kk = seg * LC + 8 * o;
-            const int kl = kk >> 5, ko = kk & 31;
-            uint32_t hi[4], lo[4];
+        for (int rt = 0; rt < RT; ++rt) {
+            if (!rows_live[rt]) continue;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const v4f x4 = xv[2 * o + (j >> 1)], d4 = dv[2 * o + (j >> 1)];
-                const int u = 2 * (j & 1);
-                split2(x4[u] * ascale * d4[u], x4[u + 1] * ascale * d4[u + 1], hi[j], lo[j]);
+            for (int o = 0; o < LC / 8; ++o) {
+                const int kk = seg * LC + 8 * o;
+                const int kl = kk >> 5, ko = kk & 31;
+                uint32_t hi[4], lo[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const v4f x4 = xv[rt][2 * o + (j >> 1)], d4 = dv[2 * o + (j >> 1)];
+                    const int u = 2 * (j & 1);
+                    split2(x4[u] * ascale[rt] * d4[u], x4[u + 1] * ascale[rt] * d4[u + 1], hi[j], lo[j]);
+                }
+                const int w0 = (ar * ORN_AST + ko) >> 1;
+                *reinterpret_cast<uint4 *>(&As[buf][kl][rt][0][w0]) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+                *reinterpret_cast<uint4 *>(&As[buf][kl][rt][1][w0]) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
             }
-            const int w0 = (ar * ORN_AST + ko) >> 1;
-            *reinterpret_cast<uint4 *>(&As[buf][kl][0][w0]) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-            *reinterpret_cast<uint4 *>(&As[buf][kl][1][w0]) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
         }
     };
     a_load(0);
-    ascale = ar < nrows ? row_scale(amax, dmx) : 0.0f;
-    if (seg == 0) s_inv[ar] = ascale != 0.0f ? 1.0f / ascale : 0.0f;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        ascale[rt] = 16 * rt + ar < nrows ? row_scale(amax[rt], dmx) : 0.0f;
+        if (seg == 0) s_inv[16 * rt + ar] = ascale[rt] != 0.0f ? 1.0f / ascale[rt] : 0.0f;
+    }
     a_store(0);
     if (NCHK > 1) a_load(1);
     __syncthreads();
 
-    v4f acc[4];
+    const int rt_live = RT > 1 && nrows > 16 ? RT : 1;  // uniform, as in k_gateup_dec
+    v4f acc[RT][4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[j] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[rt][j] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
     const int ro = c * ORN_AST + 8 * g;
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
@@ -431,13 +512,17 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
         __builtin_amdgcn_sched_barrier(0);
         if (kt + NR < KT) load_b(r, kt + NR);
         __builtin_amdgcn_sched_barrier(0);
-        const _Float16 *A = reinterpret_cast<const _Float16 *>(As[ch % NBUF][kl][0]);
-        const v8h ahi = *reinterpret_cast<const v8h *>(A + ro);
-        const v8h alo = *reinterpret_cast<const v8h *>(A + 16 * ORN_AST + ro);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            acc[j] = mfma(ahi, bq[j], acc[j]);
-            acc[j] = mfma(alo, bq[j], acc[j]);
+        for (int rt = 0; rt < RT; ++rt) {
+            if (rt >= rt_live) break;
+            const _Float16 *A = reinterpret_cast<const _Float16 *>(As[ch % NBUF][kl][rt][0]);
+            const v8h ahi = *reinterpret_cast<const v8h *>(A + ro);
+            const v8h alo = *reinterpret_cast<const v8h *>(A + 16 * ORN_AST + ro);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc[rt][j] = mfma(ahi, bq[j], acc[rt][j]);
+                acc[rt][j] = mfma(alo, bq[j], acc[rt][j]);
+            }
         }
         if (kl == 0 && ch + 1 < NCHK) {
             a_store(ch + 1);
@@ -449,22 +534,27 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
     float *row0 = dn + ((size_t)kslice * rows_max + itm.y) * D;
     const int colb = 256 * b + 64 * wave + c;
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-        const int row = 4 * g + rr;
-        const float si = s_inv[row];
-        if (row < nrows) {
-            float *o = row0 + (size_t)row * D + colb;
+    for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) o[16 * j] = acc[j][rr] * si;
+        for (int rr = 0; rr < 4; ++rr) {
+            const int row = 16 * rt + 4 * g + rr;
+            const float si = s_inv[row];
+            if (row < nrows) {
+                float *o = row0 + (size_t)row * D + colb;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) o[16 * j] = acc[rt][j][rr] * si;
+            }
         }
-    }
 }
 
 }  // namespace
 
-// Decode instances: work items of <= 16 rows; KT = D/32/ks (gate/up) or
-// H/32/ks (down) reduction steps per slice, 4 to 32; activation tiles in
-// chunks of 4 steps (LDS: 2 x 20 KB for gate/up, 2 x 10 KB for down).
+// Decode instances: work items of <= 16 rows (one row tile), or <= 32 (two,
+// for batches above 64 tokens whose hot experts span several items); KT =
+// D/32/ks (gate/up) or H/32/ks (down) reduction steps per slice, 4 to 32;
+// activation tiles in chunks of 4 steps (LDS per row tile: 2 x 20 KB for
+// gate/up, 2 x 10 KB for down), of 2 steps for two-tile gate/up, so that
+// every instance keeps at most 41 KB.
 extern "C" int ornk_dec_supported(int kt_gu, int kt_dn)
 {
     auto ok = [](int kt) { return kt == 4 || kt == 8 || kt == 16 || kt == 32; };
@@ -474,10 +564,11 @@ extern "C" int ornk_dec_supported(int kt_gu, int kt_dn)
 extern "C" int ornk_moe_gateup_dec(const ornk_moe_args *a, hipStream_t s)
 {
     const int ks = a->ks_gu;
-    if (a->D % 32 || a->H % 256 || ks < 1 || (a->D / 32) % ks || a->tchunk > 16)
+    if (a->D % 32 || a->H % 256 || ks < 1 || (a->D / 32) % ks || a->tchunk > 32)
         return hipErrorInvalidValue;
     const int KT = a->D / 32 / ks;
     if (!ornk_dec_supported(KT, 4)) return hipErrorInvalidValue;
+    const int RT = a->tchunk > 16 ? 2 : 1;
     const float *xin = a->apply_norm ? a->xn : a->x;
     hipEvent_t st = a->ev_start;  // the step's first kernel carries the start event
     if (!a->router_amax) {
@@ -486,16 +577,23 @@ extern "C" int ornk_moe_gateup_dec(const ornk_moe_args *a, hipStream_t s)
         st = nullptr;
     }
     const dim3 grid(a->items_max * 2 * (a->H / 256) * ks);
-#define ORN_GU_DEC(K)                                                                          \
-    ORN_LAUNCH_EV2(st, a->ev_stop, (k_gateup_dec<ORN_DEC_NR, K, 4>), grid, dim3(256), 0, s,    \
+#define ORN_GU_DEC(K, R)                                                                       \
+    ORN_LAUNCH_EV2(st, a->ev_stop, (k_gateup_dec<ORN_DEC_NR, K, 4 / R, R>), grid, dim3(256), 0, s, \
                    a->gu_pf, xin, a->x_amax, a->ctl, reinterpret_cast<const int4 *>(a->items), \
                    a->row_token, a->gu_part, a->T, a->D, a->H, ks, a->rows_max)
-    switch (KT) {
-    case 4: ORN_GU_DEC(4); break;
-    case 8: ORN_GU_DEC(8); break;
-    case 16: ORN_GU_DEC(16); break;
-    default: ORN_GU_DEC(32); break;
+#define ORN_GU_DEC_RT(R)                \
+    switch (KT) {                       \
+    case 4: ORN_GU_DEC(4, R); break;    \
+    case 8: ORN_GU_DEC(8, R); break;    \
+    case 16: ORN_GU_DEC(16, R); break;  \
+    default: ORN_GU_DEC(32, R); break;  \
     }
+    if (RT == 2) {
+        ORN_GU_DEC_RT(2)
+    } else {
+        ORN_GU_DEC_RT(1)
+    }
+#undef ORN_GU_DEC_RT
 #undef ORN_GU_DEC
     return hipGetLastError();
 }
@@ -513,15 +611,16 @@ extern "C" int ornk_down_dec_fuses_mid(int T, int H, int ks_gu, int ks_dn)
 extern "C" int ornk_moe_down_dec(const ornk_moe_args *a, hipStream_t s)
 {
     const int ks = a->ks_dn;
-    if (a->H % 32 || a->D % 256 || ks < 1 || (a->H / 32) % ks || a->tchunk > 16)
+    if (a->H % 32 || a->D % 256 || ks < 1 || (a->H / 32) % ks || a->tchunk > 32)
         return hipErrorInvalidValue;
     const int KT = a->H / 32 / ks;
     if (!ornk_dec_supported(4, KT)) return hipErrorInvalidValue;
+    const int RT = a->tchunk > 16 ? 2 : 1;
     const dim3 grid(a->items_max * (a->D / 256) * ks);
     const int shared_rows = a->has_shared ? a->T : 0;
-    if (ornk_down_dec_fuses_mid(a->T, a->H, a->ks_gu, ks)) {
+    if (RT == 1 && ornk_down_dec_fuses_mid(a->T, a->H, a->ks_gu, ks)) {
 #define ORN_DN_MID(KSG)                                                                         \
-    ORN_LAUNCH_EV(a, (k_down_dec<ORN_DEC_NR, 8, 4, KSG>), grid, dim3(256), 0, s, a->dn_pf,      \
+    ORN_LAUNCH_EV(a, (k_down_dec<ORN_DEC_NR, 8, 4, KSG, 1>), grid, dim3(256), 0, s, a->dn_pf,   \
                   a->mid, a->mid_amax, a->ctl, reinterpret_cast<const int4 *>(a->items),         \
                   a->dn_part, a->D, a->H, ks, a->rows_max, a->gu_part, shared_rows)
         switch (a->ks_gu) {
@@ -532,16 +631,23 @@ extern "C" int ornk_moe_down_dec(const ornk_moe_args *a, hipStream_t s)
 #undef ORN_DN_MID
         return hipGetLastError();
     }
-#define ORN_DN_DEC(K)                                                                          \
-    ORN_LAUNCH_EV(a, (k_down_dec<ORN_DEC_NR, K, 4, 0>), grid, dim3(256), 0, s, a->dn_pf, a->mid, \
-                       a->mid_amax, a->ctl, reinterpret_cast<const int4 *>(a->items),           \
+#define ORN_DN_DEC(K, R)                                                                          \
+    ORN_LAUNCH_EV(a, (k_down_dec<ORN_DEC_NR, K, 4, 0, R>), grid, dim3(256), 0, s, a->dn_pf, a->mid, \
+                       a->mid_amax, a->ctl, reinterpret_cast<const int4 *>(a->items),              \
                        a->dn_part, a->D, a->H, ks, a->rows_max, a->gu_part, shared_rows)
-    switch (KT) {
-    case 4: ORN_DN_DEC(4); break;
-    case 8: ORN_DN_DEC(8); break;
-    case 16: ORN_DN_DEC(16); break;
-    default: ORN_DN_DEC(32); break;
+#define ORN_DN_DEC_RT(R)                \
+    switch (KT) {                       \
+    case 4: ORN_DN_DEC(4, R); break;    \
+    case 8: ORN_DN_DEC(8, R); break;    \
+    case 16: ORN_DN_DEC(16, R); break;  \
+    default: ORN_DN_DEC(32, R); break;  \
     }
+    if (RT == 2) {
+        ORN_DN_DEC_RT(2)
+    } else {
+        ORN_DN_DEC_RT(1)
+    }
+#undef ORN_DN_DEC_RT
 #undef ORN_DN_DEC
     return hipGetLastError();
 }
