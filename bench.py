@@ -351,11 +351,48 @@ def measure_attention(ctx):
     return res
 
 
+def measure_dequant(ctx):
+    """The device dequant API (gpu_dequantize_tensor_buf, gguf.c:605-638) on
+    one layer's expert tensor: 256 experts x 2048 x 512 weights, Q4_K (the
+    gate / up layout) and Q6_K (down), to fp32.  HBM-bound: the quantized
+    bytes read plus 4 bytes written per weight, per call (synchronous, as the
+    API is), against 8 TB/s."""
+    n = 256 * 2048 * 512
+    L = om.lib()
+    res = {}
+    for name, typ, bsize, d_offs in (("q4k", 12, 144, (0, 2)), ("q6k", 14, 210, (208,))):
+        nb = n // 256
+        blocks = np.zeros((nb, bsize), np.uint8)
+        for off in d_offs:
+            blocks[:, off + 1] = 0x3C  # d = 1.0
+        src, dst = ctx.upload(blocks.reshape(-1)), ctx.alloc(4 * n)
+        del blocks
+        info = om.tensor_info(typ, [n])
+        if not L.gpu_dequantize_tensor_buf(ctx.ptr, src.ptr, om.C.byref(info), dst.ptr):
+            raise RuntimeError(ctx.last_error())
+        ctx.sync()
+        reps = 10
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            L.gpu_dequantize_tensor_buf(ctx.ptr, src.ptr, om.C.byref(info), dst.ptr)
+        ctx.sync()
+        dt = (time.perf_counter() - t0) / reps
+        moved = nb * bsize + 4 * n
+        res[f"dequant_{name}_256x2048x512"] = {"ms": round(dt * 1e3, 3),
+                                              "gbs": round(moved / dt / 1e9, 1),
+                                              "frac": round(moved / dt / 8e12, 4),
+                                              "bytes_per_call": moved}
+        src.free()
+        dst.free()
+    log("dequant", res)
+    return res
+
+
 # Extra configs reported beside the headline: (label, store layer, tokens).
 # Layer 1 carries a Zipf(1.1) router bias.
 EXTRA_CONFIGS = (("decode_t1", 0, 1), ("prefill_t2048", 0, 2048), ("zipf_t256", 1, 256))
 EXTRA_LABELS = [c[0] for c in EXTRA_CONFIGS] + ["file_t1", "file_t16", "file_t2048", "stack40",
-                                                 "streamed", "attention"]
+                                                 "streamed", "attention", "dequant"]
 
 
 def headline(ctx, store, args, read_gbs):
@@ -499,6 +536,8 @@ def main():
         result.setdefault("configs", {}).update(measure_streamed(ctx, args.steps))
     if not args.no_extra and want("attention"):
         result.setdefault("configs", {}).update(measure_attention(ctx))
+    if not args.no_extra and want("dequant"):
+        result.setdefault("configs", {}).update(measure_dequant(ctx))
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_budget)
     ctx.close()

@@ -8,8 +8,11 @@
 // (Q6_K), so every product below is exact in fp32; the only rounding is
 // Q4_K's final "- dmin*m", which this code performs exactly as the reference
 // does.  The half decode is the reference's integer mapping (common.h).
-// Reads are byte-granular because GGUF Q6_K blocks (210 B) are only 2-byte
-// aligned inside a tensor.
+// Whole tensors: each thread writes 4 consecutive elements with one 16-byte
+// store, reading its 4 quants with one 4-byte (Q4_K: 144-byte blocks keep
+// 4-byte alignment) or two 2-byte loads (Q6_K: 210-byte blocks are only
+// 2-byte aligned inside a tensor); pointers without that alignment take the
+// one-element-per-thread kernels, which read bytes.
 #include "common.h"
 #include "launch.h"
 
@@ -44,6 +47,60 @@ __device__ __forceinline__ float q6k_elem(const uint8_t *blk, int pos)
     const int q = (int)(lo | (((qhb >> (2 * lane)) & 3u) << 4)) - 32;
     const int sc = (int)(int8_t)blk[ORN_Q6K_OFF_SCALES + pass * 8 + lane * 2 + is];
     return d * (float)sc * (float)q;
+}
+
+// Elements pos0..pos0+3 (pos0 % 4 == 0: one sub-block, one qs run) of the
+// block at blk, with q4k_elem's arithmetic.
+__device__ __forceinline__ float4 q4k_quad(const uint8_t *blk, int pos0)
+{
+    const int sub = pos0 >> 5, chunk = pos0 >> 6, half = (pos0 >> 5) & 1, l = pos0 & 31;
+    const uint8_t *s = blk + ORN_Q4K_OFF_SCALES;
+    uint32_t sc, m;
+    if (sub < 4) {
+        sc = s[sub] & 63u;
+        m = s[sub + 4] & 63u;
+    } else {
+        sc = (s[sub + 4] & 0xFu) | (((uint32_t)s[sub - 4] >> 6) << 4);
+        m = ((uint32_t)s[sub + 4] >> 4) | (((uint32_t)s[sub] >> 6) << 4);
+    }
+    const float d_val = orn_half_to_float(orn_ld_u16(blk + ORN_Q4K_OFF_D)) * (float)sc;
+    const float min_val = orn_half_to_float(orn_ld_u16(blk + ORN_Q4K_OFF_DMIN)) * (float)m;
+    const uint32_t w = *reinterpret_cast<const uint32_t *>(blk + ORN_Q4K_OFF_QS + chunk * 32 + l);
+    const uint32_t q = half ? (w >> 4) & 0x0F0F0F0Fu : w & 0x0F0F0F0Fu;
+    return make_float4(d_val * (float)(q & 0xFFu) - min_val, d_val * (float)((q >> 8) & 0xFFu) - min_val,
+                       d_val * (float)((q >> 16) & 0xFFu) - min_val, d_val * (float)(q >> 24) - min_val);
+}
+
+// The same for Q6_K (pos0 % 4 == 0: one pass, lane and scale).
+__device__ __forceinline__ float4 q6k_quad(const uint8_t *blk, int pos0)
+{
+    const int pass = pos0 >> 7, lane = (pos0 >> 5) & 3, l = pos0 & 31, is = l >> 4;
+    const float d = orn_half_to_float(orn_ld_u16(blk + ORN_Q6K_OFF_D));
+    const uint8_t *qlp = blk + ORN_Q6K_OFF_QL + pass * 64 + ((lane & 1) ? 32 + l : l);
+    const uint8_t *qhp = blk + ORN_Q6K_OFF_QH + pass * 32 + l;
+    // every offset here is even, and the launcher checked that src is
+    const uint16_t *ql16 = reinterpret_cast<const uint16_t *>(qlp);
+    const uint16_t *qh16 = reinterpret_cast<const uint16_t *>(qhp);
+    const uint32_t qlw = (uint32_t)ql16[0] | ((uint32_t)ql16[1] << 16);
+    const uint32_t qhw = (uint32_t)qh16[0] | ((uint32_t)qh16[1] << 16);
+    const uint32_t lo = (lane < 2) ? (qlw & 0x0F0F0F0Fu) : ((qlw >> 4) & 0x0F0F0F0Fu);
+    const uint32_t hi = ((qhw >> (2 * lane)) & 0x03030303u) << 4;
+    const uint32_t q = lo | hi;  // four 6-bit values, one per byte
+    const float ds = d * (float)(int)(int8_t)blk[ORN_Q6K_OFF_SCALES + pass * 8 + lane * 2 + is];
+    return make_float4(ds * (float)((int)(q & 0xFFu) - 32), ds * (float)((int)((q >> 8) & 0xFFu) - 32),
+                       ds * (float)((int)((q >> 16) & 0xFFu) - 32), ds * (float)((int)(q >> 24) - 32));
+}
+
+// 64 threads per block of 256 elements, four blocks per work group pass.
+template <bool Q6>
+__global__ void __launch_bounds__(256) k_dequant_quad(const uint8_t *src, float4 *dst, uint64_t n_blocks)
+{
+    const int sub_blk = threadIdx.x >> 6, pos0 = 4 * (threadIdx.x & 63);
+    for (uint64_t b = (uint64_t)blockIdx.x * 4 + sub_blk; b < n_blocks; b += (uint64_t)gridDim.x * 4) {
+        const float4 v = Q6 ? q6k_quad(src + b * ORN_Q6K_BYTES, pos0)
+                            : q4k_quad(src + b * ORN_Q4K_BYTES, pos0);
+        dst[b * (ORN_QK_K / 4) + (pos0 >> 2)] = v;
+    }
 }
 
 __global__ void k_dequant_q4k(const uint8_t *src, float *dst, uint64_t n_blocks)
@@ -109,11 +166,19 @@ extern "C" int ornk_dequant(const void *src, int type, uint64_t n_elems, float *
         return hipGetLastError();
     case ORN_TYPE_Q4_K:
         if (nb == 0) return hipSuccess;
-        hipLaunchKernelGGL(k_dequant_q4k, dim3(grid_cap(nb, 1)), dim3(ORN_QK_K), 0, s, p, dst, nb);
+        if (((uintptr_t)p & 3) == 0 && ((uintptr_t)dst & 15) == 0)
+            hipLaunchKernelGGL(k_dequant_quad<false>, dim3(grid_cap(nb, 4)), dim3(256), 0, s, p,
+                               reinterpret_cast<float4 *>(dst), nb);
+        else
+            hipLaunchKernelGGL(k_dequant_q4k, dim3(grid_cap(nb, 1)), dim3(ORN_QK_K), 0, s, p, dst, nb);
         return hipGetLastError();
     case ORN_TYPE_Q6_K:
         if (nb == 0) return hipSuccess;
-        hipLaunchKernelGGL(k_dequant_q6k, dim3(grid_cap(nb, 1)), dim3(ORN_QK_K), 0, s, p, dst, nb);
+        if (((uintptr_t)p & 1) == 0 && ((uintptr_t)dst & 15) == 0)
+            hipLaunchKernelGGL(k_dequant_quad<true>, dim3(grid_cap(nb, 4)), dim3(256), 0, s, p,
+                               reinterpret_cast<float4 *>(dst), nb);
+        else
+            hipLaunchKernelGGL(k_dequant_q6k, dim3(grid_cap(nb, 1)), dim3(ORN_QK_K), 0, s, p, dst, nb);
         return hipGetLastError();
     default:
         return hipErrorInvalidValue;

@@ -201,6 +201,33 @@ def test_dequant_kquant_golden(om, ctx, golden_dir, name, typ):
     assert np.all(out[:256] == (1.0 if typ == 12 else -31.0))
 
 
+@pytest.mark.parametrize("typ,bsize,d_offs", [(12, 144, (0, 2)), (14, 210, (208,))],
+                         ids=["q4k", "q6k"])
+def test_dequant_random_blocks_match_oracle(om, ctx, typ, bsize, d_offs):
+    """4097 random super-blocks (every scale, min and quant bit pattern;
+    finite fp16 d / dmin) through the device dequant, bit for bit against the
+    oracle's restatement of gguf.c:511-571 (itself pinned by the golden
+    vectors above), host-pointer and device-resident calls."""
+    from oracle import oracle as O
+    nb = 4097
+    rng = np.random.default_rng(typ)
+    blocks = rng.integers(0, 256, (nb, bsize), dtype=np.uint8)
+    for off in d_offs:  # finite halves: exponent field below 31
+        blocks[:, off + 1] &= 0x7B
+    n = 256 * nb
+    ok, ref = O.dequant_tensor(blocks.reshape(-1), typ, n)
+    assert ok
+    info = om.tensor_info(typ, [n])
+    out = np.zeros(n, np.float32)
+    assert om.lib().gpu_dequantize_tensor_from_buf(ctx.ptr, f32p(blocks), C.byref(info), f32p(out))
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+    src, dst = ctx.upload(blocks.reshape(-1)), ctx.alloc(4 * n)
+    assert om.lib().gpu_dequantize_tensor_buf(ctx.ptr, src.ptr, C.byref(info), dst.ptr)
+    assert np.array_equal(ctx.download(dst, np.float32, n).view(np.uint32), ref.view(np.uint32))
+    src.free()
+    dst.free()
+
+
 def test_dequant_f16_f32_golden(om, ctx, golden_dir):
     g = load(golden_dir, "dequant_f16_all.npz")
     info = om.tensor_info(1, [65536])
