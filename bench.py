@@ -11,7 +11,8 @@ Prints ONE JSON line (rank 0).  Also reported in "configs": the other
 BASELINE configs measured the same way (1-token decode, 2048-token prefill,
 Zipf-skewed 256 tokens, and the 40-layer resident stack at 1 and 16 tokens;
 --no-stack skips the stack), the file-orientation store, streamed experts
-(host tier + device slots) and the attention-side gpu.h ops.
+(host tier + device slots), the attention-side gpu.h ops and the device
+dequant API.
 
 `roofline` is for the dominant kernel of the step: algorithmic bytes of the
 expert weights that kernel streams (active experts x bytes per expert) over
@@ -20,7 +21,9 @@ stream around every launch inside the timed region.
 
 `cpu_baseline` times the reference's own C CPU path (oracle/_ref, compiled
 from the reference sources: model_forward on a one-layer Ornith-shape
-model) on a bounded sample of tokens, single-threaded as the reference runs.
+model) on a bounded sample of tokens, single-threaded as the reference runs;
+its "contiguous" entry times the reference's arithmetic on a contiguous
+per-expert layout (the C99 oracle) for every config, on the same expert bytes.
 """
 from __future__ import annotations
 
@@ -214,6 +217,43 @@ def cpu_baseline(budget_s):
         dt = time.perf_counter() - t0
         return {"value": round(16 / dt, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
                 "sample": f"16-token decode batch through the oracle restatement, {dt:.2f} s"}
+
+
+def cpu_contiguous(store):
+    """CPU baseline variant (ii) for every config: the reference's arithmetic
+    on a contiguous per-expert layout (blockwise dequant + per-token matvec,
+    no cross-token reuse; the C99 oracle, one thread) over the same expert
+    bytes and activations as the GPU configs.  decode_t1 / decode_t16 run in
+    full (median of 3 after one warm-up); prefill_t2048 and zipf_t256 time
+    their first 32 tokens and extrapolate linearly (tokens are independent)."""
+    from oracle import oracle as O
+    E1 = E + 1
+    layers = {}
+    for l, zipf in ((0, 0.0), (1, 1.1)):
+        W = om.synth_normal(SEED, om.synth_stream(l, om.SYN_ROUTER, 0), D * E, 0.02).reshape(D, E)
+        bias = om.synth_zipf_bias(SEED, om.synth_stream(l, om.SYN_ZIPF, 0), E, zipf) if zipf else None
+        mats = [store.get_experts(l, m, 0, E1) for m in (om.MAT_GATE, om.MAT_UP, om.MAT_DOWN)]
+        layers[l] = (W, bias, mats)
+    out = {}
+    for label, layer, T, sample in (("decode_t1", 0, 1, 1), ("decode_t16", 0, 16, 16),
+                                    ("prefill_t2048", 0, 2048, 32), ("zipf_t256", 1, 256, 32)):
+        W, bias, (g, u, d) = layers[layer]
+        per_g, per_d = g.size // E1, d.size // E1
+        X = om.synth_normal(1, om.synth_stream(0, om.SYN_ACT, 0), T * D, 1.0).reshape(T, D)[:sample]
+
+        def run():
+            t0 = time.perf_counter()
+            O.moe_layer(D=D, H=H, E=E, k=K, x=X, router_W=W, bias=bias, gate=g[:E * per_g],
+                        up=u[:E * per_g], down=d[:E * per_d], sh_gate=g[E * per_g:],
+                        sh_up=u[E * per_g:], sh_down=d[E * per_d:])
+            return time.perf_counter() - t0
+        run()
+        dt = sorted(run() for _ in range(3 if sample <= 16 else 1))[(3 if sample <= 16 else 1) // 2]
+        out[label] = {"tokens_per_s": round(sample / dt, 2),
+                      "sample": f"{sample} of {T} tokens" + (", extrapolated linearly" if sample < T else ""),
+                      "s_per_sample": round(dt, 3)}
+    return {"variant": "contiguous layout, reference arithmetic (oracle, 1 thread)", "cores": 1,
+            "configs": out}
 
 
 def stack_active_experts(ctx, st, n_layers, T):
@@ -528,6 +568,8 @@ def main():
                 log(label, extra[label]["tokens_per_s"], "tok/s")
             fst.close()
         result["configs"] = extra
+    # CPU variant (ii) reads the experts back from this store (closed next)
+    cpu_contig = cpu_contiguous(store) if not args.no_cpu and not args.only else None
     store.close()
     want = lambda label: not args.only or args.only == label  # noqa: E731
     if not args.no_stack and want("stack40"):
@@ -540,6 +582,9 @@ def main():
         result.setdefault("configs", {}).update(measure_dequant(ctx))
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_budget)
+        if cpu_contig:
+            result["cpu_baseline"]["contiguous"] = cpu_contig
+            log("cpu contiguous", cpu_contig)
     ctx.close()
     print(json.dumps(result), flush=True)
 
