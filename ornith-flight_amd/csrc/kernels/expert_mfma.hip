@@ -227,10 +227,12 @@ __device__ __forceinline__ void gateup_tile(const GuBlock &B, ATiles<ROWS, 4> &A
         load_b(rb, k + 4);
         __builtin_amdgcn_sched_barrier(0);
         mma_step<NTT>(As.t[buf][0], As.t[buf][1], bq, acc, c, g);
-        if (a_live) {
-            accm = mfma(*reinterpret_cast<const v8h *>(&As.t[buf][2][mro]), bm, accm);
-            accm = mfma(*reinterpret_cast<const v8h *>(&As.t[buf][3][mro]), bm, accm);
-        }
+        // the mins tile of row tile `wave` (every wave: a wave past the
+        // item's row tiles reads prepared zero rows and its result is never
+        // stored), branch-free so that the next step's activation
+        // preparation below shares one scheduling region with the MFMAs
+        accm = mfma(*reinterpret_cast<const v8h *>(&As.t[buf][2][mro]), bm, accm);
+        accm = mfma(*reinterpret_cast<const v8h *>(&As.t[buf][3][mro]), bm, accm);
         pin_a(ra);
         const int nb = buf ^ 1;
         a_store_l(ra, B, k + 1 < KT ? k + 1 : KT - 1, &As.t[nb][0][B.aoff], &As.t[nb][1][B.aoff],
@@ -272,7 +274,7 @@ __device__ __forceinline__ void gateup_tile(const GuBlock &B, ATiles<ROWS, 4> &A
 // NTTMAX = 1: items of at most 16 rows (decode), one row tile, small LDS.
 // NTTMAX = 4: items of at most 64 rows (prefill), 1..4 row tiles.
 template <int NTTMAX>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
     k_gateup_mfma(ornk_gu_prefill P, const float *__restrict__ xn,
                   const float *__restrict__ x_amax, const int *__restrict__ ctl,
                   const int4 *__restrict__ items, const int *__restrict__ row_token,
