@@ -1126,7 +1126,7 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     }
     if (use_mfma) {
         a.x_amax = (float *)(ws + o_xamax);
-        a.router_amax = ornk_router_pc_supported(T, D);
+        a.router_amax = 1;  /* every routing kernel writes the rows' max |x| */
         a.mid_amax = (float *)(ws + o_midamax);
     }
 

@@ -149,7 +149,7 @@ template <int TPW>
 __global__ void __launch_bounds__(256)
     k_router_seq(const float *__restrict__ x, const float *__restrict__ Wq,
                  const float *__restrict__ bias, int T, int D, int E,
-                 float *__restrict__ logits, int *ctl)
+                 float *__restrict__ logits, int *ctl, float *__restrict__ amax)
 {
     constexpr int TB = 4 * TPW;               // tokens per block
     constexpr int XF4 = TB * ORN_RDC / 4;     // activation float4 per chunk
@@ -203,6 +203,10 @@ __global__ void __launch_bounds__(256)
     float acc[TPW];
 #pragma unroll
     for (int j = 0; j < TPW; ++j) acc[j] = 0.0f;
+    // amax (block column 0): the staging threads' running max |x| over
+    // their token's quads, folded over the token's ORN_RDC/4 threads below
+    const bool want_amax = amax && blockIdx.x == 0;
+    float xmax = 0.0f;
 
     for (int c0 = 0; c0 < nc; c0 += ORN_RPF) {
 #pragma unroll
@@ -214,7 +218,13 @@ __global__ void __launch_bounds__(256)
                 for (int i = 0; i < WPT; ++i) wl[sl][wdst[i]] = rw[p * WPT + i];
 #pragma unroll
                 for (int i = 0; i < XPT; ++i)
-                    if (xon[i]) xl[sl][tid + 256 * i] = rx[p * XPT + i];
+                    if (xon[i]) {
+                        const v4f v = rx[p * XPT + i];
+                        xl[sl][tid + 256 * i] = v;
+                        if (want_amax)
+                            xmax = fmaxf(xmax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)),
+                                                     fmaxf(fabsf(v.z), fabsf(v.w))));
+                    }
                 const int cn = min(c + ORN_RPF, nc - 1);
 #pragma unroll
                 for (int i = 0; i < WPT; ++i)
@@ -249,6 +259,15 @@ __global__ void __launch_bounds__(256)
             if (t < T) logits[(size_t)t * E + e] = bias ? acc[j] + b : acc[j];
         }
     }
+    if (want_amax) {
+        // thread q = tt * (ORN_RDC/4) + d4 staged token tt's quads d4, d4 +
+        // ORN_RDC/4, ... (XPT = 1: TB * ORN_RDC/4 <= 256 threads)
+        static_assert(XPT == 1, "one staged quad per thread and chunk");
+#pragma unroll
+        for (int off = 1; off < ORN_RDC / 4; off <<= 1) xmax = fmaxf(xmax, __shfl_xor(xmax, off, 64));
+        const int tt = tid / (ORN_RDC / 4), t = t0 + tt;
+        if (xon[0] && tid % (ORN_RDC / 4) == 0 && t < T) amax[t] = xmax;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -274,7 +293,7 @@ __device__ __forceinline__ void wave_sync()
 __global__ void __launch_bounds__(64)
     k_router_dec(const float *__restrict__ x, const float *__restrict__ Wq,
                  const float *__restrict__ bias, int T, int D, int E,
-                 float *__restrict__ logits, int *ctl)
+                 float *__restrict__ logits, int *ctl, float *__restrict__ amax)
 {
     extern __shared__ v4f xsh[];  // [D/4]
     const int lane = threadIdx.x;
@@ -294,6 +313,18 @@ __global__ void __launch_bounds__(64)
 #pragma unroll
         for (int j = 0; j < 16; ++j)
             if (lane + 64 * j < nd4) xw[lane + 64 * j] = tmp[j];
+        // max |x| of the row for the MFMA activation scaling (block column 0)
+        if (amax && blockIdx.x == 0) {
+            float mx = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                if (lane + 64 * j < nd4)
+                    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(tmp[j].x), fabsf(tmp[j].y)),
+                                         fmaxf(fabsf(tmp[j].z), fabsf(tmp[j].w))));
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+            if (lane == 0) amax[t] = mx;
+        }
     }
     wave_sync();
 
@@ -583,9 +614,8 @@ extern "C" int ornk_moe_route(const ornk_moe_args *a, hipStream_t s)
         D % (ORN_RDC * ORN_RPF) || D > 4096)
         return hipErrorInvalidValue;
     const float *xin = a->apply_norm ? a->xn : a->x;
-    float *amax = a->router_amax ? a->x_amax : nullptr;
+    float *amax = a->router_amax ? a->x_amax : nullptr;  // every routing kernel can write it
     const dim3 gd((E + 7) / 8, T);
-    if (a->router_amax && !ornk_router_pc_supported(T, D)) return hipErrorInvalidValue;
     if (ornk_router_pc_supported(T, D)) {
         // the norm runs inside the router here (ornk_moe_norm launches nothing)
         const float *xr = a->apply_norm ? a->x : xin;
@@ -604,10 +634,10 @@ extern "C" int ornk_moe_route(const ornk_moe_args *a, hipStream_t s)
 #undef ORN_RPC
     } else if (T >= 1024) {
         ORN_LAUNCH_EV(a, k_router_seq<4>, dim3((E + 63) / 64, (T + 15) / 16), dim3(256), 0, s,
-                           xin, a->router, a->bias, T, D, E, a->logits, a->ctl);
+                           xin, a->router, a->bias, T, D, E, a->logits, a->ctl, amax);
     } else {
         ORN_LAUNCH_EV(a, k_router_dec, dim3((E + 63) / 64, T), dim3(64), sizeof(float) * (size_t)D,
-                           s, xin, a->router, a->bias, T, D, E, a->logits, a->ctl);
+                           s, xin, a->router, a->bias, T, D, E, a->logits, a->ctl, amax);
     }
     return hipGetLastError();
 }
