@@ -1153,10 +1153,13 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
      * ones into slots and renumber the work items (host round trip) */
     if (st->cache && (rc = orn_cache_prepare(ctx, st->cache, layer, &a))) return rc;
     if (file) {
-        if ((rc = launch_k(ctx, "moe_file_prep_x", ornk_file_prep_x, &a))) return rc;
+        /* decode sizes: the router wrote the file kernels' activations */
+        if (!ornk_router_pc_supported(T, D) &&
+            (rc = launch_k(ctx, "moe_file_prep_x", ornk_file_prep_x, &a)))
+            return rc;
         if ((rc = launch_k(ctx, "moe_gateup_file", ornk_file_gateup, &a))) return rc;
+        /* the mid step also writes the down kernel's hi/lo activations */
         if ((rc = launch_k(ctx, "moe_mid", ornk_moe_mid, &a))) return rc;
-        if ((rc = launch_k(ctx, "moe_file_prep_mid", ornk_file_prep_mid, &a))) return rc;
         if ((rc = launch_k(ctx, "moe_down_file", ornk_file_down, &a))) return rc;
         if ((rc = launch_k(ctx, "moe_combine", ornk_moe_combine, &a))) return rc;
         ctx->last_ctl = a.ctl;

@@ -21,11 +21,12 @@
 //   Q6_K (v_mfma_f32_16x16x16_f16): sub-block scales are int8 (|sc * q| up
 //     to 4096, not exact in fp16), so B = q - 32 and each 16-value
 //     sub-block is one step: acc += (d * sc)(column) * P.
-// Activations come from k_prep_rows, which splits each row (times a power
-// of two s, |x*s| < 2^14) into fp16 hi + lo once per forward, and reach
-// the waves through one LDS tile per super-block and work group; products of
-// hi and lo with the exact B accumulate in fp32, and outputs are scaled
-// back by 1/s.
+// Activations come from k_prep_rows (the expert inputs) and from the mid
+// step (k_mid, expert_valu.hip, for the down kernel), which split each row
+// (times a power of two s, |x*s| < 2^14) into fp16 hi + lo once per
+// forward, and reach the waves through one LDS tile per super-block and
+// work group; products of hi and lo with the exact B accumulate in fp32,
+// and outputs are scaled back by 1/s.
 //
 // Any permutation of k applied to both A and B leaves a dot product
 // unchanged; the loads use two: within each group of 8 consecutive values
@@ -42,15 +43,6 @@ using namespace orn_mfma;
 namespace {
 
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
-
-// Power of two s with amax * s in [2^13, 2^14); 1 for 0 or non-finite.
-__device__ __forceinline__ float prep_scale(float amax)
-{
-    if (!(amax > 0.0f) || !(amax <= 3.0e38f)) return 1.0f;
-    int e = 13 - ilogbf(amax);
-    e = e < -126 ? -126 : (e > 126 ? 126 : e);
-    return ldexpf(1.0f, e);
-}
 
 // Activation tile of one super-block in LDS: [hi, lo][16 rows][256 values]
 // (row stride padded to 264 halves), staged once per work group from the
@@ -518,16 +510,6 @@ extern "C" int ornk_file_gateup(const ornk_moe_args *a, hipStream_t s)
         ORN_LAUNCH_EV(a, k_gu_file<1>, grid, dim3(256), 0, s, a->gate, a->up, f.xh, f.xl, f.xinv,
                       f.xsh, f.xsl, a->ctl, reinterpret_cast<const int4 *>(a->items),
                       a->row_token, a->gu_part, a->D, a->H, a->ks_gu, a->rows_max);
-    return hipGetLastError();
-}
-
-// mid rows -> hi/lo (rows past the live count ctl[2] are skipped).
-extern "C" int ornk_file_prep_mid(const ornk_moe_args *a, hipStream_t s)
-{
-    if (!ornk_file_supported(a->D, a->H)) return hipErrorInvalidValue;
-    const ornk_file_ws &f = a->fw;
-    ORN_LAUNCH_EV(a, k_prep_rows<false>, dim3(a->rows_max), dim3(256), 0, s, a->mid, a->H,
-                  a->ctl + 2, f.mh, f.ml, f.minv, (uint16_t *)nullptr, (uint16_t *)nullptr);
     return hipGetLastError();
 }
 

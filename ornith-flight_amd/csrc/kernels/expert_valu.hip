@@ -19,6 +19,7 @@
 // index, so one 144/210-byte block holds 256 consecutive outputs of one row.
 #include "common.h"
 #include "launch.h"
+#include "mfma_ops.h"
 
 
 namespace {
@@ -203,12 +204,17 @@ __global__ void __launch_bounds__(256)
 // ---------------------------------------------------------------------------
 // KMAX > 0 (= ks): the partials of a value are loaded together, one memory
 // round trip per thread; KMAX = 0: any ks, four partials at a time.
+// With fh (file-orientation stores) the row is also written as the down
+// kernel's activations: hi/lo fp16 of mid * s (s = prep_scale(max |mid|)) in
+// the pair order of k_prep_rows (expert_file.hip), and finv[r] = 1/s.
 template <int KMAX>
 __global__ void __launch_bounds__(256)
     k_mid(const float *__restrict__ gu_part, const int *__restrict__ ctl, float *__restrict__ mid,
-          int H, int ks, int rows_max, int shared_rows, float *__restrict__ row_amax)
+          int H, int ks, int rows_max, int shared_rows, float *__restrict__ row_amax,
+          uint32_t *__restrict__ fh, uint32_t *__restrict__ fl, float *__restrict__ finv)
 {
     __shared__ float red[4];
+    __shared__ __align__(16) float vrow[2048];  // the row, when fh (H <= 2048)
     const int r = blockIdx.x;
     if (r >= ctl[2]) return;
     float amax = 0.0f;
@@ -255,15 +261,33 @@ __global__ void __launch_bounds__(256)
         }
         const float v = act * u;
         mid[(size_t)r * H + h] = v;
+        if (fh) vrow[h] = v;
         amax = fmaxf(amax, fabsf(v));
     }
-    if (row_amax) {  // max |mid| of the row, for the MFMA down step's scaling
+    if (row_amax || fh) {  // max |mid| of the row, for the down step's scaling
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
         if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
         __syncthreads();
-        if (threadIdx.x == 0)
-            row_amax[r] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        if (row_amax && threadIdx.x == 0) row_amax[r] = amax;
+    }
+    if (fh) {
+        const int tid = threadIdx.x;
+        const float s = orn_mfma::prep_scale(amax);
+        if (tid < (H >> 3)) {  // 8 consecutive values a thread, as k_prep_rows
+            const v4f a = *reinterpret_cast<const v4f *>(&vrow[8 * tid]) * s;
+            const v4f b = *reinterpret_cast<const v4f *>(&vrow[8 * tid + 4]) * s;
+            uint32_t hv[4], lv[4];
+            orn_mfma::split2(a.x, a.z, hv[0], lv[0]);
+            orn_mfma::split2(a.y, a.w, hv[1], lv[1]);
+            orn_mfma::split2(b.x, b.z, hv[2], lv[2]);
+            orn_mfma::split2(b.y, b.w, hv[3], lv[3]);
+            const size_t o = (size_t)r * (H >> 1) + 4 * tid;  // u32 words
+            *reinterpret_cast<uint4 *>(fh + o) = make_uint4(hv[0], hv[1], hv[2], hv[3]);
+            *reinterpret_cast<uint4 *>(fl + o) = make_uint4(lv[0], lv[1], lv[2], lv[3]);
+        }
+        if (tid == 0) finv[r] = 1.0f / s;
     }
 }
 
@@ -518,7 +542,7 @@ extern "C" int ornk_moe_mid(const ornk_moe_args *a, hipStream_t s)
 #define ORN_MID(K)                                                                             \
     ORN_LAUNCH_EV(a, k_mid<K>, dim3(a->rows_max), dim3(256), 0, s, a->gu_part, a->ctl, a->mid,  \
                        a->H, a->ks_gu, a->rows_max, a->has_shared ? a->T : 0,                 \
-                       a->use_mfma ? a->mid_amax : nullptr)
+                       a->use_mfma ? a->mid_amax : nullptr, a->fw.mh, a->fw.ml, a->fw.minv)
     switch (a->ks_gu) {
     case 1: ORN_MID(1); break;
     case 2: ORN_MID(2); break;

@@ -226,7 +226,6 @@ int ornk_file_supported(int D, int H);
 int ornk_file_down_cols(void);
 int ornk_file_prep_x(const ornk_moe_args *a, hipStream_t s);
 int ornk_file_gateup(const ornk_moe_args *a, hipStream_t s);
-int ornk_file_prep_mid(const ornk_moe_args *a, hipStream_t s);
 int ornk_file_down(const ornk_moe_args *a, hipStream_t s);
 int ornk_rowmax(const float *x, int rows, int D, float *out, hipEvent_t start, hipStream_t s);
 int ornk_moe_combine(const ornk_moe_args *a, hipStream_t s);

@@ -125,4 +125,14 @@ __device__ __forceinline__ v4f mfma(v8h a, v8h b, v4f c)
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// Row scale of the file-orientation activations: the power of two s with
+// amax * s in [2^13, 2^14); 1 for 0 or non-finite.
+__device__ __forceinline__ float prep_scale(float amax)
+{
+    if (!(amax > 0.0f) || !(amax <= 3.0e38f)) return 1.0f;
+    int e = 13 - ilogbf(amax);
+    e = e < -126 ? -126 : (e > 126 ? 126 : e);
+    return ldexpf(1.0f, e);
+}
+
 }  // namespace orn_mfma

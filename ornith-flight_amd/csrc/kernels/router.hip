@@ -13,6 +13,7 @@
 // the dispatch that follows it: dispatch.hip.
 #include "common.h"
 #include "launch.h"
+#include "mfma_ops.h"
 
 #include <float.h>
 #include <limits.h>
@@ -380,14 +381,18 @@ __global__ void __launch_bounds__(64)
 // column 0), writes max_k |x[t][k]| for the MFMA activation scaling.  With
 // norm_w the input is first replaced by its rmsnorm (one thread runs the
 // norm's sequential sum while the producer's first weight loads are in
-// flight; block column 0 writes the normalised rows to xn_out).
+// flight; block column 0 writes the normalised rows to xn_out).  With fxh
+// (file-orientation stores) block column 0's producer wave, done before the
+// consumer's chain is, also writes the row as the file kernels' activations
+// (the outputs of k_prep_rows<true>, expert_file.hip, with its arithmetic).
 // ---------------------------------------------------------------------------
 template <int ND>
 __global__ void __launch_bounds__(128)
     k_router_pc(const float *__restrict__ x, const float *__restrict__ Wq,
                 const float *__restrict__ bias, int T, int E, float *__restrict__ logits,
                 int *ctl, float *__restrict__ amax, const float *__restrict__ norm_w,
-                float *__restrict__ xn_out)
+                float *__restrict__ xn_out, uint32_t *__restrict__ fxh, uint32_t *__restrict__ fxl,
+                float *__restrict__ fxinv, uint16_t *__restrict__ fxsh, uint16_t *__restrict__ fxsl)
 {
     constexpr int D = 32 * ND, NR = ND < 16 ? ND : 16;
     constexpr int C = ND < 8 ? ND : 8, NC = ND / C;
@@ -459,7 +464,7 @@ __global__ void __launch_bounds__(128)
                                      fmaxf(fabsf(tmp[i].z), fabsf(tmp[i].w))));
             }
         }
-        if (amax && blockIdx.x == 0) {
+        if ((amax || fxh) && blockIdx.x == 0) {
 #pragma unroll
             for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
             if (lane == 0) mx_s[wave] = mx;
@@ -490,6 +495,40 @@ __global__ void __launch_bounds__(128)
 #pragma unroll
                 for (int s = 0; s < C; ++s) step((c + 2) * C + s);
             }
+        }
+        if (fxh && blockIdx.x == 0) {
+            // hi/lo of x*s in groups of 8 (pair order [0,2,1,3,4,6,5,7]) and
+            // the 32-value sub-block sums / 32, lane l taking groups l + 64i
+            const float sc = orn_mfma::prep_scale(fmaxf(mx_s[0], mx_s[1]));
+            constexpr int NG = D / 8;
+#pragma unroll
+            for (int i = 0; i < (NG + 63) / 64; ++i) {
+                const int g = lane + 64 * i;
+                const bool on = g < NG;
+                const v4f a = xs[on ? 2 * g : 0] * sc, b = xs[on ? 2 * g + 1 : 0] * sc;
+                if (on) {
+                    uint32_t h[4], l[4];
+                    orn_mfma::split2(a.x, a.z, h[0], l[0]);
+                    orn_mfma::split2(a.y, a.w, h[1], l[1]);
+                    orn_mfma::split2(b.x, b.z, h[2], l[2]);
+                    orn_mfma::split2(b.y, b.w, h[3], l[3]);
+                    const size_t o = (size_t)t * (D >> 1) + 4 * g;
+                    *reinterpret_cast<uint4 *>(fxh + o) = make_uint4(h[0], h[1], h[2], h[3]);
+                    *reinterpret_cast<uint4 *>(fxl + o) = make_uint4(l[0], l[1], l[2], l[3]);
+                }
+                float sm = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
+                sm += __shfl_xor(sm, 1, 64);
+                sm += __shfl_xor(sm, 2, 64);
+                if (on && (g & 3) == 0) {
+                    sm *= 0.03125f;
+                    const _Float16 th = (_Float16)sm;
+                    const _Float16 tl = (_Float16)(sm - (float)th);
+                    const size_t o = (size_t)t * (D >> 5) + (g >> 2);
+                    fxsh[o] = __builtin_bit_cast(uint16_t, th);
+                    fxsl[o] = __builtin_bit_cast(uint16_t, tl);
+                }
+            }
+            if (lane == 0) fxinv[t] = 1.0f / sc;
         }
         return;
     }
@@ -623,7 +662,8 @@ extern "C" int ornk_moe_route(const ornk_moe_args *a, hipStream_t s)
         float *xo = a->apply_norm ? a->xn : nullptr;
 #define ORN_RPC(N)                                                                              \
     ORN_LAUNCH_EV(a, k_router_pc<N>, gd, dim3(128), 0, s, xr, a->router, a->bias, T, E,         \
-                       a->logits, a->ctl, amax, nw, xo)
+                       a->logits, a->ctl, amax, nw, xo, a->fw.xh, a->fw.xl, a->fw.xinv,         \
+                       a->fw.xsh, a->fw.xsl)
         switch (D) {
         case 256: ORN_RPC(8); break;
         case 512: ORN_RPC(16); break;
