@@ -236,6 +236,15 @@ int gpu_moe_store_set_router(gpu_context *ctx, ornith_moe_store *store, int laye
 int gpu_moe_store_set_norm(gpu_context *ctx, ornith_moe_store *store, int layer,
                            const float *w);
 
+/* Shared-expert gate of one layer (no reference counterpart: model.c:
+ * 1003-1007 adds the shared expert ungated and the reference loads no
+ * ffn_gate_inp_shexp).  w [D] is the layer's blk.N.ffn_gate_inp_shexp.weight
+ * (Qwen-MoE models gate their shared expert with it), or NULL to remove
+ * it.  Applied only when ORN_MOE_SHEXP_GATE is set: the shared expert's
+ * output is then scaled by sigmoid(w . xin) per token. */
+int gpu_moe_store_set_shexp_gate(gpu_context *ctx, ornith_moe_store *store, int layer,
+                                 const float *w);
+
 /* Fill one layer from the deterministic synthetic generator (orn_synth_*),
  * with an optional Zipf(s) router bias when zipf_s > 0.  The blocks and the
  * router are generated on the device (the same bytes as the host
@@ -319,6 +328,9 @@ enum { ORN_ROUTE_RENORM = 0, ORN_ROUTE_LITERAL = 1 };
  * calls, their addresses may not.  Uploading to the store drops the
  * recordings.  Ignored while kernel profiling is on. */
 #define ORN_MOE_GRAPH 16u
+/* Scale the shared expert by its gate (gpu_moe_store_set_shexp_gate; a
+ * layer without one is refused with ORN_EINVAL).  Not in the reference. */
+#define ORN_MOE_SHEXP_GATE 32u
 
 typedef struct {
     int route_mode; /* ORN_ROUTE_RENORM (default, model_get_routing) or ORN_ROUTE_LITERAL */
@@ -335,6 +347,7 @@ typedef struct {
 
 /* One MoE block for n_tokens rows of x ([T][D] fp32):
  *   out = (resid + shared(xin)) + sum_a w_a * expert_a(xin),
+ *   (shared(xin) scaled by sigmoid(gate . xin) with ORN_MOE_SHEXP_GATE),
  *   xin = (flags & ORN_MOE_NORM) ? rmsnorm(x) : x;  resid may be NULL (zeros).
  * idx_out ([T][k] uint32) and w_out ([T][k] fp32) may be NULL.  out may not
  * alias x or resid. */

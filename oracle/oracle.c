@@ -356,11 +356,11 @@ static int fetch_shared(const orc_moe_cfg *c, const void *p, int type, int K, in
  * selected expert is dequantized once and applied to all tokens that chose
  * it); every (token, expert) result is the same fp32 sequence the reference
  * computes, and the per-token combine runs in selection order afterwards. */
-int orc_moe_layer(const orc_moe_cfg *c, int T, const float *x, const float *resid,
-                  const float *norm_w, const float *router_W, const float *bias,
-                  const void *gate, const void *up, const void *down,
-                  const void *sh_gate, const void *sh_up, const void *sh_down,
-                  float *out, uint32_t *idx_out, float *w_out)
+int orc_moe_layer_ex(const orc_moe_cfg *c, int T, const float *x, const float *resid,
+                     const float *norm_w, const float *router_W, const float *bias,
+                     const void *gate, const void *up, const void *down,
+                     const void *sh_gate, const void *sh_up, const void *sh_down,
+                     const float *shexp_gate, float *out, uint32_t *idx_out, float *w_out)
 {
     if (!c || !x || !out || !router_W || !gate || !up || !down || T < 0) return -1;
     const int D = c->D, H = c->H, E = c->E, K = c->k;
@@ -399,7 +399,17 @@ int orc_moe_layer(const orc_moe_cfg *c, int T, const float *x, const float *resi
         for (int t = 0; t < T; ++t) {
             orc_expert_ffn(ffn_x + (size_t)t * D, Wg, Wu, Wd, D, H, 0, tmp);
             float *a = acc + (size_t)t * D;
-            for (int i = 0; i < D; ++i) a[i] = a[i] + tmp[i];
+            if (shexp_gate) {
+                /* sigmoid(shexp_gate . ffn_x) times the shared output
+                 * (no reference counterpart: model.c:1003-1007 adds the
+                 * shared expert ungated) */
+                float dot = 0.0f;
+                for (int i = 0; i < D; ++i) dot += ffn_x[(size_t)t * D + i] * shexp_gate[i];
+                const float g = 1.0f / (1.0f + expf(-dot));
+                for (int i = 0; i < D; ++i) a[i] = a[i] + g * tmp[i];
+            } else {
+                for (int i = 0; i < D; ++i) a[i] = a[i] + tmp[i];
+            }
         }
     }
 
@@ -512,4 +522,14 @@ void orc_deltanet_step(float *state, const float *Q, const float *K, const float
         for (int j = 0; j < dim; ++j) sum += Q[j] * state[(size_t)j * dim + i];
         out[i] = sum;
     }
+}
+
+int orc_moe_layer(const orc_moe_cfg *c, int T, const float *x, const float *resid,
+                  const float *norm_w, const float *router_W, const float *bias,
+                  const void *gate, const void *up, const void *down,
+                  const void *sh_gate, const void *sh_up, const void *sh_down,
+                  float *out, uint32_t *idx_out, float *w_out)
+{
+    return orc_moe_layer_ex(c, T, x, resid, norm_w, router_W, bias, gate, up, down, sh_gate,
+                            sh_up, sh_down, NULL, out, idx_out, w_out);
 }

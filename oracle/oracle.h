@@ -123,6 +123,17 @@ int orc_moe_layer(const orc_moe_cfg *cfg, int T, const float *x, const float *re
                   const void *sh_gate, const void *sh_up, const void *sh_down,
                   float *out, uint32_t *idx_out, float *w_out);
 
+/* orc_moe_layer with an optional shared-expert gate (no reference
+ * counterpart: the reference loads no ffn_gate_inp_shexp and adds the shared
+ * expert ungated, model.c:1003-1007).  shexp_gate [D] (NULL: none) scales the
+ * shared expert's output by sigmoid(sum_i ffn_x[i] * shexp_gate[i]), the dot
+ * a sequential fp32 sum, as Qwen-MoE models gate their shared expert. */
+int orc_moe_layer_ex(const orc_moe_cfg *cfg, int T, const float *x, const float *resid,
+                     const float *norm_w, const float *router_W, const float *bias,
+                     const void *gate, const void *up, const void *down,
+                     const void *sh_gate, const void *sh_up, const void *sh_down,
+                     const float *shexp_gate, float *out, uint32_t *idx_out, float *w_out);
+
 /* ops.metal:113-139 (= model.c:599-622 for one head): the pairs (i, i+1),
  * i < rot = min(head_dim, 64), of n_heads heads of x [n_heads][head_dim]
  * rotated by pos * inv_freq, inv_freq = 1/theta^(i/rot) rounded once from

@@ -65,6 +65,8 @@ def lib():
                                     C.c_void_p, C.c_void_p, C.c_void_p,
                                     C.c_void_p, C.c_void_p, C.c_void_p,
                                     C.c_void_p, C.c_void_p, C.c_void_p]
+        L.orc_moe_layer_ex.restype = C.c_int
+        L.orc_moe_layer_ex.argtypes = [C.POINTER(MoECfg), C.c_int] + [C.c_void_p] * 15
         L.orc_rope.restype = None
         L.orc_rope.argtypes = [f32p, C.c_int, C.c_int, C.c_int, C.c_float]
         L.orc_attention.restype = None
@@ -167,8 +169,9 @@ def topk(logits, k, mode=MODE_RENORM):
 def moe_layer(*, D, H, E, k, x, router_W, gate, up, down, sh_gate=None, sh_up=None,
               sh_down=None, resid=None, norm_w=None, bias=None, mode=MODE_RENORM,
               layout=LAYOUT_CONTIGUOUS, types=(TYPE_Q4_K, TYPE_Q4_K, TYPE_Q6_K),
-              sh_types=(TYPE_Q4_K, TYPE_Q4_K, TYPE_Q6_K)):
-    """Runs orc_moe_layer; returns (out[T,D], idx[T,k], w[T,k])."""
+              sh_types=(TYPE_Q4_K, TYPE_Q4_K, TYPE_Q6_K), shexp_gate=None):
+    """Runs orc_moe_layer (orc_moe_layer_ex with a shared-expert gate);
+    returns (out[T,D], idx[T,k], w[T,k])."""
     x = np.ascontiguousarray(x, np.float32).reshape(-1, D)
     T = x.shape[0]
     cfg = MoECfg(D, H, E, k, mode, layout, *types, *sh_types)
@@ -177,8 +180,13 @@ def moe_layer(*, D, H, E, k, x, router_W, gate, up, down, sh_gate=None, sh_up=No
     w = np.zeros((T, k), np.float32)
     keep = [np.ascontiguousarray(a) if a is not None else None for a in
             (resid, norm_w, router_W, bias, gate, up, down, sh_gate, sh_up, sh_down)]
-    rc = lib().orc_moe_layer(C.byref(cfg), T, _ptr(x), *[_ptr(a) for a in keep],
-                             _ptr(out), _ptr(idx), _ptr(w))
+    if shexp_gate is None:
+        rc = lib().orc_moe_layer(C.byref(cfg), T, _ptr(x), *[_ptr(a) for a in keep],
+                                 _ptr(out), _ptr(idx), _ptr(w))
+    else:
+        g = np.ascontiguousarray(shexp_gate, np.float32)
+        rc = lib().orc_moe_layer_ex(C.byref(cfg), T, _ptr(x), *[_ptr(a) for a in keep], _ptr(g),
+                                    _ptr(out), _ptr(idx), _ptr(w))
     if rc != 0:
         raise RuntimeError(f"orc_moe_layer failed rc={rc}")
     return out, idx, w

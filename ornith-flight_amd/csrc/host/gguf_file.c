@@ -575,6 +575,25 @@ int gpu_moe_store_load_gguf(gpu_context *ctx, ornith_moe_store *st, const orn_gg
                 break;
             }
             rc = gpu_moe_store_set_norm(ctx, st, sl, fb);
+            if (rc) break;
+        }
+        /* the shared-expert gate (Qwen-MoE files; the reference ignores it),
+         * when the file has it: applied under ORN_MOE_SHEXP_GATE */
+        snprintf(name, sizeof name, "blk.%d.ffn_gate_inp_shexp.weight", fl);
+        if (sh->has_shared && (t = orn_gguf_find_tensor(g, name))) {
+            if ((t->type != ORN_TYPE_F32 && t->type != ORN_TYPE_F16) || t->n_elems != D ||
+                orn_gguf_read_tensor_data(g, t, buf, stage) != t->size_bytes) {
+                rc = orn_set_err(ctx, ORN_EUNSUPPORTED, "load_gguf: %s is not %llu f32/f16", name,
+                                 (unsigned long long)D);
+                break;
+            }
+            if (t->type == ORN_TYPE_F32) {
+                memcpy(fb, buf, (size_t)D * sizeof(float));
+            } else {
+                for (uint64_t j = 0; j < D; ++j)
+                    fb[j] = orn_quirk_half((uint16_t)(buf[2 * j] | (buf[2 * j + 1] << 8)));
+            }
+            if ((rc = gpu_moe_store_set_shexp_gate(ctx, st, sl, fb))) break;
         }
     }
     free(buf);

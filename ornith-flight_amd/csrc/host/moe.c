@@ -43,6 +43,8 @@ struct ornith_moe_store {
     float *bias;              /* [L][E] */
     int *has_bias;            /* host [L] */
     float *norm;              /* [L][D] */
+    float *shexp_gate;        /* [L][D] shared-expert gate vectors */
+    unsigned char *has_shexp_gate; /* host [L] */
     /* Prefill (MFMA) layouts, present when sh.prefill_layout is set (built
      * by prefill_pack.c; per layer and expert slot):
      *   pq[m]  gate/up nibbles [D/32][H/256][4][64][4] u32   (D*H/2 bytes)
@@ -273,6 +275,8 @@ static void store_free(ornith_moe_store *st)
     hipFree(st->router_q);
     hipFree(st->bias);
     hipFree(st->norm);
+    hipFree(st->shexp_gate);
+    free(st->has_shexp_gate);
     for (int m = 0; m < 2; ++m) {
         hipFree(st->pq[m]);
         hipFree(st->psc[m]);
@@ -307,12 +311,19 @@ ornith_moe_store *gpu_moe_store_create(gpu_context *ctx, const ornith_moe_shape 
                  E = (size_t)shape->n_experts;
     st->blocks_per_matrix = D * H / 256;
     const size_t nb = L * E1 * st->blocks_per_matrix;
-    size_t sizes[7] = {nb * 144, nb * 144, nb * 208, nb * 2, L * E * D * 4, L * E * 4, L * D * 4};
-    void **ptrs[7] = {(void **)&st->gate, (void **)&st->up, (void **)&st->down_body,
+    size_t sizes[8] = {nb * 144, nb * 144, nb * 208, nb * 2, L * E * D * 4, L * E * 4, L * D * 4,
+                       L * D * 4};
+    void **ptrs[8] = {(void **)&st->gate, (void **)&st->up, (void **)&st->down_body,
                       (void **)&st->down_d, (void **)&st->router_q, (void **)&st->bias,
-                      (void **)&st->norm};
+                      (void **)&st->norm, (void **)&st->shexp_gate};
     const int cached = shape->cache_slots > 0;
-    for (int i = cached ? 4 : 0; i < 7; ++i) {
+    st->has_shexp_gate = (unsigned char *)calloc(L, 1);
+    if (!st->has_shexp_gate) {
+        orn_set_err(ctx, ORN_ENOMEM, "store tables");
+        store_free(st);
+        return NULL;
+    }
+    for (int i = cached ? 4 : 0; i < 8; ++i) {
         if (hipMalloc(ptrs[i], sizes[i]) != hipSuccess ||
             hipMemsetAsync(*ptrs[i], 0, sizes[i], ctx->stream) != hipSuccess) {
             orn_set_err(ctx, ORN_ENOMEM, "store allocation of %zu bytes failed", sizes[i]);
@@ -636,6 +647,26 @@ int gpu_moe_store_set_norm(gpu_context *ctx, ornith_moe_store *st, int layer, co
                                                hipMemcpyHostToDevice, ctx->stream),
                            "upload norm");
     hipStreamSynchronize(ctx->stream);
+    return rc;
+}
+
+int gpu_moe_store_set_shexp_gate(gpu_context *ctx, ornith_moe_store *st, int layer,
+                                 const float *w)
+{
+    if (!ctx || !st) return ORN_EINVAL;
+    if (layer < 0 || layer >= st->sh.n_layers) return orn_set_err(ctx, ORN_EINVAL, "bad layer");
+    if (w && !st->sh.has_shared)
+        return orn_set_err(ctx, ORN_EINVAL, "shared-expert gate on a store without a shared expert");
+    graphs_clear(st);
+    st->has_shexp_gate[layer] = 0;
+    if (!w) return ORN_OK;
+    const size_t D = (size_t)st->sh.d_model;
+    int rc = orn_hip_check(ctx, hipMemcpyAsync(st->shexp_gate + (size_t)layer * D, w,
+                                               D * sizeof(float), hipMemcpyHostToDevice,
+                                               ctx->stream),
+                           "upload shared-expert gate");
+    hipStreamSynchronize(ctx->stream);
+    if (!rc) st->has_shexp_gate[layer] = 1;
     return rc;
 }
 
@@ -1090,6 +1121,12 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     a.router = st->router_q + (size_t)layer * E * D;
     a.bias = st->has_bias[layer] ? st->bias + (size_t)layer * E : NULL;
     a.norm_w = st->norm + (size_t)layer * D;
+    if (flags & ORN_MOE_SHEXP_GATE) {
+        if (!st->has_shexp_gate[layer])
+            return orn_set_err(ctx, ORN_EINVAL,
+                               "ORN_MOE_SHEXP_GATE: layer %d has no shared-expert gate", layer);
+        a.shexp_gate = st->shexp_gate + (size_t)layer * D;
+    }
     a.x = x;
     a.resid = resid;
     a.out = out;

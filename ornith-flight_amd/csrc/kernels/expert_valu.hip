@@ -450,15 +450,32 @@ __global__ void __launch_bounds__(256)
 // ---------------------------------------------------------------------------
 // KS = ks (compile time, 1..16) and K = k (8, or 0: any k <= 16): every
 // load of a thread is issued before the first add.
+// sg (the shared-expert gate, NULL: none): the shared term is scaled by
+// sigmoid(sg . xin[t]), the dot formed by every work group of the token in
+// the same fixed order (8-strided per thread, then a butterfly per wave and
+// the four waves in order).
 template <int KS, int K>
 __global__ void __launch_bounds__(256)
     k_combine(const float *__restrict__ dn_part, const int *__restrict__ pair_row,
               const float *__restrict__ w, const float *__restrict__ resid,
-              float *__restrict__ out, int T, int D, int k, int rows_max, int has_shared)
+              float *__restrict__ out, int T, int D, int k, int rows_max, int has_shared,
+              const float *__restrict__ sg, const float *__restrict__ xin)
 {
     constexpr int KK = K > 0 ? K : 16;
     const int t = blockIdx.x;
     const int c = blockIdx.y * blockDim.x + threadIdx.x;
+    float gsh = 1.0f;
+    if (sg) {  // uniform over the work group
+        __shared__ float red[4];
+        float p = 0.0f;
+        for (int i = threadIdx.x; i < D; i += blockDim.x) p += xin[(size_t)t * D + i] * sg[i];
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) p += __shfl_xor(p, off, 64);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = p;
+        __syncthreads();
+        const float dot = ((red[0] + red[1]) + red[2]) + red[3];
+        gsh = 1.0f / (1.0f + expf(-dot));
+    }
     if (t >= T || c >= D) return;
     const int kk = K > 0 ? K : k;
     const size_t kstride = (size_t)rows_max * D;
@@ -494,7 +511,7 @@ __global__ void __launch_bounds__(256)
         }
     }
     float acc = rv;
-    if (has_shared) acc = acc + ysh;
+    if (has_shared) acc = acc + gsh * ysh;  // gsh = 1 without a gate: acc + ysh exactly
     float routed = 0.0f;
 #pragma unroll
     for (int a = 0; a < KK; ++a)
@@ -589,7 +606,8 @@ extern "C" int ornk_moe_combine(const ornk_moe_args *a, hipStream_t s)
     const dim3 grid(a->T, (a->D + 255) / 256);
 #define ORN_CMB(KS, K)                                                                          \
     ORN_LAUNCH_EV(a, (k_combine<KS, K>), grid, dim3(256), 0, s, a->dn_part, a->pair_row, a->w,  \
-                       a->resid, a->out, a->T, a->D, a->k, a->rows_max, a->has_shared)
+                       a->resid, a->out, a->T, a->D, a->k, a->rows_max, a->has_shared,        \
+                       a->has_shared ? a->shexp_gate : nullptr, a->xn)
 #define ORN_CMB_K(KS)                  \
     if (a->k == 8) ORN_CMB(KS, 8);     \
     else ORN_CMB(KS, 0)

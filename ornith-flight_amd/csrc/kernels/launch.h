@@ -164,6 +164,7 @@ typedef struct {
     const float *router, *bias, *norm_w;
     const float *x, *resid;
     float *out;
+    const float *shexp_gate; /* [D] or NULL: the shared expert scaled by sigmoid(gate . xin) */
     /* workspace */
     float *xn;        /* [T][D]  expert input (x or rmsnorm(x)) */
     float *logits;    /* [T][E] */

@@ -20,7 +20,7 @@ TYPE_F32, TYPE_F16, TYPE_Q4_K, TYPE_Q6_K = 0, 1, 12, 14
 MAT_GATE, MAT_UP, MAT_DOWN = 0, 1, 2
 ROUTE_RENORM, ROUTE_LITERAL = 0, 1
 MOE_ASYNC, MOE_NORM = 1, 2
-MOE_PATH_VALU, MOE_PATH_MFMA, MOE_GRAPH = 4, 8, 16
+MOE_PATH_VALU, MOE_PATH_MFMA, MOE_GRAPH, MOE_SHEXP_GATE = 4, 8, 16, 32
 SYN_GATE, SYN_UP, SYN_DOWN, SYN_ROUTER, SYN_ACT, SYN_ZIPF = 1, 2, 3, 4, 5, 6
 GPU_BUF_DEFAULT, GPU_BUF_SHARED, GPU_BUF_CONSTANT = 0, 1, 2
 Q4K_BYTES, Q6K_BYTES = 144, 210
@@ -37,7 +37,7 @@ EXPORTED = [
     "gpu_dequantize_tensor_buf", "gpu_dequantize_expert_slice_buf",
     "gpu_moe_store_create", "gpu_moe_store_destroy", "gpu_moe_store_bytes",
     "gpu_moe_store_set_experts", "gpu_moe_store_get_experts", "gpu_moe_store_set_router",
-    "gpu_moe_store_set_norm",
+    "gpu_moe_store_set_norm", "gpu_moe_store_set_shexp_gate",
     "gpu_moe_store_fill_synthetic", "gpu_moe_forward", "gpu_moe_forward_noalloc",
     "gpu_moe_forward_stack",
     "gpu_moe_last_stats", "gpu_moe_last_logits", "gpu_probe_read_bandwidth",
@@ -151,6 +151,7 @@ def lib():
         "gpu_moe_store_get_experts": (i, [vp, vp, i, i, i, i, vp]),
         "gpu_moe_store_set_router": (i, [vp, vp, i, vp, vp]),
         "gpu_moe_store_set_norm": (i, [vp, vp, i, vp]),
+        "gpu_moe_store_set_shexp_gate": (i, [vp, vp, i, vp]),
         "gpu_moe_store_fill_synthetic": (i, [vp, vp, i, u64, f]),
         "gpu_moe_forward": (i, [vp, vp, i, vp, i, vp, vp, vp, vp, C.POINTER(MoEOpts)]),
         "gpu_moe_forward_noalloc": (i, [vp, vp, i, vp, i, vp, vp, vp, vp, C.POINTER(MoEOpts)]),
@@ -359,6 +360,13 @@ class Store:
     def set_norm(self, layer, w):
         w = np.ascontiguousarray(w, np.float32)
         self.ctx.check(lib().gpu_moe_store_set_norm(self.ctx.ptr, self.ptr, layer, _p(w)), "set_norm")
+
+    def set_shexp_gate(self, layer, w):
+        """The layer's shared-expert gate [D] (None removes it); applied with
+        MOE_SHEXP_GATE."""
+        wp = None if w is None else _p(np.ascontiguousarray(w, np.float32))
+        self.ctx.check(lib().gpu_moe_store_set_shexp_gate(self.ctx.ptr, self.ptr, layer, wp),
+                       "set_shexp_gate")
 
     def fill_synthetic(self, layer, seed, zipf_s=0.0):
         self.ctx.check(lib().gpu_moe_store_fill_synthetic(self.ctx.ptr, self.ptr, layer, seed, zipf_s),

@@ -28,6 +28,7 @@ int gpu_moe_store_set_experts(gpu_context *c, ornith_moe_store *s, int l, int m,
 int gpu_moe_store_set_router(gpu_context *c, ornith_moe_store *s, int l, const float *w,
                              const float *b) { return 0; }
 int gpu_moe_store_set_norm(gpu_context *c, ornith_moe_store *s, int l, const float *w) { return 0; }
+int gpu_moe_store_set_shexp_gate(gpu_context *c, ornith_moe_store *s, int l, const float *w) { return 0; }
 
 static uint64_t rng_state = 0x9E3779B97F4A7C15ull;
 static uint64_t next(void)

@@ -313,6 +313,33 @@ def test_file_layout_parity_ornith(om, ctx, ornith_file, T):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("T", [16, 100])
+def test_file_layout_shexp_gate(om, ctx, ornith_file, T):
+    """The optional shared-expert gate (ORN_MOE_SHEXP_GATE) on the file
+    path, with NORM and resid = x, against the oracle's gated layer."""
+    D, H, E, k = 2048, 512, 256, 8
+    syn, st = ornith_file
+    rng = np.random.default_rng(70 + T)
+    nw = (1.0 + 0.25 * rng.standard_normal(D)).astype(np.float32)
+    gv = (0.02 * rng.standard_normal(D)).astype(np.float32)
+    st.set_norm(0, nw)
+    st.set_shexp_gate(0, gv)
+    try:
+        x = rng.standard_normal((T, D)).astype(np.float32)
+        out, idx, w = forward_full(ctx, st, x, k, flags=om.MOE_NORM | om.MOE_SHEXP_GATE, resid=x)
+        sub = np.arange(T) if T <= 16 else np.unique(np.linspace(0, T - 1, 24).astype(int))
+        ref, ridx, _ = oracle_file(syn, D, H, E, k, x[sub], norm_w=nw, resid=x[sub],
+                                   shexp_gate=gv)
+        assert np.array_equal(idx[sub], ridx)
+        e = row_err(out[sub], ref)
+        say(f"  gated T={T}: max row err {e.max():.2e}")
+        assert e.max() <= TOL
+    finally:
+        st.set_shexp_gate(0, None)
+        st.set_norm(0, np.ones(D, np.float32))
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("T,flags,mode", [(16, "norm", 0), (100, "norm", 0), (16, "", 1),
                                           (100, "norm", 1)])
 def test_file_layout_norm_resid_literal(om, ctx, ornith_file, T, flags, mode):

@@ -47,10 +47,12 @@ def ctx(om):
     c.close()
 
 
-def model_file(om, path, D, H, E, layers, router_f16=False, norm=True, seed=3):
+def model_file(om, path, D, H, E, layers, router_f16=False, norm=True, seed=3, shexp_gate=False):
     """Write a GGUF whose layers `layers` carry synthetic MoE tensors (the
     bytes of SyntheticLayer(seed, l)); returns {layer: (syn, router_file,
-    norm_w)} where router_file is the [E][D] fp32 router as stored."""
+    norm_w, gate)} where router_file is the [E][D] fp32 router as stored and
+    gate the shared-expert gate as the loader decodes it (with shexp_gate:
+    ffn_gate_inp_shexp.weight, f16 when router_f16, else f32; else None)."""
     rng = np.random.default_rng(seed)
     md = [("general.architecture", "str", "qwen35moe"), ("qwen35moe.block_count", "u32", 40),
           ("qwen35moe.expert_count", "u32", E), ("qwen35moe.embedding_length", "u32", D),
@@ -70,6 +72,15 @@ def model_file(om, path, D, H, E, layers, router_f16=False, norm=True, seed=3):
             rfile = np.ascontiguousarray(syn.router.T)  # [E][D]: W[e*D + d]
             rbytes, rtype = rfile, om.TYPE_F32
         nw = (1.0 + 0.25 * rng.standard_normal(D)).astype(np.float32) if norm else None
+        gate = None
+        if shexp_gate:
+            g16 = (0.05 * rng.standard_normal(D)).astype(np.float16)
+            if router_f16:
+                gate = np.array([O.fp16_to_fp32(int(h)) for h in g16.view(np.uint16)], np.float32)
+                tensors.append((f"blk.{l}.ffn_gate_inp_shexp.weight", om.TYPE_F16, [D], g16))
+            else:
+                gate = g16.astype(np.float32)
+                tensors.append((f"blk.{l}.ffn_gate_inp_shexp.weight", om.TYPE_F32, [D], gate))
         tensors += [
             (f"blk.{l}.attn_norm.weight", om.TYPE_F32, [D], np.ones(D, np.float32)),
             (f"blk.{l}.ffn_gate_exps.weight", om.TYPE_Q4_K, [D, H, E], syn.gate[:E * per_q4]),
@@ -82,7 +93,7 @@ def model_file(om, path, D, H, E, layers, router_f16=False, norm=True, seed=3):
         ]
         if norm:
             tensors.append((f"blk.{l}.post_attention_norm.weight", om.TYPE_F32, [D], nw))
-        info[l] = (syn, rfile, nw)
+        info[l] = (syn, rfile, nw, gate)
     W.write_gguf(path, md, tensors)
     return info
 
@@ -115,7 +126,7 @@ def path():
 def test_load_gguf_equals_set_experts(om, ctx, path, shape, router_f16):
     D, H, E = shape
     k = 8
-    info = model_file(om, path, D, H, E, layers=[2, 3], router_f16=router_f16)
+    info = model_file(om, path, D, H, E, layers=[2, 3], router_f16=router_f16, shexp_gate=True)
     say(f"model file {os.path.getsize(path) / 1e6:.1f} MB, shape {shape}, f16 router {router_f16}")
     loaded = om.Store(ctx, 2, D, H, E, k, True, prefill_layout=False, file_layout=True)
     direct = om.Store(ctx, 2, D, H, E, k, True, prefill_layout=False, file_layout=True)
@@ -126,16 +137,18 @@ def test_load_gguf_equals_set_experts(om, ctx, path, shape, router_f16):
             assert list(t.dims) == [H, D, E, 1] and t.type == om.TYPE_Q6_K
             loaded.load_gguf(g, file_first_layer=2, store_first_layer=0, n_layers=2)
         for sl, fl in ((0, 2), (1, 3)):
-            syn, rfile, nw = info[fl]
+            syn, rfile, nw, gv = info[fl]
             for name, m in (("gate", om.MAT_GATE), ("up", om.MAT_UP), ("down", om.MAT_DOWN)):
                 assert np.array_equal(loaded.get_experts(sl, m, 0, E + 1), getattr(syn, name)), name
                 direct.set_experts(sl, m, 0, getattr(syn, name), E + 1)
             direct.set_router(sl, rfile)
             direct.set_norm(sl, nw)
+            direct.set_shexp_gate(sl, gv)
         say("  expert bytes in the store == the file's")
         for sl, fl in ((0, 2), (1, 3)):
-            syn, rfile, nw = info[fl]
-            for T, flags in ((1, 0), (16, om.MOE_NORM), (40, 0)):
+            syn, rfile, nw, gv = info[fl]
+            for T, flags in ((1, 0), (16, om.MOE_NORM), (40, 0),
+                             (16, om.MOE_NORM | om.MOE_SHEXP_GATE)):
                 x = np.random.default_rng(100 * sl + T).standard_normal((T, D)).astype(np.float32)
                 a = forward(ctx, loaded, sl, x, k, flags)
                 b = forward(ctx, direct, sl, x, k, flags)
@@ -147,7 +160,8 @@ def test_load_gguf_equals_set_experts(om, ctx, path, shape, router_f16):
                                            gate=syn.routed("gate"), up=syn.routed("up"),
                                            down=syn.routed("down"), sh_gate=syn.shared("gate"),
                                            sh_up=syn.shared("up"), sh_down=syn.shared("down"),
-                                           layout=O.LAYOUT_FILE)
+                                           layout=O.LAYOUT_FILE,
+                                           shexp_gate=gv if flags & om.MOE_SHEXP_GATE else None)
                 assert np.array_equal(a[1], ridx), (sl, T)
                 err = (np.abs(a[0].astype(np.float64) - ref).max(axis=1) /
                        np.abs(ref).max(axis=1)).max()

@@ -62,12 +62,12 @@ class Layer:
             self.store.load_layer(l, s)
             self.syn.append(s)
 
-    def oracle(self, x, l=0, mode=O.MODE_RENORM, resid=None, norm_w=None):
+    def oracle(self, x, l=0, mode=O.MODE_RENORM, resid=None, norm_w=None, shexp_gate=None):
         s = self.syn[l]
         return O.moe_layer(D=self.D, H=self.H, E=self.E, k=self.k, x=x, resid=resid, norm_w=norm_w,
                            router_W=s.router, bias=s.bias, gate=s.routed("gate"), up=s.routed("up"),
                            down=s.routed("down"), sh_gate=s.shared("gate"), sh_up=s.shared("up"),
-                           sh_down=s.shared("down"), mode=mode)
+                           sh_down=s.shared("down"), mode=mode, shexp_gate=shexp_gate)
 
     def oracle_routing(self, x, l=0, mode=O.MODE_RENORM):
         s = self.syn[l]
@@ -171,6 +171,47 @@ def test_skewed_batch_on_decode_items(om, ctx):
             g, gi, _ = run(ctx, L, x, flags=om.MOE_PATH_MFMA | om.MOE_GRAPH)
             assert np.array_equal(gi, idx)
             assert np.array_equal(g.view(np.uint32), out.view(np.uint32)), i
+    finally:
+        L.store.close()
+
+
+@pytest.mark.parametrize("T", [1, 16, 150])
+@pytest.mark.parametrize("path", ["valu", "mfma"])
+def test_shexp_gate(om, ctx, T, path):
+    """The optional shared-expert gate (ORN_MOE_SHEXP_GATE; not in the
+    reference): against the oracle's gated layer with NORM and a residual;
+    a stored gate changes nothing without the flag; the flag on a layer
+    without a gate is refused; graph replays are bit-identical."""
+    L = Layer(om, ctx, 256, 256, 16, 8, seed=13, n_layers=2)
+    try:
+        rng = np.random.default_rng(T)
+        gv = (rng.standard_normal(256) * 0.05).astype(np.float32)
+        nw = rng.uniform(0.5, 1.5, 256).astype(np.float32)
+        L.store.set_norm(0, nw)
+        x = act(om, 500 + T, T, 256)
+        resid = act(om, 600 + T, T, 256, 1)
+        pf = om.MOE_PATH_VALU if path == "valu" else om.MOE_PATH_MFMA
+        plain, _, _ = run(ctx, L, x, resid=resid, flags=pf | om.MOE_NORM)
+        L.store.set_shexp_gate(0, gv)
+        same, _, _ = run(ctx, L, x, resid=resid, flags=pf | om.MOE_NORM)
+        assert np.array_equal(same.view(np.uint32), plain.view(np.uint32))
+        flags = pf | om.MOE_NORM | om.MOE_SHEXP_GATE
+        out, idx, w = run(ctx, L, x, resid=resid, flags=flags)
+        ref, ridx, _ = L.oracle(x, resid=resid, norm_w=nw, shexp_gate=gv)
+        assert np.array_equal(idx, ridx)
+        err = row_err(out, ref)
+        say(f"  gated T={T} {path}: max row err {err.max():.2e}, "
+            f"max |gated - ungated| {np.abs(out - plain).max():.3f}")
+        assert err.max() <= TOL
+        assert np.abs(out - plain).max() > 1e-3 * np.abs(plain).max()  # the gate acts
+        for i in range(3):
+            g, _, _ = run(ctx, L, x, resid=resid, flags=flags | om.MOE_GRAPH)
+            assert np.array_equal(g.view(np.uint32), out.view(np.uint32)), i
+        with pytest.raises(RuntimeError, match="no shared-expert gate"):
+            run(ctx, L, x, flags=flags, l=1)
+        L.store.set_shexp_gate(0, None)
+        with pytest.raises(RuntimeError, match="no shared-expert gate"):
+            run(ctx, L, x, flags=flags)
     finally:
         L.store.close()
 

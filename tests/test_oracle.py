@@ -273,9 +273,10 @@ def test_moe_layer_golden_ornith_shape(golden_dir):
     assert np.array_equal(bits(out), bits(g["expected"]))
 
 
-def np_moe_fp64(D, H, E, k, x, W, gate, up, down, sh, bias=None):
+def np_moe_fp64(D, H, E, k, x, W, gate, up, down, sh, bias=None, shexp_gate=None):
     """fp64 brute force of the contiguous-layout, renormalised layer with an
-    independent (vectorised) dequant; returns (out, idx)."""
+    independent (vectorised) dequant (and, with shexp_gate, the shared
+    expert scaled by sigmoid(shexp_gate . x)); returns (out, idx)."""
     nb = D * H // 256
 
     def mats(q4, q6):
@@ -297,6 +298,8 @@ def np_moe_fp64(D, H, E, k, x, W, gate, up, down, sh, bias=None):
         Wg, Wd = mats(sh[0], sh[2])
         Wu = np_q4k(sh[1]).astype(np.float64).reshape(D, H)
         y = ffn(xv, Wg, Wu, Wd, False)
+        if shexp_gate is not None:
+            y = y / (1.0 + np.exp(-(xv @ shexp_gate.astype(np.float64))))
         lg = xv @ W.astype(np.float64) + (0 if bias is None else bias)
         order = np.argsort(-lg, kind="stable")[:k]
         ww = np.exp(lg[order] - lg[order[0]])
@@ -329,5 +332,47 @@ def test_contiguous_layout_vs_fp64():
                             bias=syn.bias.astype(np.float64))
     assert np.array_equal(idx.astype(np.int64), ridx)
     assert np.allclose(w.sum(axis=1), 1.0, atol=1e-6)
+    err = np.abs(out - ref).max(axis=1) / np.abs(ref).max(axis=1)
+    assert err.max() < 1e-5, err
+
+
+def test_shexp_gate_special_cases_and_fp64():
+    """The optional shared-expert gate of orc_moe_layer_ex (no reference
+    counterpart), pinned by the values sigmoid takes exactly: a dot of +huge
+    (gate 1) reproduces the ungated layer bit for bit, -huge (gate 0) the
+    layer without a shared expert bit for bit, a zero vector (gate 1/2 exactly)
+    their mean; and a random gate against the fp64 brute force."""
+    import ornith_moe as om
+    D, H, E, k, T = 256, 256, 16, 8, 5
+    syn = om.SyntheticLayer(7, 0, D, H, E, True)
+    x = om.synth_normal(7, om.synth_stream(0, om.SYN_ACT, 0), T * D, 1.0).reshape(T, D)
+    resid = om.synth_normal(8, om.synth_stream(0, om.SYN_ACT, 1), T * D, 1.0).reshape(T, D)
+    common = dict(D=D, H=H, E=E, k=k, x=x, resid=resid, router_W=syn.router,
+                  gate=syn.routed("gate"), up=syn.routed("up"), down=syn.routed("down"))
+    shared = dict(sh_gate=syn.shared("gate"), sh_up=syn.shared("up"), sh_down=syn.shared("down"))
+    ungated, _, _ = O.moe_layer(**common, **shared)
+    no_shared, _, _ = O.moe_layer(**common)
+    # per row, a gate vector along the row's sign pattern with a huge scale:
+    # a dot of about +1e32 (expf(-dot) = 0: gate exactly 1) or, negated,
+    # -1e32 (expf(-dot) = inf: gate exactly 0)
+    for t in range(T):
+        g_pos = (np.float32(1e30) * np.sign(x[t])).astype(np.float32)
+        one, _, _ = O.moe_layer(**{**common, "x": x[t:t + 1], "resid": resid[t:t + 1]}, **shared,
+                                shexp_gate=g_pos)
+        zero, _, _ = O.moe_layer(**{**common, "x": x[t:t + 1], "resid": resid[t:t + 1]}, **shared,
+                                 shexp_gate=-g_pos)
+        assert np.array_equal(one.view(np.uint32), ungated[t:t + 1].view(np.uint32))
+        assert np.array_equal(zero.view(np.uint32), no_shared[t:t + 1].view(np.uint32))
+    half, _, _ = O.moe_layer(**common, **shared, shexp_gate=np.zeros(D, np.float32))
+    mid = 0.5 * (ungated.astype(np.float64) + no_shared)
+    assert np.abs(half - mid).max() <= 1e-5 * np.abs(mid).max()
+    assert np.abs(half - ungated).max() > 1e-3 * np.abs(mid).max()  # the gate acts
+    rng = np.random.default_rng(3)
+    gv = (rng.standard_normal(D) * 0.05).astype(np.float32)
+    out, idx, _ = O.moe_layer(**{**common, "resid": None}, **shared, shexp_gate=gv)
+    ref, ridx = np_moe_fp64(D, H, E, k, x, syn.router, syn.routed("gate"), syn.routed("up"),
+                            syn.routed("down"), [syn.shared(m) for m in ("gate", "up", "down")],
+                            shexp_gate=gv)
+    assert np.array_equal(idx.astype(np.int64), ridx)
     err = np.abs(out - ref).max(axis=1) / np.abs(ref).max(axis=1)
     assert err.max() < 1e-5, err
