@@ -155,6 +155,12 @@ def roofline_for(kernels, stats, T, workload):
                "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
                "kernel": name, "bytes_per_launch": amount,
                "avg_us": round(kernels[name]["avg_us"], 2)}
+        if name.endswith(("_dec", "_file")):
+            # the matrix-core kernels' useful flops too (both bounds reported)
+            fl = rows * 2 * D * 2 * H if "gateup" in name else rows * 2 * H * D
+            out["mfma"] = {"achieved": round(fl / avg_s / 1e12, 1), "peak": MFMA_F16_PEAK_TFLOPS,
+                           "unit": "TFLOP/s", "frac": round(fl / avg_s / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+                           "flops_per_launch": fl}
     else:
         ach = amount / avg_s / 1e12
         # the same kernel's weight bytes against HBM (both bounds are reported
