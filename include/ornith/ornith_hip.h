@@ -186,8 +186,8 @@ typedef struct ornith_moe_store ornith_moe_store;
 
 typedef struct {
     int n_layers;   /* 40 for Ornith */
-    int d_model;    /* D = 2048; multiple of 256 */
-    int hidden;     /* H = 512 (expert_feed_forward_length); multiple of 256, <= 1024 */
+    int d_model;    /* D = 2048; 256 times a power of two, or a multiple of 2048 */
+    int hidden;     /* H = 512 (expert_feed_forward_length); 256, 512 or 1024 */
     int n_experts;  /* E = 256 (<= 256) */
     int top_k;      /* k = 8 (<= 16) */
     int has_shared; /* 1: one always-on shared expert (model.c:1001-1007) */

@@ -244,10 +244,19 @@ int orn_prof_kernel(gpu_context *ctx, const char *name, hipEvent_t *start, hipEv
 /* ---------------------------------------------------------------------------
  * Store
  * ------------------------------------------------------------------------- */
+/* The matvec kernels spread a wave's 64 lanes over 8 lanes per 256-wide
+ * block: D / 256 and H / 256 must divide 64 (powers of two), or D / 256 be a
+ * multiple of 8 (whole column groups). */
+static int widths_ok(int D, int H)
+{
+    const int nd = D / 256, nh = H / 256;
+    return D > 0 && D % 256 == 0 && ((nd & (nd - 1)) == 0 || nd % 8 == 0) && H > 0 &&
+           H % 256 == 0 && H <= 1024 && (nh & (nh - 1)) == 0;
+}
+
 static int shape_ok(const ornith_moe_shape *s)
 {
-    return s && s->n_layers > 0 && s->d_model > 0 && s->d_model % 256 == 0 && s->hidden > 0 &&
-           s->hidden % 256 == 0 && s->hidden <= 1024 && s->n_experts > 0 &&
+    return s && s->n_layers > 0 && widths_ok(s->d_model, s->hidden) && s->n_experts > 0 &&
            s->n_experts <= 256 && s->top_k > 0 && s->top_k <= 16 && s->top_k <= s->n_experts &&
            (s->has_shared == 0 || s->has_shared == 1) && s->d_model % 128 == 0 &&
            (s->prefill_layout == 0 || s->prefill_layout == 1) &&
@@ -929,6 +938,7 @@ static plan_t make_plan(const ornith_moe_shape *sh, int T, int use_mfma)
         int kdn = pow2_floor(2048 / (est_items * (D / 256)) > 0 ? 2048 / (est_items * (D / 256)) : 1);
         while (kdn > 1 && (H / 32) % kdn) kdn /= 2;
         if (kdn > H / 32) kdn = H / 32;
+        if (kdn > 16) kdn = 16; /* the combine sums at most 16 slices */
         p.ks_gu = kg;
         p.ks_dn = kdn;
         if (p.tchunk <= 32) {

@@ -202,14 +202,93 @@ __global__ void __launch_bounds__(256)
 // the shared expert (unclamped silu, gpu.c:176-186); all others are routed
 // (clamped silu, model.c:340-344).
 // ---------------------------------------------------------------------------
-// KMAX > 0 (= ks): the partials of a value are loaded together, one memory
-// round trip per thread; KMAX = 0: any ks, four partials at a time.
-// With fh (file-orientation stores) the row is also written as the down
+// Two kernels, bit-identical (each value sums its split-K partials from 0.0f
+// in slice order, then the same activation), chosen by ks as measured:
+//
+// k_mid_wave: one wave per row (ks <= 2); lane l takes the NG groups of 4
+// consecutive values 4*(l + 64i) .. +3 (H = 256*NG), so each load
+// instruction of a wave reads 1 KB in one piece, and all of a row's partials
+// are in flight together.
+//
+// With fh (file-orientation stores) the row goes out only as the down
 // kernel's activations: hi/lo fp16 of mid * s (s = prep_scale(max |mid|)) in
-// the pair order of k_prep_rows (expert_file.hip), and finv[r] = 1/s.
+// the pair order of k_prep_rows (expert_file.hip: the words of a 4-value
+// group are the pairs (0, 2) and (1, 3)), and finv[r] = 1/s; the fp32 mid,
+// which the file down kernel does not read, is not written.
+template <int NG, int KS>
+__global__ void __launch_bounds__(64)
+    k_mid_wave(const float *__restrict__ gu_part, const int *__restrict__ ctl,
+               float *__restrict__ mid, int H, int rows_max, int shared_rows,
+               float *__restrict__ row_amax, uint32_t *__restrict__ fh, uint32_t *__restrict__ fl,
+               float *__restrict__ finv)
+{
+    const int lane = threadIdx.x;
+    const int r = blockIdx.x;
+    if (r >= ctl[2]) return;
+    const size_t kstride = (size_t)rows_max * 2 * H;
+    const float *p = gu_part + (size_t)r * 2 * H + 4 * lane;
+    v4f lg[KS][NG], lu[KS][NG];
+#pragma unroll
+    for (int j = 0; j < KS; ++j)
+#pragma unroll
+        for (int i = 0; i < NG; ++i) {
+            lg[j][i] = *reinterpret_cast<const v4f *>(p + j * kstride + 256 * i);
+            lu[j][i] = *reinterpret_cast<const v4f *>(p + j * kstride + H + 256 * i);
+        }
+    const bool shared_row = r < shared_rows;
+    float amax = 0.0f;
+    v4f m[NG];
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+        v4f g = {0.0f, 0.0f, 0.0f, 0.0f}, u = g;
+#pragma unroll
+        for (int j = 0; j < KS; ++j) {
+            g = g + lg[j][i];
+            u = u + lu[j][i];
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float gv = g[e];
+            float act;
+            if (shared_row) {
+                act = gv / (1.0f + expf(-gv));
+            } else {
+                if (gv < -50.0f) act = 0.0f;
+                else if (gv > 50.0f) act = gv;
+                else act = gv / (1.0f + expf(-gv));
+            }
+            m[i][e] = act * u[e];
+            amax = fmaxf(amax, fabsf(m[i][e]));
+        }
+        if (!fh) *reinterpret_cast<v4f *>(mid + (size_t)r * H + 4 * lane + 256 * i) = m[i];
+    }
+    if (!row_amax && !fh) return;
+    // max |mid| of the row, for the down step's scaling (order-free)
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    if (row_amax && lane == 0) row_amax[r] = amax;
+    if (fh) {
+        const float sc = orn_mfma::prep_scale(amax);
+#pragma unroll
+        for (int i = 0; i < NG; ++i) {
+            const v4f a = m[i] * sc;
+            uint32_t h0, h1, l0, l1;
+            orn_mfma::split2(a.x, a.z, h0, l0);
+            orn_mfma::split2(a.y, a.w, h1, l1);
+            const size_t o = (size_t)r * (H >> 1) + 2 * lane + 128 * i;  // u32 words
+            *reinterpret_cast<uint2 *>(fh + o) = make_uint2(h0, h1);
+            *reinterpret_cast<uint2 *>(fl + o) = make_uint2(l0, l1);
+        }
+        if (lane == 0) finv[r] = 1.0f / sc;
+    }
+}
+
+// k_mid_wg: one work group per row, a thread per value (ks >= 4).  KMAX > 0
+// (= ks): the partials of a value are loaded together, one memory round trip
+// per thread; KMAX = 0: any ks, four partials at a time.
 template <int KMAX>
 __global__ void __launch_bounds__(256)
-    k_mid(const float *__restrict__ gu_part, const int *__restrict__ ctl, float *__restrict__ mid,
+    k_mid_wg(const float *__restrict__ gu_part, const int *__restrict__ ctl, float *__restrict__ mid,
           int H, int ks, int rows_max, int shared_rows, float *__restrict__ row_amax,
           uint32_t *__restrict__ fh, uint32_t *__restrict__ fl, float *__restrict__ finv)
 {
@@ -260,8 +339,8 @@ __global__ void __launch_bounds__(256)
             else act = g / (1.0f + expf(-g));
         }
         const float v = act * u;
-        mid[(size_t)r * H + h] = v;
         if (fh) vrow[h] = v;
+        else mid[(size_t)r * H + h] = v;
         amax = fmaxf(amax, fabsf(v));
     }
     if (row_amax || fh) {  // max |mid| of the row, for the down step's scaling
@@ -532,7 +611,7 @@ extern "C" int ornk_moe_norm(const ornk_moe_args *a, hipStream_t s)
 extern "C" int ornk_moe_gateup(const ornk_moe_args *a, hipStream_t s)
 {
     const int NB = a->H / 256;
-    if (a->H % 256 || NB < 1 || 8 * NB > 64) return hipErrorInvalidValue;
+    if (a->H % 256 || NB < 1 || 64 % (8 * NB)) return hipErrorInvalidValue;
     const int RW = 64 / (8 * NB);
     const int RK = a->D / a->ks_gu;
     if (a->D % a->ks_gu || RK % (4 * RW * ORN_NPF)) return hipErrorInvalidValue;
@@ -556,13 +635,34 @@ extern "C" int ornk_moe_gateup(const ornk_moe_args *a, hipStream_t s)
 
 extern "C" int ornk_moe_mid(const ornk_moe_args *a, hipStream_t s)
 {
+    const int H = a->H, ks = a->ks_gu;
+    if (H % 256 || H > 1024 || ks < 1) return hipErrorInvalidValue;
+    // measured: one wave per row wins at ks <= 2 (prefill: 20.6 against 27.7
+    // us), four waves per row at ks >= 4 (7.9 against 9.3 us at 256 skewed
+    // tokens, where a wave per row leaves 9 waves per CU)
+    const int shared_rows = a->has_shared ? a->T : 0;
+    float *amax = a->use_mfma ? a->mid_amax : nullptr;
+    const ornk_file_ws &f = a->fw;
+    if (ks <= 2) {
+#define ORN_MIDW(NG, KS)                                                                      \
+    ORN_LAUNCH_EV(a, (k_mid_wave<NG, KS>), dim3(a->rows_max), dim3(64), 0, s, a->gu_part,     \
+                  a->ctl, a->mid, H, a->rows_max, shared_rows, amax, f.mh, f.ml, f.minv)
+        switch ((H / 256) * 4 + ks) {
+        case 4 + 1: ORN_MIDW(1, 1); break;
+        case 4 + 2: ORN_MIDW(1, 2); break;
+        case 8 + 1: ORN_MIDW(2, 1); break;
+        case 8 + 2: ORN_MIDW(2, 2); break;
+        case 16 + 1: ORN_MIDW(4, 1); break;
+        case 16 + 2: ORN_MIDW(4, 2); break;
+        default: return hipErrorInvalidValue;  // H = 768: refused by the store
+        }
+#undef ORN_MIDW
+        return hipGetLastError();
+    }
 #define ORN_MID(K)                                                                             \
-    ORN_LAUNCH_EV(a, k_mid<K>, dim3(a->rows_max), dim3(256), 0, s, a->gu_part, a->ctl, a->mid,  \
-                       a->H, a->ks_gu, a->rows_max, a->has_shared ? a->T : 0,                 \
-                       a->use_mfma ? a->mid_amax : nullptr, a->fw.mh, a->fw.ml, a->fw.minv)
-    switch (a->ks_gu) {
-    case 1: ORN_MID(1); break;
-    case 2: ORN_MID(2); break;
+    ORN_LAUNCH_EV(a, k_mid_wg<K>, dim3(a->rows_max), dim3(256), 0, s, a->gu_part, a->ctl,      \
+                  a->mid, H, ks, a->rows_max, shared_rows, amax, f.mh, f.ml, f.minv)
+    switch (ks) {
     case 4: ORN_MID(4); break;
     case 8: ORN_MID(8); break;
     case 16: ORN_MID(16); break;
@@ -578,7 +678,7 @@ extern "C" int ornk_moe_down(const ornk_moe_args *a, hipStream_t s)
     if (a->D % 256 || NBD < 1) return hipErrorInvalidValue;
     const int CR = 8 * NBD;
     const int CRg = CR < 64 ? CR : 64;
-    if (CR > 64 && CR % 64) return hipErrorInvalidValue;
+    if (CR > 64 ? CR % 64 : 64 % CR) return hipErrorInvalidValue;
     const int ncg = CR > 64 ? CR / 64 : 1;
     const int RW = 64 / CRg;
     const int RH = a->H / a->ks_dn;

@@ -260,7 +260,8 @@ def oracle_file(syn, D, H, E, k, x, **kw):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("shape,T", [((256, 256, 16), 1), ((256, 256, 16), 3),
-                                     ((256, 256, 16), 37)])
+                                     ((256, 256, 16), 37), ((256, 1024, 16), 1),
+                                     ((256, 1024, 16), 100)])
 def test_file_layout_parity(om, ctx, shape, T):
     D, H, E = shape
     k = 8

@@ -138,6 +138,34 @@ def test_small_layer_mfma_parity(om, ctx, small, T, mode):
     assert err.max() <= TOL
 
 
+def test_hidden_width_1024(om, ctx):
+    """Experts 1024 wide (four groups of 256 per lane in the mid step), on
+    the VALU and the automatic path, T = 1, 16, 150."""
+    H = 1024
+    L = Layer(om, ctx, 256, H, 16, 8, seed=23)
+    try:
+        for T in (1, 16, 150):
+            for flags in (om.MOE_PATH_VALU, 0):
+                say(f"H={H} T={T} flags={flags}")
+                x = act(om, 900 + T, T, L.D)
+                out, idx, w = run(ctx, L, x, flags=flags)
+                ref, ridx, rw = L.oracle(x)
+                assert np.array_equal(idx, ridx)
+                err = row_err(out, ref)
+                say("  max row err", err.max())
+                assert err.max() <= TOL
+    finally:
+        L.store.close()
+
+
+def test_store_refuses_widths_the_kernels_cannot_map(om, ctx):
+    """D / 256 and H / 256 must spread evenly over a wave's lanes."""
+    for D, H in ((768, 256), (1280, 256), (256, 768), (256, 2048)):
+        with pytest.raises(RuntimeError, match="unsupported MoE shape"):
+            om.Store(ctx, 1, D, H, 16, 8, True)
+    om.Store(ctx, 1, 4096, 256, 16, 8, True, prefill_layout=False).close()
+
+
 def test_skewed_batch_on_decode_items(om, ctx):
     """A batch of more than 64 tokens averaging at most 16 rows per expert,
     Zipf-skewed: the hot experts are split into 16-row items of the decode
