@@ -675,6 +675,12 @@ extern "C" int ornk_moe_route(const ornk_moe_args *a, hipStream_t s)
     } else if (T >= 1024) {
         ORN_LAUNCH_EV(a, k_router_seq<4>, dim3((E + 63) / 64, (T + 15) / 16), dim3(256), 0, s,
                            xin, a->router, a->bias, T, D, E, a->logits, a->ctl, amax);
+    } else if (T >= 384) {
+        // 4 tokens per block: enough blocks for every CU (measured at 512
+        // tokens: 36.5 us against 49.5 us for k_router_dec; at 256, 31 us
+        // against 25-34 us)
+        ORN_LAUNCH_EV(a, k_router_seq<1>, dim3((E + 63) / 64, (T + 3) / 4), dim3(256), 0, s,
+                           xin, a->router, a->bias, T, D, E, a->logits, a->ctl, amax);
     } else {
         ORN_LAUNCH_EV(a, k_router_dec, dim3((E + 63) / 64, T), dim3(64), sizeof(float) * (size_t)D,
                            s, xin, a->router, a->bias, T, D, E, a->logits, a->ctl, amax);

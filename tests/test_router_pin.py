@@ -115,8 +115,10 @@ def test_router_dec_logits_bit_exact(om, ctx, store, T, norm):
     check(om, ctx, store, T, 0, norm)
 
 
-def test_router_seq_logits_bit_exact(om, ctx, store):
-    check(om, ctx, store, 2048, 0, False)
+@pytest.mark.parametrize("T", [400, 2048])
+def test_router_seq_logits_bit_exact(om, ctx, store, T):
+    """LDS-staged chains: 4 tokens per block (T < 1024), 16 (T >= 1024)."""
+    check(om, ctx, store, T, 0, T == 400)
 
 
 @pytest.mark.parametrize("T", [1, 16, 256])
