@@ -434,10 +434,27 @@ def measure_dequant(ctx):
     return res
 
 
+def wide_q6_store(ctx):
+    """Layer 0 of the headline store with every Q6_K sub-scale redrawn over
+    [-128, 127] and each block's first at -128 or 127 (a quantizer sets the
+    largest sub-block of a block to the range's end): sc * q then exceeds
+    fp16's exact integers and the down kernels split it in two operands."""
+    st = om.Store(ctx, 1, D, H, E, K, True)
+    st.fill_synthetic(0, SEED)
+    blocks = st.get_experts(0, om.MAT_DOWN, 0, E + 1).reshape(-1, om.Q6K_BYTES)
+    rng = np.random.default_rng(SEED)
+    sc = rng.integers(-128, 128, size=(blocks.shape[0], 16))
+    sc[:, 0] = np.where(rng.random(blocks.shape[0]) < 0.5, -128, 127)
+    blocks[:, 192:208] = sc.astype(np.int8).view(np.uint8)
+    st.set_experts(0, om.MAT_DOWN, 0, blocks.reshape(-1), E + 1)
+    return st
+
+
 # Extra configs reported beside the headline: (label, store layer, tokens).
 # Layer 1 carries a Zipf(1.1) router bias.
 EXTRA_CONFIGS = (("decode_t1", 0, 1), ("prefill_t2048", 0, 2048), ("zipf_t256", 1, 256))
-EXTRA_LABELS = [c[0] for c in EXTRA_CONFIGS] + ["file_t1", "file_t16", "file_t2048", "stack40",
+EXTRA_LABELS = [c[0] for c in EXTRA_CONFIGS] + ["file_t1", "file_t16", "file_t2048", "q6wide_t1",
+                                                 "q6wide_t16", "q6wide_t2048", "stack40",
                                                  "streamed", "attention", "dequant"]
 
 
@@ -555,14 +572,12 @@ def main():
             log(label, extra[label]["tokens_per_s"], "tok/s")
         # Experts in GGUF file orientation (input index fastest, as real
         # files store them): a store of its own, same synthetic bytes.
-        if not args.only or args.only.startswith("file_"):
-            fst = om.Store(ctx, 1, D, H, E, K, True, prefill_layout=False, file_layout=True)
-            fst.fill_synthetic(0, SEED)
-            for label, Tn in (("file_t1", 1), ("file_t16", 16), ("file_t2048", 2048)):
+        def side_store(prefix, st):
+            for label, Tn in ((prefix + "t1", 1), (prefix + "t16", 16), (prefix + "t2048", 2048)):
                 if args.only and label != args.only:
                     continue
                 steps = max(5, args.steps // (20 if Tn >= 256 else 1))
-                ms_x, kern_x, st_x = measure(ctx, fst, 0, Tn, steps, max(2, args.warmup // 4))
+                ms_x, kern_x, st_x = measure(ctx, st, 0, Tn, steps, max(2, args.warmup // 4))
                 _, roof_x = roofline_for(kern_x, st_x, Tn, label.split("_")[-1])
                 if roof_x["bound"] == "hbm":
                     roof_x["frac_of_measured"] = round(roof_x["achieved"] / read_gbs, 4)
@@ -572,7 +587,16 @@ def main():
                                 "dominant": roof_x,
                                 "kernels_us": {n: round(v["avg_us"], 2) for n, v in kern_x.items()}}
                 log(label, extra[label]["tokens_per_s"], "tok/s")
-            fst.close()
+            st.close()
+
+        if not args.only or args.only.startswith("file_"):
+            fst = om.Store(ctx, 1, D, H, E, K, True, prefill_layout=False, file_layout=True)
+            fst.fill_synthetic(0, SEED)
+            side_store("file_", fst)
+        # The headline layer with Q6_K sub-scales over the whole int8 range,
+        # as real quantizers emit them (the down kernels' wide instances).
+        if not args.only or args.only.startswith("q6wide_"):
+            side_store("q6wide_", wide_q6_store(ctx))
         result["configs"] = extra
     # CPU variant (ii) reads the experts back from this store (closed next)
     cpu_contig = cpu_contiguous(store) if not args.no_cpu and not args.only else None

@@ -315,9 +315,10 @@ enum { ORN_ROUTE_RENORM = 0, ORN_ROUTE_LITERAL = 1 };
 /* Expert-product kernels.  Default: the MFMA kernels (prefill layout, fp16
  * hi+lo activations, fp32 accumulate; decode-shaped instances up to 64
  * tokens, grouped GEMMs above) when the batch has at least
- * ORN_MOE_MFMA_MIN_TOKENS tokens, the store keeps the prefill layouts and
- * every Q6_K sub-block scale of the layer has |sc| <= 64; else the VALU
- * matvec kernels (fp32 throughout). */
+ * ORN_MOE_MFMA_MIN_TOKENS tokens and the store keeps the prefill layouts
+ * (Q6_K sub-block scales of any magnitude: above 64 the down kernels split
+ * sc * q in two exact fp16 operands); else the VALU matvec kernels (fp32
+ * throughout). */
 #define ORN_MOE_PATH_VALU 4u /* force the VALU kernels */
 #define ORN_MOE_PATH_MFMA 8u /* force the MFMA kernels (EUNSUPPORTED if unavailable) */
 #define ORN_MOE_MFMA_MIN_TOKENS 1

@@ -1047,15 +1047,16 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     if (file && (flags & (ORN_MOE_PATH_VALU | ORN_MOE_PATH_MFMA)))
         return orn_set_err(ctx, ORN_EUNSUPPORTED,
                            "a file-layout store has one expert path; do not force one");
-    /* The MFMA path needs the prefill layouts and Q6_K sub-scales with
-     * |sc| <= 64 (so that sc * q is exact in fp16). */
-    const int mfma_ok = sh->prefill_layout && st->q6_scmax[layer] <= 64;
+    /* The MFMA path needs the prefill layouts.  Q6_K sub-scales above 64 in
+     * magnitude (real quantizers emit them up to 128) take the down kernels'
+     * wide instances, which split sc * q in two exact fp16 operands. */
+    const int mfma_ok = sh->prefill_layout;
     int use_mfma = mfma_ok && T >= ORN_MOE_MFMA_MIN_TOKENS;
     if (flags & ORN_MOE_PATH_VALU) use_mfma = 0;
     if (flags & ORN_MOE_PATH_MFMA) {
         if (!mfma_ok)
             return orn_set_err(ctx, ORN_EUNSUPPORTED,
-                               "MFMA path needs the prefill layout and |Q6_K scale| <= 64");
+                               "MFMA path needs the prefill layout");
         use_mfma = 1;
     }
     if (file) use_mfma = 0;  /* the mid and combine steps run as on the VALU path */
@@ -1156,6 +1157,7 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     a.mid = (float *)(ws + o_mid);
     a.dn_part = (float *)(ws + o_dn);
     a.use_mfma = use_mfma;
+    a.q6_wide = st->q6_scmax && st->q6_scmax[layer] > 64; /* held by MFMA-layout stores */
     if (use_mfma && !st->cache) {  /* a streamed store's slot arrays come from the cache */
         const size_t slot0 = (size_t)layer * E1, DH = (size_t)D * H;
         for (int m = 0; m < 2; ++m) {

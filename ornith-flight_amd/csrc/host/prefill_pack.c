@@ -8,7 +8,8 @@
  * the kernels use directly:
  *
  *   B[k][n] = sc(k, n) * q(k, n)   exact in fp16 (|B| <= 945 for Q4_K,
- *                                   <= 2048 for Q6_K when |sc| <= 64)
+ *                                   <= 2048 for Q6_K when |sc| <= 64; the
+ *                                   down kernels split larger ones in two)
  *   W[k][n] = d(k, b) * B[k][n] - dmin(k, b) * m(k, n)     (Q4_K, gguf.c:43-61)
  *   W[k][n] = d(k, b) * B[k][n]                            (Q6_K, gguf.c:64-86)
  *

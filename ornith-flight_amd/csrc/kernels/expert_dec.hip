@@ -322,8 +322,9 @@ struct DnRing {
     uint4 q0, q1, sc[4];
 };
 
-template <int NR, int KT, int KC, int KSG, int RT>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT > 1 ? 2 : 3)))
+// WIDE: Q6_K sub-scales up to |128| (q6_b2: three MFMAs per tile and step).
+template <int NR, int KT, int KC, int KSG, int RT, bool WIDE>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT > 1 || WIDE ? 2 : 3)))
     k_down_dec(ornk_dn_prefill P, const float *__restrict__ mid,
                const float *__restrict__ mid_amax, const int *__restrict__ ctl,
                const int4 *__restrict__ items, float *__restrict__ dn, int D, int H, int ks,
@@ -504,11 +505,18 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT > 1
     for (int kt = 0; kt < KT; ++kt) {
         const int ch = kt / KC, kl = kt % KC;
         DnRing &r = st[kt % NR];
-        v8h bq[4];
-        bq[0] = q6_b(r.q0.x, r.q0.y, r.sc[0]);
-        bq[1] = q6_b(r.q0.z, r.q0.w, r.sc[1]);
-        bq[2] = q6_b(r.q1.x, r.q1.y, r.sc[2]);
-        bq[3] = q6_b(r.q1.z, r.q1.w, r.sc[3]);
+        v8h bq[4], bq2[WIDE ? 4 : 1];
+        if (WIDE) {
+            q6_b2(r.q0.x, r.q0.y, r.sc[0], bq[0], bq2[0]);
+            q6_b2(r.q0.z, r.q0.w, r.sc[1], bq[1], bq2[WIDE ? 1 : 0]);
+            q6_b2(r.q1.x, r.q1.y, r.sc[2], bq[2], bq2[WIDE ? 2 : 0]);
+            q6_b2(r.q1.z, r.q1.w, r.sc[3], bq[3], bq2[WIDE ? 3 : 0]);
+        } else {
+            bq[0] = q6_b(r.q0.x, r.q0.y, r.sc[0]);
+            bq[1] = q6_b(r.q0.z, r.q0.w, r.sc[1]);
+            bq[2] = q6_b(r.q1.x, r.q1.y, r.sc[2]);
+            bq[3] = q6_b(r.q1.z, r.q1.w, r.sc[3]);
+        }
         __builtin_amdgcn_sched_barrier(0);
         if (kt + NR < KT) load_b(r, kt + NR);
         __builtin_amdgcn_sched_barrier(0);
@@ -522,6 +530,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT > 1
             for (int j = 0; j < 4; ++j) {
                 acc[rt][j] = mfma(ahi, bq[j], acc[rt][j]);
                 acc[rt][j] = mfma(alo, bq[j], acc[rt][j]);
+                if (WIDE) acc[rt][j] = mfma(ahi, bq2[WIDE ? j : 0], acc[rt][j]);
             }
         }
         if (kl == 0 && ch + 1 < NCHK) {
@@ -618,34 +627,47 @@ extern "C" int ornk_moe_down_dec(const ornk_moe_args *a, hipStream_t s)
     const int RT = a->tchunk > 16 ? 2 : 1;
     const dim3 grid(a->items_max * (a->D / 256) * ks);
     const int shared_rows = a->has_shared ? a->T : 0;
+    const bool wide = a->q6_wide != 0;
     if (RT == 1 && ornk_down_dec_fuses_mid(a->T, a->H, a->ks_gu, ks)) {
-#define ORN_DN_MID(KSG)                                                                         \
-    ORN_LAUNCH_EV(a, (k_down_dec<ORN_DEC_NR, 8, 4, KSG, 1>), grid, dim3(256), 0, s, a->dn_pf,   \
+#define ORN_DN_MID(KSG, W)                                                                      \
+    ORN_LAUNCH_EV(a, (k_down_dec<ORN_DEC_NR, 8, 4, KSG, 1, W>), grid, dim3(256), 0, s, a->dn_pf, \
                   a->mid, a->mid_amax, a->ctl, reinterpret_cast<const int4 *>(a->items),         \
                   a->dn_part, a->D, a->H, ks, a->rows_max, a->gu_part, shared_rows)
+#define ORN_DN_MID_W(KSG)         \
+    if (wide) ORN_DN_MID(KSG, true); \
+    else ORN_DN_MID(KSG, false)
         switch (a->ks_gu) {
-        case 4: ORN_DN_MID(4); break;
-        case 8: ORN_DN_MID(8); break;
-        default: ORN_DN_MID(16); break;
+        case 4: ORN_DN_MID_W(4); break;
+        case 8: ORN_DN_MID_W(8); break;
+        default: ORN_DN_MID_W(16); break;
         }
+#undef ORN_DN_MID_W
 #undef ORN_DN_MID
         return hipGetLastError();
     }
-#define ORN_DN_DEC(K, R)                                                                          \
-    ORN_LAUNCH_EV(a, (k_down_dec<ORN_DEC_NR, K, 4, 0, R>), grid, dim3(256), 0, s, a->dn_pf, a->mid, \
-                       a->mid_amax, a->ctl, reinterpret_cast<const int4 *>(a->items),              \
-                       a->dn_part, a->D, a->H, ks, a->rows_max, a->gu_part, shared_rows)
-#define ORN_DN_DEC_RT(R)                \
-    switch (KT) {                       \
-    case 4: ORN_DN_DEC(4, R); break;    \
-    case 8: ORN_DN_DEC(8, R); break;    \
-    case 16: ORN_DN_DEC(16, R); break;  \
-    default: ORN_DN_DEC(32, R); break;  \
+#define ORN_DN_DEC(K, R, W)                                                                       \
+    ORN_LAUNCH_EV(a, (k_down_dec<ORN_DEC_NR, K, 4, 0, R, W>), grid, dim3(256), 0, s, a->dn_pf,    \
+                  a->mid, a->mid_amax, a->ctl, reinterpret_cast<const int4 *>(a->items),         \
+                  a->dn_part, a->D, a->H, ks, a->rows_max, a->gu_part, shared_rows)
+#define ORN_DN_DEC_RT(R, W)                \
+    switch (KT) {                          \
+    case 4: ORN_DN_DEC(4, R, W); break;    \
+    case 8: ORN_DN_DEC(8, R, W); break;    \
+    case 16: ORN_DN_DEC(16, R, W); break;  \
+    default: ORN_DN_DEC(32, R, W); break;  \
     }
     if (RT == 2) {
-        ORN_DN_DEC_RT(2)
+        if (wide) {
+            ORN_DN_DEC_RT(2, true)
+        } else {
+            ORN_DN_DEC_RT(2, false)
+        }
     } else {
-        ORN_DN_DEC_RT(1)
+        if (wide) {
+            ORN_DN_DEC_RT(1, true)
+        } else {
+            ORN_DN_DEC_RT(1, false)
+        }
     }
 #undef ORN_DN_DEC_RT
 #undef ORN_DN_DEC

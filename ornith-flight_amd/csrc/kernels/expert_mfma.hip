@@ -97,10 +97,12 @@ struct ATiles {
 };
 
 // Row tiles 0..NTT-1 x this wave's 4 column tiles: acc[tt][j] += A[tt] * B[j]
-// for the hi and lo halves of A.
-template <int NTT>
+// for the hi and lo halves of A; with WIDE, B[j] = bq[j] + bq2[j] (q6_b2:
+// the correction bq2 takes A's hi half only).
+template <int NTT, bool WIDE = false>
 __device__ __forceinline__ void mma_step(const _Float16 *Ahi, const _Float16 *Alo,
-                                         const v8h (&bq)[4], v4f (&acc)[NTT][4], int c, int g)
+                                         const v8h (&bq)[4], v4f (&acc)[NTT][4], int c, int g,
+                                         const v8h *bq2 = nullptr)
 {
 #pragma unroll
     for (int tt = 0; tt < NTT; ++tt) {
@@ -111,6 +113,7 @@ __device__ __forceinline__ void mma_step(const _Float16 *Ahi, const _Float16 *Al
         for (int j = 0; j < 4; ++j) {
             acc[tt][j] = mfma(ahi, bq[j], acc[tt][j]);
             acc[tt][j] = mfma(alo, bq[j], acc[tt][j]);
+            if (WIDE) acc[tt][j] = mfma(ahi, bq2[j], acc[tt][j]);
         }
     }
 }
@@ -368,7 +371,7 @@ struct DnBlock {
     int aoff, NBD, b, kt0, KT;
 };
 
-template <int NTT, int ROWS>
+template <int NTT, int ROWS, bool WIDE>
 __device__ __forceinline__ void down_tile(const DnBlock &B, ATiles<ROWS, 2> &As, const float *s_inv,
                                           float *dn_row0, int D, int col0, int nrows)
 {
@@ -395,33 +398,38 @@ __device__ __forceinline__ void down_tile(const DnBlock &B, ATiles<ROWS, 2> &As,
     ARaw ar;
     uint4 qv[2];
     uint4 sv[4];
-    v8h bq[4];
+    v8h bq[4], bq2[WIDE ? 4 : 1];
+    auto build_b = [&]() {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t w0 = j & 1 ? qv[j >> 1].z : qv[j >> 1].x;
+            const uint32_t w1 = j & 1 ? qv[j >> 1].w : qv[j >> 1].y;
+            if (WIDE) q6_b2(w0, w1, sv[j], bq[j], bq2[WIDE ? j : 0]);
+            else bq[j] = q6_b(w0, w1, sv[j]);
+        }
+    };
     if (a_live) {
         a_load<false>(ar, B.mrow, B.dva, nullptr, 0);
         a_store<false>(ar, B.ascale, &As.t[0][0][B.aoff], &As.t[0][1][B.aoff], nullptr, nullptr);
     }
     b_load(0, qv, sv);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) bq[j] = q6_b(j & 1 ? qv[j >> 1].z : qv[j >> 1].x,
-                                             j & 1 ? qv[j >> 1].w : qv[j >> 1].y, sv[j]);
+    build_b();
     __syncthreads();
 
     for (int kt = 0; kt < B.KT - 1; ++kt) {
         const int cur = kt & 1, nxt = cur ^ 1;
         if (a_live) a_load<false>(ar, B.mrow, B.dva, nullptr, 32 * (kt + 1));
         b_load(kt + 1, qv, sv);
-        mma_step<NTT>(As.t[cur][0], As.t[cur][1], bq, acc, c, g);
+        mma_step<NTT, WIDE>(As.t[cur][0], As.t[cur][1], bq, acc, c, g, bq2);
         if (a_live)
             a_store<false>(ar, B.ascale, &As.t[nxt][0][B.aoff], &As.t[nxt][1][B.aoff], nullptr,
                            nullptr);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) bq[j] = q6_b(j & 1 ? qv[j >> 1].z : qv[j >> 1].x,
-                                                 j & 1 ? qv[j >> 1].w : qv[j >> 1].y, sv[j]);
+        build_b();
         __syncthreads();
     }
     {
         const int cur = (B.KT - 1) & 1;
-        mma_step<NTT>(As.t[cur][0], As.t[cur][1], bq, acc, c, g);
+        mma_step<NTT, WIDE>(As.t[cur][0], As.t[cur][1], bq, acc, c, g, bq2);
     }
 
 #pragma unroll
@@ -438,7 +446,8 @@ __device__ __forceinline__ void down_tile(const DnBlock &B, ATiles<ROWS, 2> &As,
     }
 }
 
-template <int NTTMAX>
+// WIDE: Q6_K sub-scales up to |128| (q6_b2: three MFMAs per tile and step).
+template <int NTTMAX, bool WIDE>
 __global__ void __launch_bounds__(256)
     k_down_mfma(ornk_dn_prefill P, const float *__restrict__ mid,
                 const float *__restrict__ mid_amax, const int *__restrict__ ctl,
@@ -486,13 +495,13 @@ __global__ void __launch_bounds__(256)
     float *row0 = dn + ((size_t)kslice * rows_max + itm.y) * D;
     const int col0 = 256 * b;
     if (NTTMAX == 1) {
-        down_tile<1, ROWS>(B, As, s_inv, row0, D, col0, nrows);
+        down_tile<1, ROWS, WIDE>(B, As, s_inv, row0, D, col0, nrows);
     } else {
         switch ((nrows + 15) >> 4) {
-        case 1: down_tile<1, ROWS>(B, As, s_inv, row0, D, col0, nrows); break;
-        case 2: down_tile<2, ROWS>(B, As, s_inv, row0, D, col0, nrows); break;
-        case 3: down_tile<3, ROWS>(B, As, s_inv, row0, D, col0, nrows); break;
-        default: down_tile<4, ROWS>(B, As, s_inv, row0, D, col0, nrows); break;
+        case 1: down_tile<1, ROWS, WIDE>(B, As, s_inv, row0, D, col0, nrows); break;
+        case 2: down_tile<2, ROWS, WIDE>(B, As, s_inv, row0, D, col0, nrows); break;
+        case 3: down_tile<3, ROWS, WIDE>(B, As, s_inv, row0, D, col0, nrows); break;
+        default: down_tile<4, ROWS, WIDE>(B, As, s_inv, row0, D, col0, nrows); break;
         }
     }
 }
@@ -567,13 +576,17 @@ extern "C" int ornk_moe_down_mfma(const ornk_moe_args *a, hipStream_t s)
     if (a->H % 32 || a->D % 256 || ks < 1 || (a->H / 32) % ks || a->tchunk > ORN_MT)
         return hipErrorInvalidValue;
     const dim3 grid(a->items_max * (a->D / 256) * ks);
-    if (a->tchunk <= 16)
-        ORN_LAUNCH_EV(a, k_down_mfma<1>, grid, dim3(256), 0, s, a->dn_pf, a->mid, a->mid_amax,
-                           a->ctl, reinterpret_cast<const int4 *>(a->items), a->dn_part, a->D,
-                           a->H, ks, a->rows_max);
-    else
-        ORN_LAUNCH_EV(a, k_down_mfma<4>, grid, dim3(256), 0, s, a->dn_pf, a->mid, a->mid_amax,
-                           a->ctl, reinterpret_cast<const int4 *>(a->items), a->dn_part, a->D,
-                           a->H, ks, a->rows_max);
+#define ORN_DNM(N, W)                                                                           \
+    ORN_LAUNCH_EV(a, (k_down_mfma<N, W>), grid, dim3(256), 0, s, a->dn_pf, a->mid, a->mid_amax, \
+                  a->ctl, reinterpret_cast<const int4 *>(a->items), a->dn_part, a->D, a->H, ks, \
+                  a->rows_max)
+    if (a->tchunk <= 16) {
+        if (a->q6_wide) ORN_DNM(1, true);
+        else ORN_DNM(1, false);
+    } else {
+        if (a->q6_wide) ORN_DNM(4, true);
+        else ORN_DNM(4, false);
+    }
+#undef ORN_DNM
     return hipGetLastError();
 }

@@ -188,6 +188,8 @@ typedef struct {
     float *x_amax;    /* [T] max |xin| per token */
     int router_amax;  /* 1: the routing step writes x_amax (else the MFMA launchers do) */
     float *mid_amax;  /* [rows_max] max |mid| per row (written by the mid step) */
+    int q6_wide;      /* 1: some Q6_K sub-scale of the layer exceeds 64 in magnitude (the
+                         down kernels split sc * q in two exact fp16 operands) */
     /* File-orientation path: gate/up [E+1][H][D/256] Q4_K blocks, down body
      * and d [E+1][D][H/256] (the blocks in file order) */
     ornk_file_ws fw;

@@ -10,7 +10,8 @@
 //   y[r][n] = sum_k x[r][k] * W[k][n]
 //           = sum_k A[r][k] * B[k][n] - sum_k Am[r][k] * m[k][n]
 // with B = sc*q (an integer, |B| <= 945 for Q4_K and <= 2048 for Q6_K when
-// |sc| <= 64, so exact in fp16), A = x*d and Am = x*dmin.  A is scaled per
+// |sc| <= 64, so exact in fp16; larger Q6_K scales add an exact correction
+// operand, q6_b2), A = x*d and Am = x*dmin.  A is scaled per
 // row by a power of two s_r (|A| < 2^14, no fp16 overflow) and split into
 // fp16 hi + lo (hi = A rounded toward zero, lo = the exact remainder rounded
 // toward zero): A = hi + lo to about 2^-21 relative, so two MFMAs (hi, lo)
@@ -118,6 +119,32 @@ __device__ __forceinline__ v8h q6_b(uint32_t q0, uint32_t q1, uint4 sc)
         o[i] = as_u32(qv * as_v2h(s[i]));
     }
     return to_v8h(o[0], o[1], o[2], o[3]);
+}
+
+// Q6_K B operand for any sub-scale (|sc| <= 128, as real quantizers emit):
+// B = sc * q (|B| <= 4096) as b1 + b2 with b1 = fp16(sc * q) rounded to
+// nearest and b2 = sc * q - b1 from one fma, exact (an integer of magnitude
+// <= 1: fp16 holds every integer up to 2048 and every even one up to 4096).
+// The kernels add A_hi*b1 + A_lo*b1 + A_hi*b2; the dropped A_lo*b2 is below
+// 2^-21 of |A*B|, the order of the activation split itself.
+__device__ __forceinline__ void q6_b2(uint32_t q0, uint32_t q1, uint4 sc, v8h &b1, v8h &b2)
+{
+    const uint32_t s[4] = {sc.x, sc.y, sc.z, sc.w};
+    const uint32_t p[4] = {__builtin_amdgcn_perm(0x64646464u, q0, 0x04010400u),
+                           __builtin_amdgcn_perm(0x64646464u, q0, 0x04030402u),
+                           __builtin_amdgcn_perm(0x64646464u, q1, 0x04010400u),
+                           __builtin_amdgcn_perm(0x64646464u, q1, 0x04030402u)};
+    uint32_t o1[4], o2[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const v2h qv = as_v2h(p[i]) + (v2h){(_Float16)-1056.0f, (_Float16)-1056.0f};
+        const v2h sv = as_v2h(s[i]);
+        const v2h bh = qv * sv;
+        o1[i] = as_u32(bh);
+        o2[i] = as_u32(__builtin_elementwise_fma(qv, sv, -bh));
+    }
+    b1 = to_v8h(o1[0], o1[1], o1[2], o1[3]);
+    b2 = to_v8h(o2[0], o2[1], o2[2], o2[3]);
 }
 
 __device__ __forceinline__ v4f mfma(v8h a, v8h b, v4f c)

@@ -273,24 +273,38 @@ def test_mfma_needs_prefill_layout(om, ctx):
     L.store.close()
 
 
-def test_q6_scale_above_64_uses_valu(om, ctx):
-    """A Q6_K sub-scale with |sc| > 64 makes sc*q inexact in fp16: the layer
-    then routes every batch to the VALU kernels (and refuses a forced MFMA)."""
-    D, H, E, k = 256, 256, 16, 8
+def wide_q6_scales(down, seed):
+    """Q6_K sub-scales over the whole int8 range, as real quantizers emit
+    them (the largest sub-block of a block at -128 or 127)."""
+    blocks = down.reshape(-1, 210).copy()
+    rng = np.random.default_rng(seed)
+    sc = rng.integers(-128, 128, size=(blocks.shape[0], 16))
+    sc[:, 0] = np.where(rng.random(blocks.shape[0]) < 0.5, -128, 127)
+    blocks[:, 192:208] = sc.astype(np.int8).view(np.uint8)
+    return blocks.reshape(-1)
+
+
+@pytest.mark.parametrize("T", [1, 16, 40, 100, 150])
+def test_q6_wide_scales_on_mfma(om, ctx, T):
+    """Q6_K sub-scales up to |128| make sc*q inexact as one fp16 operand; the
+    down kernels then split it in two exact operands (decode items, fused
+    mid at T <= 64, two-tile items, grouped GEMMs) and stay on the MFMA path."""
+    D, H, E, k = 512, 512, 32, 8
     L = Layer(om, ctx, D, H, E, k, seed=23)
-    s = L.syn[0]
-    down = s.down.reshape(-1, 210).copy()
-    down[5, 192 + 3] = np.uint8(90)
-    s.down = down.reshape(-1)
-    L.store.set_experts(0, om.MAT_DOWN, 0, s.routed("down"), E)
-    x = act(om, 24, 150, D)
-    out, idx, _ = run(ctx, L, x)
-    ref, ridx, _ = L.oracle(x)
-    assert np.array_equal(idx, ridx)
-    assert row_err(out, ref).max() <= TOL
-    with pytest.raises(RuntimeError):
-        run(ctx, L, x[:4], flags=om.MOE_PATH_MFMA)
-    L.store.close()
+    try:
+        s = L.syn[0]
+        s.down = wide_q6_scales(s.down, 7)
+        L.store.set_experts(0, om.MAT_DOWN, 0, s.down, E + 1)
+        x = act(om, 24 + T, T, D)
+        ref, ridx, _ = L.oracle(x)
+        for flags in (0, om.MOE_PATH_MFMA, om.MOE_PATH_VALU):
+            out, idx, _ = run(ctx, L, x, flags=flags)
+            assert np.array_equal(idx, ridx)
+            err = row_err(out, ref)
+            say(f"  T={T} flags={flags}: max row err {err.max():.2e}")
+            assert err.max() <= TOL
+    finally:
+        L.store.close()
 
 
 def write(om, ctx, buf, arr):
