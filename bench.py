@@ -48,6 +48,7 @@ DN_BYTES = (D * H // 256) * 210          # down per expert: 860,160
 EXPERT_BYTES = GU_BYTES + DN_BYTES       # 2,039,808
 FLOP_PER_PAIR = 2 * (2 * D * H + H * D)  # 6,291,456
 MFMA_F16_PEAK_TFLOPS = 2500.0            # MI355X dense fp16 matrix peak
+VALU_F32_PEAK_TFLOPS = 157.3             # MI355X fp32 vector peak (an FMA = 2 flops)
 HBM_PEAK_GBS = 8000.0
 SEED = 1234
 
@@ -56,12 +57,12 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def measure(ctx, store, layer, T, steps, warmup, x_seed=1, stack_layers=0, ep=(0, 0)):
+def measure(ctx, store, layer, T, steps, warmup, x_seed=1, stack_layers=0, ep=(0, 0), flags=0):
     x = om.synth_normal(x_seed, om.synth_stream(0, om.SYN_ACT, 0), T * D, 1.0).reshape(T, D)
     xb = ctx.upload(x)
     ob = ctx.alloc(x.nbytes)
     L = om.lib()
-    opts = om.MoEOpts(om.ROUTE_RENORM, om.MOE_ASYNC, ep[0], ep[1])
+    opts = om.MoEOpts(om.ROUTE_RENORM, om.MOE_ASYNC | flags, ep[0], ep[1])
 
     def step():
         if stack_layers:
@@ -141,9 +142,11 @@ def roofline_for(kernels, stats, T, workload):
             "moe_gateup_dec": ("hbm", slots * GU_BYTES), "moe_down_dec": ("hbm", slots * DN_BYTES),
             "moe_gateup_mfma": ("mfma", rows * 2 * D * 2 * H), "moe_down_mfma": ("mfma", rows * 2 * H * D),
             "moe_gateup_file": ("hbm", slots * GU_BYTES), "moe_down_file": ("hbm", slots * DN_BYTES)}
-    if T >= 64:  # the file kernels at prefill sizes: matrix-core bound
+    if T >= 64:  # prefill sizes: the file kernels matrix-core bound, the VALU ones vector bound
         work["moe_gateup_file"] = ("mfma", rows * 2 * D * 2 * H)
         work["moe_down_file"] = ("mfma", rows * 2 * H * D)
+        work["moe_gateup"] = ("valu", rows * 2 * D * 2 * H)
+        work["moe_down"] = ("valu", rows * 2 * H * D)
     present = [n for n in work if n in kernels]
     name = max(present, key=lambda n: kernels[n]["avg_us"] * kernels[n]["calls_per_step"])
     bound, amount = work[name]
@@ -167,8 +170,9 @@ def roofline_for(kernels, stats, T, workload):
         # for matrix-core kernels: mixed batches sit between them)
         wbytes = slots * (GU_BYTES if "gateup" in name else DN_BYTES)
         hbm = wbytes / avg_s / 1e9
-        out = {"bound": "mfma", "achieved": round(ach, 1), "peak": MFMA_F16_PEAK_TFLOPS,
-               "unit": "TFLOP/s", "frac": round(ach / MFMA_F16_PEAK_TFLOPS, 4), "traffic": traffic,
+        peak = MFMA_F16_PEAK_TFLOPS if bound == "mfma" else VALU_F32_PEAK_TFLOPS
+        out = {"bound": bound, "achieved": round(ach, 1), "peak": peak,
+               "unit": "TFLOP/s", "frac": round(ach / peak, 4), "traffic": traffic,
                "kernel": name, "flops_per_launch": amount,
                "avg_us": round(kernels[name]["avg_us"], 2),
                "hbm": {"achieved": round(hbm, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -453,7 +457,8 @@ def wide_q6_store(ctx):
 # Extra configs reported beside the headline: (label, store layer, tokens).
 # Layer 1 carries a Zipf(1.1) router bias.
 EXTRA_CONFIGS = (("decode_t1", 0, 1), ("prefill_t2048", 0, 2048), ("zipf_t256", 1, 256))
-EXTRA_LABELS = [c[0] for c in EXTRA_CONFIGS] + ["file_t1", "file_t16", "file_t2048", "q6wide_t1",
+EXTRA_LABELS = [c[0] for c in EXTRA_CONFIGS] + ["valu_t1", "valu_t16", "valu_t2048", "file_t1",
+                                                 "file_t16", "file_t2048", "q6wide_t1",
                                                  "q6wide_t16", "q6wide_t2048", "stack40",
                                                  "streamed", "attention", "dequant"]
 
@@ -572,12 +577,13 @@ def main():
             log(label, extra[label]["tokens_per_s"], "tok/s")
         # Experts in GGUF file orientation (input index fastest, as real
         # files store them): a store of its own, same synthetic bytes.
-        def side_store(prefix, st):
+        def side_store(prefix, st, flags=0, close=True):
             for label, Tn in ((prefix + "t1", 1), (prefix + "t16", 16), (prefix + "t2048", 2048)):
                 if args.only and label != args.only:
                     continue
                 steps = max(5, args.steps // (20 if Tn >= 256 else 1))
-                ms_x, kern_x, st_x = measure(ctx, st, 0, Tn, steps, max(2, args.warmup // 4))
+                ms_x, kern_x, st_x = measure(ctx, st, 0, Tn, steps, max(2, args.warmup // 4),
+                                             flags=flags)
                 _, roof_x = roofline_for(kern_x, st_x, Tn, label.split("_")[-1])
                 if roof_x["bound"] == "hbm":
                     roof_x["frac_of_measured"] = round(roof_x["achieved"] / read_gbs, 4)
@@ -587,8 +593,13 @@ def main():
                                 "dominant": roof_x,
                                 "kernels_us": {n: round(v["avg_us"], 2) for n, v in kern_x.items()}}
                 log(label, extra[label]["tokens_per_s"], "tok/s")
-            st.close()
+            if close:
+                st.close()
 
+        # The fp32 VALU kernels on the headline layer (the path of a store
+        # kept without the MFMA layouts, and the reference-order fallback).
+        if not args.only or args.only.startswith("valu_"):
+            side_store("valu_", store, om.MOE_PATH_VALU, close=False)
         if not args.only or args.only.startswith("file_"):
             fst = om.Store(ctx, 1, D, H, E, K, True, prefill_layout=False, file_layout=True)
             fst.fill_synthetic(0, SEED)
