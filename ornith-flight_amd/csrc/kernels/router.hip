@@ -386,6 +386,12 @@ __global__ void __launch_bounds__(64)
 // consumer's chain is, also writes the row as the file kernels' activations
 // (the outputs of k_prep_rows<true>, expert_file.hip, with its arithmetic).
 // ---------------------------------------------------------------------------
+// Steps per chunk of the product ring (three chunks).  With the x*x buffer
+// folded into the ring a group holds 20 KB of LDS at D = 2048 (40 KB with
+// chunks of 8 and a separate buffer): measured route step 9.5 -> 9.2 us at
+// 16 tokens, 18.6 -> 13.4 at 32, 28.5 -> 26.7 at 64.
+#define ORN_PC_CHUNK 4
+
 template <int ND>
 __global__ void __launch_bounds__(128)
     k_router_pc(const float *__restrict__ x, const float *__restrict__ Wq,
@@ -395,10 +401,14 @@ __global__ void __launch_bounds__(128)
                 float *__restrict__ fxinv, uint16_t *__restrict__ fxsh, uint16_t *__restrict__ fxsl)
 {
     constexpr int D = 32 * ND, NR = ND < 16 ? ND : 16;
-    constexpr int C = ND < 8 ? ND : 8, NC = ND / C;
+    constexpr int C = ND < ORN_PC_CHUNK ? ND : ORN_PC_CHUNK, NC = ND / C;
+    constexpr int NPB = 3 * C * 64 > D / 4 ? 3 * C * 64 : D / 4;
     __shared__ v4f xs[D / 4];
-    __shared__ v4f ps[D / 4];  // x*x, with norm_w
-    __shared__ v4f pb[3 * C][64];
+    // the product ring; before the chain starts, x*x for the rmsnorm (with
+    // norm_w), so that a CU holds more groups
+    __shared__ v4f pbuf[NPB];
+    v4f *const ps = pbuf;
+    v4f(*const pb)[64] = reinterpret_cast<v4f(*)[64]>(pbuf);
     __shared__ float inv_s, mx_s[2];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the roles branch per wave
