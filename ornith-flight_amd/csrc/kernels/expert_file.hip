@@ -18,9 +18,14 @@
 //     of 32), then acc += d(column) * P; the mins term is one more MFMA per
 //     super-block over the rows' sub-block sums: acc -= dmin(column) *
 //     sum_j m(column, j) * xsum(row, j).
-//   Q6_K (v_mfma_f32_16x16x16_f16): sub-block scales are int8 (|sc * q| up
-//     to 4096, not exact in fp16), so B = q - 32 and each 16-value
-//     sub-block is one step: acc += (d * sc)(column) * P.
+//   Q6_K (v_mfma_f32_16x16x32_f16): sub-block scales are int8, so |sc * q|
+//     reaches 4096, past fp16's exact integers; B = sc * (q - 32) goes in
+//     as b1 = fp16(B) plus the exact remainder b2 = B - b1 (|b2| <= 1, one
+//     fma), A_hi*b1 + A_lo*b1 + A_hi*b2 per step (the dropped A_lo*b2 is
+//     below 2^-21 of |A*B|), P = sum over one super-block, acc += d(column)
+//     * P.  (Steps of one 16-value sub-block on v_mfma_f32_16x16x16_f16
+//     with the scale applied to each step's result ran 47.3 against 25.8
+//     us at 16 tokens: twice the loads and four fp32 fmas per step.)
 // Activations come from k_prep_rows (the expert inputs) and from the mid
 // step (k_mid, expert_valu.hip, for the down kernel), which split each row
 // (times a power of two s, |x*s| < 2^14) into fp16 hi + lo once per
@@ -396,67 +401,83 @@ __global__ void __launch_bounds__(256)
             scs[ct][2] = scw.z;
             scs[ct][3] = scw.w;
         }
-        // every q word of the super-block is requested before the first is
-        // used (one memory round trip per super-block)
-        uint32_t qa[2][2][ORN_FDN][3];
+        // Lane group g takes l = 8g .. 8g+7 of every 32-value quarter: the
+        // 8 bytes ql[64hn + 32(Q&1) + 8g ..] and qh[32hn + 8g ..] hold them
+        // for all four Q; every word of the super-block is requested before
+        // the first is used (one memory round trip per super-block).
+        uint2 qa[2][2][ORN_FDN], qb[2][ORN_FDN];
 #pragma unroll
         for (int hn = 0; hn < 2; ++hn)
 #pragma unroll
-            for (int is = 0; is < 2; ++is)
-#pragma unroll
-                for (int ct = 0; ct < ORN_FDN; ++ct) {
-                    const int l0 = 16 * is + 4 * g;
-                    qa[hn][is][ct][0] = *reinterpret_cast<const uint32_t *>(blk[ct] + 64 * hn + l0);
-                    qa[hn][is][ct][1] = *reinterpret_cast<const uint32_t *>(blk[ct] + 64 * hn + 32 + l0);
-                    qa[hn][is][ct][2] = *reinterpret_cast<const uint32_t *>(blk[ct] + 128 + 32 * hn + l0);
-                }
+            for (int ct = 0; ct < ORN_FDN; ++ct) {
+                qa[hn][0][ct] = *reinterpret_cast<const uint2 *>(blk[ct] + 64 * hn + 8 * g);
+                qa[hn][1][ct] = *reinterpret_cast<const uint2 *>(blk[ct] + 64 * hn + 32 + 8 * g);
+                qb[hn][ct] = *reinterpret_cast<const uint2 *>(blk[ct] + 128 + 32 * hn + 8 * g);
+            }
         FileTileT<RT> &As = Ab[NB == 2 ? (s & 1) : 0];
         stage_tile<RT, true>(As, mh, ml, src, H, s, nrows);
+        v4f ps[RT][ORN_FDN];  // this super-block's sums, before d
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < ORN_FDN; ++ct) ps[rt][ct] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int hn = 0; hn < 2; ++hn) {
 #pragma unroll
-            for (int is = 0; is < 2; ++is) {
-                const int l0 = 16 * is + 4 * g;  // this lane's 4 positions l0 .. l0+3
+            for (int Q = 0; Q < 4; ++Q) {
+                const int kl = 128 * hn + 32 * Q + 8 * g;  // this lane's 8 values, k - 256 s
+                v8h xa[RT], xb[RT];
 #pragma unroll
-                for (int Q = 0; Q < 4; ++Q) {
-                    const int kl = 128 * hn + 32 * Q + l0;  // k - 256 s
-                    v4h xa[RT], xb[RT];
+                for (int rt = 0; rt < RT; ++rt) {
+                    if (rt < nrt) {
+                        xa[rt] = *reinterpret_cast<const v8h *>(&As.v[0][16 * rt + c][kl]);
+                        xb[rt] = *reinterpret_cast<const v8h *>(&As.v[1][16 * rt + c][kl]);
+                    }
+                }
+                const int sb = 8 * hn + 2 * Q + (g >> 1);  // the 16-value sub-block of l
+#pragma unroll
+                for (int ct = 0; ct < ORN_FDN; ++ct) {
+                    const uint2 ql = qa[hn][Q & 1][ct], qh = qb[hn][ct];
+                    // bytes q + 32 (0..63): low 4 bits from ql, high 2 from qh
+                    const uint32_t w0 = ((ql.x >> (4 * (Q >> 1))) & 0x0F0F0F0Fu) |
+                                        (((qh.x >> (2 * Q)) & 0x03030303u) << 4);
+                    const uint32_t w1 = ((ql.y >> (4 * (Q >> 1))) & 0x0F0F0F0Fu) |
+                                        (((qh.y >> (2 * Q)) & 0x03030303u) << 4);
+                    // B = sc * (q - 32), |B| <= 4096, as b1 + b2 (q6_b2's
+                    // remainder form) in the prep's pair order
+                    const int scv = (int)(int8_t)((scs[ct][sb >> 2] >> (8 * (sb & 3))) & 0xFFu);
+                    const v2h sv = {(_Float16)scv, (_Float16)scv};
+                    const uint32_t p[4] = {__builtin_amdgcn_perm(0x64646464u, w0, 0x04020400u),
+                                           __builtin_amdgcn_perm(0x64646464u, w0, 0x04030401u),
+                                           __builtin_amdgcn_perm(0x64646464u, w1, 0x04020400u),
+                                           __builtin_amdgcn_perm(0x64646464u, w1, 0x04030401u)};
+                    uint32_t o1[4], o2[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const v2h qv = as_v2h(p[i]) + (v2h){(_Float16)-1056.0f, (_Float16)-1056.0f};
+                        const v2h bh = qv * sv;
+                        o1[i] = as_u32(bh);
+                        o2[i] = as_u32(__builtin_elementwise_fma(qv, sv, -bh));
+                    }
+                    const v8h b1 = to_v8h(o1[0], o1[1], o1[2], o1[3]);
+                    const v8h b2 = to_v8h(o2[0], o2[1], o2[2], o2[3]);
 #pragma unroll
                     for (int rt = 0; rt < RT; ++rt) {
                         if (rt < nrt) {
-                            xa[rt] = *reinterpret_cast<const v4h *>(&As.v[0][16 * rt + c][kl]);
-                            xb[rt] = *reinterpret_cast<const v4h *>(&As.v[1][16 * rt + c][kl]);
-                        }
-                    }
-                    const int sb = 8 * hn + 2 * Q + is;  // sub-block scale index
-#pragma unroll
-                    for (int ct = 0; ct < ORN_FDN; ++ct) {
-                        const uint32_t ql = (Q & 1) ? qa[hn][is][ct][1] : qa[hn][is][ct][0];
-                        // bytes 0..63: low 4 bits from ql, high 2 from qh
-                        const uint32_t qv = ((ql >> (4 * (Q >> 1))) & 0x0F0F0F0Fu) |
-                                            (((qa[hn][is][ct][2] >> (2 * Q)) & 0x03030303u) << 4);
-                        // fp16 pairs (1024 + byte) in the order (b0, b2), (b1, b3),
-                        // then - 1056: q - 32 exactly
-                        const v2h off = {(_Float16)-1056.0f, (_Float16)-1056.0f};
-                        const uint32_t p0 = as_u32(as_v2h(__builtin_amdgcn_perm(0x64646464u, qv, 0x04020400u)) + off);
-                        const uint32_t p1 = as_u32(as_v2h(__builtin_amdgcn_perm(0x64646464u, qv, 0x04030401u)) + off);
-                        const v4h bq = __builtin_bit_cast(v4h, make_uint2(p0, p1));
-                        const int scv = (int)(int8_t)((scs[ct][sb >> 2] >> (8 * (sb & 3))) & 0xFFu);
-                        const float dsc = d[ct] * (float)scv;  // exact: 11-bit d times 8-bit sc
-#pragma unroll
-                        for (int rt = 0; rt < RT; ++rt) {
-                            if (rt < nrt) {
-                                v4f P = {0.0f, 0.0f, 0.0f, 0.0f};
-                                P = __builtin_amdgcn_mfma_f32_16x16x16f16(xa[rt], bq, P, 0, 0, 0);
-                                P = __builtin_amdgcn_mfma_f32_16x16x16f16(xb[rt], bq, P, 0, 0, 0);
-#pragma unroll
-                                for (int r = 0; r < 4; ++r) acc[rt][ct][r] = fmaf(dsc, P[r], acc[rt][ct][r]);
-                            }
+                            ps[rt][ct] = mfma(xa[rt], b1, ps[rt][ct]);
+                            ps[rt][ct] = mfma(xb[rt], b1, ps[rt][ct]);
+                            ps[rt][ct] = mfma(xa[rt], b2, ps[rt][ct]);
                         }
                     }
                 }
             }
         }
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < ORN_FDN; ++ct)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[rt][ct][r] = fmaf(d[ct], ps[rt][ct][r], acc[rt][ct][r]);
     }
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
