@@ -114,3 +114,26 @@ def test_q6k_prefill_layout_rebuilds_weights(L):
             q = int(qb6[kt, b, nt // 4, 16 * g + c, nt % 4, e]) - 32
             W[k, n] = d2[b, k] * (sc4[kt, b, nt, kk] * q)
     assert np.array_equal(W.astype(np.float32).view(np.uint32), ref.view(np.uint32))
+
+
+def test_q6_wide_operand_split_is_exact():
+    """The down kernels' operand for Q6_K sub-scales above 64 (mfma_ops.h
+    q6_b2, expert_file.hip k_dn_file): b1 = fp16(sc * q) rounded to nearest
+    even, b2 = sc * q - b1 from one fma.  Over every int8 scale and every
+    q - 32 in [-32, 31]: b2 is an integer of magnitude <= 1 (exact in fp16),
+    b1 + b2 == sc * q, and b2 == 0 exactly where |sc * q| <= 2048 or the
+    product is even; the products that need b2 occur (so a kernel that
+    dropped it would be wrong on real scales)."""
+    sc = np.arange(-128, 128, dtype=np.int64)[:, None]
+    q = np.arange(-32, 32, dtype=np.int64)[None, :]
+    exact = sc * q
+    # fp16 products of two fp16 integers: one rounding of the exact value
+    b1 = (sc.astype(np.float16) * q.astype(np.float16)).astype(np.float64)
+    assert np.all(np.isfinite(b1))
+    b2 = exact - b1
+    assert np.all(b2 == np.round(b2)) and np.abs(b2).max() <= 1
+    assert np.all(b2.astype(np.float16).astype(np.float64) == b2)
+    assert np.all(b1 + b2 == exact)
+    small = (np.abs(exact) <= 2048) | (exact % 2 == 0)
+    assert np.all(b2[small] == 0) and np.all(b2[~small] != 0)
+    assert (~small).sum() > 0 and np.abs(sc).max() == 128
