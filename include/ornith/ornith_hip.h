@@ -367,7 +367,10 @@ int gpu_moe_forward(gpu_context *ctx, ornith_moe_store *store, int layer, const 
  * with the needed size in gpu_last_error(); ORN_MOE_GRAPH is refused
  * (instantiating a graph allocates).  Every call on one GPU shares that
  * GPU's scratch: calls that overlap on one GPU (two contexts, or
- * ORN_MOE_ASYNC calls on different streams) race. */
+ * ORN_MOE_ASYNC calls on different streams) race.  After such a call,
+ * gpu_moe_last_logits and gpu_moe_last_stats on this context read that
+ * scratch: they report this call only until the next noalloc call on the
+ * same GPU, from any context. */
 #define ORN_NOALLOC_SCRATCH_BYTES (32u << 20)
 int gpu_moe_forward_noalloc(gpu_context *ctx, ornith_moe_store *store, int layer,
                             const gpu_buffer *x, int n_tokens, const gpu_buffer *resid,
@@ -387,12 +390,15 @@ int gpu_moe_forward_stack(gpu_context *ctx, ornith_moe_store *store, int first_l
  * ran on (the sums of model.c:1017-1025 plus the bias).  Copies
  * min(max_floats, T*E) floats to the host array `out` and stores T*E in
  * *n_floats (0 before any forward).  No reference counterpart: a test and
- * measurement helper like gpu_moe_last_stats. */
+ * measurement helper like gpu_moe_last_stats.  After gpu_moe_forward_noalloc
+ * the values live in the device's shared scratch and are valid only until
+ * the next noalloc call on that GPU. */
 int gpu_moe_last_logits(gpu_context *ctx, float *out, size_t max_floats, size_t *n_floats);
 
 /* Counters of the last forward: number of active expert slots (incl. the
  * shared expert), token rows, and tokens whose top-k ran the literal
- * exchange selection (tied or non-finite logits among the top k+1). */
+ * exchange selection (tied or non-finite logits among the top k+1).  After
+ * gpu_moe_forward_noalloc: valid until the next noalloc call on that GPU. */
 int gpu_moe_last_stats(gpu_context *ctx, int *n_slots, int *n_rows, int *n_literal);
 
 /* ---------------------------------------------------------------------------

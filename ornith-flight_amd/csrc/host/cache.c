@@ -68,7 +68,12 @@ struct orn_cache {
     int n_loads[2];
     hipStream_t copy;
     hipEvent_t pf_ev;
-    int pf_pending;
+    /* pf_pending: the compute stream has not yet been made to wait for the
+     * last prefetch batch.  pf_list_busy: that batch's load list (list 1,
+     * read by its gather kernel when the kernel runs) may still be unread;
+     * cleared only once the host has waited for pf_ev (or quiesced the copy
+     * stream), never by the compute stream's wait. */
+    int pf_pending, pf_list_busy;
     ornith_moe_cache_stats stats;
     size_t dev_bytes, host_bytes;
 };
@@ -234,8 +239,9 @@ void orn_cache_slot_arrays(orn_cache *c, ornk_moe_args *a)
 /* Before the host tier of a layer is rewritten: no copy may still read it. */
 int orn_cache_quiesce(gpu_context *ctx, orn_cache *c)
 {
-    c->pf_pending = 0;
-    return orn_hip_check(ctx, hipStreamSynchronize(c->copy), "expert cache: copy stream");
+    const int rc = orn_hip_check(ctx, hipStreamSynchronize(c->copy), "expert cache: copy stream");
+    if (!rc) c->pf_pending = c->pf_list_busy = 0;
+    return rc;
 }
 
 /* Experts [first, first + n) of a layer changed in the host tier: their
@@ -431,10 +437,14 @@ int orn_cache_prefetch(gpu_context *ctx, orn_cache *c, int layer, const int *exp
 {
     int rc = check_ids(ctx, c, layer, experts, n);
     if (rc) return rc;
-    /* the previous prefetch batch's list must have been read */
-    if (c->pf_pending &&
-        (rc = orn_hip_check(ctx, hipEventSynchronize(c->pf_ev), "expert cache: prefetch")))
-        return rc;
+    /* the previous prefetch batch's list must have been read, whether or not
+     * a forward has joined that batch since (a join only orders the compute
+     * stream; the gather may still be queued on the copy stream) */
+    if (c->pf_list_busy) {
+        if ((rc = orn_hip_check(ctx, hipEventSynchronize(c->pf_ev), "expert cache: prefetch")))
+            return rc;
+        c->pf_list_busy = 0;
+    }
     memset(c->slot_need, 0, (size_t)c->C);
     for (int i = 0; i < n; ++i) {
         const int key = layer * c->E1 + experts[i];
@@ -453,9 +463,17 @@ int orn_cache_prefetch(gpu_context *ctx, orn_cache *c, int layer, const int *exp
     }
     memset(c->slot_need, 0, (size_t)c->C);
     if (c->n_loads[1] == 0) return ORN_OK;
-    if ((rc = flush_loads(ctx, c, c->copy, 1))) return rc;
-    rc = orn_hip_check(ctx, hipEventRecord(c->pf_ev, c->copy), "expert cache: prefetch event");
-    if (!rc) c->pf_pending = 1;
+    c->pf_list_busy = 1; /* list 1 is read by the gather when it runs */
+    rc = flush_loads(ctx, c, c->copy, 1);
+    if (!rc)
+        rc = orn_hip_check(ctx, hipEventRecord(c->pf_ev, c->copy), "expert cache: prefetch event");
+    if (!rc) {
+        c->pf_pending = 1;
+    } else {
+        /* no event covers what was enqueued: wait for the copy stream */
+        hipStreamSynchronize(c->copy);
+        c->pf_list_busy = 0;
+    }
     return rc;
 }
 

@@ -28,6 +28,10 @@ static int whole_blocks(int type, uint64_t n)
     return !(type == ORN_TYPE_Q4_K || type == ORN_TYPE_Q6_K) || n % ORN_QK_K == 0;
 }
 
+/* Element counts whose byte sizes (input and fp32 output, padded) cannot
+ * wrap a size_t: a larger tensor could never be resident anyway. */
+static int fits(uint64_t n) { return n <= (uint64_t)(SIZE_MAX / 16); }
+
 static uint64_t slice_experts(const orn_tensor_info *t)
 {
     if (t->n_dims == 0 || t->n_dims > 4) return 0;
@@ -40,6 +44,7 @@ bool gpu_dequantize_tensor_from_buf(gpu_context *ctx, const void *data,
     if (!ctx || !data || !tensor || !output) return false;
     if (!supported(tensor->type)) return false;
     const uint64_t n = tensor->n_elems;
+    if (!fits(n)) return false;
     const size_t in_bytes = orn_row_size(tensor->type, n);
     const uint64_t n_out = written_elems(tensor->type, n);
     if (n_out == 0) return true;
@@ -69,6 +74,7 @@ bool gpu_dequantize_expert_slice_from_buf(gpu_context *ctx, const void *data,
     if (E == 0) return false;
     if (!supported(tensor->type)) return false;
     const uint64_t n = tensor->n_elems;
+    if (!fits(n)) return false;
     /* A partial trailing super-block would be read past the tensor's bytes
      * (undefined in the reference); refuse instead of touching it. */
     if (!whole_blocks(tensor->type, n)) return false;

@@ -280,6 +280,10 @@ static int parse(orn_gguf *g, cursor *c)
         }
         if (!rd(c, &ty, 4) || !rd(c, &t->offset, 8)) return 0;
         t->type = (int)ty;
+        /* F32 / F16 byte sizes are 4n / 2n: refuse counts where that wraps
+         * (the wrapped size would pass the checks against the file size) */
+        if ((ty == ORN_TYPE_F32 && n > SIZE_MAX / 4) || (ty == ORN_TYPE_F16 && n > SIZE_MAX / 2))
+            return fail(c, "tensor byte size overflows");
         t->n_elems = (size_t)n;
         t->size_bytes = orn_row_size((int)ty, n);
     }

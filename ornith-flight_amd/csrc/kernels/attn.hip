@@ -38,9 +38,13 @@ __global__ void k_rope(float *Q, float *K, int head_dim, int n_q, int n_k, int r
 }
 
 // attention.metal:17-68: out[r][c] = sum_t e^(s_rt) V[t][c] / sum_t e^(s_rt),
-// s_rt = (Q[r] . K[t]) * scale, every key for every query (no mask).  The
-// exponent is taken relative to the running row maximum (online softmax),
-// which gives the same quotient wherever the unshifted one is finite.
+// s_rt = (Q[r] . K[t]) * scale, every key for every query (no mask), where
+// the shader divides only when the sum exceeds 1e-10 and otherwise returns
+// the unnormalised sum; so does this kernel.  The exponent is taken relative
+// to the running row maximum m (online softmax): the unshifted sums are
+// e^m times the shifted ones.  Where the shader's unshifted e^s overflows
+// (scores above ~88, which make its output Inf or NaN) this kernel still
+// returns the softmax.
 //
 // Work group: 256 threads, ATT_R = 16 query rows; keys in tiles of ATT_T =
 // 16 staged in LDS (K with a padded row stride, so the 16 keys a row group
@@ -106,11 +110,14 @@ __global__ __launch_bounds__(256) void k_attention(float *out, const float *Q, c
         }
     }
     if (row0 + r >= seq) return;
-    const float inv = 1.0f / l;
+    // attention.metal:60-62: normalise only when the unshifted sum e^m * l
+    // exceeds 1e-10; else the unnormalised sum e^m * acc
+    const float em = expf(m);
+    const float f = em * l > 1e-10f ? 1.0f / l : em;
 #pragma unroll
     for (int c = 0; c < ATT_MAXD / 16; ++c) {
         const int col = j + 16 * c;
-        if (col < hd) out[(size_t)(row0 + r) * hd + col] = acc[c] * inv;
+        if (col < hd) out[(size_t)(row0 + r) * hd + col] = acc[c] * f;
     }
 }
 

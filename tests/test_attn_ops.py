@@ -174,6 +174,32 @@ def test_gpu_attention_large_scores(om, ctx):
 
 
 @pytest.mark.gpu
+def test_gpu_attention_tiny_sums_unnormalised(om, ctx):
+    """Every score of a row near -35: the shader's sum of e^s stays below
+    1e-10, so it skips the division and returns the weighted sum itself
+    (attention.metal:60-62); rows with ordinary scores are normalised."""
+    rng = np.random.default_rng(9)
+    seq, hd = 40, 64
+    u = rng.standard_normal(hd)
+    u /= np.linalg.norm(u)
+    Q = f32(rng.standard_normal((seq, hd)) * 0.05)
+    Q[:20] += f32(u * 14.0)  # rows 0..19: scores ~ -35
+    K = f32(-u * 20.0 + rng.standard_normal((seq, hd)) * 0.02)
+    V = f32(rng.standard_normal((seq, hd)))
+    ref = O.attention(Q, K, V)
+    assert np.abs(ref[:20]).max() < 1e-12 < np.abs(ref[20:]).max()
+    bufs = [ctx.upload(a) for a in (Q, K, V)]
+    ob = ctx.alloc(Q.nbytes)
+    om.lib().gpu_attention(ctx.ptr, ob.ptr, bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, seq, hd)
+    got = ctx.download(ob, np.float32, Q.shape)
+    for rows in (slice(0, 20), slice(20, seq)):
+        err = np.abs(got[rows] - ref[rows]).max() / np.abs(ref[rows]).max()
+        assert err < 1e-5, (rows, err)
+    for b in bufs + [ob]:
+        b.free()
+
+
+@pytest.mark.gpu
 def test_gpu_attention_refuses_wide_heads(om, ctx):
     seq, hd = 4, 320
     bufs = [ctx.upload(np.ones((seq, hd), np.float32)) for _ in range(4)]

@@ -352,9 +352,12 @@ def test_refuses_malformed(om, tmpfile):
         "unknown array element type": header(0, 1) + s("k") + struct.pack("<IIQ", 9, 77, 1),
         "truncated": header(1, 0) + s("t") + struct.pack("<I", 2) + struct.pack("<Q", 4),
         "overflows": header(1, 0) + tinfo("t", [2**32, 2**32, 2], 0, 0),
+        # element counts that fit, byte sizes that wrap to 4 and 2 bytes
+        "byte size overflows": header(1, 0) + tinfo("t", [2**62 + 1], 0, 0),
+        "byte size overflows ": header(1, 0) + tinfo("t", [2**63 + 1], 1, 0),
     }
     for why, data in cases.items():
-        with pytest.raises(ValueError, match=why):
+        with pytest.raises(ValueError, match=why.strip()):
             om.GGUF(tmpfile(data))
 
 

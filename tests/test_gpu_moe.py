@@ -1,8 +1,13 @@
 """GPU parity tests of the routed-MoE layer against the oracle.
 
-Bar (BASELINE north_star): top-k expert indices bit-exact; layer outputs with
-max_i|y_i - y_ref_i| / max_i|y_ref_i| <= 1e-3 per token row (fp32
-accumulate); dequantized weights bit-exact (test_gpu_backend.py).
+Bar: top-k expert indices bit-exact; layer outputs with
+max_i|y_i - y_ref_i| / max_i|y_ref_i| <= 1e-5 per token row; dequantized
+weights bit-exact (test_gpu_backend.py).  The north star allows 1e-3, but a
+kernel that dropped one term of its arithmetic (an activation lo plane, the
+mins lo term, the Q6_K remainder operand) would still pass 1e-3 at the
+Ornith shape; tests/test_mfma_emulation.py shows each such drop moves the
+output by 7e-5 or more, while the shipped arithmetic sits ~1e-6 from the
+oracle (whose own fp32 chains are ~1e-6 from exact products).
 
 Oracle sizes: the oracle runs every token at small shapes and at the Ornith
 shape for T <= 16; for T = 256 / 2048 it runs a stated subset of tokens
@@ -19,7 +24,7 @@ from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
 
-TOL = 1e-3
+TOL = 1e-5
 
 
 def say(*a):

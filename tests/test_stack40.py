@@ -12,7 +12,8 @@ gpu_moe_forward_stack (x <- x + MoE_l(rmsnorm(x)), model.c:992-1144 per
 layer) and checks that it equals the chain of 40 single-layer forwards bit
 for bit, and teacher-forces layers 0, 19 and 39 against the oracle
 (orc_moe_layer with the rmsnorm and the residual): indices exact, outputs
-within 1e-3 per row (measured ~1e-6).
+within 1e-5 per row (measured ~1e-6; the bar that catches a dropped term
+of the MFMA arithmetic, tests/test_mfma_emulation.py).
 """
 import sys
 
@@ -24,7 +25,7 @@ from oracle import oracle as O
 pytestmark = pytest.mark.gpu
 
 D, H, E, K = 2048, 512, 256, 8
-TOL = 1e-3
+TOL = 1e-5
 
 
 def say(*a):

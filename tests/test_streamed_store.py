@@ -4,6 +4,10 @@ device slots with the reference's tiering policy (memory.c:79-421: hot-store
 pins, LRU eviction, prefetch).
 
 Pinned by:
+  * the oracle: every streamed forward against orc_moe_layer (the
+    reference's MoE block restated, engine/src/model.c:992-1144) on the same
+    bytes -- indices exact, outputs within 1e-5 per row -- including the
+    Ornith shape and the file orientation;
   * equality: every forward of a streamed store equals the same forward of a
     resident store holding the same bytes, bit for bit (outputs, indices,
     weights, logits) -- decode, MFMA and file-orientation paths, layers
@@ -14,14 +18,20 @@ Pinned by:
     then ascending expert id) predicts hits, misses and evictions exactly
     from the resident store's routing;
   * prefetch and pin semantics (prefetched experts are hits, pinned ones are
-    never evicted) and the refusals (too few slots, ORN_MOE_GRAPH).
+    never evicted) and the refusals (too few slots, ORN_MOE_GRAPH);
+  * a prefetch issued while an asynchronous forward that joined the previous
+    prefetch is still in flight (the load list must not be rewritten before
+    the earlier gather has read it).
 """
 import sys
 
 import numpy as np
 import pytest
 
+from oracle import oracle as O
+
 pytestmark = pytest.mark.gpu
+TOL = 1e-5  # the parity bar of the resident forwards (tests/test_gpu_moe.py)
 
 
 def say(*a):
@@ -41,6 +51,28 @@ def ctx(om):
     c = om.Context()
     yield c
     c.close()
+
+
+def row_err(out, ref):
+    scale = np.abs(ref).max(axis=1)
+    assert np.all(scale > 0) and np.all(np.isfinite(out))
+    return np.abs(out.astype(np.float64) - ref).max(axis=1) / scale
+
+
+def check_oracle(syn, x, k, got, norm_w=None, layout=None):
+    """A streamed forward's (out, idx, w, ...) against the oracle."""
+    D, E = x.shape[1], syn.E
+    H = syn.nb * 256 // D
+    kw = {} if layout is None else {"layout": layout}
+    ref, ridx, rw = O.moe_layer(D=D, H=H, E=E, k=k, x=x, router_W=syn.router, bias=syn.bias,
+                                norm_w=norm_w, gate=syn.routed("gate"), up=syn.routed("up"),
+                                down=syn.routed("down"), sh_gate=syn.shared("gate"),
+                                sh_up=syn.shared("up"), sh_down=syn.shared("down"), **kw)
+    assert np.array_equal(got[1], ridx)
+    assert np.allclose(got[2], rw, rtol=1e-5, atol=1e-7)
+    err = row_err(got[0], ref).max()
+    assert err <= TOL, err
+    return err
 
 
 def fwd(ctx, st, layer, x, k, flags=0):
@@ -94,8 +126,11 @@ def needed(idx, w, E, has_shared=True):
 
 
 def make_pair(om, ctx, L, D, H, E, k, slots, seed=5, prefill=True):
+    """A resident and a streamed store of the same L layers, plus the host
+    copies (syns, norm weights) for the oracle."""
     res = om.Store(ctx, L, D, H, E, k, True, prefill_layout=prefill)
     stm = om.Store(ctx, L, D, H, E, k, True, prefill_layout=prefill, cache_slots=slots)
+    syns, norms = [], []
     for l in range(L):
         syn = om.SyntheticLayer(seed, l, D, H, E, True, 1.1 if l == 1 else 0.0)
         res.load_layer(l, syn)
@@ -103,13 +138,16 @@ def make_pair(om, ctx, L, D, H, E, k, slots, seed=5, prefill=True):
         nw = np.random.default_rng(l).uniform(0.5, 1.5, D).astype(np.float32)
         res.set_norm(l, nw)
         stm.set_norm(l, nw)
-    return res, stm
+        syns.append(syn)
+        norms.append(nw)
+    return res, stm, syns, norms
 
 
 def test_streamed_equals_resident_and_policy(om, ctx):
     L, D, H, E, k, C = 3, 256, 256, 16, 8, 20
-    res, stm = make_pair(om, ctx, L, D, H, E, k, C)
+    res, stm, syns, norms = make_pair(om, ctx, L, D, H, E, k, C)
     model = CacheModel(C)
+    worst = 0.0
     try:
         st0 = stm.cache_stats()
         assert st0["slots"] == C and st0["resident"] == 0 and st0["host_bytes"] > 0
@@ -120,6 +158,8 @@ def test_streamed_equals_resident_and_policy(om, ctx):
             x = rng.standard_normal((T, D)).astype(np.float32)
             a = fwd(ctx, stm, l, x, k, flags)
             b = fwd(ctx, res, l, x, k, flags)
+            worst = max(worst, check_oracle(syns[l], x, k, a,
+                                            norm_w=norms[l] if flags & om.MOE_NORM else None))
             for u, v in zip(a, b):
                 assert np.array_equal(u.view(np.uint32), v.view(np.uint32)), (i, l, T)
             model.forward(l, needed(b[1], b[2], E))
@@ -127,8 +167,9 @@ def test_streamed_equals_resident_and_policy(om, ctx):
             assert (s["hits"], s["misses"], s["evictions"]) == \
                 (model.hits, model.misses, model.evictions), (i, s, vars(model))
         s = stm.cache_stats()
-        say(f"  {len(steps)} forwards bit-identical; hits {s['hits']} misses {s['misses']} "
-            f"evictions {s['evictions']} uploaded {s['bytes_uploaded'] / 1e6:.1f} MB")
+        say(f"  {len(steps)} forwards bit-identical, max row err vs oracle {worst:.2e}; hits "
+            f"{s['hits']} misses {s['misses']} evictions {s['evictions']} uploaded "
+            f"{s['bytes_uploaded'] / 1e6:.1f} MB")
         assert s["evictions"] > 0 and s["hits"] > 0
         # the host tier holds exactly what was uploaded
         syn = om.SyntheticLayer(5, 2, D, H, E, True)
@@ -140,7 +181,7 @@ def test_streamed_equals_resident_and_policy(om, ctx):
 
 def test_prefetch_and_pin(om, ctx):
     L, D, H, E, k, C = 3, 256, 256, 16, 8, 12
-    res, stm = make_pair(om, ctx, L, D, H, E, k, C, prefill=False)
+    res, stm, syns, _ = make_pair(om, ctx, L, D, H, E, k, C, prefill=False)
     try:
         rng = np.random.default_rng(2)
         x = rng.standard_normal((1, D)).astype(np.float32)
@@ -150,6 +191,7 @@ def test_prefetch_and_pin(om, ctx):
         s = stm.cache_stats()
         assert s["prefetches"] == len(want) and s["resident"] == len(want)
         a = fwd(ctx, stm, 1, x, k)
+        check_oracle(syns[1], x, k, a)
         for u, v in zip(a, b):
             assert np.array_equal(u.view(np.uint32), v.view(np.uint32))
         s = stm.cache_stats(reset=True)
@@ -161,6 +203,7 @@ def test_prefetch_and_pin(om, ctx):
             l = 1 + i % 2
             x = rng.standard_normal((1, D)).astype(np.float32)
             a, b = fwd(ctx, stm, l, x, k), fwd(ctx, res, l, x, k)
+            check_oracle(syns[l], x, k, a)
             assert np.array_equal(a[0].view(np.uint32), b[0].view(np.uint32))
         assert stm.cache_stats()["evictions"] > 0
         stm.cache_stats(reset=True)
@@ -221,14 +264,17 @@ def test_streamed_file_layout_and_device_fill(om, ctx):
             stm.fill_synthetic(l, 77 + l)
         syn = om.SyntheticLayer(77, 0, D, H, E, True)
         assert np.array_equal(stm.get_experts(0, om.MAT_UP, 0, E + 1), syn.up)
-        del syn
         rng = np.random.default_rng(4)
+        syns = [syn, om.SyntheticLayer(78, 1, D, H, E, True)]
+        worst = 0.0
         for i, (l, T) in enumerate([(0, 1), (1, 4), (0, 4), (1, 1), (0, 1)]):
             x = rng.standard_normal((T, D)).astype(np.float32)
             a, b = fwd(ctx, stm, l, x, k), fwd(ctx, res, l, x, k)
+            worst = max(worst, check_oracle(syns[l], x, k, a))
             for u, v in zip(a, b):
                 assert np.array_equal(u.view(np.uint32), v.view(np.uint32)), (i, l, T)
-        say(f"  Ornith shape, 48 slots: {stm.cache_stats()}")
+        del syns
+        say(f"  Ornith shape, 48 slots: max row err vs oracle {worst:.2e}; {stm.cache_stats()}")
         syn = om.SyntheticLayer(31, 0, 256, 256, 16, True)
         for st in (fres, fstm):
             for name, m in (("gate", om.MAT_GATE), ("up", om.MAT_UP), ("down", om.MAT_DOWN)):
@@ -237,8 +283,56 @@ def test_streamed_file_layout_and_device_fill(om, ctx):
         for T in (1, 2, 1):
             x = rng.standard_normal((T, 256)).astype(np.float32)
             a, b = fwd(ctx, fstm, 0, x, k), fwd(ctx, fres, 0, x, k)
+            check_oracle(syn, x, k, a, layout=O.LAYOUT_FILE)
             for u, v in zip(a, b):
                 assert np.array_equal(u.view(np.uint32), v.view(np.uint32)), T
     finally:
         for s in (res, stm, fres, fstm):
             s.close()
+
+
+def test_prefetch_during_async_forward(om, ctx):
+    """Prefetch, an asynchronous forward that joins it, a second prefetch
+    issued before that forward has finished, then a forward of the second
+    batch: the second prefetch must not rewrite the first batch's load list
+    before the first gather has read it (else slots would hold the wrong
+    experts while the cache maps them as correct).  Every forward against
+    the resident store bit for bit and the oracle; then two more forwards
+    per batch, which reuse the prefetched slots."""
+    L, D, H, E, k, C = 2, 256, 256, 16, 4, 20  # room for both batches: no eviction
+    res, stm, syns, _ = make_pair(om, ctx, L, D, H, E, k, C, seed=8)
+    try:
+        rng = np.random.default_rng(6)
+        xs = [rng.standard_normal((2, D)).astype(np.float32) for _ in range(2)]
+        want = [needed(*fwd(ctx, res, l, xs[l], k)[1:3], E) for l in range(2)]
+        assert len(want[0]) + len(want[1]) <= C
+        xb = ctx.upload(xs[0])
+        ob, ib, wb = ctx.alloc(xs[0].nbytes), ctx.alloc(2 * k * 4), ctx.alloc(2 * k * 4)
+        try:
+            stm.prefetch(0, want[0])
+            stm.forward(0, xb, 2, ob, idx=ib, w=wb, flags=om.MOE_ASYNC)
+            stm.prefetch(1, want[1])  # while the forward above may still run
+            second = fwd(ctx, stm, 1, xs[1], k)
+            ctx.sync()
+            first = (ctx.download(ob, np.float32, xs[0].shape),
+                     ctx.download(ib, np.uint32, (2, k)), ctx.download(wb, np.float32, (2, k)))
+        finally:
+            for b in (xb, ob, ib, wb):
+                b.free()
+        s = stm.cache_stats()
+        say(f"  prefetch/async/prefetch: {s}")
+        assert s["prefetch_hits"] == len(want[0]) + len(want[1]) and s["misses"] == 0
+        for l, got in ((0, first), (1, second)):
+            check_oracle(syns[l], xs[l], k, got)
+            ref = fwd(ctx, res, l, xs[l], k)
+            for u, v in zip(got[:3], ref[:3]):
+                assert np.array_equal(u.view(np.uint32), v.view(np.uint32)), l
+        for _ in range(2):
+            for l in range(2):
+                a, b = fwd(ctx, stm, l, xs[l], k), fwd(ctx, res, l, xs[l], k)
+                for u, v in zip(a, b):
+                    assert np.array_equal(u.view(np.uint32), v.view(np.uint32)), l
+        assert stm.cache_stats()["misses"] == 0
+    finally:
+        res.close()
+        stm.close()

@@ -4,7 +4,9 @@ the device's fixed scratch array instead of an allocated workspace.
 It runs the same kernels with the same plan as gpu_moe_forward, so its
 outputs, indices and weights must equal gpu_moe_forward's bit for bit.  Two
 calls in a row, the second with a smaller batch, check that the scratch's
-leftover contents from the first call do not leak into the second.
+leftover contents from the first call do not leak into the second.  Batches
+of more than 16 tokens (separate selection and dispatch launches) and a
+file-orientation store are covered too.
 """
 import sys
 
@@ -60,9 +62,10 @@ def test_noalloc_equals_forward(om, ctx, shape, flags):
     store = om.Store(ctx, 1, D, H, E, k, True)
     try:
         store.fill_synthetic(0, 77)
-        # two calls in a row: the second is smaller and follows the first
-        # with the scratch still holding the first call's buffers
-        for T in (16, 3):
+        # calls in a row, each smaller than the one before, with the scratch
+        # still holding the previous call's buffers (40 tokens: selection and
+        # dispatch as two launches)
+        for T in (40, 16, 3):
             x = act(om, 900 + T, T, D)
             resid = act(om, 950 + T, T, D) if flags else None
             got = call(om, ctx, store, x, k, True, flags, resid)
@@ -76,6 +79,27 @@ def test_noalloc_equals_forward(om, ctx, shape, flags):
         ref = call(om, ctx, store, x, k, False, flags)
         for g, r in zip(got, ref):
             assert np.array_equal(g.view(np.uint32), r.view(np.uint32))
+    finally:
+        store.close()
+
+
+def test_noalloc_file_layout(om, ctx):
+    """A file-orientation store (the kernels real GGUF files run): the same
+    bit-for-bit equality, 40 then 16 then 3 tokens."""
+    D, H, E, k = 256, 256, 16, 8
+    syn = om.SyntheticLayer(41, 0, D, H, E, True)
+    store = om.Store(ctx, 1, D, H, E, k, True, prefill_layout=False, file_layout=True)
+    try:
+        for name, m in (("gate", om.MAT_GATE), ("up", om.MAT_UP), ("down", om.MAT_DOWN)):
+            store.set_experts(0, m, 0, getattr(syn, name), E + 1)
+        store.set_router(0, np.ascontiguousarray(syn.router.T))
+        for T in (40, 16, 3):
+            x = act(om, 700 + T, T, D)
+            got = call(om, ctx, store, x, k, True)
+            ref = call(om, ctx, store, x, k, False)
+            for g, r, what in zip(got, ref, ("out", "idx", "w")):
+                assert np.array_equal(g.view(np.uint32), r.view(np.uint32)), (T, what)
+            say(f"  file layout T={T}: bit-identical to gpu_moe_forward")
     finally:
         store.close()
 
