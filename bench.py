@@ -401,6 +401,43 @@ def measure_attention(ctx):
     return res
 
 
+def measure_lm_head(ctx):
+    """gpu_matmul at the shape of the reference's LM head (model.c:1219-1231:
+    logits[i] = sum_d x[d] * W[d][i], D = 2048, vocab 248,320 from
+    model.c:120) for one token and for 16 (M = 1, 16): an fp32 B of 2.03 GB
+    streamed once per call (per 16 rows), bit-identical to the CPU backend's
+    sequential sums.  HBM-bound at M = 1: (K*N + M*K + M*N) * 4 bytes per call
+    against 8 TB/s; at M = 16 also 2*M*N*K flops against the fp32 vector
+    peak (157.3 TFLOP/s).  Synchronous calls, as the API is."""
+    K, N = 2048, 248320
+    L = om.lib()
+    Bb = ctx.upload(np.full((K, N), 0.5, np.float32))
+    res = {}
+    for M in (1, 16):
+        Ab = ctx.upload(np.full((M, K), 0.25, np.float32))
+        Cb = ctx.alloc(M * N * 4)
+        L.gpu_matmul(ctx.ptr, Cb.ptr, Ab.ptr, Bb.ptr, M, N, K, 0, 0)
+        reps = 10
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            L.gpu_matmul(ctx.ptr, Cb.ptr, Ab.ptr, Bb.ptr, M, N, K, 0, 0)
+        dt = (time.perf_counter() - t0) / reps
+        moved = 4 * (K * N + M * K + M * N)
+        out = {"ms": round(dt * 1e3, 3), "tokens_per_s": round(M / dt, 1),
+               "hbm": {"achieved": round(moved / dt / 1e9, 1), "peak": 8000.0, "unit": "GB/s",
+                       "frac": round(moved / dt / 8e12, 4), "bytes_per_call": moved}}
+        if M > 1:
+            tf = 2.0 * M * N * K / dt / 1e12
+            out["valu"] = {"achieved": round(tf, 2), "peak": 157.3, "unit": "TFLOP/s",
+                           "frac": round(tf / 157.3, 4)}
+        res[f"lm_head_m{M}_k{K}_n{N}"] = out
+        Ab.free()
+        Cb.free()
+    Bb.free()
+    log("lm_head", res)
+    return res
+
+
 def measure_dequant(ctx):
     """The device dequant API (gpu_dequantize_tensor_buf, gguf.c:605-638) on
     one layer's expert tensor: 256 experts x 2048 x 512 weights, Q4_K (the
@@ -460,7 +497,7 @@ EXTRA_CONFIGS = (("decode_t1", 0, 1), ("prefill_t2048", 0, 2048), ("zipf_t256", 
 EXTRA_LABELS = [c[0] for c in EXTRA_CONFIGS] + ["valu_t1", "valu_t16", "valu_t2048", "file_t1",
                                                  "file_t16", "file_t2048", "q6wide_t1",
                                                  "q6wide_t16", "q6wide_t2048", "stack40",
-                                                 "streamed", "attention", "dequant"]
+                                                 "streamed", "attention", "dequant", "lm_head"]
 
 
 def headline(ctx, store, args, read_gbs):
@@ -621,6 +658,8 @@ def main():
         result.setdefault("configs", {}).update(measure_attention(ctx))
     if not args.no_extra and want("dequant"):
         result.setdefault("configs", {}).update(measure_dequant(ctx))
+    if not args.no_extra and want("lm_head"):
+        result.setdefault("configs", {}).update(measure_lm_head(ctx))
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_budget)
         if cpu_contig:

@@ -15,18 +15,81 @@ __global__ void k_fill(float *p, float v, size_t n)
     for (; i < n; i += stride) p[i] = v;
 }
 
-// gpu.c:104-115: C[i][j] = sum_k A[i][k] * B[k][j], k ascending from 0.0f.
-// One thread per output keeps the reference's summation order, so results
-// are bit-identical to the CPU backend.  B reads are coalesced over j.
-__global__ void k_matmul(float *C, const float *A, const float *B, int M, int N, int K)
+// gpu.c:104-115: C[i][j] = sum_k A[i][k] * B[k][j], a sequential fp32 sum
+// from 0.0f with k ascending and separately rounded products, so results are
+// bit-identical to the CPU backend.  A thread owns NC adjacent columns for MT
+// rows (a block-row of A, MT <= 16), so every B element is read once per MT
+// rows: the kernel streams B, which is what bounds it at small M (an LM head
+// reads K*N floats per token), and with NC = 4 a lane's B load is one 16-byte
+// word.  A is staged in LDS in chunks of MM_KC columns (every lane reads the
+// same words: broadcast); the MM_U B loads of a turn are issued before their
+// products.  Rows past M are zero in LDS and never stored.
+constexpr int MM_KC = 256, MM_U = 8;
+
+template <int NC>
+struct ColVec;
+template <>
+struct ColVec<1> {
+    typedef float T;
+    static __device__ __forceinline__ float at(float v, int) { return v; }
+};
+template <>
+struct ColVec<4> {
+    typedef v4f T;
+    static __device__ __forceinline__ float at(v4f v, int c) { return v[c]; }
+};
+
+template <int MT, int NC>
+__global__ void __launch_bounds__(256) k_matmul(float *C, const float *A, const float *B, int M,
+                                                int N, int K)
 {
-    int j = blockIdx.x * blockDim.x + threadIdx.x;
-    int i = blockIdx.y;
-    if (j >= N || i >= M) return;
-    const float *a = A + (size_t)i * K;
-    float sum = 0.0f;
-    for (int k = 0; k < K; ++k) sum += a[k] * B[(size_t)k * N + j];
-    C[(size_t)i * N + j] = sum;
+    typedef typename ColVec<NC>::T bvec;
+    __shared__ __align__(16) float As[MT][MM_KC];
+    const int j = (blockIdx.x * 256 + threadIdx.x) * NC;  // first column of this thread
+    const int i0 = blockIdx.y * MT;
+    const bool live = j < N;  // NC > 1 only when N % NC == 0: all NC columns exist
+    const bvec *b = reinterpret_cast<const bvec *>(B + (live ? j : 0));
+    const size_t ldb = (size_t)N / NC;  // row stride of B in bvec units
+    float acc[MT][NC];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc[i][c] = 0.0f;
+    for (int k0 = 0; k0 < K; k0 += MM_KC) {
+        const int kc = K - k0 < MM_KC ? K - k0 : MM_KC;
+        __syncthreads();  // the previous chunk is consumed
+        for (int e = threadIdx.x; e < MT * MM_KC; e += 256) {
+            const int i = e / MM_KC, k = e - i * MM_KC;
+            As[i][k] = (i0 + i < M && k < kc) ? A[(size_t)(i0 + i) * K + k0 + k] : 0.0f;
+        }
+        __syncthreads();
+        int k = 0;
+        for (; k + MM_U <= kc; k += MM_U) {
+            bvec bv[MM_U];
+#pragma unroll
+            for (int u = 0; u < MM_U; ++u) bv[u] = b[(size_t)(k0 + k + u) * ldb];
+#pragma unroll
+            for (int u = 0; u < MM_U; ++u)
+#pragma unroll
+                for (int i = 0; i < MT; ++i)
+#pragma unroll
+                    for (int c = 0; c < NC; ++c)
+                        acc[i][c] += As[i][k + u] * ColVec<NC>::at(bv[u], c);
+        }
+        for (; k < kc; ++k) {
+            const bvec bk = b[(size_t)(k0 + k) * ldb];
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int c = 0; c < NC; ++c) acc[i][c] += As[i][k] * ColVec<NC>::at(bk, c);
+        }
+    }
+    if (!live) return;
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+        if (i0 + i < M)
+#pragma unroll
+            for (int c = 0; c < NC; ++c) C[(size_t)(i0 + i) * N + j + c] = acc[i][c];
 }
 
 // gpu.c:144-156 per row: ss is the reference's sequential fp32 sum of the
@@ -160,8 +223,30 @@ extern "C" int ornk_matmul_f32(float *C, const float *A, const float *B, int M, 
                                hipStream_t s)
 {
     if (M <= 0 || N <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_matmul, dim3(blocks_for((size_t)N, 256), M), dim3(256), 0, s, C, A, B, M,
-                       N, K);
+    // rows per block-row: the smallest power of two >= M, at most 16 (a
+    // register per row and column); larger M runs ceil(M/16) block-rows.
+    // Up to 4 rows a thread takes 4 columns (one 16-byte B load per step)
+    // where N allows it (N % 4 == 0 keeps every row 16-byte aligned).
+    const int mt = M > 8 ? 16 : M > 4 ? 8 : M > 2 ? 4 : M;
+    const int nc = (mt <= 4 && N % 4 == 0 && ((uintptr_t)B & 15) == 0) ? 4 : 1;
+    const dim3 grid(blocks_for(((size_t)N + nc - 1) / nc, 256), (M + mt - 1) / mt);
+#define ORN_MM(MT_, NC_) hipLaunchKernelGGL((k_matmul<MT_, NC_>), grid, dim3(256), 0, s, C, A, B, M, N, K)
+    if (nc == 4) {
+        switch (mt) {
+        case 1: ORN_MM(1, 4); break;
+        case 2: ORN_MM(2, 4); break;
+        default: ORN_MM(4, 4); break;
+        }
+    } else {
+        switch (mt) {
+        case 1: ORN_MM(1, 1); break;
+        case 2: ORN_MM(2, 1); break;
+        case 4: ORN_MM(4, 1); break;
+        case 8: ORN_MM(8, 1); break;
+        default: ORN_MM(16, 1); break;
+        }
+    }
+#undef ORN_MM
     return hipGetLastError();
 }
 

@@ -110,6 +110,37 @@ def test_matmul_known_answers(om, ctx):
     assert np.array_equal(ctx.download(o2, np.float32, 16), exp)
 
 
+def seq_matmul(A, B):
+    """gpu.c:104-115 in numpy: every C[i][j] a sequential fp32 sum from 0 of
+    the fp32 products A[i][k] * B[k][j], k ascending."""
+    M, K = A.shape
+    C = np.zeros((M, B.shape[1]), np.float32)
+    for k in range(K):
+        C = (C + (A[:, k:k + 1] * B[k:k + 1, :]).astype(np.float32)).astype(np.float32)
+    return C
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 4, 0), (1, 4097, 300), (1, 1000, 13), (2, 1000, 1),
+                                   (3, 4096, 300), (5, 7, 257), (16, 1000, 300),
+                                   (17, 4097, 13), (40, 1024, 520)])
+def test_matmul_tiled_bit_exact(om, ctx, M, N, K):
+    """gpu_matmul at M > 1 and odd shapes (row blocks of 1..16 rows, one or
+    four columns per thread, K past one LDS chunk of 256): bit-identical to
+    the CPU backend's sequential sums (gpu.c:104-115); K = 0 gives zeros."""
+    rng = np.random.default_rng(M * 1000 + N + K)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    L = om.lib()
+    Ab = ctx.upload(A) if K else ctx.alloc(4)
+    Bb = ctx.upload(B) if K else ctx.alloc(4)
+    Cb = ctx.upload(np.full((M, N), 7.0, np.float32))
+    L.gpu_matmul(ctx.ptr, Cb.ptr, Ab.ptr, Bb.ptr, M, N, K, 0, 0)
+    got = ctx.download(Cb, np.float32, (M, N))
+    assert np.array_equal(got.view(np.uint32), seq_matmul(A, B).view(np.uint32))
+    for b in (Ab, Bb, Cb):
+        b.free()
+
+
 @pytest.mark.parametrize("dim", [4, 64, 2048])
 def test_rmsnorm(om, ctx, dim):
     """t_gpu_metal.c:189-343 (1e-5 / 1e-4) -- here bit-exact with gpu.c:144-156."""
