@@ -103,6 +103,38 @@ __global__ void __launch_bounds__(256) k_dequant_quad(const uint8_t *src, float4
     }
 }
 
+// Q4_K with 16-byte accesses (src and dst 16-byte aligned; a 144-byte block is
+// nine 16-byte words): 16 lanes per block, lane l writes outputs 16l..16l+15
+// of sub-block j = l/2 from one header word (d, dmin, scales; the same word
+// for the block's 16 lanes) and one word of quants, bytes 16 + 32(l/4) +
+// 16(l&1) .. +15 (low nibbles for even j, high for odd), with the reference's
+// arithmetic: d1 = d*sc, m1 = dmin*m, y = d1*q - m1 (gguf.c:43-61).
+__global__ void __launch_bounds__(256) k_dequant_q4k16(const uint4 *__restrict__ src,
+                                                       v4f *__restrict__ dst, uint64_t n_blocks)
+{
+    const int l = threadIdx.x & 15;
+    const int j = l >> 1;
+    for (uint64_t b = (uint64_t)blockIdx.x * 16 + (threadIdx.x >> 4); b < n_blocks;
+         b += (uint64_t)gridDim.x * 16) {
+        const uint4 *blk = src + b * (ORN_Q4K_BYTES / 16);
+        const uint4 hd = blk[0];
+        const uint4 qw = blk[1 + 2 * (l >> 2) + (l & 1)];
+        uint32_t sc, m;
+        orn_scale_min_k4(j, hd.y, hd.z, hd.w, sc, m);
+        const float d1 = orn_half_to_float(hd.x & 0xFFFFu) * (float)sc;
+        const float m1 = orn_half_to_float(hd.x >> 16) * (float)m;
+        const uint32_t sh = 4u * (uint32_t)(j & 1);
+        const uint32_t w[4] = {qw.x, qw.y, qw.z, qw.w};
+        v4f *o = dst + b * (ORN_QK_K / 4) + 4 * l;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t q = (w[i] >> sh) & 0x0F0F0F0Fu;
+            o[i] = (v4f){d1 * (float)(q & 0xFFu) - m1, d1 * (float)((q >> 8) & 0xFFu) - m1,
+                         d1 * (float)((q >> 16) & 0xFFu) - m1, d1 * (float)(q >> 24) - m1};
+        }
+    }
+}
+
 __global__ void k_dequant_q4k(const uint8_t *src, float *dst, uint64_t n_blocks)
 {
     for (uint64_t b = blockIdx.x; b < n_blocks; b += gridDim.x)
@@ -166,7 +198,10 @@ extern "C" int ornk_dequant(const void *src, int type, uint64_t n_elems, float *
         return hipGetLastError();
     case ORN_TYPE_Q4_K:
         if (nb == 0) return hipSuccess;
-        if (((uintptr_t)p & 3) == 0 && ((uintptr_t)dst & 15) == 0)
+        if (((uintptr_t)p & 15) == 0 && ((uintptr_t)dst & 15) == 0)
+            hipLaunchKernelGGL(k_dequant_q4k16, dim3(grid_cap(nb, 16)), dim3(256), 0, s,
+                               reinterpret_cast<const uint4 *>(p), reinterpret_cast<v4f *>(dst), nb);
+        else if (((uintptr_t)p & 3) == 0 && ((uintptr_t)dst & 15) == 0)
             hipLaunchKernelGGL(k_dequant_quad<false>, dim3(grid_cap(nb, 4)), dim3(256), 0, s, p,
                                reinterpret_cast<float4 *>(dst), nb);
         else

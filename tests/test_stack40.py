@@ -13,7 +13,10 @@ layer) and checks that it equals the chain of 40 single-layer forwards bit
 for bit, and teacher-forces layers 0, 19 and 39 against the oracle
 (orc_moe_layer with the rmsnorm and the residual): indices exact, outputs
 within 1e-5 per row (measured ~1e-6; the bar that catches a dropped term
-of the MFMA arithmetic, tests/test_mfma_emulation.py).
+of the MFMA arithmetic, tests/test_mfma_emulation.py).  End to end, without
+teacher forcing, the oracle runs its own 40-layer chain from the same input
+(generating only the experts each layer selects): every layer's indices
+must equal the stack's and the output stays within 40 x 1e-5.
 """
 import sys
 
@@ -26,6 +29,11 @@ pytestmark = pytest.mark.gpu
 
 D, H, E, K = 2048, 512, 256, 8
 TOL = 1e-5
+# The free-running 40-layer chain: each layer adds its own ~1e-6 (the
+# oracle's fp32 chains against the kernels' fp32 accumulation) to the
+# residual stream, so the end-to-end bar is the per-layer one times the
+# depth.
+E2E_TOL = 40 * TOL
 
 
 def say(*a):
@@ -112,6 +120,41 @@ def test_device_fill_file_orientation(om, ctx):
         dev.close()
 
 
+def oracle_chain(om, seed, L, x0):
+    """The reference's 40-layer MoE stack on the CPU, free running: x <- x +
+    MoE_l(rmsnorm(x)) per layer (model.c:992-1144 with weight-1 norms), each
+    layer the synthetic layer fill_synthetic(l, seed + l) writes.  Only the
+    experts a layer's routing selects (and the shared expert) are generated;
+    the other experts' bytes stay zero, which the oracle never reads.
+    Returns the input of every layer and each layer's indices."""
+    nb = D * H // 256
+    ones = np.ones(D, np.float32)
+    xs, idxs = [np.asarray(x0, np.float32)], []
+    for l in range(L):
+        sd, x = seed + l, xs[-1]
+        W = om.synth_normal(sd, om.synth_stream(l, om.SYN_ROUTER, 0), D * E, 0.02).reshape(D, E)
+        xn = O.rmsnorm(x, ones)
+        sel = set()
+        for t in range(x.shape[0]):
+            sel |= {int(e) for e in O.topk(O.router_logits(xn[t], W), K)[0]}
+        arr = {"gate": np.zeros((E + 1) * nb * 144, np.uint8),
+               "up": np.zeros((E + 1) * nb * 144, np.uint8),
+               "down": np.zeros((E + 1) * nb * 210, np.uint8)}
+        for e in sorted(sel) + [E]:
+            for name, kind, bs, fn in (("gate", om.SYN_GATE, 144, om.synth_q4k),
+                                       ("up", om.SYN_UP, 144, om.synth_q4k),
+                                       ("down", om.SYN_DOWN, 210, om.synth_q6k)):
+                arr[name][e * nb * bs:(e + 1) * nb * bs] = fn(sd, om.synth_stream(l, kind, e), nb)
+        r = {n: a[:E * nb * (210 if n == "down" else 144)] for n, a in arr.items()}
+        sh = {n: a[E * nb * (210 if n == "down" else 144):] for n, a in arr.items()}
+        out, idx, _ = O.moe_layer(D=D, H=H, E=E, k=K, x=x, resid=x, norm_w=ones, router_W=W,
+                                  gate=r["gate"], up=r["up"], down=r["down"], sh_gate=sh["gate"],
+                                  sh_up=sh["up"], sh_down=sh["down"])
+        xs.append(out)
+        idxs.append(idx)
+    return xs, idxs
+
+
 def test_stack40_resident_decode(om, ctx):
     """40 layers x 257 experts resident, T = 1 (and 16)."""
     L, seed = 40, 1234
@@ -139,6 +182,19 @@ def test_stack40_resident_decode(om, ctx):
             say(f"  T={T}: stack == 40 chained single-layer forwards, bit for bit")
             if T != 1:
                 continue
+            # end to end, no teacher forcing: the oracle's own 40-layer chain
+            # from the same input routes every layer identically, and the
+            # stack's output stays within E2E_TOL of it
+            oxs, oidx = oracle_chain(om, seed, L, x0)
+            gidx = [fwd(ctx, st, l, xs[l], om.MOE_NORM, resid=xs[l])[1] for l in range(L)]
+            for l in range(L):
+                assert np.array_equal(gidx[l], oidx[l]), l
+            errs = [(np.abs(xs[l].astype(np.float64) - oxs[l]).max(axis=1) /
+                     np.abs(oxs[l]).max(axis=1)).max() for l in range(1, L + 1)]
+            say(f"  end to end vs the oracle's own chain: every layer's indices exact; output "
+                f"error after layers 1/10/20/40: {errs[0]:.2e} {errs[9]:.2e} {errs[19]:.2e} "
+                f"{errs[39]:.2e}")
+            assert max(errs) <= E2E_TOL
             for l in (0, 19, 39):
                 syn = om.SyntheticLayer(seed + l, l, D, H, E, True)
                 ones = np.ones(D, np.float32)
