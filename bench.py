@@ -371,8 +371,9 @@ def measure_streamed(ctx, steps):
 
 def measure_attention(ctx):
     """gpu_rope / gpu_attention (the Metal backend's semantics) at Ornith's
-    head size: one head, 4096 positions, head_dim 256, fp32 VALU; 4*S^2*d
-    flops per call against the MI355X fp32 vector peak (157.3 TFLOP/s)."""
+    head size: one head, 4096 positions, head_dim 256, on the fp32 matrix
+    cores; 4*S^2*d flops per call against the MI355X dense fp32 peak
+    (157.3 TFLOP/s)."""
     S, hd = 4096, 256
     rng = np.random.default_rng(0)
     bufs = [ctx.upload(rng.standard_normal((S, hd)).astype(np.float32)) for _ in range(3)]
@@ -394,7 +395,7 @@ def measure_attention(ctx):
     for b in bufs + [ob, q, k]:
         b.free()
     res = {"attention_s4096_d256": {"ms": round(dt * 1e3, 3), "tflops": round(tf, 2),
-                                    "peak_fp32_valu_tflops": 157.3,
+                                    "bound": "mfma", "peak_fp32_tflops": 157.3,
                                     "frac": round(tf / 157.3, 4)},
            "rope_16q2k_d256_us_per_call": round(rope_us, 2)}
     log("attention", res)

@@ -320,11 +320,23 @@ void gpu_attention(gpu_context *ctx, gpu_buffer *out, const gpu_buffer *Q,
         return;
     }
     const float scale = 1.0f / sqrtf((float)head_dim);
-    orn_hip_check(ctx, (hipError_t)ornk_attention((float *)out->dev, (const float *)Q->dev,
-                                                  (const float *)K_cache->dev,
-                                                  (const float *)V_cache->dev, seq_len, head_dim,
-                                                  scale, ctx->stream),
-                  "gpu_attention");
+    if (head_dim % 4 == 0) {
+        /* matrix cores; the key splits' partials live in the context workspace */
+        const size_t wsb = ornk_attention_mma_ws(seq_len, head_dim);
+        void *ws = wsb ? orn_ws_get(ctx, wsb) : NULL;
+        if (wsb && !ws) return;
+        orn_hip_check(ctx, (hipError_t)ornk_attention_mma((float *)out->dev, (const float *)Q->dev,
+                                                          (const float *)K_cache->dev,
+                                                          (const float *)V_cache->dev, seq_len,
+                                                          head_dim, scale, ws, ctx->stream),
+                      "gpu_attention");
+    } else {
+        orn_hip_check(ctx, (hipError_t)ornk_attention((float *)out->dev, (const float *)Q->dev,
+                                                      (const float *)K_cache->dev,
+                                                      (const float *)V_cache->dev, seq_len,
+                                                      head_dim, scale, ctx->stream),
+                      "gpu_attention");
+    }
     sync_ctx(ctx);
 }
 

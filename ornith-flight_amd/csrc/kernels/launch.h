@@ -38,6 +38,11 @@ int ornk_rope(float *Q, float *K, int head_dim, int n_q, int n_k, int pos, float
 int ornk_attention(float *out, const float *Q, const float *K, const float *V, int seq, int hd,
                    float scale, hipStream_t s);
 size_t ornk_attention_lds(int hd);
+/* The same on the matrix cores (hd % 4 == 0, hd <= 256); ws holds
+ * ornk_attention_mma_ws(seq, hd) bytes (0: none needed). */
+size_t ornk_attention_mma_ws(int seq, int hd);
+int ornk_attention_mma(float *out, const float *Q, const float *K, const float *V, int seq, int hd,
+                       float scale, void *ws, hipStream_t s);
 int ornk_deltanet_step(float *state, const float *Q, const float *K, const float *V, float *out,
                        int dim, float gate, hipStream_t s);
 int ornk_kv_append(float *Kc, float *Vc, const float *Kn, const float *Vn, int pos, int hd,

@@ -135,8 +135,14 @@ def test_gpu_rope(om, ctx, hd, nq, nk, pos, theta):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("seq,hd", [(1, 64), (7, 256), (16, 128), (33, 80), (300, 256),
-                                    (1000, 64)])
+                                    (1000, 64), (1500, 256), (513, 96), (65, 4), (5, 30),
+                                    (41, 18)])
 def test_gpu_attention(om, ctx, seq, hd):
+    """Head dims that are a multiple of 4 run on the matrix cores (fp32
+    MFMA; dims padded to 64/128/256, keys split over work groups and merged
+    from 17 positions on); others (30, 18) on the VALU kernel.  Within 2e-6
+    of the oracle (fp32, the shader's order) relative to the largest
+    output."""
     rng = np.random.default_rng(seq + 7 * hd)
     Q, K, V = (f32(rng.standard_normal((seq, hd))) for _ in range(3))
     bufs = [ctx.upload(a) for a in (Q, K, V)]
