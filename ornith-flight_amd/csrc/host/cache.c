@@ -174,7 +174,7 @@ orn_cache *orn_cache_create(gpu_context *ctx, const ornith_moe_shape *sh)
             if (!rc) rc = dev_alloc(ctx, c, (void **)&c->pd[m], C * DH / 64);
             if (!rc) rc = dev_alloc(ctx, c, (void **)&c->pdm[m], C * DH / 64);
         }
-        if (!rc) rc = dev_alloc(ctx, c, (void **)&c->dq, C * DH);
+        if (!rc) rc = dev_alloc(ctx, c, (void **)&c->dq, C * ORNK_DQ_BYTES(DH));
         if (!rc) rc = dev_alloc(ctx, c, (void **)&c->dsc, C * DH / 8);
         if (!rc) rc = dev_alloc(ctx, c, (void **)&c->dd, C * DH / 64);
         if (!rc) rc = dev_alloc(ctx, c, (void **)&c->dmax, C * 3 * sizeof(float));

@@ -51,7 +51,7 @@ struct ornith_moe_store {
      *   psc[m] sub-block scales [D/32][H/256][8][32] fp16      (D*H/16)
      *   pmn[m] sub-block mins, same shape                       (D*H/16)
      *   pd[m], pdm[m]  d and dmin [H/256][D] fp32               (D*H/64 each)
-     *   dq     down q + 32 [H/32][D/256][4][64][4][8] u8      (D*H)
+     *   dq     down q + 32, 6-bit [H/32][D/256] x ORNK_DQ_UNIT   (D*H*3/4)
      *   dsc    down sub-block scales [H/32][D/256][16][32] fp16   (D*H/8)
      *   dd     down d [D/256][H] fp32                             (D*H/64)
      *   dmax   [3]: max |d|,|dmin| of gate and of up, max |d| of down */
@@ -354,7 +354,8 @@ ornith_moe_store *gpu_moe_store_create(gpu_context *ctx, const ornith_moe_shape 
         const size_t LE = L * E1, DH = D * H;
         size_t psz[14] = {LE * DH / 2, LE * DH / 2, LE * DH / 16, LE * DH / 16, LE * DH / 16,
                           LE * DH / 16, LE * DH / 64, LE * DH / 64, LE * DH / 64, LE * DH / 64,
-                          LE * DH, LE * DH / 8, LE * DH / 64, LE * 3 * sizeof(float)};
+                          LE * ORNK_DQ_BYTES(DH), LE * DH / 8, LE * DH / 64,
+                          LE * 3 * sizeof(float)};
         void **pp[14] = {(void **)&st->pq[0], (void **)&st->pq[1], (void **)&st->psc[0],
                          (void **)&st->psc[1], (void **)&st->pmn[0], (void **)&st->pmn[1],
                          (void **)&st->pd[0], (void **)&st->pd[1], (void **)&st->pdm[0],
@@ -508,7 +509,7 @@ static int upload_q6k_prefill(gpu_context *ctx, ornith_moe_store *st, int layer,
 {
     const size_t D = (size_t)st->sh.d_model, H = (size_t)st->sh.hidden, DH = D * H;
     const size_t E1 = (size_t)st->sh.n_experts + 1, nb = st->blocks_per_matrix;
-    uint8_t *qb = (uint8_t *)malloc(DH);
+    uint8_t *qb = (uint8_t *)malloc(ORNK_DQ_BYTES(DH));
     uint16_t *sc = (uint16_t *)malloc(DH / 8);
     float *d = (float *)malloc(DH / 64);
     int rc = ORN_OK;
@@ -522,8 +523,9 @@ static int upload_q6k_prefill(gpu_context *ctx, ornith_moe_store *st, int layer,
                                                (int)H, (int)D, qb, sc, d, &dmax);
         if (scmax > st->q6_scmax[layer]) st->q6_scmax[layer] = scmax;
         st->dmax_host[slot * 3 + 2] = dmax;
-        rc = orn_hip_check(ctx, hipMemcpyAsync(st->dq + slot * DH, qb, DH, hipMemcpyHostToDevice,
-                                               s), "upload prefill q6k");
+        rc = orn_hip_check(ctx, hipMemcpyAsync(st->dq + slot * ORNK_DQ_BYTES(DH), qb,
+                                               ORNK_DQ_BYTES(DH), hipMemcpyHostToDevice, s),
+                           "upload prefill q6k");
         if (!rc)
             rc = orn_hip_check(ctx, hipMemcpyAsync((uint8_t *)st->dsc + slot * (DH / 8), sc, DH / 8,
                                                    hipMemcpyHostToDevice, s), "upload q6k sc");
@@ -777,7 +779,7 @@ int gpu_moe_store_fill_synthetic(gpu_context *ctx, ornith_moe_store *st, int lay
             pa.pd[m] = (float *)((uint8_t *)st->pd[m] + slot0 * (DH / 64));
             pa.pdm[m] = (float *)((uint8_t *)st->pdm[m] + slot0 * (DH / 64));
         }
-        pa.dq = st->dq + slot0 * DH;
+        pa.dq = st->dq + slot0 * ORNK_DQ_BYTES(DH);
         pa.dsc = (uint16_t *)((uint8_t *)st->dsc + slot0 * (DH / 8));
         pa.dd = (float *)((uint8_t *)st->dd + slot0 * (DH / 64));
         pa.dmax = st->dmax + slot0 * 3;
@@ -1168,7 +1170,7 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
             a.gu_pf.pdm[m] = (const float *)((const uint8_t *)st->pdm[m] + slot0 * (DH / 64));
         }
         a.gu_pf.dmax = st->dmax + slot0 * 3;
-        a.dn_pf.dq = st->dq + slot0 * DH;
+        a.dn_pf.dq = st->dq + slot0 * ORNK_DQ_BYTES(DH);
         a.dn_pf.dsc = (const uint16_t *)((const uint8_t *)st->dsc + slot0 * (DH / 8));
         a.dn_pf.dd = (const float *)((const uint8_t *)st->dd + slot0 * (DH / 64));
         a.dn_pf.dmax = st->dmax + slot0 * 3;

@@ -19,12 +19,17 @@
  * Lane l of a 16x16x32 B operand holds k = 8*(l/16) + e (e = 0..7) of
  * column l % 16.  Q4_K words place value e at bit 4*(e/2) + 16*(e%2), so
  * ((w >> 4i) & 0x000F000F) | 0x64006400 is the fp16 pair (1024 + q_{2i},
- * 1024 + q_{2i+1}).  Q6_K stores q + 32 in one byte per value (k order).
+ * 1024 + q_{2i+1}).  Q6_K stores the 6-bit q + 32 split the same way: its
+ * low four bits in a word of that order, its high two bits in a second word
+ * (value e at bit 2*(e/2) + 16*(e%2), one byte per half-word per tile, two
+ * tiles per word), so one v_bfi and an OR give the pair.
  *
  * A kernel wave covers the four 16-column tiles 4w..4w+3 of a 256-column
- * block, so the words (Q4_K) or 8-byte groups (Q6_K) of those four tiles sit
- * side by side per lane: [K/32][M/256][4 w][64 lanes][4 tiles] -- one 16-byte
- * load (Q4_K) or two (Q6_K) per lane and reduction step.
+ * block, so the words of those four tiles sit side by side per lane:
+ * [K/32][M/256][4 w][64 lanes][4 tiles] -- one 16-byte load per lane and
+ * reduction step for Q4_K; for Q6_K one 16-byte load of nibble words and one
+ * 8-byte load of high-bit words from the step's 6144-byte unit
+ * (ORNK_DQ_UNIT: 4096 bytes of nibbles, then 2048 of high bits).
  */
 #include "internal.h"
 
@@ -130,6 +135,7 @@ int orn_pack_q6k_prefill(const uint8_t *blocks, int K, int M, uint8_t *qb, uint1
     const int NB = M / 256;
     int scmax = 0;
     float mx = 0.0f;
+    memset(qb, 0, ORNK_DQ_BYTES((size_t)K * M));
     for (int k = 0; k < K; ++k) {
         const int kt = k / 32, kk = k % 32, g = kk / 8, e = kk % 8;
         for (int b = 0; b < NB; ++b) {
@@ -147,11 +153,14 @@ int orn_pack_q6k_prefill(const uint8_t *blocks, int K, int M, uint8_t *qb, uint1
                 if (-v > scmax) scmax = -v;
                 sc[(((size_t)kt * NB + b) * 16 + nt) * 32 + kk] = int_half(v);
             }
+            uint8_t *unit = qb + ((size_t)kt * NB + b) * ORNK_DQ_UNIT;
             for (int p = 0; p < 256; ++p) {
-                const int nt = p / 16, col = p % 16;
-                const size_t o =
-                    (((((size_t)kt * NB + b) * 4 + nt / 4) * 64 + 16 * g + col) * 4 + nt % 4) * 8 + e;
-                qb[o] = (uint8_t)(q6_at(ql, qh, p) + 32);
+                const int nt = p / 16, col = p % 16, wl = (nt / 4) * 64 + 16 * g + col;
+                const uint32_t v = (uint32_t)(q6_at(ql, qh, p) + 32);
+                uint32_t *nw = (uint32_t *)(unit + (size_t)wl * 16) + nt % 4;
+                uint32_t *hw = (uint32_t *)(unit + 4096 + (size_t)wl * 8) + (nt % 4) / 2;
+                *nw |= (v & 15u) << (4 * (e / 2) + 16 * (e % 2));
+                *hw |= (v >> 4) << (2 * (e / 2) + 16 * (e % 2) + 8 * (nt % 2));
             }
         }
     }

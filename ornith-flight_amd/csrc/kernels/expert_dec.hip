@@ -32,7 +32,12 @@ typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 
-#define ORN_DEC_NR 4  // reduction steps in flight per lane
+#define ORN_DEC_NR 4  // reduction steps in flight per lane (scales in the ring)
+
+// Two-tile down instances keep the slice's scales in LDS and their ring holds
+// only quant words: every step of a slice up to 16 in flight, 8 of the
+// 32-step slices (whose scales take 32 more registers until stored).
+constexpr int dec_nr_lds(int kt) { return kt <= 16 ? kt : 8; }
 
 // Ring loads are raw buffer loads: a per-lane byte offset that stays fixed
 // (one VGPR) plus the step's wave-uniform offset in an SGPR, so NR steps in
@@ -50,10 +55,12 @@ __device__ __forceinline__ uint4 bload16(rsrc_t r, uint32_t voff, uint32_t soff)
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-__device__ __forceinline__ v2f bload8f(rsrc_t r, uint32_t voff, uint32_t soff)
+__device__ __forceinline__ uint2 bload8(rsrc_t r, uint32_t voff, uint32_t soff)
 {
-    return __builtin_bit_cast(v2f, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+    const v2u v = __builtin_bit_cast(v2u, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+    return make_uint2(v.x, v.y);
 }
+
 
 // ---------------------------------------------------------------------------
 // Gate/up (Q4_K).  Logical tile = ((item * ks + kslice) * 2 + m) * (H/256) + b;
@@ -318,8 +325,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT > 1
 // that row's max |mid| over the slice (a power of two either way: only the
 // hi/lo split point moves); the separate mid launch is skipped.
 // ---------------------------------------------------------------------------
+// One step of a lane's weights: the 6-bit values of its four column tiles
+// (a word of low nibbles per tile, the high bits of tiles 2i and 2i+1 in one
+// word; prefill_pack.c) and, unless they sit in LDS, their sub-block scales.
 struct DnRing {
-    uint4 q0, q1, sc[4];
+    uint4 qn, sc[4];
+    uint2 qc;
 };
 
 // WIDE: Q6_K sub-scales up to |128| (q6_b2: three MFMAs per tile and step).
@@ -334,20 +345,30 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT > 1
     constexpr int LC = 2 * KC;
     constexpr int KV = 32 * KT;  // reduction values of the slice
     static_assert(KSG == 0 || RT == 1, "mid is formed in the kernel for one row tile only");
+    static_assert(KSG == 0 || 32 * KT == 256, "mid is formed one value per thread");
+    static_assert(KT % 4 == 0 && NR >= 1 && NR <= KT, "slices of 4k steps");
+    // SL: the slice's scales in LDS (two-tile instances, whose many rows per
+    // item make them bandwidth-bound: the deeper ring pays); one-tile
+    // instances carry them in the ring.
+    constexpr bool SL = RT > 1;
     __shared__ __align__(16) uint32_t As[NBUF][KC][RT][2][16 * ORN_AST / 2];
+    __shared__ __align__(16) uint4 Ss[SL ? KT : 1][64];  // per step: 16 tiles x 32 scales
     __shared__ float s_inv[16 * RT];
     __shared__ __align__(16) float Ms[KSG ? 16 : 1][KSG ? KV : 4];  // the rows' mid slices
     __shared__ unsigned int s_amax[16];
 
+    // The D/256 work groups of one (item, slice) read the same gate/up
+    // partials (KSG > 0) or mid rows: XCD-aware numbering puts them on one
+    // XCD, so one L2 serves the rest.
     const int NBD = D >> 8;
     const int per_item = NBD * ks;
-    const int tile = blockIdx.x;
+    const int n_live = ctl[1] * per_item;
+    if ((int)blockIdx.x >= n_live) return;
+    const int tile = xcd_remap(blockIdx.x, n_live);
     const int b = tile % NBD;
     const int kslice = (tile / NBD) % ks;
     const int item = tile / per_item;
-    const int n_items = ctl[1];
     const int4 itm = items[item];
-    if (item >= n_items) return;
     const int e = itm.w;
     const int nrows = itm.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -355,23 +376,36 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT > 1
     const int kt0 = kslice * KT;
     const size_t DH = (size_t)D * H;
 
-    const uint32_t EQ = (uint32_t)DH, ES = (uint32_t)(DH / 8);
+    const uint32_t EQ = (uint32_t)ORNK_DQ_BYTES(DH), ES = (uint32_t)(DH / 8);
     const rsrc_t rq = make_rsrc(P.dq + (size_t)e * EQ, EQ);
     const rsrc_t rs = make_rsrc(reinterpret_cast<const uint8_t *>(P.dsc) + (size_t)e * ES, ES);
-    const uint32_t qstep = (uint32_t)NBD * 8192, sstep = (uint32_t)NBD * 1024;
-    const uint32_t q_off = (uint32_t)(((size_t)kt0 * NBD + b) * 8192) + (wave * 64 + lane) * 32;
+    const uint32_t qstep = (uint32_t)NBD * ORNK_DQ_UNIT, sstep = (uint32_t)NBD * 1024;
     const uint32_t s_off = (uint32_t)((((size_t)kt0 * NBD + b) * 16 + 4 * wave) * 64) + 16 * g;
+    const uint32_t q_off = (uint32_t)(((size_t)kt0 * NBD + b) * ORNK_DQ_UNIT) + (wave * 64 + lane) * 16;
+    const uint32_t c_off = (uint32_t)(((size_t)kt0 * NBD + b) * ORNK_DQ_UNIT) + 4096 + (wave * 64 + lane) * 8;
     auto load_b = [&](DnRing &st, int kt) {
-        st.q0 = bload16(rq, q_off, kt * qstep);
-        st.q1 = bload16(rq, q_off + 16, kt * qstep);
+        st.qn = bload16(rq, q_off, kt * qstep);
+        st.qc = bload8(rq, c_off, kt * qstep);
+        if constexpr (!SL) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) st.sc[j] = bload16(rs, s_off + 64 * j, kt * sstep);
+            for (int j = 0; j < 4; ++j) st.sc[j] = bload16(rs, s_off + 64 * j, kt * sstep);
+        }
     };
 
     const int ar = tid >> 4, seg = tid & 15;  // row ar of each row tile, as in k_gateup_dec
     int arow[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) arow[rt] = 16 * rt + ar < nrows ? 16 * rt + ar : 0;
+    // the slice's scales: KT x 64 16-byte pieces, KT/4 per thread, issued
+    // before the ring so that their wait leaves the ring in flight
+    uint4 sreg[SL ? KT / 4 : 1];
+    if constexpr (SL) {
+#pragma unroll
+        for (int i = 0; i < KT / 4; ++i) {
+            const int idx = 256 * i + tid;
+            sreg[i] = bload16(rs, (uint32_t)(((size_t)(kt0 + (idx >> 6)) * NBD + b) * 1024) + 16 * (idx & 63), 0);
+        }
+    }
     DnRing st[NR];
 #pragma unroll
     for (int i = 0; i < NR; ++i) load_b(st[i], i);
@@ -379,24 +413,34 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT > 1
 
     float amax[RT];
     if (KSG) {
+        // Thread t forms value h = t of each row (KV == 256 == threads).  The
+        // partials of MG rows (MG * KSG = 16 per array) are loaded together,
+        // so an item of 16 rows waits for 16 / MG memory latencies, not 16.
+        constexpr int NS = KSG > 0 ? KSG : 1, MG = NS >= 16 ? 1 : 16 / NS;
         const size_t sstr = (size_t)rows_max * 2 * H;  // between gate/up slices
         if (tid < 16) s_amax[tid] = 0u;
         __syncthreads();
-        for (int r = 0; r < nrows; ++r) {  // uniform
-            const float *pg = gu + (size_t)(itm.y + r) * 2 * H + 32 * kt0;
-            float lmax = 0.0f;
-            for (int h = tid; h < KV; h += 256) {
-                float gv[KSG > 0 ? KSG : 1], uv[KSG > 0 ? KSG : 1];
+        for (int r0 = 0; r0 < nrows; r0 += MG) {  // uniform
+            float gv[MG][NS], uv[MG][NS];
 #pragma unroll
-                for (int sl = 0; sl < KSG; ++sl) {
-                    gv[sl] = pg[sl * sstr + h];
-                    uv[sl] = pg[sl * sstr + H + h];
+            for (int i = 0; i < MG; ++i) {
+                if (r0 + i >= nrows) break;  // uniform
+                const float *pg = gu + (size_t)(itm.y + r0 + i) * 2 * H + 32 * kt0 + tid;
+#pragma unroll
+                for (int sl = 0; sl < NS; ++sl) {
+                    gv[i][sl] = pg[sl * sstr];
+                    uv[i][sl] = pg[sl * sstr + H];
                 }
+            }
+#pragma unroll
+            for (int i = 0; i < MG; ++i) {
+                const int r = r0 + i;
+                if (r >= nrows) break;  // uniform
                 float g = 0.0f, u = 0.0f;
 #pragma unroll
-                for (int sl = 0; sl < KSG; ++sl) {
-                    g = g + gv[sl];
-                    u = u + uv[sl];
+                for (int sl = 0; sl < NS; ++sl) {
+                    g = g + gv[i][sl];
+                    u = u + uv[i][sl];
                 }
                 float act;
                 if (itm.y + r < shared_rows) {
@@ -407,13 +451,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT > 1
                     else act = g / (1.0f + expf(-g));
                 }
                 const float v = act * u;
-                Ms[r][h] = v;
-                lmax = fmaxf(lmax, fabsf(v));
-            }
+                Ms[r][tid] = v;
+                float lmax = fabsf(v);
 #pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) lmax = fmaxf(lmax, __shfl_xor(lmax, off, 64));
-            // non-negative floats order like their bit patterns
-            if (lane == 0) atomicMax(&s_amax[r], __float_as_uint(lmax));
+                for (int off = 32; off >= 1; off >>= 1) lmax = fmaxf(lmax, __shfl_xor(lmax, off, 64));
+                // non-negative floats order like their bit patterns
+                if (lane == 0) atomicMax(&s_amax[r], __float_as_uint(lmax));
+            }
         }
         __syncthreads();
         amax[0] = __uint_as_float(s_amax[arow[0]]);
@@ -485,6 +529,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT > 1
         }
     };
     a_load(0);
+    if constexpr (SL) {
+#pragma unroll
+        for (int i = 0; i < KT / 4; ++i) {
+            const int idx = 256 * i + tid;
+            Ss[idx >> 6][idx & 63] = sreg[i];
+        }
+    }
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
         ascale[rt] = 16 * rt + ar < nrows ? row_scale(amax[rt], dmx) : 0.0f;
@@ -506,20 +557,24 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT > 1
         const int ch = kt / KC, kl = kt % KC;
         DnRing &r = st[kt % NR];
         v8h bq[4], bq2[WIDE ? 4 : 1];
-        if (WIDE) {
-            q6_b2(r.q0.x, r.q0.y, r.sc[0], bq[0], bq2[0]);
-            q6_b2(r.q0.z, r.q0.w, r.sc[1], bq[1], bq2[WIDE ? 1 : 0]);
-            q6_b2(r.q1.x, r.q1.y, r.sc[2], bq[2], bq2[WIDE ? 2 : 0]);
-            q6_b2(r.q1.z, r.q1.w, r.sc[3], bq[3], bq2[WIDE ? 3 : 0]);
-        } else {
-            bq[0] = q6_b(r.q0.x, r.q0.y, r.sc[0]);
-            bq[1] = q6_b(r.q0.z, r.q0.w, r.sc[1]);
-            bq[2] = q6_b(r.q1.x, r.q1.y, r.sc[2]);
-            bq[3] = q6_b(r.q1.z, r.q1.w, r.sc[3]);
+        {
+            const uint32_t nw[4] = {r.qn.x, r.qn.y, r.qn.z, r.qn.w};
+            const uint32_t cw[4] = {r.qc.x, r.qc.x >> 8, r.qc.y, r.qc.y >> 8};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                uint32_t p[4];
+                q6_pairs(nw[j], cw[j], p);
+                // tile 4w+j, k = 8g..8g+7
+                const uint4 sc = SL ? Ss[SL ? kt : 0][4 * (4 * wave + j) + g] : r.sc[j];
+                if (WIDE) q6_b2(p, sc, bq[j], bq2[WIDE ? j : 0]);
+                else bq[j] = q6_b(p, sc);
+            }
         }
-        __builtin_amdgcn_sched_barrier(0);
-        if (kt + NR < KT) load_b(r, kt + NR);
-        __builtin_amdgcn_sched_barrier(0);
+        if (kt + NR < KT) {
+            __builtin_amdgcn_sched_barrier(0);
+            load_b(r, kt + NR);
+            __builtin_amdgcn_sched_barrier(0);
+        }
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
             if (rt >= rt_live) break;
@@ -562,8 +617,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT > 1
 // for batches above 64 tokens whose hot experts span several items); KT =
 // D/32/ks (gate/up) or H/32/ks (down) reduction steps per slice, 4 to 32;
 // activation tiles in chunks of 4 steps (LDS per row tile: 2 x 20 KB for
-// gate/up, 2 x 10 KB for down), of 2 steps for two-tile gate/up, so that
-// every instance keeps at most 41 KB.
+// gate/up, 2 x 10 KB for down), of 2 steps for two-tile gate/up.  Two-tile
+// down instances also hold the slice's scales (1 KB per step, at most
+// 32 KB), so that every instance keeps at most 73 KB (two work groups per CU,
+// the occupancy their registers allow).
 extern "C" int ornk_dec_supported(int kt_gu, int kt_dn)
 {
     auto ok = [](int kt) { return kt == 4 || kt == 8 || kt == 16 || kt == 32; };
@@ -646,7 +703,8 @@ extern "C" int ornk_moe_down_dec(const ornk_moe_args *a, hipStream_t s)
         return hipGetLastError();
     }
 #define ORN_DN_DEC(K, R, W)                                                                       \
-    ORN_LAUNCH_EV(a, (k_down_dec<ORN_DEC_NR, K, 4, 0, R, W>), grid, dim3(256), 0, s, a->dn_pf,    \
+    ORN_LAUNCH_EV(a, (k_down_dec<R == 2 ? dec_nr_lds(K) : ORN_DEC_NR, K, 4, 0, R, W>), grid,        \
+                  dim3(256), 0, s, a->dn_pf,                                                      \
                   a->mid, a->mid_amax, a->ctl, reinterpret_cast<const int4 *>(a->items),         \
                   a->dn_part, a->D, a->H, ks, a->rows_max, a->gu_part, shared_rows)
 #define ORN_DN_DEC_RT(R, W)                \

@@ -364,7 +364,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 // dn[kslice][row][n].
 // ---------------------------------------------------------------------------
 struct DnBlock {
-    const uint4 *qb;
+    const uint8_t *qb;  // ORNK_DQ_UNIT-byte units, [H/32][D/256]
     const uint16_t *sc;
     const float *mrow, *dva;  // already offset to this slice's first step
     float ascale;
@@ -379,11 +379,11 @@ __device__ __forceinline__ void down_tile(const DnBlock &B, ATiles<ROWS, 2> &As,
     const int g = lane >> 4, c = lane & 15;
     const int NBD = B.NBD, b = B.b;
     const bool a_live = wave < NTT;
-    auto b_load = [&](int kt, uint4 (&qv)[2], uint4 (&sv)[4]) {
+    auto b_load = [&](int kt, uint4 &qn, uint2 &qc, uint4 (&sv)[4]) {
         const size_t base = (size_t)(B.kt0 + kt) * NBD + b;
-        const uint4 *qp = B.qb + ((base * 4 + wave) * 64 + lane) * 2;
-        qv[0] = qp[0];
-        qv[1] = qp[1];
+        const uint8_t *up = B.qb + base * ORNK_DQ_UNIT;
+        qn = *reinterpret_cast<const uint4 *>(up + (wave * 64 + lane) * 16);
+        qc = *reinterpret_cast<const uint2 *>(up + 4096 + (wave * 64 + lane) * 8);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             sv[j] = *reinterpret_cast<const uint4 *>(B.sc + (base * 16 + 4 * wave + j) * 32 + 8 * g);
@@ -396,30 +396,33 @@ __device__ __forceinline__ void down_tile(const DnBlock &B, ATiles<ROWS, 2> &As,
         for (int j = 0; j < 4; ++j) acc[i][j] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
 
     ARaw ar;
-    uint4 qv[2];
+    uint4 qn;
+    uint2 qc;
     uint4 sv[4];
     v8h bq[4], bq2[WIDE ? 4 : 1];
     auto build_b = [&]() {
+        const uint32_t nw[4] = {qn.x, qn.y, qn.z, qn.w};
+        const uint32_t cw[4] = {qc.x, qc.x >> 8, qc.y, qc.y >> 8};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const uint32_t w0 = j & 1 ? qv[j >> 1].z : qv[j >> 1].x;
-            const uint32_t w1 = j & 1 ? qv[j >> 1].w : qv[j >> 1].y;
-            if (WIDE) q6_b2(w0, w1, sv[j], bq[j], bq2[WIDE ? j : 0]);
-            else bq[j] = q6_b(w0, w1, sv[j]);
+            uint32_t p[4];
+            q6_pairs(nw[j], cw[j], p);
+            if (WIDE) q6_b2(p, sv[j], bq[j], bq2[WIDE ? j : 0]);
+            else bq[j] = q6_b(p, sv[j]);
         }
     };
     if (a_live) {
         a_load<false>(ar, B.mrow, B.dva, nullptr, 0);
         a_store<false>(ar, B.ascale, &As.t[0][0][B.aoff], &As.t[0][1][B.aoff], nullptr, nullptr);
     }
-    b_load(0, qv, sv);
+    b_load(0, qn, qc, sv);
     build_b();
     __syncthreads();
 
     for (int kt = 0; kt < B.KT - 1; ++kt) {
         const int cur = kt & 1, nxt = cur ^ 1;
         if (a_live) a_load<false>(ar, B.mrow, B.dva, nullptr, 32 * (kt + 1));
-        b_load(kt + 1, qv, sv);
+        b_load(kt + 1, qn, qc, sv);
         mma_step<NTT, WIDE>(As.t[cur][0], As.t[cur][1], bq, acc, c, g, bq2);
         if (a_live)
             a_store<false>(ar, B.ascale, &As.t[nxt][0][B.aoff], &As.t[nxt][1][B.aoff], nullptr,
@@ -483,7 +486,7 @@ __global__ void __launch_bounds__(256)
     B.KT = H / 32 / ks;
     B.kt0 = kslice * B.KT;
     const int k0 = 32 * B.kt0;
-    B.qb = reinterpret_cast<const uint4 *>(P.dq + (size_t)e * DH);
+    B.qb = P.dq + (size_t)e * ORNK_DQ_BYTES(DH);
     B.sc = P.dsc + (size_t)e * (DH / 16);
     const int ar = (tid >> 2) & (ROWS - 1), ao = tid & 3;
     B.mrow = mid + (size_t)(itm.y + (ar < nrows ? ar : 0)) * H + k0 + 8 * ao;

@@ -20,6 +20,19 @@
 extern "C" {
 #endif
 
+/* ---- the down (Q6_K) MFMA layout ------------------------------------------
+ * Per expert, [H/32][D/256] units of 6144 bytes, one per reduction step of
+ * 32 and 256-column block: the 6-bit values q + 32 (0..63) of the unit's
+ * 32 x 256 weights, in the lane order of the MFMA B operand (wave w, lane
+ * l = 16g + c, column tile 4w + j, values k = 8g + e, e = 0..7):
+ *   bytes 0..4095:    u32 [4][64][4] low nibbles, value e at bit
+ *                     4*(e/2) + 16*(e%2) of word (w, l, j);
+ *   bytes 4096..6143: u32 [4][64][2] high two bits, value e of tile j at bit
+ *                     2*(e/2) + 16*(e%2) + 8*(j%2) of word (w, l, j/2).
+ * 0.75 bytes per weight (the GGUF Q6_K body is 0.8125 with its scales). */
+#define ORNK_DQ_UNIT 6144u
+#define ORNK_DQ_BYTES(DH) ((size_t)(DH) / 4 * 3)
+
 /* ---- generic fp32 ops behind gpu.h --------------------------------------- */
 int ornk_fill_f32(float *p, float v, size_t n, hipStream_t s);
 #define ORNK_STREAM_GRID 16384
@@ -143,7 +156,7 @@ typedef struct {
 } ornk_gu_prefill;
 
 typedef struct {
-    const uint8_t *dq;   /* [H/32][D/256][4][64][4][8] q + 32 */
+    const uint8_t *dq;   /* [H/32][D/256] units of ORNK_DQ_UNIT bytes: q + 32 in 6 bits */
     const uint16_t *dsc; /* [H/32][D/256][16][32] fp16 sub-block scales */
     const float *dd;     /* [D/256][H] d */
     const float *dmax;   /* [E+1][3] */

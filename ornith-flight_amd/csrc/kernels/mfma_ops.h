@@ -103,15 +103,24 @@ __device__ __forceinline__ v8h q4_b(uint32_t w, uint4 sc)
     return to_v8h(o[0], o[1], o[2], o[3]);
 }
 
-// Q6_K B operand: 8 bytes q + 32 (k order), sc as above.  B = sc * q with
-// q = (1024 + (q + 32)) - 1056 exact and |sc * q| <= 2048.
-__device__ __forceinline__ v8h q6_b(uint32_t q0, uint32_t q1, uint4 sc)
+// Packed 6-bit Q6_K values of one lane and column tile (the down layout of
+// prefill_pack.c): nw holds the low four bits of the 8 values (value e at
+// bit 4*(e/2) + 16*(e%2), the v_bfi pair order of magic_pair), cw the high
+// two bits (value e at bit 2*(e/2) + 16*(e%2)).  Pair i = values (2i, 2i+1)
+// as the fp16 pair (1024 + (q + 32)): the nibbles through one v_bfi, the
+// high bits into bits 4-5 of each half.
+__device__ __forceinline__ void q6_pairs(uint32_t nw, uint32_t cw, uint32_t (&p)[4])
+{
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        p[i] = magic_pair(nw >> (4 * i)) | (((cw >> (2 * i)) & 0x00030003u) << 4);
+}
+
+// Q6_K B operand from the pairs p (k order) and sc as above.  B = sc * q
+// with q = (1024 + (q + 32)) - 1056 exact and |sc * q| <= 2048.
+__device__ __forceinline__ v8h q6_b(const uint32_t (&p)[4], uint4 sc)
 {
     const uint32_t s[4] = {sc.x, sc.y, sc.z, sc.w};
-    const uint32_t p[4] = {__builtin_amdgcn_perm(0x64646464u, q0, 0x04010400u),
-                           __builtin_amdgcn_perm(0x64646464u, q0, 0x04030402u),
-                           __builtin_amdgcn_perm(0x64646464u, q1, 0x04010400u),
-                           __builtin_amdgcn_perm(0x64646464u, q1, 0x04030402u)};
     uint32_t o[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -127,13 +136,9 @@ __device__ __forceinline__ v8h q6_b(uint32_t q0, uint32_t q1, uint4 sc)
 // <= 1: fp16 holds every integer up to 2048 and every even one up to 4096).
 // The kernels add A_hi*b1 + A_lo*b1 + A_hi*b2; the dropped A_lo*b2 is below
 // 2^-21 of |A*B|, the order of the activation split itself.
-__device__ __forceinline__ void q6_b2(uint32_t q0, uint32_t q1, uint4 sc, v8h &b1, v8h &b2)
+__device__ __forceinline__ void q6_b2(const uint32_t (&p)[4], uint4 sc, v8h &b1, v8h &b2)
 {
     const uint32_t s[4] = {sc.x, sc.y, sc.z, sc.w};
-    const uint32_t p[4] = {__builtin_amdgcn_perm(0x64646464u, q0, 0x04010400u),
-                           __builtin_amdgcn_perm(0x64646464u, q0, 0x04030402u),
-                           __builtin_amdgcn_perm(0x64646464u, q1, 0x04010400u),
-                           __builtin_amdgcn_perm(0x64646464u, q1, 0x04030402u)};
     uint32_t o1[4], o2[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {

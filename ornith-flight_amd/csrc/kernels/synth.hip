@@ -279,34 +279,44 @@ __global__ void k_pack_q4k_scales(const uint8_t *__restrict__ blocks, uint16_t *
     }
 }
 
-// Q6_K q + 32 bytes: thread = one 8-byte group (8 values of one column).
+// Q6_K q + 32 in the packed 6-bit down layout (ORNK_DQ_UNIT units): thread
+// = one lane's pair of column tiles (2jp, 2jp + 1) in one unit, writing the
+// two nibble words and the high-bit word they share.
 // Bodies: [n_e][NB][K] x 208 B in store order, d separately.
 __global__ void k_pack_q6k_bytes(const uint8_t *__restrict__ body, uint8_t *__restrict__ qb,
                                  int n_e, int K, int NB, const int *__restrict__ slots)
 {
-    const size_t per_e = (size_t)K * NB * 32;  // 8-byte groups per expert
+    const size_t per_e = (size_t)K * NB * 16;  // lane x tile pairs per expert
     const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= per_e * (size_t)n_e) return;
     const int e = slots ? slots[t / per_e] : (int)(t / per_e);
     size_t w = t % per_e;
-    const int ntl = (int)(w % 4);
-    w /= 4;
+    const int jp = (int)(w % 2);
+    w /= 2;
     const int lane = (int)(w % 64);
     w /= 64;
     const int wv = (int)(w % 4);
     w /= 4;
     const int b = (int)(w % NB);
     const int kt = (int)(w / NB);
-    const int g = lane / 16, col = lane % 16, nt = 4 * wv + ntl, p = 16 * nt + col;
+    const int g = lane / 16, col = lane % 16;
     const uint8_t *eb = body + (size_t)e * K * NB * 208;
-    uint64_t out = 0;
-    for (int ei = 0; ei < 8; ++ei) {
-        const int k = 32 * kt + 8 * g + ei;
-        const uint8_t *blk = eb + ((size_t)b * K + k) * 208;
-        const int v = q6_at(blk + ORN_Q6K_OFF_QL, blk + ORN_Q6K_OFF_QH, p) + 32;
-        out |= (uint64_t)(uint8_t)v << (8 * ei);
+    uint32_t nib[2] = {0u, 0u}, hi = 0u;
+    for (int h = 0; h < 2; ++h) {
+        const int p = 16 * (4 * wv + 2 * jp + h) + col;
+        for (int ei = 0; ei < 8; ++ei) {
+            const int k = 32 * kt + 8 * g + ei;
+            const uint8_t *blk = eb + ((size_t)b * K + k) * 208;
+            const uint32_t v = (uint32_t)(q6_at(blk + ORN_Q6K_OFF_QL, blk + ORN_Q6K_OFF_QH, p) + 32);
+            nib[h] |= (v & 15u) << (4 * (ei / 2) + 16 * (ei % 2));
+            hi |= (v >> 4) << (2 * (ei / 2) + 16 * (ei % 2) + 8 * h);
+        }
     }
-    *reinterpret_cast<uint64_t *>(qb + ((size_t)e * per_e + (t % per_e)) * 8) = out;
+    uint8_t *unit = qb + (size_t)e * ORNK_DQ_BYTES((size_t)K * NB * 256) +
+                    ((size_t)kt * NB + b) * ORNK_DQ_UNIT;
+    const int wl = wv * 64 + lane;
+    *reinterpret_cast<uint2 *>(unit + wl * 16 + 8 * jp) = make_uint2(nib[0], nib[1]);
+    *reinterpret_cast<uint32_t *>(unit + 4096 + wl * 8 + 4 * jp) = hi;
 }
 
 // Q6_K scales, d, the per-expert max |d| and the largest |scale|: thread =
@@ -374,7 +384,7 @@ extern "C" int ornk_pack_prefill(const ornk_pack_args *a, hipStream_t s)
                            a->gu[m], a->psc[m], a->pmn[m], a->pd[m], a->pdm[m], a->dmax, m, n, D,
                            H / 256, a->slots);
     }
-    hipLaunchKernelGGL(k_pack_q6k_bytes, grid_for((size_t)n * DH / 8), dim3(256), 0, s,
+    hipLaunchKernelGGL(k_pack_q6k_bytes, grid_for((size_t)n * DH / 16), dim3(256), 0, s,
                        a->down_body, a->dq, n, H, D / 256, a->slots);
     hipLaunchKernelGGL(k_pack_q6k_scales, grid_for((size_t)n * DH / 256), dim3(256), 0, s,
                        a->down_body, a->down_d, a->dsc, a->dd, a->dmax, a->scmax, n, H, D / 256,

@@ -91,7 +91,7 @@ def test_q6k_prefill_layout_rebuilds_weights(L):
     blocks[4, 208:210] = [0x00, 0x00]        # d = 0
     blocks = blocks.reshape(-1)
     KT, NB = K // 32, M // 256
-    qb = np.zeros(KT * NB * 16 * 64 * 8, np.uint8)
+    qb = np.full(KT * NB * 6144, 0xFF, np.uint8)  # the packer clears what it ORs into
     sc = np.zeros(KT * NB * 16 * 32, np.uint16)
     d = np.zeros(NB * K, np.float32)
     dmax = np.zeros(1, np.float32)
@@ -101,7 +101,17 @@ def test_q6k_prefill_layout_rebuilds_weights(L):
     ok, ref = O.dequant_tensor(blocks, Q6, K * M)
     assert ok
     ref = ref.reshape(K, M)
-    qb6 = qb.reshape(KT, NB, 4, 64, 4, 8)  # [step][block column][wave][lane][tile][k]
+    # 6144-byte unit per [step][block column]: nibble words [wave][lane][tile],
+    # then high-bit words [wave][lane][tile pair]
+    unit = qb.reshape(KT, NB, 6144)
+    nib = unit[..., :4096].copy().view(np.uint32).reshape(KT, NB, 4, 64, 4)
+    hib = unit[..., 4096:].copy().view(np.uint32).reshape(KT, NB, 4, 64, 2)
+
+    def q6(kt, b, w, l, j, e):
+        sh = 4 * (e // 2) + 16 * (e % 2)
+        hs = 2 * (e // 2) + 16 * (e % 2) + 8 * (j % 2)
+        return int((nib[kt, b, w, l, j] >> sh) & 15) | (int((hib[kt, b, w, l, j // 2] >> hs) & 3) << 4)
+
     sc4 = f16(sc).reshape(KT, NB, 16, 32)
     d2 = d.reshape(NB, K).astype(np.float64)
     W = np.zeros((K, M), np.float64)
@@ -111,7 +121,7 @@ def test_q6k_prefill_layout_rebuilds_weights(L):
         for n in range(M):
             b, p = divmod(n, 256)
             nt, c = divmod(p, 16)
-            q = int(qb6[kt, b, nt // 4, 16 * g + c, nt % 4, e]) - 32
+            q = q6(kt, b, nt // 4, 16 * g + c, nt % 4, e) - 32
             W[k, n] = d2[b, k] * (sc4[kt, b, nt, kk] * q)
     assert np.array_equal(W.astype(np.float32).view(np.uint32), ref.view(np.uint32))
 
