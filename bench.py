@@ -284,12 +284,13 @@ def stack_active_experts(ctx, st, n_layers, T):
 
 def measure_stack(ctx, steps):
     """40 Ornith-shape layers x 257 experts resident in
-    HBM (47 GB with the MFMA layouts, generated on the device), a step = one
+    HBM (generated on the device and kept in the MFMA layouts only,
+    prefill_layout = 2: 23.8 GB, 1.13x the GGUF bytes), a step = one
     gpu_moe_forward_stack over all 40 layers (rmsnorm, MoE, residual per
     layer).  40 x 257 experts cannot stay in the 256 MB last-level cache
     between steps, unlike one layer's active experts."""
     n_layers = 40
-    st = om.Store(ctx, n_layers, D, H, E, K, True)
+    st = om.Store(ctx, n_layers, D, H, E, K, True, 2)
     t0 = time.perf_counter()
     for l in range(n_layers):
         st.fill_synthetic(l, SEED + l)

@@ -191,8 +191,13 @@ typedef struct {
     int n_experts;  /* E = 256 (<= 256) */
     int top_k;      /* k = 8 (<= 16) */
     int has_shared; /* 1: one always-on shared expert (model.c:1001-1007) */
-    int prefill_layout; /* 1: also keep the MFMA (prefill) layouts of every expert,
-                           about 1.2x the quantized bytes more; 0: decode layout only */
+    int prefill_layout; /* 1: also keep the MFMA layouts of every expert (about
+                           1.13x the quantized bytes more) beside the GGUF
+                           blocks; 0: GGUF blocks only (VALU path); 2: the MFMA
+                           layouts only: blocks are packed as they are uploaded
+                           or generated and not kept (1.13x the GGUF bytes in
+                           all); gpu_moe_store_get_experts, the VALU path and
+                           cache_slots are then unavailable */
     int file_layout;    /* 1: expert matrices and router in GGUF file orientation
                            (input index fastest: ggml ne = [K, M]; see
                            gpu_moe_store_set_experts); needs prefill_layout = 0.

@@ -259,7 +259,8 @@ static int shape_ok(const ornith_moe_shape *s)
     return s && s->n_layers > 0 && widths_ok(s->d_model, s->hidden) && s->n_experts > 0 &&
            s->n_experts <= 256 && s->top_k > 0 && s->top_k <= 16 && s->top_k <= s->n_experts &&
            (s->has_shared == 0 || s->has_shared == 1) && s->d_model % 128 == 0 &&
-           (s->prefill_layout == 0 || s->prefill_layout == 1) &&
+           (s->prefill_layout >= 0 && s->prefill_layout <= 2) &&
+           (s->prefill_layout != 2 || s->cache_slots == 0) &&
            (s->file_layout == 0 || (s->file_layout == 1 && !s->prefill_layout &&
                                     ornk_file_supported(s->d_model, s->hidden))) &&
            s->cache_slots >= 0;
@@ -326,13 +327,16 @@ ornith_moe_store *gpu_moe_store_create(gpu_context *ctx, const ornith_moe_shape 
                       (void **)&st->down_d, (void **)&st->router_q, (void **)&st->bias,
                       (void **)&st->norm, (void **)&st->shexp_gate};
     const int cached = shape->cache_slots > 0;
+    /* prefill_layout = 2: the experts live in the MFMA layouts alone (the
+     * GGUF blocks are packed as they arrive and not kept) */
+    const int lean = shape->prefill_layout == 2;
     st->has_shexp_gate = (unsigned char *)calloc(L, 1);
     if (!st->has_shexp_gate) {
         orn_set_err(ctx, ORN_ENOMEM, "store tables");
         store_free(st);
         return NULL;
     }
-    for (int i = cached ? 4 : 0; i < 8; ++i) {
+    for (int i = cached || lean ? 4 : 0; i < 8; ++i) {
         if (hipMalloc(ptrs[i], sizes[i]) != hipSuccess ||
             hipMemsetAsync(*ptrs[i], 0, sizes[i], ctx->stream) != hipSuccess) {
             orn_set_err(ctx, ORN_ENOMEM, "store allocation of %zu bytes failed", sizes[i]);
@@ -570,7 +574,11 @@ int gpu_moe_store_set_experts(gpu_context *ctx, ornith_moe_store *st, int layer,
         if ((rc = orn_hip_check(ctx, hipStreamSynchronize(s), "set_experts"))) return rc;
         orn_cache_invalidate(st->cache, layer, expert_first, n);
     }
-    if (matrix != ORN_MAT_DOWN) {
+    if (st->sh.prefill_layout == 2) {  /* no GGUF copy: packed from the host blocks */
+        rc = matrix != ORN_MAT_DOWN
+                 ? upload_q4k_prefill(ctx, st, layer, matrix, expert_first, n, blocks)
+                 : upload_q6k_prefill(ctx, st, layer, expert_first, n, blocks);
+    } else if (matrix != ORN_MAT_DOWN) {
         uint8_t *tmp = (uint8_t *)malloc((size_t)n * nb * 144);
         if (!tmp) return orn_set_err(ctx, ORN_ENOMEM, "host staging");
         for (int i = 0; i < n; ++i) {
@@ -708,7 +716,24 @@ int gpu_moe_store_fill_synthetic(gpu_context *ctx, ornith_moe_store *st, int lay
     g.file = st->sh.file_layout;
     g.router = st->router_q + (size_t)layer * E * D;
     int rc;
-    if (st->cache) {
+    uint8_t *stage = NULL;  /* a lean store's one-layer staging, freed below */
+    if (st->sh.prefill_layout == 2) {
+        /* generated on the device into a one-layer staging area, packed
+         * into the MFMA layouts below, then released */
+        const size_t bytes = S * nb * 500;
+        if (hipMalloc((void **)&stage, bytes) != hipSuccess)
+            return orn_set_err(ctx, ORN_ENOMEM, "fill_synthetic: %zu bytes of staging", bytes);
+        g.gate = stage;
+        g.up = stage + S * nb * 144;
+        g.down_body = stage + S * nb * 288;
+        g.down_d = (uint16_t *)(stage + S * nb * 496);
+        rc = orn_hip_check(ctx, (hipError_t)ornk_synth_layer(&g, s), "synthetic layer");
+        if (rc) {
+            hipStreamSynchronize(s);
+            hipFree(stage);
+            return rc;
+        }
+    } else if (st->cache) {
         /* generated on the device into a one-layer staging area, then
          * copied to the host tier */
         if ((rc = orn_cache_quiesce(ctx, st->cache))) return rc;
@@ -751,14 +776,21 @@ int gpu_moe_store_fill_synthetic(gpu_context *ctx, ornith_moe_store *st, int lay
     }
     if (zipf_s > 0.0f) {
         float *b = (float *)malloc((size_t)E * sizeof(float));
-        if (!b) return orn_set_err(ctx, ORN_ENOMEM, "host staging");
+        if (!b) {
+            hipStreamSynchronize(s);
+            hipFree(stage);
+            return orn_set_err(ctx, ORN_ENOMEM, "host staging");
+        }
         orn_synth_zipf_bias(seed, orn_synth_stream(layer, ORN_SYN_ZIPF, 0), E, zipf_s, b);
         rc = orn_hip_check(ctx, hipMemcpyAsync(st->bias + (size_t)layer * E, b,
                                                (size_t)E * sizeof(float), hipMemcpyHostToDevice, s),
                            "upload bias");
         hipStreamSynchronize(s);
         free(b);
-        if (rc) return rc;
+        if (rc) {
+            hipFree(stage);
+            return rc;
+        }
     }
     st->has_bias[layer] = zipf_s > 0.0f ? 1 : 0;
     if (st->sh.prefill_layout && !st->cache) {
@@ -785,17 +817,19 @@ int gpu_moe_store_fill_synthetic(gpu_context *ctx, ornith_moe_store *st, int lay
         pa.dmax = st->dmax + slot0 * 3;
         pa.scmax = st->dev_scmax;
         rc = orn_hip_check(ctx, (hipError_t)ornk_pack_prefill(&pa, s), "prefill layouts");
-        if (rc) return rc;
         /* host mirrors: the per-slot maxima (re-uploaded by later partial
          * uploads of the layer) and the layer's largest Q6_K sub-scale */
         int scmax = 0;
-        rc = orn_hip_check(ctx, hipMemcpyAsync(st->dmax_host + slot0 * 3, pa.dmax,
-                                               (size_t)E1 * 3 * sizeof(float),
-                                               hipMemcpyDeviceToHost, s), "dmax copy");
+        if (!rc)
+            rc = orn_hip_check(ctx, hipMemcpyAsync(st->dmax_host + slot0 * 3, pa.dmax,
+                                                   (size_t)E1 * 3 * sizeof(float),
+                                                   hipMemcpyDeviceToHost, s), "dmax copy");
         if (!rc)
             rc = orn_hip_check(ctx, hipMemcpyAsync(&scmax, st->dev_scmax, sizeof(int),
                                                    hipMemcpyDeviceToHost, s), "scmax copy");
         if (!rc) rc = orn_hip_check(ctx, hipStreamSynchronize(s), "prefill layouts");
+        hipStreamSynchronize(s);
+        hipFree(stage);  /* NULL unless lean */
         if (rc) return rc;
         st->q6_scmax[layer] = scmax;
     }
@@ -813,6 +847,9 @@ int gpu_moe_store_get_experts(gpu_context *ctx, ornith_moe_store *st, int layer,
         expert_first + n > E1 || matrix < 0 || matrix > 2)
         return orn_set_err(ctx, ORN_EINVAL, "get_experts: bad layer/expert range/matrix");
     if (n == 0) return ORN_OK;
+    if (st->sh.prefill_layout == 2)
+        return orn_set_err(ctx, ORN_EUNSUPPORTED,
+                           "get_experts: a store with prefill_layout = 2 keeps no GGUF blocks");
     const int D = st->sh.d_model, H = st->sh.hidden, file = st->sh.file_layout;
     const size_t nb = st->blocks_per_matrix;
     const size_t slot0 = (size_t)layer * E1 + (size_t)expert_first;
@@ -1054,6 +1091,13 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
      * wide instances, which split sc * q in two exact fp16 operands. */
     const int mfma_ok = sh->prefill_layout;
     int use_mfma = mfma_ok && T >= ORN_MOE_MFMA_MIN_TOKENS;
+    if (sh->prefill_layout == 2) {
+        if (flags & ORN_MOE_PATH_VALU)
+            return orn_set_err(ctx, ORN_EUNSUPPORTED,
+                               "the VALU path reads GGUF blocks, which a store with "
+                               "prefill_layout = 2 does not keep");
+        use_mfma = 1;
+    }
     if (flags & ORN_MOE_PATH_VALU) use_mfma = 0;
     if (flags & ORN_MOE_PATH_MFMA) {
         if (!mfma_ok)
@@ -1125,7 +1169,7 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     a.rows_max = p.rows_max;
     a.items_max = p.items_max;
     a.tchunk = p.tchunk;
-    if (!st->cache) {  /* a streamed store's slots are set after the dispatch */
+    if (!st->cache && st->gate) {  /* a streamed store's slots are set after the dispatch */
         a.gate = st->gate + (size_t)layer * E1nb * 144;
         a.up = st->up + (size_t)layer * E1nb * 144;
         a.down_body = st->down_body + (size_t)layer * E1nb * 208;

@@ -327,12 +327,15 @@ class Context:
 class Store:
     def __init__(self, ctx: Context, n_layers, D, H, E, k, has_shared=True, prefill_layout=True,
                  file_layout=False, cache_slots=0):
-        """file_layout: experts and router in GGUF file orientation (input index
-        fastest); needs prefill_layout=False.  cache_slots > 0: experts in a
-        host tier, streamed through that many device slots."""
+        """prefill_layout: True (or 1) keeps the MFMA layouts beside the GGUF
+        blocks, 2 keeps the MFMA layouts only.  file_layout: experts and
+        router in GGUF file orientation (input index fastest); needs
+        prefill_layout=False.  cache_slots > 0: experts in a host tier,
+        streamed through that many device slots."""
         self.ctx = ctx
-        self.shape = MoEShape(n_layers, D, H, E, k, 1 if has_shared else 0,
-                              1 if prefill_layout else 0, 1 if file_layout else 0, cache_slots)
+        pl = 2 if prefill_layout == 2 else (1 if prefill_layout else 0)
+        self.shape = MoEShape(n_layers, D, H, E, k, 1 if has_shared else 0, pl,
+                              1 if file_layout else 0, cache_slots)
         self.ptr = lib().gpu_moe_store_create(ctx.ptr, C.byref(self.shape))
         if not self.ptr:
             raise RuntimeError("gpu_moe_store_create failed: " + ctx.last_error())

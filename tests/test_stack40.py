@@ -7,7 +7,8 @@ test is fed) exactly, through the store read-back; its router through the
 pinned logits; its MFMA layouts through forwards that must equal forwards of
 a store packed on the host, bit for bit.
 
-The stack test fills all 40 layers (47 GB with the MFMA layouts), runs
+The stack test fills all 40 layers (23.8 GB: a store that keeps the MFMA
+layouts only), runs
 gpu_moe_forward_stack (x <- x + MoE_l(rmsnorm(x)), model.c:992-1144 per
 layer) and checks that it equals the chain of 40 single-layer forwards bit
 for bit, and teacher-forces layers 0, 19 and 39 against the oracle
@@ -156,9 +157,10 @@ def oracle_chain(om, seed, L, x0):
 
 
 def test_stack40_resident_decode(om, ctx):
-    """40 layers x 257 experts resident, T = 1 (and 16)."""
+    """40 layers x 257 experts resident, T = 1 (and 16),
+    in a store that keeps the MFMA layouts only (prefill_layout = 2)."""
     L, seed = 40, 1234
-    st = om.Store(ctx, L, D, H, E, K, True)
+    st = om.Store(ctx, L, D, H, E, K, True, 2)
     try:
         import time
         t0 = time.time()
