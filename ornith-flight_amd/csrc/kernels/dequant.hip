@@ -92,6 +92,8 @@ __device__ __forceinline__ float4 q6k_quad(const uint8_t *blk, int pos0)
 }
 
 // 64 threads per block of 256 elements, four blocks per work group pass.
+// Outputs are written once and not read here again: non-temporal stores,
+// each instruction 1 KB contiguous per wave.
 template <bool Q6>
 __global__ void __launch_bounds__(256) k_dequant_quad(const uint8_t *src, float4 *dst, uint64_t n_blocks)
 {
@@ -99,38 +101,44 @@ __global__ void __launch_bounds__(256) k_dequant_quad(const uint8_t *src, float4
     for (uint64_t b = (uint64_t)blockIdx.x * 4 + sub_blk; b < n_blocks; b += (uint64_t)gridDim.x * 4) {
         const float4 v = Q6 ? q6k_quad(src + b * ORN_Q6K_BYTES, pos0)
                             : q4k_quad(src + b * ORN_Q4K_BYTES, pos0);
-        dst[b * (ORN_QK_K / 4) + (pos0 >> 2)] = v;
+        __builtin_nontemporal_store(__builtin_bit_cast(v4f, v),
+                                    reinterpret_cast<v4f *>(dst + b * (ORN_QK_K / 4) + (pos0 >> 2)));
     }
 }
 
-// Q4_K with 16-byte accesses (src and dst 16-byte aligned; a 144-byte block is
-// nine 16-byte words): 16 lanes per block, lane l writes outputs 16l..16l+15
-// of sub-block j = l/2 from one header word (d, dmin, scales; the same word
-// for the block's 16 lanes) and one word of quants, bytes 16 + 32(l/4) +
-// 16(l&1) .. +15 (low nibbles for even j, high for odd), with the reference's
-// arithmetic: d1 = d*sc, m1 = dmin*m, y = d1*q - m1 (gguf.c:43-61).
+// Q4_K, src and dst 16-byte aligned (a 144-byte block is nine 16-byte
+// words): 16 lanes per block and a header word (d, dmin, scales) they share.
+// Store i of lane l writes outputs 64i + 4l .. +3, so that each store
+// instruction covers 256 contiguous bytes per block (1 KB per wave, written
+// non-temporally): sub-block j = 2i + l/8, from the quant word at bytes
+// 16 + 32i + 4(l&7) (low nibbles for even j, high for odd), with the
+// reference's arithmetic: d1 = d*sc, m1 = dmin*m, y = d1*q - m1
+// (gguf.c:43-61).  (Lane l writing outputs 16l..16l+15, 64-byte strided per
+// instruction, ran at 3.4 TB/s; this at 6.2.)
 __global__ void __launch_bounds__(256) k_dequant_q4k16(const uint4 *__restrict__ src,
                                                        v4f *__restrict__ dst, uint64_t n_blocks)
 {
     const int l = threadIdx.x & 15;
-    const int j = l >> 1;
     for (uint64_t b = (uint64_t)blockIdx.x * 16 + (threadIdx.x >> 4); b < n_blocks;
          b += (uint64_t)gridDim.x * 16) {
         const uint4 *blk = src + b * (ORN_Q4K_BYTES / 16);
         const uint4 hd = blk[0];
-        const uint4 qw = blk[1 + 2 * (l >> 2) + (l & 1)];
-        uint32_t sc, m;
-        orn_scale_min_k4(j, hd.y, hd.z, hd.w, sc, m);
-        const float d1 = orn_half_to_float(hd.x & 0xFFFFu) * (float)sc;
-        const float m1 = orn_half_to_float(hd.x >> 16) * (float)m;
-        const uint32_t sh = 4u * (uint32_t)(j & 1);
-        const uint32_t w[4] = {qw.x, qw.y, qw.z, qw.w};
-        v4f *o = dst + b * (ORN_QK_K / 4) + 4 * l;
+        const uint32_t *qs = reinterpret_cast<const uint32_t *>(blk + 1);
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = qs[8 * i + (l & 7)];
+        const float d = orn_half_to_float(hd.x & 0xFFFFu), dm = orn_half_to_float(hd.x >> 16);
+        const uint32_t sh = 4u * (uint32_t)(l >> 3);
+        v4f *o = dst + b * (ORN_QK_K / 4) + l;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
+            uint32_t sc, m;
+            orn_scale_min_k4(2 * i + (l >> 3), hd.y, hd.z, hd.w, sc, m);
+            const float d1 = d * (float)sc, m1 = dm * (float)m;
             const uint32_t q = (w[i] >> sh) & 0x0F0F0F0Fu;
-            o[i] = (v4f){d1 * (float)(q & 0xFFu) - m1, d1 * (float)((q >> 8) & 0xFFu) - m1,
-                         d1 * (float)((q >> 16) & 0xFFu) - m1, d1 * (float)(q >> 24) - m1};
+            const v4f r = {d1 * (float)(q & 0xFFu) - m1, d1 * (float)((q >> 8) & 0xFFu) - m1,
+                           d1 * (float)((q >> 16) & 0xFFu) - m1, d1 * (float)(q >> 24) - m1};
+            __builtin_nontemporal_store(r, &o[16 * i]);
         }
     }
 }
@@ -138,20 +146,22 @@ __global__ void __launch_bounds__(256) k_dequant_q4k16(const uint4 *__restrict__
 __global__ void k_dequant_q4k(const uint8_t *src, float *dst, uint64_t n_blocks)
 {
     for (uint64_t b = blockIdx.x; b < n_blocks; b += gridDim.x)
-        dst[b * ORN_QK_K + threadIdx.x] = q4k_elem(src + b * ORN_Q4K_BYTES, (int)threadIdx.x);
+        __builtin_nontemporal_store(q4k_elem(src + b * ORN_Q4K_BYTES, (int)threadIdx.x),
+                                    dst + b * ORN_QK_K + threadIdx.x);
 }
 
 __global__ void k_dequant_q6k(const uint8_t *src, float *dst, uint64_t n_blocks)
 {
     for (uint64_t b = blockIdx.x; b < n_blocks; b += gridDim.x)
-        dst[b * ORN_QK_K + threadIdx.x] = q6k_elem(src + b * ORN_Q6K_BYTES, (int)threadIdx.x);
+        __builtin_nontemporal_store(q6k_elem(src + b * ORN_Q6K_BYTES, (int)threadIdx.x),
+                                    dst + b * ORN_QK_K + threadIdx.x);
 }
 
 __global__ void k_dequant_f16(const uint8_t *src, float *dst, uint64_t n)
 {
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
-        dst[i] = orn_half_to_float(orn_ld_u16(src + 2 * i));
+        __builtin_nontemporal_store(orn_half_to_float(orn_ld_u16(src + 2 * i)), dst + i);
 }
 
 // One output element per thread: linear = i*E + e, then the single-element
@@ -171,7 +181,7 @@ __global__ void k_slice(const uint8_t *src, int type, uint64_t per, uint64_t n_e
             v = orn_half_to_float(orn_ld_u16(src + 2 * lin));
         else
             v = reinterpret_cast<const float *>(src)[lin];
-        dst[i] = v;
+        __builtin_nontemporal_store(v, dst + i);
     }
 }
 
