@@ -553,7 +553,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no "
-              f"multi-GPU path (expert-parallel design is described in DESIGN.md).", file=sys.stderr)
+              f"multi-GPU path (the expert-parallel shares run one GPU's part).", file=sys.stderr)
         sys.exit(2)
 
     ctx = om.Context()

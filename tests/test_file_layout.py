@@ -347,7 +347,7 @@ def test_file_layout_shexp_gate(om, ctx, ornith_file, T):
 @pytest.mark.parametrize("T,flags,mode", [(16, "norm", 0), (100, "norm", 0), (16, "", 1),
                                           (100, "norm", 1)])
 def test_file_layout_norm_resid_literal(om, ctx, ornith_file, T, flags, mode):
-    """The call INTEGRATION.md prescribes (ORN_MOE_NORM with resid = x):
+    """The call the engine integration makes (ORN_MOE_NORM with resid = x):
     at T <= 64 the router's fused norm writes the normalised rows the
     expert steps read, above that the separate norm kernel does; and the
     literal routing mode (model.c:1027-1049)."""
