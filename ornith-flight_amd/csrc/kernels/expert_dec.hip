@@ -38,6 +38,12 @@ typedef __amdgpu_buffer_rsrc_t rsrc_t;
 // four work groups per CU, 37 KB of LDS each) instead of three with 4 steps.
 // Measured: 25.8 -> 23.7 us at 16 tokens, 6.9 -> 6.4 us at one token.
 #define ORN_DEC_NR_MID 2
+// Gate/up: 2 steps in flight and activation chunks of 2 steps.  One-tile
+// instances (20 KB of LDS, 121 registers) run four waves per SIMD: 29.7 ->
+// 29.1 us at 16 tokens (3 steps in flight spills; 5 waves with one step in
+// flight: 45.9 us); two-tile ones (40 KB, 148 registers) three: 58.7 ->
+// 52.5 us on the 256-token Zipf batch.
+#define ORN_DEC_NR_GU 2
 
 // Two-tile down instances keep the slice's scales in LDS and their ring holds
 // only quant words: every step of a slice up to 16 in flight, 8 of the
@@ -94,7 +100,7 @@ struct GuRing {
 };
 
 template <int NR, int KT, int KC, int RT>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT > 1 ? 2 : 3)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT > 1 ? 3 : 4)))
     k_gateup_dec(ornk_gu_prefill P, const float *__restrict__ xn,
                  const float *__restrict__ x_amax, const int *__restrict__ ctl,
                  const int4 *__restrict__ items, const int *__restrict__ row_token,
@@ -621,11 +627,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT > 1
 // Decode instances: work items of <= 16 rows (one row tile), or <= 32 (two,
 // for batches above 64 tokens whose hot experts span several items); KT =
 // D/32/ks (gate/up) or H/32/ks (down) reduction steps per slice, 4 to 32;
-// activation tiles in chunks of 4 steps (LDS per row tile: 2 x 20 KB for
-// gate/up, 2 x 10 KB for down), of 2 steps for two-tile gate/up.  Two-tile
-// down instances also hold the slice's scales (1 KB per step, at most
-// 32 KB), so that every instance keeps at most 73 KB (two work groups per CU,
-// the occupancy their registers allow).
+// activation tiles double-buffered in chunks of 2 steps for gate/up (LDS:
+// 2 x 10 KB per row tile) and of 4 for down (2 x 10 KB).  Two-tile down
+// instances also hold the slice's scales (1 KB per step, at most 32 KB), so
+// that every instance keeps at most 73 KB (two work groups per CU, the
+// occupancy their registers allow); one-tile instances keep at most 37 KB
+// (four work groups per CU, four waves per SIMD where their registers
+// allow).  Two-tile gate/up: 40 KB, three work groups and waves per SIMD.
 extern "C" int ornk_dec_supported(int kt_gu, int kt_dn)
 {
     auto ok = [](int kt) { return kt == 4 || kt == 8 || kt == 16 || kt == 32; };
@@ -649,7 +657,7 @@ extern "C" int ornk_moe_gateup_dec(const ornk_moe_args *a, hipStream_t s)
     }
     const dim3 grid(a->items_max * 2 * (a->H / 256) * ks);
 #define ORN_GU_DEC(K, R)                                                                       \
-    ORN_LAUNCH_EV2(st, a->ev_stop, (k_gateup_dec<ORN_DEC_NR, K, 4 / R, R>), grid, dim3(256), 0, s, \
+    ORN_LAUNCH_EV2(st, a->ev_stop, (k_gateup_dec<ORN_DEC_NR_GU, K, 2, R>), grid, dim3(256), 0, s, \
                    a->gu_pf, xin, a->x_amax, a->ctl, reinterpret_cast<const int4 *>(a->items), \
                    a->row_token, a->gu_part, a->T, a->D, a->H, ks, a->rows_max)
 #define ORN_GU_DEC_RT(R)                \
