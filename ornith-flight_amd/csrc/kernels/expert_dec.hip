@@ -36,7 +36,9 @@ typedef __amdgpu_buffer_rsrc_t rsrc_t;
 // The down instances that form mid themselves (decode batches up to 64
 // tokens) keep 2 steps in flight at 112 registers: four waves per SIMD (and
 // four work groups per CU, 37 KB of LDS each) instead of three with 4 steps.
-// Measured: 25.8 -> 23.7 us at 16 tokens, 6.9 -> 6.4 us at one token.
+// Measured: 25.8 -> 23.7 us at 16 tokens, 6.9 -> 6.4 us at one token.  Their
+// wide instances (real-range Q6_K scales) fit 128 registers the same way
+// instead of 166: 28.2 -> 26.4 us at 16 tokens.
 #define ORN_DEC_NR_MID 2
 // Gate/up: 2 steps in flight and activation chunks of 2 steps.  One-tile
 // instances (20 KB of LDS, 121 registers) run four waves per SIMD: 29.7 ->
@@ -346,7 +348,7 @@ struct DnRing {
 
 // WIDE: Q6_K sub-scales up to |128| (q6_b2: three MFMAs per tile and step).
 template <int NR, int KT, int KC, int KSG, int RT, bool WIDE>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT > 1 || WIDE ? 2 : (KSG ? 4 : 3))))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT > 1 ? 2 : KSG ? (WIDE ? 3 : 4) : WIDE ? 2 : 3)))
     k_down_dec(ornk_dn_prefill P, const float *__restrict__ mid,
                const float *__restrict__ mid_amax, const int *__restrict__ ctl,
                const int4 *__restrict__ items, float *__restrict__ dn, int D, int H, int ks,
@@ -700,7 +702,7 @@ extern "C" int ornk_moe_down_dec(const ornk_moe_args *a, hipStream_t s)
     const bool wide = a->q6_wide != 0;
     if (RT == 1 && ornk_down_dec_fuses_mid(a->T, a->H, a->ks_gu, ks)) {
 #define ORN_DN_MID(KSG, W)                                                                      \
-    ORN_LAUNCH_EV(a, (k_down_dec<W ? ORN_DEC_NR : ORN_DEC_NR_MID, 8, 4, KSG, 1, W>), grid, dim3(256), 0, s, a->dn_pf, \
+    ORN_LAUNCH_EV(a, (k_down_dec<ORN_DEC_NR_MID, 8, 4, KSG, 1, W>), grid, dim3(256), 0, s, a->dn_pf, \
                   a->mid, a->mid_amax, a->ctl, reinterpret_cast<const int4 *>(a->items),         \
                   a->dn_part, a->D, a->H, ks, a->rows_max, a->gu_part, shared_rows)
 #define ORN_DN_MID_W(KSG)         \
