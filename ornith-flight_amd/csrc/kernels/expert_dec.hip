@@ -357,6 +357,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT > 1
     constexpr int NCHK = KT / KC, NBUF = NCHK > 1 ? 2 : 1;
     constexpr int LC = 2 * KC;
     constexpr int KV = 32 * KT;  // reduction values of the slice
+    static_assert(LC % 8 == 0 && KT % KC == 0, "a thread stores whole 8-value groups of a chunk");
     static_assert(KSG == 0 || RT == 1, "mid is formed in the kernel for one row tile only");
     static_assert(KSG == 0 || 32 * KT == 256, "mid is formed one value per thread");
     static_assert(KT % 4 == 0 && NR >= 1 && NR <= KT, "slices of 4k steps");

@@ -110,12 +110,12 @@ def test_router_pc_logits_bit_exact(om, ctx, store, T, norm):
 
 
 @pytest.mark.parametrize("norm", [False, True], ids=["x", "rmsnorm"])
-@pytest.mark.parametrize("T", [100, 256])
+@pytest.mark.parametrize("T", [65, 100, 256, 383])
 def test_router_dec_logits_bit_exact(om, ctx, store, T, norm):
     check(om, ctx, store, T, 0, norm)
 
 
-@pytest.mark.parametrize("T", [400, 2048])
+@pytest.mark.parametrize("T", [384, 400, 1023, 1024, 2048])
 def test_router_seq_logits_bit_exact(om, ctx, store, T):
     """LDS-staged chains: 4 tokens per block (T < 1024), 16 (T >= 1024)."""
     check(om, ctx, store, T, 0, T == 400)
