@@ -237,17 +237,41 @@ __global__ void __launch_bounds__(256)
                 __syncthreads();
                 const v4f *wr = &wl[sl][lane * ORN_RWS4];
                 const v4f *xr = &xl[sl][wave * TPW * (ORN_RDC / 4)];
+                // Each quad's LDS reads are issued before the previous
+                // quad's arithmetic (two register sets; the empty asm keeps
+                // the reads above it and the arithmetic below it): 78 ->
+                // 71-74 us at 2048 tokens.  Groups of two quads ran 74-77,
+                // and of four took a wave per SIMD in registers.
+                constexpr int RG = 1, NG = ORN_RDC / 4 / RG;
+                v4f wA[RG], wB[RG], xA[TPW][RG], xB[TPW][RG];
+                auto rd = [&](v4f (&w)[RG], v4f (&xv)[TPW][RG], int g) {
 #pragma unroll
-                for (int d4 = 0; d4 < ORN_RDC / 4; ++d4) {
-                    const v4f wv = wr[d4];
+                    for (int q = 0; q < RG; ++q) {
+                        w[q] = wr[RG * g + q];
 #pragma unroll
-                    for (int j = 0; j < TPW; ++j) {
-                        const v4f xv = xr[j * (ORN_RDC / 4) + d4];
-                        acc[j] = acc[j] + xv.x * wv.x;
-                        acc[j] = acc[j] + xv.y * wv.y;
-                        acc[j] = acc[j] + xv.z * wv.z;
-                        acc[j] = acc[j] + xv.w * wv.w;
+                        for (int j = 0; j < TPW; ++j) xv[j][q] = xr[j * (ORN_RDC / 4) + RG * g + q];
                     }
+                };
+                rd(wA, xA, 0);
+#pragma unroll
+                for (int g = 0; g < NG; ++g) {
+                    v4f(&wc)[RG] = (g & 1) ? wB : wA;
+                    v4f(&wn)[RG] = (g & 1) ? wA : wB;
+                    v4f(&xc)[TPW][RG] = (g & 1) ? xB : xA;
+                    v4f(&xn)[TPW][RG] = (g & 1) ? xA : xB;
+                    if (g + 1 < NG) rd(wn, xn, g + 1);
+#pragma unroll
+                    for (int j = 0; j < TPW; ++j) asm volatile("" : "+v"(acc[j])::"memory");
+#pragma unroll
+                    for (int q = 0; q < RG; ++q)
+#pragma unroll
+                        for (int j = 0; j < TPW; ++j) {
+                            const v4f xv = xc[j][q], wv = wc[q];
+                            acc[j] = acc[j] + xv.x * wv.x;
+                            acc[j] = acc[j] + xv.y * wv.y;
+                            acc[j] = acc[j] + xv.z * wv.z;
+                            acc[j] = acc[j] + xv.w * wv.w;
+                        }
                 }
             }
         }
