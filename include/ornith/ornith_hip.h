@@ -337,6 +337,18 @@ enum { ORN_ROUTE_RENORM = 0, ORN_ROUTE_LITERAL = 1 };
 /* Scale the shared expert by its gate (gpu_moe_store_set_shexp_gate; a
  * layer without one is refused with ORN_EINVAL).  Not in the reference. */
 #define ORN_MOE_SHEXP_GATE 32u
+/* Routing of the smallest decode batches (up to 4 tokens, D a power-of-two
+ * multiple of 256 up to 4096, E <= 256).  By default the router logits are fp64 sums
+ * of the reference's fp32 products with a rigorous bound on their distance
+ * from the reference's sequential fp32 chain (model.c:1017-1025); the top-k
+ * selection equals the chain's exactly (where the bounds do not decide it,
+ * the undecided experts run the chain itself), and logits, selection and
+ * dispatch run in one launch.  The logits gpu_moe_last_logits reports are
+ * then those sums rounded to fp32 (within a few ulp of the chain's), and the
+ * weights follow from them.  With this flag every logit is the chain's,
+ * bit for bit, on every batch size (a slower router at decode sizes).  Not
+ * in the reference. */
+#define ORN_MOE_EXACT_LOGITS 64u
 
 typedef struct {
     int route_mode; /* ORN_ROUTE_RENORM (default, model_get_routing) or ORN_ROUTE_LITERAL */
@@ -405,6 +417,11 @@ int gpu_moe_last_logits(gpu_context *ctx, float *out, size_t max_floats, size_t 
  * exchange selection (tied or non-finite logits among the top k+1).  After
  * gpu_moe_forward_noalloc: valid until the next noalloc call on that GPU. */
 int gpu_moe_last_stats(gpu_context *ctx, int *n_slots, int *n_rows, int *n_literal);
+/* Tokens of the last forward whose certified routing (see
+ * ORN_MOE_EXACT_LOGITS) ran the reference's exact chain for some of their
+ * logits because the bounds did not decide the selection (0 for the exact
+ * routers).  No reference counterpart: a test and measurement helper. */
+int gpu_moe_last_chained(gpu_context *ctx, int *n_chained);
 
 /* ---------------------------------------------------------------------------
  * Kernel timing with HIP events recorded on the context's stream around every

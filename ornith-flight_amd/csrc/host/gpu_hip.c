@@ -68,6 +68,7 @@ void gpu_destroy(gpu_context *ctx)
     hipStreamSynchronize(ctx->stream);
     gpu_profile_enable(ctx, 0);
     orn_ws_release(ctx);
+    if (ctx->sync) hipFree(ctx->sync);
     if (ctx->ctl_host) hipHostFree(ctx->ctl_host);
     hipStreamDestroy(ctx->stream);
     memset(ctx, 0, sizeof *ctx);

@@ -43,6 +43,11 @@ struct gpu_context {
     /* this device's fixed scratch, resolved by the first
      * gpu_moe_forward_noalloc call on the context (NULL until then) */
     void *scratch;
+    /* counters and the generation word of the certified routing kernel
+     * (ORNK_SYNC_BYTES, zeroed on the stream at allocation; the kernel keeps
+     * its counter at zero between launches).  Its own allocation: the
+     * workspace is shared with other ops and is reallocated as it grows. */
+    int *sync;
     /* device counters read back after a forward */
     int *ctl_host; /* pinned mirror of the last forward's counters */
     int *last_ctl; /* device counters of the last forward (inside the workspace) */

@@ -104,6 +104,26 @@ void *orn_ws_get(gpu_context *ctx, size_t bytes)
     return ctx->ws.base;
 }
 
+/* The certified routing kernel's counter area: allocated on first use and
+ * zeroed by a fill kernel on the context's stream (ordered before the
+ * kernels that use it; a null-stream memset would not be). */
+static int *ctx_sync(gpu_context *ctx)
+{
+    if (ctx->sync) return ctx->sync;
+    void *p = NULL;
+    if (hipMalloc(&p, ORNK_SYNC_BYTES) != hipSuccess) {
+        orn_set_err(ctx, ORN_ENOMEM, "allocation of the routing counters failed");
+        return NULL;
+    }
+    if (ornk_fill_f32((float *)p, 0.0f, ORNK_SYNC_BYTES / 4, ctx->stream) != hipSuccess) {
+        hipFree(p);
+        orn_set_err(ctx, ORN_EHIP, "routing counter initialisation failed");
+        return NULL;
+    }
+    ctx->sync = (int *)p;
+    return ctx->sync;
+}
+
 void orn_ws_release(gpu_context *ctx)
 {
     if (ctx->ws.base) hipFree(ctx->ws.base);
@@ -1112,11 +1132,25 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     if (file) use_mfma = 0;  /* the mid and combine steps run as on the VALU path */
     plan_t p = file ? make_plan_file(sh, T) : make_plan(sh, T, use_mfma);
 
-    size_t off = 0;
+    /* Certified routing of the smallest decode batches (router_cert.hip):
+     * logits, top-k and dispatch in one launch.  Streamed stores keep it too
+     * (the slot list is read back after the dispatch either way). */
+    const int cert = !(flags & ORN_MOE_EXACT_LOGITS) && ornk_route_cert_supported(T, D, E, k);
+
+    /* the fixed scratch keeps its first ORNK_SYNC_BYTES for the routing
+     * counters (zeroed when the scratch is first resolved); otherwise they
+     * have an allocation of their own */
+    size_t off = fixed_ws ? ORNK_SYNC_BYTES : 0;
+    int *sync = NULL;
+    if (cert) {
+        sync = fixed_ws ? (int *)fixed_ws : ctx_sync(ctx);
+        if (!sync) return ORN_ENOMEM;
+    }
 #define CARVE(name, bytes)       \
     size_t name = off;           \
     off += ALIGN256((size_t)(bytes))
     CARVE(o_xn, (flags & ORN_MOE_NORM) ? (size_t)T * D * 4 : 0);
+    CARVE(o_est, cert ? (size_t)T * E * 8 : 0); /* tagged (S, B) words */
     CARVE(o_logits, (size_t)T * E * 4);
     CARVE(o_idx, (size_t)T * k * 4);
     CARVE(o_w, (size_t)T * k * 4);
@@ -1193,6 +1227,8 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     a.out = out;
     a.xn = a.apply_norm ? (float *)(ws + o_xn) : (float *)x;
     a.logits = (float *)(ws + o_logits);
+    a.sync = sync;
+    a.route_est = cert ? (double *)(ws + o_est) : NULL;
     /* the selection is written straight into the caller's buffers if given */
     a.idx = idx_out ? idx_out : (uint32_t *)(ws + o_idx);
     a.w = w_out ? w_out : (float *)(ws + o_w);
@@ -1243,17 +1279,22 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     int rc;
     /* A separate norm kernel runs only where the router does not fuse the
      * norm (profiled only then, so that every recorded step is a kernel). */
-    if (a.apply_norm && !ornk_router_pc_supported(T, D) &&
-        (rc = launch(ctx, "moe_norm", ornk_moe_norm, &a)))
-        return rc;
-    if ((rc = launch_k(ctx, "moe_route", ornk_moe_route, &a))) return rc;
-    if ((rc = launch_k(ctx, "moe_dispatch", ornk_moe_dispatch, &a))) return rc;
+    if (cert) {
+        /* the norm, logits, selection and dispatch in one launch */
+        if ((rc = launch_k(ctx, "moe_route", ornk_moe_route_cert, &a))) return rc;
+    } else {
+        if (a.apply_norm && !ornk_router_pc_supported(T, D) &&
+            (rc = launch(ctx, "moe_norm", ornk_moe_norm, &a)))
+            return rc;
+        if ((rc = launch_k(ctx, "moe_route", ornk_moe_route, &a))) return rc;
+        if ((rc = launch_k(ctx, "moe_dispatch", ornk_moe_dispatch, &a))) return rc;
+    }
     /* streamed experts: read the dispatch's experts back, load the missing
      * ones into slots and renumber the work items (host round trip) */
     if (st->cache && (rc = orn_cache_prepare(ctx, st->cache, layer, &a))) return rc;
     if (file) {
-        /* decode sizes: the router wrote the file kernels' activations */
-        if (!ornk_router_pc_supported(T, D) &&
+        /* decode sizes: the exact router wrote the file kernels' activations */
+        if ((cert || !ornk_router_pc_supported(T, D)) &&
             (rc = launch_k(ctx, "moe_file_prep_x", ornk_file_prep_x, &a)))
             return rc;
         if ((rc = launch_k(ctx, "moe_gateup_file", ornk_file_gateup, &a))) return rc;
@@ -1460,6 +1501,12 @@ int gpu_moe_forward_noalloc(gpu_context *ctx, ornith_moe_store *st, int layer,
          * array (looked up once per device, with the device current) */
         hipError_t e = hipSetDevice(ctx->device);
         if (e == hipSuccess) e = (hipError_t)ornk_scratch_resolve(ctx->device, &ctx->scratch);
+        /* its first ORNK_SYNC_BYTES are counters that must start at zero (the
+         * kernels that use them leave them zeroed); a fill kernel, not a
+         * memset, so that a caller may capture this call into a graph */
+        if (e == hipSuccess)
+            e = (hipError_t)ornk_fill_f32((float *)ctx->scratch, 0.0f, ORNK_SYNC_BYTES / 4,
+                                          ctx->stream);
         if (e != hipSuccess) {
             ctx->scratch = NULL;
             return orn_set_err(ctx, ORN_EUNSUPPORTED,
@@ -1548,6 +1595,20 @@ int gpu_moe_last_logits(gpu_context *ctx, float *out, size_t max_floats, size_t 
         if (rc) return rc;
     }
     return orn_hip_check(ctx, hipStreamSynchronize(ctx->stream), "logits copy");
+}
+
+int gpu_moe_last_chained(gpu_context *ctx, int *n_chained)
+{
+    if (!ctx || !n_chained) return ORN_EINVAL;
+    *n_chained = 0;
+    if (!ctx->last_ctl) return ORN_OK;
+    int rc = orn_hip_check(ctx, hipMemcpyAsync(ctx->ctl_host, ctx->last_ctl, 16 * sizeof(int),
+                                               hipMemcpyDeviceToHost, ctx->stream),
+                           "stats copy");
+    if (rc) return rc;
+    rc = orn_hip_check(ctx, hipStreamSynchronize(ctx->stream), "stats copy");
+    if (!rc) *n_chained = ctx->ctl_host[4];
+    return rc;
 }
 
 int gpu_moe_last_stats(gpu_context *ctx, int *n_slots, int *n_rows, int *n_literal)

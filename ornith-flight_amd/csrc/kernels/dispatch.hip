@@ -56,24 +56,9 @@ __global__ void __launch_bounds__(256)
 // Dispatch core, one work group of 1024 threads; sel_idx/sel_w may live in
 // LDS or global memory (visible to the whole group on entry).
 // ---------------------------------------------------------------------------
-struct DispatchLds {
-    int cnt[1024];
-    int cursor[1024];
-    int rowoff[1024];
-    int wtot[3][16];
-};
+
 
 #define ORN_DU 8  // pairs read per thread at a time in dispatch_group
-
-// Expert of a selected pair if it is dispatched here, else 0xFFFFFFFF: the
-// pair is skipped when w < 1e-6 (model.c:1066) or its expert lies outside
-// this forward's share [ep_lo, ep_lo + ep_n) (another rank's).
-template <typename IdxT>
-__device__ __forceinline__ uint32_t dispatch_key(IdxT idx, float w, int ep_lo, int ep_n)
-{
-    const uint32_t e = (uint32_t)idx;
-    return !(w < 1e-6f) && e - (uint32_t)ep_lo < (uint32_t)ep_n ? e : 0xFFFFFFFFu;
-}
 
 // Keys of pairs p0 + 1024 u, u < ORN_DU (0xFFFFFFFF past P).  The loads
 // are unconditional, at an index clamped to P - 1 (P >= 1 when called), so
@@ -186,83 +171,6 @@ __device__ void dispatch_group(DispatchLds &L, const IdxT *sel_idx, const float 
     }
     if (has_shared)
         for (int t = tid; t < T; t += 1024) row_token[L.rowoff[0] + t] = t;
-}
-
-// The dispatch of a small batch (T * k <= 1024 pairs, E + 1 <= 320 slot
-// candidates) by one wave: no work-group barrier, the same outputs as
-// dispatch_group (slot j = 0 the shared expert, j = e + 1 routed expert e;
-// slots, row ranges and items in j order; rows of an expert in any order).
-// Lane l takes the candidates j = 5l .. 5l+4, so the scans over j are a
-// lane-local sum and one wave scan.
-template <typename IdxT>
-__device__ void dispatch_wave(DispatchLds &L, const IdxT *lidx, const float *lw, int T, int k,
-                              int E, int ep_lo, int ep_n, int has_shared, int *ctl,
-                              int *slot_expert, int *slot_off, int *slot_cnt, int *row_token,
-                              int *pair_row, int4 *items, int items_max, int tchunk)
-{
-    constexpr int JPL = 5;
-    const int lane = threadIdx.x & 63;
-    const int NJ = E + 1, P = T * k, j0 = JPL * lane;
-#pragma unroll
-    for (int i = 0; i < JPL; ++i) {
-        L.cnt[j0 + i] = 0;
-        L.cursor[j0 + i] = 0;
-    }
-    wave_sync();
-    for (int p = lane; p < P; p += 64) {
-        const uint32_t key = dispatch_key(lidx[p], lw[p], ep_lo, ep_n);
-        if (key != 0xFFFFFFFFu) atomicAdd(&L.cnt[key + 1], 1);
-    }
-    wave_sync();
-    int c[JPL], nit[JPL], sc = 0, sn = 0, sf = 0;
-#pragma unroll
-    for (int i = 0; i < JPL; ++i) {
-        const int j = j0 + i;
-        c[i] = j >= NJ ? 0 : j == 0 ? (has_shared ? T : 0) : L.cnt[j];
-        nit[i] = (c[i] + tchunk - 1) / tchunk;
-        sc += c[i];
-        sn += nit[i];
-        sf += c[i] > 0 ? 1 : 0;
-    }
-    const int ic = wave_incl_scan(sc), in = wave_incl_scan(sn), iflag = wave_incl_scan(sf);
-    int roff = ic - sc, ioff = in - sn, slot = iflag - sf;
-#pragma unroll
-    for (int i = 0; i < JPL; ++i) {
-        const int j = j0 + i;
-        L.rowoff[j] = roff;
-        if (c[i] > 0) {
-            const int ex = j == 0 ? E : j - 1;
-            slot_expert[slot] = ex;
-            slot_off[slot] = roff;
-            slot_cnt[slot] = c[i];
-            for (int q = 0; q < nit[i] && ioff + q < items_max; ++q) {
-                const int r0 = q * tchunk;
-                items[ioff + q] = make_int4(slot, roff + r0, min(tchunk, c[i] - r0), ex);
-            }
-            ++slot;
-        }
-        roff += c[i];
-        ioff += nit[i];
-    }
-    if (lane == 63) {
-        ctl[0] = iflag;
-        ctl[1] = in < items_max ? in : items_max;
-        ctl[2] = ic;
-    }
-    wave_sync();
-    for (int p = lane; p < P; p += 64) {
-        const uint32_t key = dispatch_key(lidx[p], lw[p], ep_lo, ep_n);
-        if (key == 0xFFFFFFFFu) {  // skipped, or another rank's expert
-            pair_row[p] = -1;
-            continue;
-        }
-        const int j = (int)key + 1;
-        const int r = L.rowoff[j] + atomicAdd(&L.cursor[j], 1);
-        row_token[r] = p / k;
-        pair_row[p] = r;
-    }
-    if (has_shared)
-        for (int t = lane; t < T; t += 64) row_token[L.rowoff[0] + t] = t;
 }
 
 __global__ void __launch_bounds__(1024)

@@ -211,6 +211,11 @@ typedef struct {
     /* File-orientation path: gate/up [E+1][H][D/256] Q4_K blocks, down body
      * and d [E+1][D][H/256] (the blocks in file order) */
     ornk_file_ws fw;
+    /* Certified routing (router_cert.hip): T*E 64-bit handoff words, and a
+     * 4 KB counter area that starts zeroed (the kernel keeps its counter at
+     * zero between launches and advances a generation word in it). */
+    double *route_est;
+    int *sync;
     /* Profiling: if set, the expert-product launchers launch their main kernel
      * with hipExtLaunchKernel so that these events carry its start and end. */
     hipEvent_t ev_start, ev_stop;
@@ -226,6 +231,15 @@ int ornk_router_pc_supported(int T, int D);
  * skipped): one token, 16 gate/up split-K slices, 8-step down slices. */
 int ornk_down_dec_fuses_mid(int T, int H, int ks_gu, int ks_dn);
 int ornk_moe_dispatch(const ornk_moe_args *a, hipStream_t s);
+/* Certified routing of decode batches: logits, top-k and dispatch in one
+ * launch (router_cert.hip); replaces ornk_moe_route + ornk_moe_dispatch
+ * (and the norm step) for T <= ORN_CERT_MAX_T.  The logits it reports are
+ * fp64 sums rounded to fp32 (the reference's exact chain for tokens whose
+ * selection needed it); the selection equals the exact chain's. */
+#define ORN_CERT_MAX_T 4
+#define ORNK_SYNC_BYTES 4096u
+int ornk_route_cert_supported(int T, int D, int E, int k);
+int ornk_moe_route_cert(const ornk_moe_args *a, hipStream_t s);
 /* items[i].w (i < min(ctl[1], items_max)) and slot_expert[s] (s < min(ctl[0],
  * slots_max)) replaced by remap[] of themselves: expert ids -> cache slots. */
 int ornk_remap_items(int *items, int *slot_expert, const int *ctl, const int *remap,

@@ -21,6 +21,7 @@ MAT_GATE, MAT_UP, MAT_DOWN = 0, 1, 2
 ROUTE_RENORM, ROUTE_LITERAL = 0, 1
 MOE_ASYNC, MOE_NORM = 1, 2
 MOE_PATH_VALU, MOE_PATH_MFMA, MOE_GRAPH, MOE_SHEXP_GATE = 4, 8, 16, 32
+MOE_EXACT_LOGITS = 64
 SYN_GATE, SYN_UP, SYN_DOWN, SYN_ROUTER, SYN_ACT, SYN_ZIPF = 1, 2, 3, 4, 5, 6
 GPU_BUF_DEFAULT, GPU_BUF_SHARED, GPU_BUF_CONSTANT = 0, 1, 2
 Q4K_BYTES, Q6K_BYTES = 144, 210
@@ -40,7 +41,8 @@ EXPORTED = [
     "gpu_moe_store_set_norm", "gpu_moe_store_set_shexp_gate",
     "gpu_moe_store_fill_synthetic", "gpu_moe_forward", "gpu_moe_forward_noalloc",
     "gpu_moe_forward_stack",
-    "gpu_moe_last_stats", "gpu_moe_last_logits", "gpu_probe_read_bandwidth",
+    "gpu_moe_last_stats", "gpu_moe_last_chained", "gpu_moe_last_logits",
+    "gpu_probe_read_bandwidth",
     "gpu_profile_enable", "gpu_profile_reset", "gpu_profile_count", "gpu_profile_name",
     "gpu_profile_total_ms", "gpu_profile_calls",
     "orn_synth_stream", "orn_synth_q4k", "orn_synth_q6k", "orn_synth_normal",
@@ -157,6 +159,7 @@ def lib():
         "gpu_moe_forward_noalloc": (i, [vp, vp, i, vp, i, vp, vp, vp, vp, C.POINTER(MoEOpts)]),
         "gpu_moe_forward_stack": (i, [vp, vp, i, i, vp, vp, i, C.POINTER(MoEOpts)]),
         "gpu_moe_last_stats": (i, [vp, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+        "gpu_moe_last_chained": (i, [vp, C.POINTER(C.c_int)]),
         "gpu_moe_last_logits": (i, [vp, vp, sz, C.POINTER(C.c_size_t)]),
         "gpu_probe_read_bandwidth": (i, [vp, sz, i, C.POINTER(C.c_double)]),
         "gpu_profile_enable": (i, [vp, i]), "gpu_profile_reset": (None, [vp]),
@@ -403,6 +406,13 @@ class Store:
         a, b, c = C.c_int(), C.c_int(), C.c_int()
         self.ctx.check(lib().gpu_moe_last_stats(self.ctx.ptr, C.byref(a), C.byref(b), C.byref(c)), "stats")
         return {"n_slots": a.value, "n_rows": b.value, "n_literal": c.value}
+
+    def last_chained(self):
+        """Tokens of the last forward whose certified routing ran exact chains
+        (gpu_moe_last_chained)."""
+        n = C.c_int()
+        self.ctx.check(lib().gpu_moe_last_chained(self.ctx.ptr, C.byref(n)), "chained")
+        return n.value
 
     def last_logits(self, T):
         """Router logits [T][E] of the context's last forward (gpu_moe_last_logits)."""

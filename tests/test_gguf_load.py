@@ -147,8 +147,10 @@ def test_load_gguf_equals_set_experts(om, ctx, path, shape, router_f16):
         say("  expert bytes in the store == the file's")
         for sl, fl in ((0, 2), (1, 3)):
             syn, rfile, nw, gv = info[fl]
-            for T, flags in ((1, 0), (16, om.MOE_NORM), (40, 0),
-                             (16, om.MOE_NORM | om.MOE_SHEXP_GATE)):
+            # the exact chain routers, so that the logits compare bit for bit
+            ex = om.MOE_EXACT_LOGITS
+            for T, flags in ((1, ex), (16, om.MOE_NORM | ex), (40, ex),
+                             (16, om.MOE_NORM | om.MOE_SHEXP_GATE | ex)):
                 x = np.random.default_rng(100 * sl + T).standard_normal((T, D)).astype(np.float32)
                 a = forward(ctx, loaded, sl, x, k, flags)
                 b = forward(ctx, direct, sl, x, k, flags)

@@ -13,6 +13,11 @@ with and without a Zipf router bias, and for the file-orientation store
 order fails these tests, where index equality alone would not see it.
 The selection weights are compared to the oracle's within 2e-6 relative
 (the device's expf against glibc's); the indices exactly.
+
+Decode batches of up to 4 tokens route by default through the certified kernel
+(router_cert.hip), whose logits are fp64 sums within a proven bound of
+these chains (tests/test_router_cert.py); every call here passes
+ORN_MOE_EXACT_LOGITS, which selects the exact chains at every size.
 """
 import sys
 
@@ -86,7 +91,7 @@ def check(om, ctx, store, T, layer, norm):
     st, syn, norms = store
     s = syn[layer]
     x = act(om, 1000 + T + 7 * layer, T)
-    flags = om.MOE_NORM if norm else 0
+    flags = (om.MOE_NORM if norm else 0) | om.MOE_EXACT_LOGITS
     logits, idx, w = forward(om, ctx, st, x, layer, flags)
     xin = O.rmsnorm(x, norms[layer]) if norm else x
     ref = O.router_logits_rows(xin, s.router, s.bias)
@@ -136,7 +141,7 @@ def test_file_orientation_router_bit_exact(om, ctx, T):
         W = om.synth_normal(SEED, om.synth_stream(0, om.SYN_ROUTER, 0), D * E, 0.02).reshape(D, E)
         st.set_router(0, np.ascontiguousarray(W.T))  # file orientation: [E][D]
         x = act(om, 77 + T, T)
-        logits, idx, _ = forward(om, ctx, st, x, 0, 0)
+        logits, idx, _ = forward(om, ctx, st, x, 0, om.MOE_EXACT_LOGITS)
         ref = O.router_logits_rows(x, W)
         assert np.array_equal(logits.view(np.uint32), ref.view(np.uint32))
         for t in range(T):
