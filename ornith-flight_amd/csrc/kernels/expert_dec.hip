@@ -101,33 +101,42 @@ struct GuRing {
     uint4 mn;      // mins of sub-block 2w + (c & 1) at k = 8g..8g+7
 };
 
+// LDS of one gate/up tile: activation tiles (hi/lo of A and Am) per chunk.
+template <int KT, int KC, int RT>
+struct GuLds {
+    uint32_t As[KT / KC > 1 ? 2 : 1][KC][RT][4][16 * ORN_AST / 2];
+    float s_inv[16 * RT];
+};
+
+// One gate/up tile (work group); returns false for a tile past the
+// dispatched items.
 template <int NR, int KT, int KC, int RT>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT > 1 ? 3 : 4)))
-    k_gateup_dec(ornk_gu_prefill P, const float *__restrict__ xn,
-                 const float *__restrict__ x_amax, const int *__restrict__ ctl,
-                 const int4 *__restrict__ items, const int *__restrict__ row_token,
-                 float *__restrict__ gu, int T, int D, int H, int ks, int rows_max)
+__device__ __forceinline__ bool gateup_dec_tile(GuLds<KT, KC, RT> &L, const ornk_gu_prefill &P,
+                                                const float *__restrict__ xn,
+                                                const float *__restrict__ x_amax, int n_items,
+                                                const int4 *__restrict__ items,
+                                                const int *__restrict__ row_token,
+                                                float *__restrict__ gu, int D, int H, int ks,
+                                                int rows_max, int tile)
 {
     constexpr int NCHK = KT / KC, NBUF = NCHK > 1 ? 2 : 1;
     constexpr int LC = 2 * KC;  // activation values a thread prepares per chunk
     constexpr int GV = LC < 8 ? LC : 8;  // values per LDS store (8: 16 bytes, 4: 8 bytes)
     static_assert(LC % GV == 0 && (GV == 4 || GV == 8), "chunks of 2 or 4k steps");
-    __shared__ __align__(16) uint32_t As[NBUF][KC][RT][4][16 * ORN_AST / 2];
-    __shared__ float s_inv[16 * RT];
+    auto &As = L.As;
+    auto &s_inv = L.s_inv;
 
     // The item and the live item count are read together; work groups past
     // the dispatched items then leave.
     const int NB = H >> 8;
     const int per_item = 2 * NB * ks;
-    const int tile = blockIdx.x;
     const int b = tile % NB;
     const int m = (tile / NB) & 1;
     const int kslice = (tile / (2 * NB)) % ks;
     const int item = tile / per_item;
     const int tid = threadIdx.x;
-    const int n_items = ctl[1];
+    if (item >= n_items) return false;
     const int4 itm = items[item];
-    if (item >= n_items) return;
     const int e = itm.w;
     const int nrows = itm.z;
     const int lane = tid & 63, wave = tid >> 6;
@@ -324,6 +333,19 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT > 1
                 o[48] = (acc[rt][3][rr] - m1) * si;
             }
         }
+    return true;
+}
+
+template <int NR, int KT, int KC, int RT>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT > 1 ? 3 : 4)))
+    k_gateup_dec(ornk_gu_prefill P, const float *__restrict__ xn,
+                 const float *__restrict__ x_amax, const int *__restrict__ ctl,
+                 const int4 *__restrict__ items, const int *__restrict__ row_token,
+                 float *__restrict__ gu, int T, int D, int H, int ks, int rows_max)
+{
+    __shared__ __align__(16) GuLds<KT, KC, RT> L;
+    gateup_dec_tile<NR, KT, KC, RT>(L, P, xn, x_amax, ctl[1], items, row_token, gu, D, H,
+                                           ks, rows_max, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -347,12 +369,28 @@ struct DnRing {
 };
 
 // WIDE: Q6_K sub-scales up to |128| (q6_b2: three MFMAs per tile and step).
+// LDS of one down tile.  SL: the slice's scales in LDS (two-tile instances,
+// whose many rows per item make them bandwidth-bound: the deeper ring
+// pays); one-tile instances carry them in the ring.
+template <int KT, int KC, int KSG, int RT>
+struct DnLds {
+    static constexpr bool SL = RT > 1;
+    uint32_t As[KT / KC > 1 ? 2 : 1][KC][RT][2][16 * ORN_AST / 2];
+    uint4 Ss[SL ? KT : 1][64];  // per step: 16 tiles x 32 scales
+    float s_inv[16 * RT];
+    float Ms[KSG ? 16 : 1][KSG ? 32 * KT : 4];  // the rows' mid slices
+    unsigned int s_amax[16];
+};
+
+// One down tile (logical tile number `tile`, after any XCD remapping).
 template <int NR, int KT, int KC, int KSG, int RT, bool WIDE>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT > 1 ? 2 : KSG ? (WIDE ? 3 : 4) : WIDE ? 2 : 3)))
-    k_down_dec(ornk_dn_prefill P, const float *__restrict__ mid,
-               const float *__restrict__ mid_amax, const int *__restrict__ ctl,
-               const int4 *__restrict__ items, float *__restrict__ dn, int D, int H, int ks,
-               int rows_max, const float *__restrict__ gu, int shared_rows)
+__device__ __forceinline__ void down_dec_tile(DnLds<KT, KC, KSG, RT> &L, const ornk_dn_prefill &P,
+                                              const float *__restrict__ mid,
+                                              const float *__restrict__ mid_amax,
+                                              const int4 *__restrict__ items,
+                                              float *__restrict__ dn, int D, int H, int ks,
+                                              int rows_max, const float *__restrict__ gu,
+                                              int shared_rows, int tile)
 {
     constexpr int NCHK = KT / KC, NBUF = NCHK > 1 ? 2 : 1;
     constexpr int LC = 2 * KC;
@@ -361,24 +399,15 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT > 1
     static_assert(KSG == 0 || RT == 1, "mid is formed in the kernel for one row tile only");
     static_assert(KSG == 0 || 32 * KT == 256, "mid is formed one value per thread");
     static_assert(KT % 4 == 0 && NR >= 1 && NR <= KT, "slices of 4k steps");
-    // SL: the slice's scales in LDS (two-tile instances, whose many rows per
-    // item make them bandwidth-bound: the deeper ring pays); one-tile
-    // instances carry them in the ring.
     constexpr bool SL = RT > 1;
-    __shared__ __align__(16) uint32_t As[NBUF][KC][RT][2][16 * ORN_AST / 2];
-    __shared__ __align__(16) uint4 Ss[SL ? KT : 1][64];  // per step: 16 tiles x 32 scales
-    __shared__ float s_inv[16 * RT];
-    __shared__ __align__(16) float Ms[KSG ? 16 : 1][KSG ? KV : 4];  // the rows' mid slices
-    __shared__ unsigned int s_amax[16];
+    auto &As = L.As;
+    auto &Ss = L.Ss;
+    auto &s_inv = L.s_inv;
+    auto &Ms = L.Ms;
+    auto &s_amax = L.s_amax;
 
-    // The D/256 work groups of one (item, slice) read the same gate/up
-    // partials (KSG > 0) or mid rows: XCD-aware numbering puts them on one
-    // XCD, so one L2 serves the rest.
     const int NBD = D >> 8;
     const int per_item = NBD * ks;
-    const int n_live = ctl[1] * per_item;
-    if ((int)blockIdx.x >= n_live) return;
-    const int tile = xcd_remap(blockIdx.x, n_live);
     const int b = tile % NBD;
     const int kslice = (tile / NBD) % ks;
     const int item = tile / per_item;
@@ -625,6 +654,25 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT > 1
         }
 }
 
+template <int NR, int KT, int KC, int KSG, int RT, bool WIDE>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT > 1 ? 2 : KSG ? (WIDE ? 3 : 4) : WIDE ? 2 : 3)))
+    k_down_dec(ornk_dn_prefill P, const float *__restrict__ mid,
+               const float *__restrict__ mid_amax, const int *__restrict__ ctl,
+               const int4 *__restrict__ items, float *__restrict__ dn, int D, int H, int ks,
+               int rows_max, const float *__restrict__ gu, int shared_rows)
+{
+    __shared__ __align__(16) DnLds<KT, KC, KSG, RT> L;
+    // The D/256 work groups of one (item, slice) read the same gate/up
+    // partials (KSG > 0) or mid rows: XCD-aware numbering puts them on one
+    // XCD, so one L2 serves the rest.
+    const int n_live = ctl[1] * (D >> 8) * ks;
+    if ((int)blockIdx.x >= n_live) return;
+    down_dec_tile<NR, KT, KC, KSG, RT, WIDE>(L, P, mid, mid_amax, items, dn, D, H, ks,
+                                                    rows_max, gu, shared_rows,
+                                                    xcd_remap(blockIdx.x, n_live));
+}
+
+
 }  // namespace
 
 // Decode instances: work items of <= 16 rows (one row tile), or <= 32 (two,
@@ -747,3 +795,4 @@ extern "C" int ornk_moe_down_dec(const ornk_moe_args *a, hipStream_t s)
 #undef ORN_DN_DEC
     return hipGetLastError();
 }
+

@@ -202,12 +202,14 @@ __device__ __forceinline__ uint64_t ld_word(const uint64_t *p)
                              __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Read a tagged word: until its low byte is `tag` (bounded; false if the
-// bound ran out, which the callers treat as "no value").
+// Read a tagged word: until its low byte is `tag` (bounded by 20 ms of the
+// 100 MHz real-time counter; false if the bound ran out, which the callers
+// treat as "no value").
 __device__ __forceinline__ bool ld_tagged(const uint64_t *p, uint32_t tag, uint64_t &v)
 {
     v = ld_word(p);
-    for (int it = 0; (uint32_t)(v & 0xFFu) != tag && it < (1 << 20); ++it) {
+    const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+    while ((uint32_t)(v & 0xFFu) != tag && __builtin_amdgcn_s_memrealtime() - t0 < 2000000ull) {
         __builtin_amdgcn_s_sleep(1);
         v = ld_word(p);
     }
