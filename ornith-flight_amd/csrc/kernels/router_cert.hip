@@ -437,37 +437,6 @@ __device__ __forceinline__ int select_cert(float (&sfv)[4], float (&bfv)[4], boo
     return path;
 }
 
-// Sequential fp32 sum of x[i]^2, i ascending (the rmsnorm's sum of squares in
-// the reference's order, gpu.c:144-156), for one lane: batches of 32 values
-// read from LDS one batch ahead of the adds.
-template <int NB>
-__device__ __forceinline__ float lds_seq_sumsq(const v4f *p4)
-{
-    float ss = 0.0f;
-    v4f A[8], B[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) A[i] = p4[i];
-#pragma unroll
-    for (int bt = 0; bt < NB; ++bt) {
-        v4f(&cur)[8] = (bt & 1) ? B : A;
-        v4f(&nxt)[8] = (bt & 1) ? A : B;
-        if (bt + 1 < NB) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) nxt[i] = p4[8 * (bt + 1) + i];
-        }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            ss = ss + cur[i].x * cur[i].x;
-            ss = ss + cur[i].y * cur[i].y;
-            ss = ss + cur[i].z * cur[i].z;
-            ss = ss + cur[i].w * cur[i].w;
-        }
-        asm volatile("" : "+v"(ss));
-    }
-    return ss;
-}
-
 template <int NQ>
 __global__ void __launch_bounds__(256) k_route_cert(CertArgs P)
 {
@@ -486,6 +455,7 @@ __global__ void __launch_bounds__(256) k_route_cert(CertArgs P)
             int pidx[CERT_TPG * 16];
             float pw[CERT_TPG * 16];
         } sd;
+        v4f sq[CERT_TPG * D / 4];  // the rmsnorm's squares
     };
     __shared__ Lds2 U;
     auto &part_t = U.parts.t;
@@ -521,9 +491,17 @@ __global__ void __launch_bounds__(256) k_route_cert(CertArgs P)
         // the layer's rmsnorm (gpu.c:144-156): sequential sum of squares by
         // lane 0 of wave t, then x <- w * (x * inv); group eg = 0 writes the
         // normalised rows for the expert steps
+        // (the squares first, by every thread, into the union's space, so that
+        // the one chain per token is adds only)
         __shared__ float inv_s[CERT_TPG];
+        v4f *sq = U.sq;
+        for (int i = tid; i < nt * (D / 4); i += 256) {
+            const v4f v = reinterpret_cast<const v4f *>(xs[0])[i];
+            sq[i] = v * v;
+        }
+        __syncthreads();
         if (wave < nt && lane == 0) {
-            const float ss = lds_seq_sumsq<D / 32>(reinterpret_cast<const v4f *>(xs[wave]));
+            const float ss = orn_lds_seq_sum32_n<D / 32>(sq + wave * (D / 4));
             inv_s[wave] = 1.0f / sqrtf(ss / (float)D + 1e-6f);
         }
         __syncthreads();
