@@ -1150,7 +1150,7 @@ static int moe_forward_dev(gpu_context *ctx, ornith_moe_store *st, int layer, co
     size_t name = off;           \
     off += ALIGN256((size_t)(bytes))
     CARVE(o_xn, (flags & ORN_MOE_NORM) ? (size_t)T * D * 4 : 0);
-    CARVE(o_est, cert ? (size_t)T * E * 8 : 0); /* tagged (S, B) words */
+    CARVE(o_est, cert ? (size_t)T * (E + 1) * 8 : 0); /* tagged (S, B) words, rmsnorm scales */
     CARVE(o_logits, (size_t)T * E * 4);
     CARVE(o_idx, (size_t)T * k * 4);
     CARVE(o_w, (size_t)T * k * 4);

@@ -40,10 +40,24 @@
 // chain ran); the logits buffer receives the same values.
 //
 // One launch: E/4 work groups of 4 waves; work group eg forms the sums of
-// experts 4eg..4eg+3 for every token (with ORN_MOE_NORM after the layer's
-// rmsnorm, computed in the reference's order inside every group); the last
-// work group to finish (a counter) selects (wave t: token t) and dispatches
-// (select.h dispatch_one / dispatch_wave).  Measured at T = 16 the serial
+// experts 4eg..4eg+3 for every token; the last work group to finish (a
+// counter) selects (wave t: token t) and dispatches (select.h dispatch_one /
+// dispatch_wave).
+//
+// With the layer's rmsnorm (ORN_MOE_NORM, gpu.c:144-156) the reference's
+// products are p_i = fl(fl(w_i * fl(x_i * inv)) * W(i, e)), inv from a
+// sequential fp32 sum of squares (another 2048 dependent adds).  That chain
+// runs in one extra work group, in parallel with the sums, which take the
+// scale out: the groups sum q_i = fl(fl(x_i * w_i) * W(i, e)) into T and
+// bound |chain - inv T| <= inv B_T with
+//   B_T = u (A_q + 5.0001 n u Q) / (1 - n u) + 5.0001 u Q,
+// A_q = sum |partial sums of q|, Q = sum |q_i| (p_i and inv q_i differ by
+// at most 5 roundings of |p_i|, which moves every partial sum by at most
+// 5.0001 u inv Q).  The extra group publishes inv (a tagged word), the
+// normalised rows and their max |x|; the selecting group waits for inv and
+// forms S = inv T (+ bias) and B = inv B_T (+ the bias add's rounding) --
+// exact products of fp32 values in fp64 -- before the selection, and
+// rebuilds the normalised rows for the exact chains.  Measured at T = 16 the serial
 // per-wave phases (selection ~3 us, dispatch ~2-3 us) and the handoffs
 // between token groups cost more than the exact chains save, so larger
 // batches keep the exact routers (router.hip, dispatch.hip).
@@ -71,13 +85,14 @@ enum { SYNC64_GEN = 1 };
 struct CertArgs {
     const float *x, *router, *bias, *norm_w;
     float *xn, *x_amax, *logits;
-    uint64_t *est;   // [T][E] tagged (S, B) words
+    uint64_t *est;   // [T][E] tagged (S, B) words, then [T] tagged rmsnorm scales
     int *sync;
     uint32_t *idx;
     float *w;
     int *ctl, *slot_expert, *slot_off, *slot_cnt, *row_token, *pair_row;
     int4 *items;
     int T, E, k, mode, ep_lo, ep_n, has_shared, items_max, tchunk;
+    int ngroups;  // expert work groups (with the rmsnorm, one more group runs its chain)
 };
 
 __device__ __forceinline__ double readlane_d(double v, int l)
@@ -448,6 +463,7 @@ __global__ void __launch_bounds__(256) k_route_cert(CertArgs P)
         struct {
             double t[CERT_TPG][CERT_NCH][CERT_EPG];
             float a[CERT_TPG][CERT_NCH][CERT_EPG];
+            float q[CERT_TPG][CERT_NCH][CERT_EPG];
         } parts;
         struct {
             SelLds sel[CERT_TPG];
@@ -460,6 +476,7 @@ __global__ void __launch_bounds__(256) k_route_cert(CertArgs P)
     __shared__ Lds2 U;
     auto &part_t = U.parts.t;
     auto &part_a = U.parts.a;
+    auto &part_q = U.parts.q;
     auto &sel = U.sd.sel;
     __shared__ float mx_s[CERT_TPG][4];
     __shared__ int flag_s, lit_s, chain_s;
@@ -473,30 +490,20 @@ __global__ void __launch_bounds__(256) k_route_cert(CertArgs P)
     // this launch's tag (the generation the previous launch left)
     // (bit 7 set: a zeroed word never carries a tag)
     const uint32_t tag = ((uint32_t)ld_word(&sync64[SYNC64_GEN]) & 0x7Fu) | 0x80u;
+    uint64_t *const inv_word = P.est + (size_t)T * E;  // [T] tagged rmsnorm scales
+    const bool norm = P.norm_w != nullptr;
 
-    // ---- sums: lane (j, el) covers chunk j (values L*j ..) of expert el ----
-    const int el = lane & 3, j = 16 * wave + (lane >> 2);
-    const int e = CERT_EPG * eg + el;
-    const int ec = min(e, E - 1);  // lanes past E compute a copy, never stored
-    v4f wr[NQ];
-#pragma unroll
-    for (int q = 0; q < NQ; ++q) wr[q] = Wq4[(size_t)(NQ * j + q) * E + ec];
-    for (int i = tid; i < nt * (D / 4); i += 256) {
-        const int t = i / (D / 4), c = i % (D / 4);
-        reinterpret_cast<v4f *>(xs[t])[c] =
-            reinterpret_cast<const v4f *>(P.x + (size_t)(t0 + t) * D)[c];
-    }
-    __syncthreads();
-    if (P.norm_w) {
-        // the layer's rmsnorm (gpu.c:144-156): sequential sum of squares by
-        // lane 0 of wave t, then x <- w * (x * inv); group eg = 0 writes the
-        // normalised rows for the expert steps
-        // (the squares first, by every thread, into the union's space, so that
-        // the one chain per token is adds only)
+    if (norm && eg == P.ngroups) {
+        // ---- the rmsnorm's group (gpu.c:144-156): the sequential sum of
+        // squares by lane 0 of wave t (the squares first, by every thread,
+        // so that the chain is adds only), then xn = w * (x * inv) and max
+        // |xn| for the expert steps, and inv for the selecting group ----
         __shared__ float inv_s[CERT_TPG];
         v4f *sq = U.sq;
         for (int i = tid; i < nt * (D / 4); i += 256) {
-            const v4f v = reinterpret_cast<const v4f *>(xs[0])[i];
+            const int t = i / (D / 4), c = i % (D / 4);
+            const v4f v = reinterpret_cast<const v4f *>(P.x + (size_t)(t0 + t) * D)[c];
+            reinterpret_cast<v4f *>(xs[t])[c] = v;
             sq[i] = v * v;
         }
         __syncthreads();
@@ -505,17 +512,47 @@ __global__ void __launch_bounds__(256) k_route_cert(CertArgs P)
             inv_s[wave] = 1.0f / sqrtf(ss / (float)D + 1e-6f);
         }
         __syncthreads();
-        for (int i = tid; i < nt * (D / 4); i += 256) {
-            const int t = i / (D / 4), c = i % (D / 4);
-            v4f *p = reinterpret_cast<v4f *>(xs[t]) + c;
-            const v4f wn = reinterpret_cast<const v4f *>(P.norm_w)[c];
-            const v4f v = wn * (*p * inv_s[t]);
-            *p = v;
-            if (eg == 0) reinterpret_cast<v4f *>(P.xn + (size_t)(t0 + t) * D)[c] = v;
+        for (int t = 0; t < nt; ++t) {
+            float mx = 0.0f;
+            for (int c = tid; c < D / 4; c += 256) {
+                const v4f wn = reinterpret_cast<const v4f *>(P.norm_w)[c];
+                const v4f v = wn * (reinterpret_cast<const v4f *>(xs[t])[c] * inv_s[t]);
+                reinterpret_cast<v4f *>(P.xn + (size_t)(t0 + t) * D)[c] = v;
+                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+            }
+            if (P.x_amax) {
+#pragma unroll
+                for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+                if (lane == 0) mx_s[t][wave] = mx;
+            }
         }
         __syncthreads();
+        if (P.x_amax && tid < nt)
+            P.x_amax[t0 + tid] =
+                fmaxf(fmaxf(mx_s[tid][0], mx_s[tid][1]), fmaxf(mx_s[tid][2], mx_s[tid][3]));
+        if (tid < nt)
+            st_word(&inv_word[t0 + tid],
+                    ((uint64_t)__float_as_uint(inv_s[tid]) << 32) | (uint64_t)tag);
+        return;
     }
-    if (P.x_amax && eg == 0) {
+
+    // ---- sums: lane (j, el) covers chunk j (values L*j ..) of expert el ----
+    const int el = lane & 3, j = 16 * wave + (lane >> 2);
+    const int e = CERT_EPG * eg + el;
+    const int ec = min(e, E - 1);  // lanes past E compute a copy, never stored
+    v4f wr[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) wr[q] = Wq4[(size_t)(NQ * j + q) * E + ec];
+    // the rows (with the rmsnorm: x * w, whose products with W differ from
+    // the reference's by the scale inv and 5 roundings)
+    for (int i = tid; i < nt * (D / 4); i += 256) {
+        const int t = i / (D / 4), c = i % (D / 4);
+        v4f v = reinterpret_cast<const v4f *>(P.x + (size_t)(t0 + t) * D)[c];
+        if (norm) v = v * reinterpret_cast<const v4f *>(P.norm_w)[c];
+        reinterpret_cast<v4f *>(xs[t])[c] = v;
+    }
+    __syncthreads();
+    if (P.x_amax && eg == 0 && !norm) {
         // max |x| per token for the MFMA activation scaling
         for (int t = 0; t < nt; ++t) {
             float mx = 0.0f;
@@ -533,10 +570,10 @@ __global__ void __launch_bounds__(256) k_route_cert(CertArgs P)
     for (int t = 0; t < nt; ++t) {
         const v4f *xr = reinterpret_cast<const v4f *>(xs[t]) + NQ * j;
         double l = 0.0;
-        float A = 0.0f;
+        float A = 0.0f, Q = 0.0f;
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
-            const v4f p = xr[q] * wr[q];  // the reference's fp32 products
+            const v4f p = xr[q] * wr[q];  // the reference's fp32 products (rmsnorm: q_i)
             l += (double)p.x;
             A += fabsf((float)l);
             l += (double)p.y;
@@ -545,9 +582,11 @@ __global__ void __launch_bounds__(256) k_route_cert(CertArgs P)
             A += fabsf((float)l);
             l += (double)p.w;
             A += fabsf((float)l);
+            if (norm) Q += (fabsf(p.x) + fabsf(p.y)) + (fabsf(p.z) + fabsf(p.w));
         }
         part_t[t][j][el] = l;
         part_a[t][j][el] = A;
+        if (norm) part_q[t][j][el] = Q;
     }
     __syncthreads();
 
@@ -555,13 +594,14 @@ __global__ void __launch_bounds__(256) k_route_cert(CertArgs P)
     // (ce, r) with r covering chunks 4r .. 4r+3 of expert ce ----
     if (wave < nt) {
         const int t = wave, ce = lane >> 4, r = lane & 15;
-        double tc[4], tl = 0.0;
+        double tc[4], tl = 0.0, ql = 0.0;
         float ac[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             tc[i] = part_t[t][4 * r + i][ce];
             ac[i] = part_a[t][4 * r + i][ce];
             tl += tc[i];
+            if (norm) ql += (double)part_q[t][4 * r + i][ce];
         }
         // DPP row scans (a row = one expert): O = the sum before lane r's
         // chunks; row totals land in lane 15
@@ -574,21 +614,30 @@ __global__ void __launch_bounds__(256) k_route_cert(CertArgs P)
             O += tc[i];
         }
         sabs = row_incl_scan_d(sabs);
+        if (norm) ql = row_incl_scan_d(ql);
         double Sv = inc;
         const int eo = CERT_EPG * eg + ce;
         if (r == 15 && eo < E) {
             double n = (double)D;
-            if (P.bias) {
-                Sv += (double)P.bias[eo];
-                sabs += fabs(Sv);
-                n += 1.0;
-            }
             const double u = 0x1p-24;
-            double Bv = u * sabs * (1.0 + 1e-3) / (1.0 - n * u) + 1e-30;
+            double Bv;
+            if (norm) {
+                // T and B_T (the bias and inv join in the selecting group)
+                const double qa = ql * (1.0 + 1e-3);
+                Bv = u * (sabs + 5.0001 * n * u * qa) * (1.0 + 1e-3) / (1.0 - n * u) +
+                     5.0001 * u * qa + 1e-30;
+            } else {
+                if (P.bias) {
+                    Sv += (double)P.bias[eo];
+                    sabs += fabs(Sv);
+                    n += 1.0;
+                }
+                Bv = u * sabs * (1.0 + 1e-3) / (1.0 - n * u) + 1e-30;
+                P.logits[(size_t)(t0 + t) * E + eo] = (float)Sv;
+            }
             // a partial sum beyond 1e38 could overflow the fp32 chain
             if (!(sabs < 1e38)) Bv = INFINITY;
             st_word(&P.est[(size_t)(t0 + t) * E + eo], pack_est(Sv, Bv, tag));
-            P.logits[(size_t)(t0 + t) * E + eo] = (float)Sv;
         }
     }
 
@@ -598,7 +647,7 @@ __global__ void __launch_bounds__(256) k_route_cert(CertArgs P)
     if (tid == 0) {
         const int old = __hip_atomic_fetch_add(&P.sync[SYNC_GROUP], 1, __ATOMIC_RELAXED,
                                                __HIP_MEMORY_SCOPE_AGENT);
-        flag_s = old == (int)gridDim.x - 1;
+        flag_s = old == P.ngroups - 1;
         if (flag_s)
             __hip_atomic_store(&P.sync[SYNC_GROUP], 0, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
@@ -626,6 +675,52 @@ __global__ void __launch_bounds__(256) k_route_cert(CertArgs P)
                 unpack_est(wv[i], sfv[i], bfv[i]);
                 if (!(fabsf(sfv[i]) < 3e38f)) bad = true;
             }
+        }
+        if (norm) {
+            // inv from the rmsnorm's group (its chain ran beside the sums);
+            // S = inv T + bias and B = inv B_T + the bias add's rounding,
+            // then the reference's normalised row for the exact chains
+            uint64_t iw;
+            float inv;
+            if (ld_tagged(&inv_word[t], tag, iw)) {
+                inv = __uint_as_float((uint32_t)(iw >> 32));
+            } else {
+                // not published within the bound: this wave runs the chain
+                float *row = xs[wave];
+                for (int c = lane; c < D; c += 64) {
+                    const float v = P.x[(size_t)t * D + c];
+                    row[c] = v * v;
+                }
+                wave_sync();
+                float ss = 0.0f;
+                if (lane == 0)
+                    ss = orn_lds_seq_sum32_n<D / 32>(reinterpret_cast<const v4f *>(row));
+                ss = __shfl(ss, 0, 64);
+                inv = 1.0f / sqrtf(ss / (float)D + 1e-6f);
+                wave_sync();
+            }
+            const double u = 0x1p-24;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int ee = lane + 64 * i;
+                if (ee >= E) continue;
+                double Sc = (double)inv * (double)sfv[i];  // exact
+                double Bc = (double)inv * (double)bfv[i];
+                if (P.bias) {
+                    Sc += (double)P.bias[ee];
+                    Bc += u * (fabs(Sc) + Bc) * (1.0 + 1e-6) + 1e-30;
+                }
+                const float sf = (float)Sc;
+                sfv[i] = sf;
+                bfv[i] = (fabs(Sc) < 3e38 && Bc < 1e30) ? f_up(Bc + fabs(Sc - (double)sf))
+                                                         : 1.7e38f;
+                P.logits[(size_t)t * E + ee] = sf;
+                if (!(fabsf(sf) < 3e38f)) bad = true;
+            }
+            float *row = xs[wave];
+            for (int c = lane; c < D; c += 64)
+                row[c] = P.norm_w[c] * (P.x[(size_t)t * D + c] * inv);
+            wave_sync();
         }
         bad = __ballot(bad) != 0ull;
         uint32_t *io = P.idx + (size_t)t * k;
@@ -708,7 +803,8 @@ extern "C" int ornk_moe_route_cert(const ornk_moe_args *a, hipStream_t s)
     P.has_shared = a->has_shared;
     P.items_max = a->items_max;
     P.tchunk = a->tchunk;
-    const dim3 grid((E + CERT_EPG - 1) / CERT_EPG);
+    P.ngroups = (E + CERT_EPG - 1) / CERT_EPG;
+    const dim3 grid(P.ngroups + (P.norm_w ? 1 : 0));  // + the rmsnorm's group
     switch (D / 256) {
     case 1: ORN_LAUNCH_EV(a, k_route_cert<1>, grid, dim3(256), 0, s, P); break;
     case 2: ORN_LAUNCH_EV(a, k_route_cert<2>, grid, dim3(256), 0, s, P); break;

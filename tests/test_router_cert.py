@@ -160,17 +160,23 @@ def tie_store(om, ctx):
     st.close()
 
 
+@pytest.mark.parametrize("norm", [False, True], ids=["x", "rmsnorm"])
 @pytest.mark.parametrize("mode", [0, 1], ids=["renorm", "literal"])
 @pytest.mark.parametrize("kind", ["near", "exact", "near_k"])
-def test_cert_engineered_ties(om, ctx, tie_store, kind, mode):
+def test_cert_engineered_ties(om, ctx, tie_store, kind, mode, norm):
     """A router column rewritten from the token's top expert (near: scaled
     by 1 + 2^-20, a logit ~1e-6 away; exact: a copy, an exact tie) or from
     its k-th (near_k: the selection boundary).  The bounds cannot decide;
-    the selection must still equal the oracle's."""
+    the selection must still equal the oracle's.  With the rmsnorm the
+    selecting group rebuilds the normalised row from the scale the norm's
+    group published, so the chained logits are the reference's bit for bit."""
     st, s = tie_store
     x = act(om, 4321, 1)
+    nw = (1.0 + 0.25 * np.random.default_rng(12).standard_normal(D)).astype(np.float32)
+    st.set_norm(0, nw)
+    xin = O.rmsnorm(x, nw) if norm else x
     W = np.array(s.router, np.float32, copy=True)
-    ref0 = O.router_logits(x[0], W)
+    ref0 = O.router_logits(xin[0], W)
     order = np.argsort(-ref0.astype(np.float64), kind="stable")
     src = order[0] if kind != "near_k" else order[K - 1]
     dst = order[40]
@@ -180,8 +186,8 @@ def test_cert_engineered_ties(om, ctx, tie_store, kind, mode):
         W[:, dst] = (W[:, src] * np.float32(1.0 + 2.0 ** -20)).astype(np.float32)
     st.set_router(0, W)
     try:
-        logits, idx, w, _, chained = run(om, ctx, st, x, 0, 0, mode)
-        ref, ridx, rw = oracle_routing(x, W, None, mode)
+        logits, idx, w, _, chained = run(om, ctx, st, x, 0, om.MOE_NORM if norm else 0, mode)
+        ref, ridx, rw = oracle_routing(xin, W, None, mode)
         say(f"{kind} mode={mode}: logits {ref[0, src]!r} {ref[0, dst]!r}, chained {chained}, "
             f"idx {idx[0].tolist()} ref {ridx[0].tolist()}")
         assert chained == 1
