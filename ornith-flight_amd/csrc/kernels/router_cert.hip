@@ -280,8 +280,10 @@ __device__ __forceinline__ void cswap(Slot &a, Slot &b)
 // weights to io/wo and S.lidx/S.lw; logits_row gets the fp32 values the
 // weights come from.  Returns 0 (certified), 1 (candidates chained) or 2
 // (every logit chained).
+template <class PrepRow>
 __device__ __forceinline__ int select_cert(float (&sfv)[4], float (&bfv)[4], bool bad,
-                                           const float *xrow, const v4f *Wq4, const float *bias,
+                                           const float *xrow, PrepRow prep_row,
+                                           const v4f *Wq4, const float *bias,
                                            int D, int E, int k, int mode, uint32_t *io, float *wo,
                                            float *logits_row, SelLds &S, int *n_lit)
 {
@@ -368,6 +370,7 @@ __device__ __forceinline__ int select_cert(float (&sfv)[4], float (&bfv)[4], boo
     // One call site each for the certificate and the chains (the loop runs
     // at most twice: every inlined copy costs registers).
     int path = 0;
+    bool row_ready = false;
     for (;;) {
         if (!bad && certify()) break;
         int n = 0;
@@ -396,6 +399,10 @@ __device__ __forceinline__ int select_cert(float (&sfv)[4], float (&bfv)[4], boo
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 if (valid[i]) S.cand[lane + 64 * i] = lane + 64 * i;
+        }
+        if (!row_ready) {
+            prep_row();  // the row the chains read (the rmsnorm's: rebuilt here)
+            row_ready = true;
         }
         wave_sync();
         for (int c = lane; c < n; c += 64)
@@ -512,6 +519,9 @@ __global__ void __launch_bounds__(256) k_route_cert(CertArgs P)
             inv_s[wave] = 1.0f / sqrtf(ss / (float)D + 1e-6f);
         }
         __syncthreads();
+        if (tid < nt)
+            st_word(&inv_word[t0 + tid],
+                    ((uint64_t)__float_as_uint(inv_s[tid]) << 32) | (uint64_t)tag);
         for (int t = 0; t < nt; ++t) {
             float mx = 0.0f;
             for (int c = tid; c < D / 4; c += 256) {
@@ -530,9 +540,6 @@ __global__ void __launch_bounds__(256) k_route_cert(CertArgs P)
         if (P.x_amax && tid < nt)
             P.x_amax[t0 + tid] =
                 fmaxf(fmaxf(mx_s[tid][0], mx_s[tid][1]), fmaxf(mx_s[tid][2], mx_s[tid][3]));
-        if (tid < nt)
-            st_word(&inv_word[t0 + tid],
-                    ((uint64_t)__float_as_uint(inv_s[tid]) << 32) | (uint64_t)tag);
         return;
     }
 
@@ -665,6 +672,25 @@ __global__ void __launch_bounds__(256) k_route_cert(CertArgs P)
         const uint64_t *er = P.est + (size_t)t * E;
 #pragma unroll
         for (int i = 0; i < 4; ++i) wv[i] = ld_word(&er[min(lane + 64 * i, E - 1)]);
+        // with the rmsnorm: the token's scale, which its group publishes once
+        // its chain (run beside the sums) ends; read while the words above
+        // are in flight
+        float inv = 1.0f;
+        if (norm) {
+            uint64_t iw = ld_word(&inv_word[t]);
+            if ((uint32_t)(iw & 0xFFu) != tag && !ld_tagged(&inv_word[t], tag, iw)) {
+                // not published within the bound: the chain here (lane 0)
+                float ss = 0.0f;
+                if (lane == 0) {
+                    const float *xr = P.x + (size_t)t * D;
+                    for (int c = 0; c < D; ++c) ss = ss + xr[c] * xr[c];
+                }
+                ss = __shfl(ss, 0, 64);
+                inv = 1.0f / sqrtf(ss / (float)D + 1e-6f);
+            } else {
+                inv = __uint_as_float((uint32_t)(iw >> 32));
+            }
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int ee = lane + 64 * i;
@@ -677,28 +703,7 @@ __global__ void __launch_bounds__(256) k_route_cert(CertArgs P)
             }
         }
         if (norm) {
-            // inv from the rmsnorm's group (its chain ran beside the sums);
-            // S = inv T + bias and B = inv B_T + the bias add's rounding,
-            // then the reference's normalised row for the exact chains
-            uint64_t iw;
-            float inv;
-            if (ld_tagged(&inv_word[t], tag, iw)) {
-                inv = __uint_as_float((uint32_t)(iw >> 32));
-            } else {
-                // not published within the bound: this wave runs the chain
-                float *row = xs[wave];
-                for (int c = lane; c < D; c += 64) {
-                    const float v = P.x[(size_t)t * D + c];
-                    row[c] = v * v;
-                }
-                wave_sync();
-                float ss = 0.0f;
-                if (lane == 0)
-                    ss = orn_lds_seq_sum32_n<D / 32>(reinterpret_cast<const v4f *>(row));
-                ss = __shfl(ss, 0, 64);
-                inv = 1.0f / sqrtf(ss / (float)D + 1e-6f);
-                wave_sync();
-            }
+            // S = inv T + bias and B = inv B_T + the bias add's rounding
             const double u = 0x1p-24;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -717,16 +722,22 @@ __global__ void __launch_bounds__(256) k_route_cert(CertArgs P)
                 P.logits[(size_t)t * E + ee] = sf;
                 if (!(fabsf(sf) < 3e38f)) bad = true;
             }
-            float *row = xs[wave];
-            for (int c = lane; c < D; c += 64)
-                row[c] = P.norm_w[c] * (P.x[(size_t)t * D + c] * inv);
-            wave_sync();
         }
         bad = __ballot(bad) != 0ull;
         uint32_t *io = P.idx + (size_t)t * k;
         float *wo = P.w + (size_t)t * k;
-        const int path = select_cert(sfv, bfv, bad, xs[wave], Wq4, P.bias, D, E, k, P.mode, io,
-                                     wo, P.logits + (size_t)t * E, sel[wave], &lit_s);
+        // the exact chains read the reference's normalised row: rebuilt from
+        // x, w and the published scale only if a chain runs
+        auto prep_row = [&]() {
+            if (!norm) return;
+            const v4f *x4 = reinterpret_cast<const v4f *>(P.x + (size_t)t * D);
+            const v4f *w4 = reinterpret_cast<const v4f *>(P.norm_w);
+            v4f *r4 = reinterpret_cast<v4f *>(xs[wave]);
+#pragma unroll
+            for (int c = lane; c < D / 4; c += 64) r4[c] = w4[c] * (x4[c] * inv);
+        };
+        const int path = select_cert(sfv, bfv, bad, xs[wave], prep_row, Wq4, P.bias, D, E, k,
+                                     P.mode, io, wo, P.logits + (size_t)t * E, sel[wave], &lit_s);
         if (lane == 0 && path) atomicAdd(&chain_s, 1);
     }
     __syncthreads();
