@@ -280,9 +280,9 @@ __device__ __forceinline__ void cswap(Slot &a, Slot &b)
 // weights to io/wo and S.lidx/S.lw; logits_row gets the fp32 values the
 // weights come from.  Returns 0 (certified), 1 (candidates chained) or 2
 // (every logit chained).
-template <class PrepRow>
+template <class PrepRow, class Rescale>
 __device__ __forceinline__ int select_cert(float (&sfv)[4], float (&bfv)[4], bool bad,
-                                           const float *xrow, PrepRow prep_row,
+                                           const float *xrow, PrepRow prep_row, Rescale rescale,
                                            const v4f *Wq4, const float *bias,
                                            int D, int E, int k, int mode, uint32_t *io, float *wo,
                                            float *logits_row, SelLds &S, int *n_lit)
@@ -370,9 +370,22 @@ __device__ __forceinline__ int select_cert(float (&sfv)[4], float (&bfv)[4], boo
     // One call site each for the certificate and the chains (the loop runs
     // at most twice: every inlined copy costs registers).
     int path = 0;
-    bool row_ready = false;
+    bool row_ready = false, scaled = false;
     for (;;) {
-        if (!bad && certify()) break;
+        const bool ok = !bad && certify();
+        if (!scaled) {
+            // values given up to a positive scale (the caller's T-space):
+            // the certificate holds for any scale; the weights and chains
+            // need the values themselves
+            bool nf = false;
+            const float sc = rescale(nf);
+            if (sc != 0.0f) my_v = (float)((double)sc * (double)my_v);
+            if (nf) bad = true;
+            scaled = true;
+            if (ok && !bad) break;
+        } else if (ok) {
+            break;
+        }
         int n = 0;
         bool isc[4] = {false, false, false, false};
         int pos[4] = {0, 0, 0, 0};
@@ -675,8 +688,14 @@ __global__ void __launch_bounds__(256) k_route_cert(CertArgs P)
         // with the rmsnorm: the token's scale, which its group publishes once
         // its chain (run beside the sums) ends; read while the words above
         // are in flight
+        // with the rmsnorm: the token's scale, which its group publishes once
+        // its chain (run beside the sums) ends.  Without a bias and in the
+        // renormalising mode the selection is scale-invariant, so the first
+        // certificate runs on (T, B_T) before the scale is read (select_cert
+        // calls rescale() after it); otherwise the scale comes first.
+        const bool tspace = norm && !P.bias && P.mode == 0;
         float inv = 1.0f;
-        if (norm) {
+        auto get_inv = [&]() {
             uint64_t iw = ld_word(&inv_word[t]);
             if ((uint32_t)(iw & 0xFFu) != tag && !ld_tagged(&inv_word[t], tag, iw)) {
                 // not published within the bound: the chain here (lane 0)
@@ -690,21 +709,11 @@ __global__ void __launch_bounds__(256) k_route_cert(CertArgs P)
             } else {
                 inv = __uint_as_float((uint32_t)(iw >> 32));
             }
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int ee = lane + 64 * i;
-            sfv[i] = 0.0f;
-            bfv[i] = 0.0f;
-            if (ee < E) {
-                if ((uint32_t)(wv[i] & 0xFFu) != tag && !ld_tagged(&er[ee], tag, wv[i])) bad = true;
-                unpack_est(wv[i], sfv[i], bfv[i]);
-                if (!(fabsf(sfv[i]) < 3e38f)) bad = true;
-            }
-        }
-        if (norm) {
-            // S = inv T + bias and B = inv B_T + the bias add's rounding
+        };
+        // S = inv T + bias and B = inv B_T + the bias add's rounding
+        auto apply_scale = [&]() {
             const double u = 0x1p-24;
+            bool nf = false;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int ee = lane + 64 * i;
@@ -720,9 +729,31 @@ __global__ void __launch_bounds__(256) k_route_cert(CertArgs P)
                 bfv[i] = (fabs(Sc) < 3e38 && Bc < 1e30) ? f_up(Bc + fabs(Sc - (double)sf))
                                                          : 1.7e38f;
                 P.logits[(size_t)t * E + ee] = sf;
-                if (!(fabsf(sf) < 3e38f)) bad = true;
+                if (!(fabsf(sf) < 3e38f)) nf = true;
+            }
+            return __ballot(nf) != 0ull;
+        };
+        if (norm && !tspace) get_inv();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int ee = lane + 64 * i;
+            sfv[i] = 0.0f;
+            bfv[i] = 0.0f;
+            if (ee < E) {
+                if ((uint32_t)(wv[i] & 0xFFu) != tag && !ld_tagged(&er[ee], tag, wv[i])) bad = true;
+                unpack_est(wv[i], sfv[i], bfv[i]);
+                if (!(fabsf(sfv[i]) < 3e38f)) bad = true;
             }
         }
+        if (norm && !tspace && apply_scale()) bad = true;
+        // after select_cert's first certificate (T-space only): the scale,
+        // then the values in logit units; returns the scale (0: nothing done)
+        auto rescale = [&](bool &nf) -> float {
+            if (!tspace) return 0.0f;
+            get_inv();
+            nf = apply_scale();
+            return inv;
+        };
         bad = __ballot(bad) != 0ull;
         uint32_t *io = P.idx + (size_t)t * k;
         float *wo = P.w + (size_t)t * k;
@@ -736,8 +767,9 @@ __global__ void __launch_bounds__(256) k_route_cert(CertArgs P)
 #pragma unroll
             for (int c = lane; c < D / 4; c += 64) r4[c] = w4[c] * (x4[c] * inv);
         };
-        const int path = select_cert(sfv, bfv, bad, xs[wave], prep_row, Wq4, P.bias, D, E, k,
-                                     P.mode, io, wo, P.logits + (size_t)t * E, sel[wave], &lit_s);
+        const int path = select_cert(sfv, bfv, bad, xs[wave], prep_row, rescale, Wq4, P.bias, D,
+                                     E, k, P.mode, io, wo, P.logits + (size_t)t * E, sel[wave],
+                                     &lit_s);
         if (lane == 0 && path) atomicAdd(&chain_s, 1);
     }
     __syncthreads();
