@@ -124,33 +124,54 @@ __device__ inline void select_token(const float *__restrict__ lg, int E, int k, 
 
     // Lane r < k ends up holding the r-th selected (value, index).  The
     // rounds compare integer keys of the finite logits (same order, one
-    // integer max per reduction step).
+    // integer max per reduction step).  Each lane sorts its four (key, e)
+    // descending once and offers its head; a round's maximum must be offered
+    // by one lane only (equal heads: a tie), and the winner drops its head.
+    // An expert equal to the winner in the winner's own lane comes up as
+    // the next round's maximum, equal to the previous one, which the
+    // strict-order check catches (after the k-th it no longer matters).
     float my_v = 0.0f, mx = 0.0f, prev = 0.0f;
     int my_e = 0;
     if (!slow) {
+        int sk[4], se[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sk[i] = key[i];
+            se[i] = lane + 64 * i;
+        }
+        auto cs = [&](int a, int b) {
+            const bool sw = sk[b] > sk[a];
+            const int ka = sk[a], kb = sk[b], ea = se[a], eb = se[b];
+            sk[a] = sw ? kb : ka;
+            sk[b] = sw ? ka : kb;
+            se[a] = sw ? eb : ea;
+            se[b] = sw ? ea : eb;
+        };
+        cs(0, 1);
+        cs(2, 3);
+        cs(0, 2);
+        cs(1, 3);
+        cs(1, 2);
         const int rounds = k < E ? k + 1 : k;
         for (int r = 0; r < rounds; ++r) {
-            const int mk = wave_max_key(max(max(key[0], key[1]), max(key[2], key[3])));
-            const float m = key_value(mk);
-            uint64_t b[4];
-            int cnt = 0;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                b[i] = __ballot(key[i] == mk);
-                cnt += __popcll(b[i]);
-            }
-            if (cnt != 1) {  // a tie (or a -0/+0 pair): take the literal path
+            const int mk = wave_max_key(sk[0]);
+            const uint64_t bl = __ballot(sk[0] == mk);
+            if (__popcll(bl) != 1) {  // a tie (or a -0/+0 pair): take the literal path
                 slow = true;
                 break;
             }
-            int e = 0;
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (b[i]) e = 64 * i + __ffsll((unsigned long long)b[i]) - 1;
-            const bool hit = lane == (e & 63);  // the winner's lane; e >> 6 is uniform
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (hit && (e >> 6) == i) key[i] = INT_MIN;
+            const int owner = __ffsll((unsigned long long)bl) - 1;
+            const int e = __builtin_amdgcn_readlane(se[0], owner);
+            const float m = key_value(mk);
+            if (lane == owner) {
+                sk[0] = sk[1];
+                se[0] = se[1];
+                sk[1] = sk[2];
+                se[1] = se[2];
+                sk[2] = sk[3];
+                se[2] = se[3];
+                sk[3] = INT_MIN;
+            }
             if (r == 0) {
                 mx = m;
             } else {
