@@ -30,7 +30,7 @@
 #include <math.h>
 
 // Fused selection + dispatch up to 16 tokens (one token per wave): a wave
-// selects one token in ~3.5 us, so from 17 tokens on the separate k_select
+// selects one token in ~2 us, so from 17 tokens on the separate k_select
 // (a wave per token over many work groups) and k_dispatch launches are
 // faster (measured at 64 tokens: 13.6 against 24.4 us).
 #define ORN_FUSED_SELECT_T 16
