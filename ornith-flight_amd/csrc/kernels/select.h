@@ -280,13 +280,14 @@ __device__ __forceinline__ int dispatch_one(const int *lidx, const float *lw, in
                                             int items_max, int *slot_e)
 {
     const int lane = threadIdx.x & 63;
-    auto kept = [&](int j) {  // pair j survives the skip rule (model.c:1066) and is this share's
-        return !(lw[j] < 1e-6f) && (uint32_t)(lidx[j] - ep_lo) < (uint32_t)ep_n;
-    };
-    const bool valid = lane < k && kept(lane);
     const int e = lane < k ? lidx[lane] : 0;
+    const float wl = lane < k ? lw[lane] : 0.0f;
+    // pair `lane` survives the skip rule (model.c:1066) and is this share's
+    const bool valid = lane < k && !(wl < 1e-6f) && (uint32_t)(e - ep_lo) < (uint32_t)ep_n;
+    const uint64_t kb = __ballot(valid);
     int rank = 0;  // among the kept pairs, by expert id (the ids are distinct)
-    for (int j = 0; j < k; ++j) rank += (kept(j) && lidx[j] < e) ? 1 : 0;
+    for (int j = 0; j < k; ++j)
+        rank += (((kb >> j) & 1ull) && __builtin_amdgcn_readlane(e, j) < e) ? 1 : 0;
     const int hs = has_shared ? 1 : 0;
     const int n_slots = hs + __popcll(__ballot(valid));
     if (valid) {
